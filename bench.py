@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Headline benchmark: batched token sampling on one MI355X.
+
+Workload (the metric's shape): 128 rows x 248,320 bf16 logits,
+near-flat N(0, 0.1), top_k off, top_p 0.95, repetition / presence / frequency
+penalties over 32,768-token int32 histories, an independent Philox stream per row.
+One step = one ``vi_sample_rows`` call over all 128 rows (all rows take the
+full-vocabulary route: exactly one kernel launch).  Five distinct input sets
+(~402 MB) rotate across steps so the 256 MB Infinity Cache cannot serve repeats.
+
+Prints ONE JSON line: rows/s (whole job), achieved HBM GB/s of the kernel against
+MI355X's 8 TB/s peak (per-launch HIP events on the launch stream), the oracle's
+CPU rate on the same inputs, and a GPU-vs-oracle parity count for one step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sampled rows/sec + achieved HBM GB/s (% peak) at 128×248,320 bf16 logits"
+PEAK_GBPS = 8000.0
+ROWS, VOCAB, HISTORY, SETS = 128, 248_320, 32_768, 5
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--rows", type=int, default=ROWS)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+def traffic_from_profiles() -> float | None:
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/, if recorded)."""
+    f = ROOT / "profiles" / "full_kernel_config5_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}); rows are independent, "
+              "so N GPUs would run N copies of this step (see DESIGN.md, 'More than one GPU').", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import voidinfer_amd as vi
+    from voidinfer_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    assert vi.load().vi_init() == 0, "device is not gfx950"
+    rows = args.rows
+    print(f"[bench] generating {SETS} input sets of {rows}x{VOCAB} bf16 + {HISTORY}-token histories",
+          file=sys.stderr, flush=True)
+    sets = []
+    for s in range(SETS):
+        g = torch.Generator(device=dev)
+        g.manual_seed(1000 + s)
+        logits = (torch.randn(rows, VOCAB, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+        hist = torch.randint(0, VOCAB, (rows * HISTORY,), generator=g, device=dev, dtype=torch.int32)
+        offs = torch.arange(rows + 1, device=dev, dtype=torch.int64) * HISTORY
+        p = workloads.lane_params(rows, 5000 + s, top_k_choices=(0,), top_p_choices=(0.95,),
+                                  min_p_choices=(0.0,))
+        sets.append((logits, hist, offs, p, vi.to_device_bytes(p, dev)))
+    routes = ops.route_mask(sets[0][3])
+    assert routes == vi.ROUTE_FULL, routes
+
+    lib = vi.load()
+    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+    stats = torch.empty(rows * 32, dtype=torch.uint8, device=dev)
+    nb = lib.vi_sample_workspace_bytes(rows, VOCAB, HISTORY)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+    calls = []
+    for logits, hist, offs, _, p_dev in sets:
+        calls.append((logits.data_ptr(), 0, rows, VOCAB, VOCAB, p_dev.data_ptr(), hist.data_ptr(), offs.data_ptr(),
+                      HISTORY, tokens.data_ptr(), None, None, VOCAB, stats.data_ptr(), routes, ws.data_ptr(), nb,
+                      sptr))
+    fn = lib.vi_sample_rows
+
+    for i in range(args.warmup):
+        st = fn(*calls[i % SETS])
+        assert st == 0, st
+    torch.cuda.synchronize()
+
+    K = args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    print(f"[bench] timing {K} steps", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        starts[i].record(stream)
+        fn(*calls[i % SETS])
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch_ms = np.array([starts[i].elapsed_time(ends[i]) for i in range(K)])
+    total_ms = starts[0].elapsed_time(ends[-1])
+    ms_per_step = total_ms / K
+    rows_per_s = rows * K / (total_ms / 1e3)
+    kernel_ms = float(per_launch_ms.mean())
+    bytes_per_launch = rows * (VOCAB * 2 + HISTORY * 4)
+    achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
+
+    # stream-read probe (measured HBM read rate) over a 1 GiB buffer
+    probe = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    probe.fill_(1)
+    sink = torch.empty(2048, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ops.probe_read(probe, sink)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(10):
+        ops.probe_read(probe, sink)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    probe_gbps = (1 << 30) * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9
+    del probe
+
+    # parity of one step against the CPU oracle, and the CPU baseline on the same inputs
+    logits0, hist0, offs0, p0, p0_dev = sets[0]
+    fn(*calls[0])
+    torch.cuda.synchronize()
+    gpu_tok = tokens.cpu().numpy().copy()
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        import oracle
+        bits = logits0.view(torch.int16).cpu().numpy().view(np.uint16)
+        h = hist0.cpu().numpy()
+        o = offs0.cpu().numpy()
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 64)
+        oracle.lib()
+        t = time.perf_counter()
+        w_tok, _, _, _, margins = oracle.sample_rows(bits, oracle.BF16, p0, h, o, threads=threads)
+        cpu_s = time.perf_counter() - t
+        mism = [r for r in range(rows) if w_tok[r] != gpu_tok[r]]
+        unexplained = [r for r in mism if not (margins[r, 0] < 1e-6 or margins[r, 1] < 1e-6)]
+        parity = {"rows": rows, "mismatches": len(mism), "unexplained": len(unexplained)}
+        cpu = {"value": rows / cpu_s, "unit": "rows/s", "cores": threads, "kind": "port",
+               "sample": f"one full step of the workload ({rows} rows x {VOCAB} bf16, {HISTORY}-token "
+                         f"histories, input set 0) through oracle/liboracle.so (C++ restatement)"}
+
+    out = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config5: 128 lanes x 248,320 bf16 logits N(0,0.1), top_k off, top_p 0.95, "
+                               "rep/presence/frequency penalties over 32,768-token histories, Philox per row",
+                   "rows": rows, "vocabulary": VOCAB, "history": HISTORY, "input_sets": SETS,
+                   "kernel": "full_kernel<bf16> (voidinfer_amd/csrc/sample_full.hip)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_GBPS, "traffic": traffic_from_profiles(),
+                     "bytes_per_launch": bytes_per_launch, "kernel_ms": kernel_ms,
+                     "kernel_ms_p50": float(np.median(per_launch_ms)),
+                     "probe_read_gbps": probe_gbps, "frac_of_probe": achieved / probe_gbps},
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "host_wall_s": wall,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,229 @@
+/*
+ * voidinfer_sampling.h — C ABI of the MI355X (gfx950) token-sampling library.
+ *
+ * Plain pointers and sizes only; every entry point returns a vi_status and never
+ * throws.  Device pointers are HIP device memory; `stream` is a hipStream_t passed
+ * as void* (NULL = the default stream).  All launches are stream-ordered and
+ * asynchronous: no entry point synchronizes the host, so they are safe to record
+ * into a HIP graph (workspaces are carved, never allocated, inside a call).
+ *
+ * Each entry point names the reference interface it replaces
+ * (The8Darkness/voidinfer, file:line).
+ */
+#ifndef VOIDINFER_SAMPLING_H
+#define VOIDINFER_SAMPLING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+typedef int vi_status;
+enum {
+    VI_OK = 0,
+    VI_ERR_INVALID = 1,      /* bad argument (extent, null pointer, range)          */
+    VI_ERR_UNSUPPORTED = 2,  /* valid request outside what the kernels implement     */
+    VI_ERR_WORKSPACE = 3,    /* workspace missing, too small or misaligned           */
+    VI_ERR_LAUNCH = 4,       /* HIP launch / runtime error                           */
+    VI_ERR_DEVICE = 5        /* device query failed / not gfx950                     */
+};
+
+/* ---- logit storage types ----------------------------------------------- */
+enum { VI_BF16 = 0, VI_F16 = 1, VI_F32 = 2 };
+
+/* ---- per-row output flags (vi_sample_rows / vi_verify_rows) ------------ */
+enum {
+    VI_FLAG_NONFINITE = 1u,     /* a non-finite logit was skipped                       */
+    VI_FLAG_EMPTY = 2u,         /* no finite logit: token = vocabulary (invalid)        */
+    VI_FLAG_ZERO_Q = 4u,        /* verify: drafted token has zero draft probability     */
+    VI_FLAG_NO_RESIDUAL = 8u,   /* verify: residual mass <= 1e-9, corrected from p      */
+    VI_FLAG_BAD_HISTORY = 16u,  /* a history token outside [0, vocabulary) was ignored  */
+    VI_FLAG_ERROR = 0x80000000u /* the kernel could not finish this row (see status)    */
+};
+
+/* 16-byte decision row; identical layout to Exl3GreedyRow
+ * (src/exl3/greedy_packet.h:22-26). */
+typedef struct vi_greedy_row {
+    uint64_t serial;
+    int32_t token;
+    uint32_t nonfinite;
+} vi_greedy_row;
+
+/* Request sampling configuration of the coupled (reference-semantics) route;
+ * field-for-field Exl3DeviceSampling (src/exl3/sampled_select.h:17-28). */
+typedef struct vi_device_sampling {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    uint64_t seed;
+    float presence_penalty;
+    int32_t reserved;
+    const int32_t* first_occurrence; /* device int32[vocabulary] or NULL */
+} vi_device_sampling;
+
+/* First-occurrence value of a token that was never generated
+ * (kExl3AbsentOccurrence, src/exl3/sampled_select.h:16). */
+#define VI_ABSENT_OCCURRENCE 0x7f7f7f7f
+
+/* Per-row parameters of the batched (extended-semantics) sampler.  One row is
+ * one lane's next-token distribution.  Per row: history tokens get
+ * x' = (x>0 ? x/rep : x*rep) - freq*count - presence, stored back in the logit
+ * dtype; z = x' * (1/T); tokens sorted by (z desc, id asc); the first
+ * min(top_k, finite) form the cap set; weights w = exp(z - z_max); the support
+ * is the cap-set prefix cut at the first w < min_p and after the first
+ * cumulative w >= top_p * sum(cap set); the token is the first support entry
+ * whose cumulative w exceeds u * sum(support), u the Philox uniform of
+ * (seed, lane, position).  48 bytes. */
+typedef struct vi_row_params {
+    float temperature;        /* 0 = (penalized) argmax                               */
+    float top_p;              /* (0,1]; 1 disables                                    */
+    float min_p;              /* [0,1]; 0 disables                                    */
+    float repetition_penalty; /* > 0; 1 disables (HF convention)                      */
+    float presence_penalty;   /* OpenAI convention; 0 disables                        */
+    float frequency_penalty;  /* OpenAI convention; 0 disables                        */
+    int32_t top_k;            /* 0 disables                                           */
+    uint32_t lane;            /* Philox counter word: request lane                    */
+    uint64_t seed;            /* Philox key                                           */
+    int32_t position;         /* Philox counter word: absolute position of the token  */
+    uint32_t reserved;
+} vi_row_params;
+
+/* Optional per-row diagnostics of vi_sample_rows. */
+typedef struct vi_sample_stats {
+    uint32_t flags;           /* VI_FLAG_*                                            */
+    uint32_t support;         /* tokens in the truncated support                      */
+    uint32_t finite;          /* finite logits in the row                             */
+    uint32_t reserved;
+    double support_mass;      /* sum of exp(z - z_max) over the support               */
+    double uniform;           /* the Philox uniform the draw consumed                 */
+} vi_sample_stats;
+
+/* ---- device / library ----------------------------------------------------
+ * Workspaces are caller-owned device memory of the size the matching
+ * *_workspace_bytes returns.  A workspace must be zero-filled once before its
+ * first use (its arrival counters and barriers start at zero); every kernel
+ * leaves it reusable (self-resetting counters), so no per-call memset is needed.
+ * Calls that share one workspace must be ordered on one stream. */
+
+/* Fails with VI_ERR_DEVICE unless the current HIP device is gfx950. */
+vi_status vi_init(void);
+const char* vi_status_string(vi_status status);
+/* Version of this ABI (bumped on any layout change). */
+uint32_t vi_abi_version(void);
+
+/* ---- greedy argmax --------------------------------------------------------
+ * Replaces exl3_launch_greedy_packet (src/exl3/greedy_packet.cuh:256-272) and
+ * the exact_row_score_kernel argmax (src/exl3/text_model.cu:11393-11420).
+ * Per row: largest finite value, lowest id on ties, any non-finite flagged and
+ * skipped; token = vocabulary when no value is finite.  Rows are unbounded
+ * (the reference caps at 16). */
+size_t vi_greedy_workspace_bytes(int rows, int vocabulary);
+vi_status vi_greedy_rows(const void* logits, int dtype, int rows, int vocabulary,
+                         int64_t row_stride, uint64_t serial, vi_greedy_row* out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- exact top-k ------------------------------------------------------------
+ * Replaces dflash2_topk16_for_test / launch_dflash_topk16_segmented
+ * (src/exl3/dflash2_draft.cu:2366-2420; dflash2_draft.h:198-202).
+ * Exact top-k (1 <= k <= 64, k <= vocabulary) in (value desc, id asc) order;
+ * rows containing NaN keep the reference's serial-insertion semantics
+ * (dflash2_draft.cu:1827-1862).  `logprobs` (optional) receives
+ * value - logsumexp(row) (NaN for rows with a non-finite value);
+ * `nonfinite_flag` (optional) is set to 1 when any value of any row is
+ * non-finite (dflash_nonfinite_flag_kernel, dflash2_draft.cu:2473-2485). */
+size_t vi_topk_workspace_bytes(int rows, int vocabulary, int k);
+vi_status vi_topk_rows(const void* logits, int dtype, int rows, int vocabulary,
+                       int64_t row_stride, int k, int64_t* ids, float* values,
+                       float* logprobs, uint32_t* nonfinite_flag,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- coupled sampled packet (reference semantics) ----------------------------
+ * Replaces exl3_launch_sampled_packet (src/exl3/sampled_select.cuh:362-377):
+ * presence-penalized top-min(top_k,20) candidates, min_p / top_p truncation and
+ * the Gumbel-max draw keyed by (seed, first_key + depth[r], token).  `depths`
+ * and `inputs` are host arrays of `rows` entries or NULL, exactly as the
+ * reference's spans.  rows <= 16 (the reference's packet capacity). */
+size_t vi_sampled_packet_workspace_bytes(int rows, int vocabulary);
+vi_status vi_sampled_packet(const void* scores, int dtype, int rows, int vocabulary,
+                            int64_t row_stride, const vi_device_sampling* cfg,
+                            int first_key, const int32_t* depths, int n_depths,
+                            const int32_t* inputs, int n_inputs, uint64_t serial,
+                            vi_greedy_row* out, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* First-occurrence table maintenance; replaces exl3_presence_reset /
+ * _truncate / _record (src/exl3/sampled_select.h:33-35,
+ * src/exl3/text_model.cu:12139-12173). */
+vi_status vi_presence_reset(int32_t* table, int vocabulary, void* stream);
+vi_status vi_presence_truncate(int32_t* table, int vocabulary, int from, void* stream);
+vi_status vi_presence_record(int32_t* table, int vocabulary, int first,
+                             const int64_t* tokens, size_t count, void* stream);
+
+/* ---- batched sampler (extended semantics) ----------------------------------
+ * New batched entry for many lanes (the reference's packet stops at 16 rows,
+ * sampled_select.cuh:200-216): per-row temperature, top-k, top-p, min-p,
+ * repetition / presence / frequency penalties over the lane's int32 history
+ * histories[history_offsets[r] .. history_offsets[r+1]), and a Philox4x32-10
+ * inverse-CDF draw keyed by (seed, lane, position).  `params`, `histories`,
+ * `history_offsets` and every output are device pointers.  Optional outputs:
+ * `uniforms` (double[rows]), `probs` (float[rows][probs_stride], the filtered
+ * distribution), `stats`.  `max_history` bounds every row's history length
+ * (it sizes the workspace); a longer history fails that row.  Supported:
+ * bf16/fp16 logits for any row; fp32 logits for rows with 1 <= top_k <= 64 or
+ * temperature 0.  A row the kernels cannot finish gets token -1 and
+ * VI_FLAG_ERROR in its stats. */
+/* route_mask: which kernels run.  VI_ROUTE_TOPK serves rows with temperature 0
+ * or 1 <= top_k <= 64, VI_ROUTE_FULL every other row; rows whose route is not in
+ * the mask are left unwritten.  VI_ROUTE_ALL (or 0) runs both. */
+enum { VI_ROUTE_TOPK = 1u, VI_ROUTE_FULL = 2u, VI_ROUTE_ALL = 3u };
+size_t vi_sample_workspace_bytes(int rows, int vocabulary, int64_t max_history);
+vi_status vi_sample_rows(const void* logits, int dtype, int rows, int vocabulary,
+                         int64_t row_stride, const vi_row_params* params,
+                         const int32_t* histories, const int64_t* history_offsets,
+                         int64_t max_history, int32_t* tokens, double* uniforms, float* probs,
+                         int64_t probs_stride, vi_sample_stats* stats, uint32_t route_mask,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- DFlash2 verification ---------------------------------------------------
+ * Replaces the host decisions decide_exl3_outer_prefix
+ * (src/exl3/exact_outer_reference.h:68-82) in greedy mode and
+ * Exl3IndependentAcceptanceReference::evaluate
+ * (src/exl3/sampled_acceptance_reference.h:48-88) in sampled mode, applied per
+ * lane over `drafts` drafted positions with the target softmax fused in.
+ * target: [lanes][target_rows][target_stride], target_rows = drafts or
+ * drafts + 1 (bonus row); draft: [lanes][drafts][draft_stride];
+ * drafted: int32 [lanes][drafts]; params: one vi_row_params per lane (its
+ * `position` is the absolute position of drafted row 0); terminal: optional
+ * device list of stop tokens.  Outputs: accepted[lanes], committed
+ * [lanes][drafts + 1] (unused slots = -1), committed_count[lanes],
+ * lane_flags[lanes] (optional).  Sampled mode requires 1 <= top_k <= 64. */
+enum { VI_VERIFY_GREEDY = 0, VI_VERIFY_SAMPLED = 1 };
+size_t vi_verify_workspace_bytes(int lanes, int drafts, int vocabulary);
+vi_status vi_verify_rows(int mode, const void* target, int target_dtype,
+                         int64_t target_stride, int target_rows,
+                         const void* draft, int draft_dtype, int64_t draft_stride,
+                         int lanes, int drafts, int vocabulary,
+                         const int32_t* drafted, const vi_row_params* params,
+                         const int64_t* terminal, int n_terminal,
+                         int32_t* accepted, int32_t* committed,
+                         int32_t* committed_count, uint32_t* lane_flags,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- measurement helpers ------------------------------------------------------
+ * Stream-read probe (the gfx950 analogue of tools/hbm_bandwidth_probe.cu:1-45):
+ * reads `bytes` from `src` with 16-byte loads and writes one word per
+ * workgroup to `sink` (2048 words). */
+vi_status vi_probe_read(const void* src, size_t bytes, uint32_t* sink, void* stream);
+/* Plain device copy of `bytes` (16-byte aligned), the FETCH_SIZE calibration
+ * kernel. */
+vi_status vi_probe_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOIDINFER_SAMPLING_H */

@@ -1,0 +1,103 @@
+"""GPU DFlash2 verification vs the oracle.
+
+Greedy mode: decide_exl3_outer_prefix over the target rows' argmax, bit-exact
+(accepted lengths, committed ids, stop tokens, bonus row).  Sampled mode: the FP64
+rejection rule of sampled_acceptance_reference.h on the filtered target / draft
+distributions (T .7, top_p .8, top_k 20), Philox u_a / u_c; accepted lengths and
+committed ids must be bit-exact except where |u_a - min(1, p/q)| < 1e-9 at a
+decided position (reported by the oracle).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def sampler_from_draft(orc, params):
+    rng = np.random.default_rng(99)
+
+    def draw(row_f32, lane, j):
+        bits = row_f32.astype(np.float16).view(np.uint16)
+        prob, _ = orc.row_distribution(bits, 1, params[lane])
+        return int(rng.choice(prob.size, p=prob / prob.sum()))
+    return draw
+
+
+def run(orc, dev, mode, tbits, dbits, drafted, p, lanes, drafts, terminal=()):
+    import voidinfer_amd as vi
+    t = to_dev(tbits, 0, dev)
+    d = to_dev(dbits, 1, dev) if dbits is not None else None
+    dr = torch.from_numpy(np.ascontiguousarray(drafted, dtype=np.int32)).to(dev)
+    g = vi.verify_rows(mode, t, dr, lanes, drafts, draft=d, params=p, terminal=terminal)
+    w = orc.verify_rows(mode, tbits, 0, dbits, 1, lanes, drafts, drafted, p, terminal)
+    return g, w
+
+
+def assert_same(g, w, exempt_lanes=()):
+    ga, gc, gn, gf = g
+    wa, wc, wn, wf, _ = w
+    for l in range(len(wa)):
+        if l in exempt_lanes:
+            continue
+        assert ga[l] == wa[l] and gn[l] == wn[l] and np.array_equal(gc[l], wc[l]) and gf[l] == wf[l], (
+            l, ga[l], wa[l], gc[l], wc[l], gf[l], wf[l])
+
+
+@pytest.mark.parametrize("bonus", [False, True])
+def test_greedy_prefix(orc, dev, bonus):
+    from voidinfer_amd import workloads as W
+    lanes, drafts = 8, 16
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, bonus=bonus)
+    # make lanes accept 0..drafts tokens: copy the target's argmax into the drafts
+    trows = drafts + 1 if bonus else drafts
+    targ = orc.greedy_rows(tb, 0)["token"].reshape(lanes, trows)
+    for l in range(lanes):
+        k = (2 * l + 1) % (drafts + 1) if l < lanes - 1 else drafts
+        drafted[l, :k] = targ[l, :k]
+    g, w = run(orc, dev, 0, tb, None, drafted, p, lanes, drafts)
+    assert_same(g, w)
+    assert w[0].max() == drafts
+
+
+def test_greedy_terminal_stop(orc, dev):
+    from voidinfer_amd import workloads as W
+    lanes, drafts = 4, 8
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, vocab=20_000)
+    targ = orc.greedy_rows(tb, 0)["token"].reshape(lanes, drafts)
+    drafted[:] = targ
+    term = [int(targ[1, 3]), int(targ[2, 0])]
+    g, w = run(orc, dev, 0, tb, None, drafted, p, lanes, drafts, terminal=term)
+    assert_same(g, w)
+    assert w[0][1] <= 4 and w[0][2] == 1
+
+
+@pytest.mark.parametrize("bonus", [False, True])
+def test_sampled_rejection(orc, dev, bonus):
+    from voidinfer_amd import workloads as W
+    lanes, drafts = 8, 16
+    p0 = W.config4(lanes=lanes, drafts=drafts, vocab=W.V_QWEN, bonus=bonus)[3]
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, bonus=bonus, sample_fn=sampler_from_draft(orc, p0))
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    margins = w[4]
+    exempt = {l for l in range(lanes) if np.min(margins[l]) < 1e-9}
+    assert_same(g, w, exempt)
+    assert len(exempt) <= 1
+
+
+def test_sampled_many_lanes_small_vocab(orc, dev, rng):
+    from voidinfer_amd import workloads as W
+    lanes, drafts, vocab = 64, 6, 3000
+    p0 = W.config4(lanes=lanes, drafts=drafts, vocab=vocab)[3]
+    p0["top_k"] = rng.choice([1, 5, 20, 64], lanes)
+    p0["top_p"] = rng.choice([0.5, 0.9, 1.0], lanes)
+    p0["min_p"] = rng.choice([0.0, 0.1], lanes)
+    p0["temperature"] = rng.choice([0.0, 0.5, 1.0], lanes)
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, vocab=vocab, sample_fn=sampler_from_draft(orc, p0))
+    p[:] = p0
+    drafted[::5, 2] = 0        # some zero-q proposals
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-9}
+    assert_same(g, w, exempt)

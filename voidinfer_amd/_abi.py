@@ -1,0 +1,106 @@
+"""ctypes view of include/voidinfer_sampling.h (the C ABI of libvoidinfer_sampling.so).
+
+Struct layouts are mirrored twice: as numpy dtypes (for building device arrays of
+parameters / reading outputs) and as ctypes structures (for by-pointer host
+arguments).  ``load()`` raises ImportError when the built library is missing, so
+no caller can silently fall back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libvoidinfer_sampling.so"
+
+BF16, F16, F32 = 0, 1, 2
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_DEVICE = range(6)
+FLAG_NONFINITE, FLAG_EMPTY, FLAG_ZERO_Q, FLAG_NO_RESIDUAL, FLAG_BAD_HISTORY = 1, 2, 4, 8, 16
+FLAG_ERROR = 0x80000000
+VERIFY_GREEDY, VERIFY_SAMPLED = 0, 1
+ROUTE_TOPK, ROUTE_FULL, ROUTE_ALL = 1, 2, 3
+ABSENT_OCCURRENCE = 0x7F7F7F7F
+
+GREEDY_ROW = np.dtype([("serial", "<u8"), ("token", "<i4"), ("nonfinite", "<u4")])
+ROW_PARAMS = np.dtype([
+    ("temperature", "<f4"), ("top_p", "<f4"), ("min_p", "<f4"),
+    ("repetition_penalty", "<f4"), ("presence_penalty", "<f4"), ("frequency_penalty", "<f4"),
+    ("top_k", "<i4"), ("lane", "<u4"), ("seed", "<u8"), ("position", "<i4"), ("reserved", "<u4"),
+])
+SAMPLE_STATS = np.dtype([
+    ("flags", "<u4"), ("support", "<u4"), ("finite", "<u4"), ("reserved", "<u4"),
+    ("support_mass", "<f8"), ("uniform", "<f8"),
+])
+assert GREEDY_ROW.itemsize == 16 and ROW_PARAMS.itemsize == 48 and SAMPLE_STATS.itemsize == 32
+
+
+class DeviceSampling(C.Structure):
+    """vi_device_sampling == Exl3DeviceSampling (src/exl3/sampled_select.h:17-28)."""
+    _fields_ = [
+        ("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
+        ("seed", C.c_uint64), ("presence_penalty", C.c_float), ("reserved", C.c_int32),
+        ("first_occurrence", C.c_void_p),
+    ]
+
+
+assert C.sizeof(DeviceSampling) == 40
+
+_vp, _i, _i64, _u64, _sz, _u32 = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_size_t, C.c_uint32
+
+SIGNATURES = {
+    "vi_init": ([], _i),
+    "vi_status_string": ([_i], C.c_char_p),
+    "vi_abi_version": ([], _u32),
+    "vi_greedy_workspace_bytes": ([_i, _i], _sz),
+    "vi_greedy_rows": ([_vp, _i, _i, _i, _i64, _u64, _vp, _vp, _sz, _vp], _i),
+    "vi_topk_workspace_bytes": ([_i, _i, _i], _sz),
+    "vi_topk_rows": ([_vp, _i, _i, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i),
+    "vi_sampled_packet_workspace_bytes": ([_i, _i], _sz),
+    "vi_sampled_packet": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, _vp, _i, _vp, _i, _u64,
+                           _vp, _vp, _sz, _vp], _i),
+    "vi_presence_reset": ([_vp, _i, _vp], _i),
+    "vi_presence_truncate": ([_vp, _i, _i, _vp], _i),
+    "vi_presence_record": ([_vp, _i, _i, _vp, _sz, _vp], _i),
+    "vi_sample_workspace_bytes": ([_i, _i, _i64], _sz),
+    "vi_sample_rows": ([_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _u32, _vp, _sz,
+                        _vp], _i),
+    "vi_verify_workspace_bytes": ([_i, _i, _i], _sz),
+    "vi_verify_rows": ([_i, _vp, _i, _i64, _i, _vp, _i, _i64, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                        _vp, _sz, _vp], _i),
+    "vi_probe_read": ([_vp, _sz, _vp, _vp], _i),
+    "vi_probe_copy": ([_vp, _vp, _sz, _vp], _i),
+}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load the in-tree library (ImportError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m voidinfer_amd.build` "
+                "(there is no CPU fallback)")
+        lib = C.CDLL(str(LIB_PATH))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+class VIError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        msg = load().vi_status_string(status).decode()
+        super().__init__(f"{what}: {msg} (status {status})")
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        if status == ERR_INVALID:
+            raise ValueError(f"{what}: invalid argument")
+        raise VIError(status, what)

@@ -1,0 +1,134 @@
+// greedy.hip — greedy argmax rows (the gfx950 replacement of
+// exl3_greedy_packet_{,wide_,split_}kernel, src/exl3/greedy_packet.cuh:15-246).
+//
+// Semantics (greedy_packet.cuh:12-14): per row, the largest finite value with
+// the lowest index on ties; non-finite values are skipped and flagged; index =
+// vocabulary when no value is finite.  Only comparisons, so the partition of the
+// row into slices cannot change the answer.
+//
+// Shape: grid (slices, rows), 256 threads.  Each workgroup reduces one slice of
+// one row (16-byte loads, wave64 xor-shuffle reduction, 4-wave LDS reduction);
+// with more than one slice the last workgroup of a row to arrive (self-resetting
+// arrival counter, as greedy_packet.cuh:139-246) reduces the slice partials in
+// slice order.  Roofline: HBM, V x sizeof(logit) bytes per row.
+#include "row_scan.h"
+#include "vi_internal.h"
+
+namespace vi {
+namespace {
+
+constexpr int kGreedyThreads = 256;
+
+struct GreedyPartial {
+    float best;
+    int index;
+    uint32_t bad;
+    uint32_t pad;
+};
+
+__device__ __forceinline__ void greedy_combine(float& best, int& index, float ob, int oi) {
+    if (ob > best || (ob == best && oi < index)) { best = ob; index = oi; }
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
+    const void* logits, int vocabulary, int64_t stride, int slice_len, uint64_t serial,
+    vi_greedy_row* out, GreedyPartial* partials, uint32_t* arrivals) {
+    const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
+    const void* row = static_cast<const unsigned char*>(logits) + size_t(r) * size_t(stride) * sizeof(typename Elem<DT>::Bits);
+    const int begin = slice * slice_len, end = min(vocabulary, begin + slice_len);
+    float best = -kInfF;
+    int index = vocabulary;
+    bool bad = false;
+    scan_slice<DT, VEC, kGreedyThreads>(row, begin, end, [&](uint32_t bits, int id, bool ok) {
+        if (!ok) return;
+        const float x = Elem<DT>::decode(bits);
+        if (!Elem<DT>::finite_bits(bits)) { bad = true; return; }
+        if (x > best || (x == best && id < index)) { best = x; index = id; }
+    });
+#pragma unroll
+    for (int o = 32; o; o >>= 1) greedy_combine(best, index, shfl_xor_f(best, o), shfl_xor_i(index, o));
+    const bool wave_bad = ballot(bad) != 0;
+    __shared__ float s_best[kGreedyThreads / kWave];
+    __shared__ int s_index[kGreedyThreads / kWave];
+    __shared__ uint32_t s_bad[kGreedyThreads / kWave];
+    __shared__ bool s_last;
+    const int wave = threadIdx.x / kWave, lane = lane_id();
+    if (lane == 0) { s_best[wave] = best; s_index[wave] = index; s_bad[wave] = wave_bad; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t b = 0;
+        for (int w = 0; w < kGreedyThreads / kWave; ++w) { greedy_combine(best, index, s_best[w], s_index[w]); b |= s_bad[w]; }
+        if (slices == 1) {
+            out[r].serial = serial; out[r].token = index; out[r].nonfinite = b;
+            return;
+        }
+        GreedyPartial& p = partials[size_t(r) * slices + slice];
+        p.best = best; p.index = index; p.bad = b;
+        __threadfence();
+        s_last = atomicAdd(&arrivals[r], 1u) == uint32_t(slices - 1);
+    }
+    if (slices == 1) return;
+    __syncthreads();
+    if (!s_last || wave != 0) return;
+    __threadfence();
+    best = -kInfF; index = vocabulary;
+    uint32_t b = 0;
+    for (int s = lane; s < slices; s += kWave) {
+        const GreedyPartial p = partials[size_t(r) * slices + s];
+        greedy_combine(best, index, p.best, p.index);
+        b |= p.bad;
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) greedy_combine(best, index, shfl_xor_f(best, o), shfl_xor_i(index, o));
+    const bool any_bad = ballot(b != 0) != 0;
+    if (lane == 0) {
+        arrivals[r] = 0u;
+        out[r].serial = serial; out[r].token = index; out[r].nonfinite = any_bad ? 1u : 0u;
+    }
+}
+
+}  // namespace
+
+GreedyPlan greedy_plan(int rows, int vocabulary) {
+    // Aim for >= 1024 workgroups (4 per CU) with slices of >= 4096 logits.
+    int slices = rows >= 1024 ? 1 : (1024 + rows - 1) / rows;
+    slices = std::min(slices, std::max(1, vocabulary / 4096));
+    slices = std::max(1, std::min(slices, 128));
+    const int len = slice_len_for(vocabulary, slices);
+    slices = (vocabulary + len - 1) / len;
+    return {slices, len};
+}
+
+size_t greedy_workspace(int rows, int vocabulary) {
+    const GreedyPlan p = greedy_plan(rows, vocabulary);
+    if (p.slices == 1) return 0;
+    return align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256) + align_up(size_t(rows) * 4, 256);
+}
+
+vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                        uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
+                        hipStream_t stream) {
+    const GreedyPlan p = greedy_plan(rows, vocabulary);
+    GreedyPartial* partials = nullptr;
+    uint32_t* arrivals = nullptr;
+    if (p.slices > 1) {
+        Carver c(ws, ws_bytes);
+        partials = c.take<GreedyPartial>(size_t(rows) * p.slices);
+        arrivals = c.take<uint32_t>(size_t(rows));
+        if (!c.ok) return VI_ERR_WORKSPACE;
+    }
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && ((stride * elem_size(dtype)) % 16 == 0);
+    const dim3 grid(p.slices, rows), block(kGreedyThreads);
+#define VI_GREEDY_LAUNCH(DT, V) \
+    hipLaunchKernelGGL((greedy_kernel<DT, V>), grid, block, 0, stream, logits, vocabulary, stride, p.slice_len, serial, out, partials, arrivals)
+    switch (dtype) {
+        case VI_BF16: if (vec) VI_GREEDY_LAUNCH(VI_BF16, true); else VI_GREEDY_LAUNCH(VI_BF16, false); break;
+        case VI_F16: if (vec) VI_GREEDY_LAUNCH(VI_F16, true); else VI_GREEDY_LAUNCH(VI_F16, false); break;
+        default: if (vec) VI_GREEDY_LAUNCH(VI_F32, true); else VI_GREEDY_LAUNCH(VI_F32, false); break;
+    }
+#undef VI_GREEDY_LAUNCH
+    return launch_status();
+}
+
+}  // namespace vi

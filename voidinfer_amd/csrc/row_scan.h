@@ -1,0 +1,59 @@
+// row_scan.h — the streaming loop shared by the slice kernels: each workgroup
+// walks [begin, end) of one logit row with 16-byte loads (four in flight per
+// thread) or, for rows whose stride breaks 16-byte alignment, with coalesced
+// element loads.  `fn(bits, id, valid)` sees every element once; loop trip
+// counts are wave-uniform (lanes past the end get valid = false), so callers may
+// use cross-lane operations inside `fn`.  The visiting order is irrelevant to
+// the callers (all of them reduce with order-free comparisons).
+#pragma once
+
+#include "vi_device.h"
+
+namespace vi {
+
+template <int DT, bool VEC, int NT, class F>
+__device__ __forceinline__ void scan_slice(const void* row, int begin, int end, F&& fn) {
+    constexpr int P = Elem<DT>::kPerVec;
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+        // begin is a multiple of 64 elements; full vectors first, then the tail.
+        const int nvec = (end - begin) / P;
+        const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
+        constexpr int U = 4;
+        for (int vb = 0; vb < nvec; vb += U * NT) {
+            uint4 d[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = vb + u * NT + tid;
+                d[u] = v < nvec ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = vb + u * NT + tid;
+                const bool ok = v < nvec;
+#pragma unroll
+                for (int j = 0; j < P; ++j) fn(vec_bits<DT>(d[u], j), begin + v * P + j, ok);
+            }
+        }
+        for (int ib = begin + nvec * P; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    } else {
+        for (int ib = begin; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    }
+}
+
+// Slice boundaries: slice s of `slices` covers [s*len, min(V,(s+1)*len)), len a
+// multiple of 64 elements.
+__host__ __device__ inline int slice_len_for(int vocabulary, int slices) {
+    const int len = (vocabulary + slices - 1) / slices;
+    return (len + 63) / 64 * 64;
+}
+
+}  // namespace vi

@@ -1,0 +1,660 @@
+// topk.hip — exact top-k selection over logit rows and the samplers built on it.
+//
+// One kernel family, three consumers:
+//  * kModeTopk   — DFlash2 draft top-k (dflash2_draft.cu:1827-2342): ids and raw
+//                  values in (value desc, id asc) order, NaN rows in the serial
+//                  insertion order of dflash_topk16_serial_row, plus log-probs.
+//  * kModePacket — the coupled reference sampler (sampled_select.cuh:79-279):
+//                  presence-penalized top-min(top_k,20) candidates, min_p/top_p
+//                  truncation and the Gumbel-max draw.
+//  * kModeSample — rows of the batched sampler whose support lies in a top-k
+//                  list (1 <= top_k <= 64, or temperature 0).
+//
+// Shape: grid (slices, rows), 256 threads (4 waves).  Each wave keeps a sorted
+// top-K list distributed over its lanes (lane i = rank i, K <= 64): an element
+// is offered only if it beats the list's K-th entry (one compare + ballot per
+// element), and accepted candidates are inserted with a ballot/ds_bpermute
+// shift.  The four wave lists merge in LDS, each workgroup publishes its slice
+// list, and the last workgroup of a row to arrive (self-resetting counter)
+// merges the slice lists and finishes the row.  Roofline: HBM, V x sizeof(logit)
+// per row; the per-element work is a compare and a ballot.
+#include <math.h>
+
+#include "row_scan.h"
+#include "vi_internal.h"
+
+namespace vi {
+namespace {
+
+constexpr int kTopkThreads = 256;
+constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kMaxK = 64;
+constexpr int kInvalidId = 0x7fffffff;
+
+struct SliceHeader {
+    uint32_t flags;     // bit0 non-finite seen, bit1 NaN seen, bit2 bad history, bit3 error
+    uint32_t valid;     // finite elements (sampler rows)
+    float lse_max;      // log-sum-exp partial (top-k mode)
+    float pad;
+    double lse_sum;
+};
+constexpr uint32_t kSliceNonfinite = 1u, kSliceNan = 2u, kSliceBadHistory = 4u, kSliceError = 8u;
+
+struct TopkArgs {
+    const void* logits;
+    int vocabulary;
+    int64_t stride;
+    int slice_len;
+    float* pval;            // [rows][slices][kMaxK]
+    int* pidx;
+    SliceHeader* phdr;      // [rows][slices]
+    uint32_t* arrivals;     // [rows]
+    // kModeTopk
+    int k;
+    int64_t* ids;
+    float* values;
+    float* logprobs;
+    uint32_t* nonfinite_flag;
+    // kModePacket
+    vi_device_sampling cfg;
+    PacketKeys keys;
+    uint64_t serial;
+    vi_greedy_row* out_rows;
+    // kModeSample
+    const vi_row_params* params;
+    const uint2* hash;      // [rows][hash_slots] (token+1, count)
+    const uint32_t* row_flags;  // [rows] from the hash builder (bad history / error)
+    int hash_shift;         // 32 - log2(hash_slots)
+    int hash_slots;
+    const int64_t* offsets;
+    int32_t* tokens;
+    double* uniforms;
+    float* probs;
+    int64_t probs_stride;
+    vi_sample_stats* stats;
+    int full_rows_unsupported;  // fp32 logits: rows outside the top-k route fail
+    // kModeVerify: sorted lists of the filtered rows
+    int params_div;         // params index = row / params_div
+    float* lval;            // [rows][kMaxK]
+    int* lidx;
+    uint32_t* lvalid;       // [rows]
+    uint32_t* lflags;       // [rows]
+};
+
+// ----------------------------------------------------------- wave-resident list
+struct WaveList {
+    float v = -kInfF;   // this lane's entry (rank = lane)
+    int i = kInvalidId;
+    float kv = -kInfF;  // entry K-1, wave-uniform
+    int ki = kInvalidId;
+};
+
+__device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci) {
+    const int lane = lane_id();
+    const uint64_t m = ballot(lane < K && better(cv, ci, L.v, L.i));
+    if (!m) return;
+    const int pos = __builtin_ctzll(m);
+    const float pv = shift_up_f(L.v);
+    const int pi = shift_up_i(L.i);
+    if (lane == pos) { L.v = cv; L.i = ci; }
+    else if (lane > pos && lane < K) { L.v = pv; L.i = pi; }
+    L.kv = readlane_f(L.v, K - 1);
+    L.ki = readlane_i(L.i, K - 1);
+}
+
+// Offer one candidate per lane (wave-uniform call).
+__device__ __forceinline__ void list_offer(WaveList& L, int K, bool ok, float v, int id) {
+    uint64_t m = ballot(ok && better(v, id, L.kv, L.ki));
+    while (m) {
+        const int src = __builtin_ctzll(m);
+        m &= m - 1;
+        const float cv = readlane_f(v, src);
+        const int ci = readlane_i(id, src);
+        if (better(cv, ci, L.kv, L.ki)) list_insert(L, K, cv, ci);
+    }
+}
+
+// Count of `token` in the row's history hash (0 if absent).
+__device__ __forceinline__ uint32_t hash_count(const uint2* table, int shift, int slots, int token) {
+    uint32_t s = (uint32_t(token) * 0x9E3779B1u) >> shift;
+    for (int probe = 0; probe < slots; ++probe) {
+        const uint2 e = table[s];
+        if (e.x == uint32_t(token) + 1u) return e.y;
+        if (e.x == 0u) return 0u;
+        s = (s + 1u) & uint32_t(slots - 1);
+    }
+    return 0u;
+}
+
+// Largest finite magnitude a penalty could push past the dtype's range.
+template <int DT> __device__ __forceinline__ float overflow_guard() {
+    if constexpr (DT == VI_F16) return 16384.0f;
+    else return 1.0e37f;
+}
+
+// ------------------------------------------------------- NaN rows (top-k mode)
+// dflash_topk16_serial_row (dflash2_draft.cu:1827-1862), generalized to k.
+template <int DT>
+__device__ void serial_topk_row(const void* row, int vocabulary, int k, float* vals, int* ids) {
+    int count = 0;
+    for (int c = 0; c < vocabulary; ++c) {
+        const float value = Elem<DT>::decode(load_bits<DT>(row, c));
+        if (count < k) {
+            int j = count;
+            while (j > 0 && vals[j - 1] < value) { vals[j] = vals[j - 1]; ids[j] = ids[j - 1]; --j; }
+            vals[j] = value; ids[j] = c; ++count;
+        } else if (value > vals[k - 1]) {
+            int j = k - 1;
+            while (j > 0 && vals[j - 1] < value) { vals[j] = vals[j - 1]; ids[j] = ids[j - 1]; --j; }
+            vals[j] = value; ids[j] = c;
+        }
+    }
+}
+
+// ------------------------------------------------------------- finishing steps
+// Coupled draw over the sorted candidates (sampled_select.cuh:79-116); nvcc's
+// default contraction fuses the two multiply-adds, restated with fmaf.
+__device__ int packet_draw(const vi_device_sampling& cfg, int key, int cap, const float* cand_val,
+                           const int* cand_idx) {
+    if (!(cfg.temperature > 0.0f)) return 0;
+    const float inv_temp = 1.0f / cfg.temperature;
+    const float m = cand_val[0] * inv_temp;
+    float prob[20];
+    float sum = 0.0f;
+    for (int j = 0; j < cap; ++j) { prob[j] = expf(fmaf(cand_val[j], inv_temp, -m)); sum += prob[j]; }
+    const float min_p_thresh = cfg.min_p > 0.0f ? cfg.min_p * prob[0] : -1.0f;
+    const bool top_p_active = cfg.top_p < 1.0f;
+    const float top_p_target = cfg.top_p * sum;
+    float cum = 0.0f;
+    int support = 0;
+    for (int j = 0; j < cap; ++j) {
+        if (min_p_thresh >= 0.0f && prob[j] < min_p_thresh) break;
+        cum += prob[j];
+        support = j + 1;
+        if (top_p_active && cum >= top_p_target) break;
+    }
+    if (support < 1) support = 1;
+    int best = 0;
+    float best_value = -kInfF;
+    for (int j = 0; j < support; ++j) {
+        const float value = fmaf(cand_val[j], inv_temp, gumbel(cfg.seed, key, cand_idx[j]));
+        if (j == 0 || value > best_value) { best_value = value; best = j; }
+    }
+    return best;
+}
+
+// Extended sampler finish over the sorted top-`cap` list (fp64 weights,
+// min_p / top_p prefix cuts, Philox inverse CDF in sorted order).
+__device__ void sample_finish(const vi_row_params& p, int cap, const float* z, const int* ids,
+                              int vocabulary, int32_t* token_out, double* uniform_out, float* probs_row,
+                              vi_sample_stats* stats_out, uint32_t flags, uint32_t valid) {
+    int32_t token = vocabulary;
+    double u = 0.0, sn = 0.0;
+    int support = 0;
+    if (valid == 0) {
+        flags |= VI_FLAG_EMPTY;
+    } else if (!(p.temperature > 0.0f)) {
+        token = ids[0]; support = 1; sn = 1.0;
+        if (probs_row) probs_row[token] = 1.0f;
+    } else {
+        double w[kMaxK];
+        const double z0 = double(z[0]);
+        double s = 0.0;
+        for (int j = 0; j < cap; ++j) { w[j] = exp(double(z[j]) - z0); s += w[j]; }
+        const double minp = double(p.min_p), target = double(p.top_p) * s;
+        double cum = 0.0;
+        for (int j = 0; j < cap; ++j) {
+            if (p.min_p > 0.0f && w[j] < minp * w[0]) break;
+            cum += w[j];
+            support = j + 1;
+            if (p.top_p < 1.0f && cum >= target) break;
+        }
+        if (support < 1) support = 1;
+        for (int j = 0; j < support; ++j) sn += w[j];
+        u = philox_uniform(p.seed, p.lane, p.position, 0u);
+        const double t = u * sn;
+        int pick = support - 1;
+        cum = 0.0;
+        for (int j = 0; j < support; ++j) {
+            cum += w[j];
+            if (cum > t) { pick = j; break; }
+        }
+        token = ids[pick];
+        if (probs_row)
+            for (int j = 0; j < support; ++j) probs_row[ids[j]] = float(w[j] / sn);
+    }
+    *token_out = token;
+    if (uniform_out) *uniform_out = u;
+    if (stats_out) {
+        stats_out->flags = flags;
+        stats_out->support = uint32_t(support);
+        stats_out->finite = valid;
+        stats_out->reserved = 0u;
+        stats_out->support_mass = sn;
+        stats_out->uniform = u;
+    }
+}
+
+// ------------------------------------------------------------------- the kernel
+template <int DT, bool VEC, int MODE>
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
+    const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    const void* row = static_cast<const unsigned char*>(a.logits) + size_t(r) * size_t(a.stride) * sizeof(typename Elem<DT>::Bits);
+    const int begin = slice * a.slice_len, end = min(a.vocabulary, begin + a.slice_len);
+
+    // ---- per-row configuration
+    int K = 1;
+    vi_row_params p{};
+    float inv_t = 1.0f;
+    bool lookups = false, lookup_all = false;
+    const uint2* table = nullptr;
+    int key = 0, path[17], path_count = 0;
+    float slack = 0.0f;
+    if constexpr (MODE == kModeTopk) {
+        K = a.k;
+    } else if constexpr (MODE == kModePacket) {
+        K = 20;
+        if (a.cfg.top_k > 0 && a.cfg.top_k < K) K = a.cfg.top_k;
+        if (a.vocabulary < K) K = a.vocabulary;
+        key = a.keys.first + a.keys.depth[r];
+        if (a.keys.inputs > r) {
+            for (int j = 0; j < a.keys.depth[r] && j < a.keys.inputs; ++j) path[path_count++] = a.keys.input[j];
+            path[path_count++] = a.keys.input[r];
+        }
+        slack = a.cfg.presence_penalty < 0.0f ? -a.cfg.presence_penalty : 0.0f;
+    } else if constexpr (MODE == kModeVerify) {
+        p = a.params[r / a.params_div];
+        if (p.temperature > 0.0f) { K = p.top_k; inv_t = 1.0f / p.temperature; }
+    } else {
+        p = a.params[r];
+        if (!topk_route(p)) {
+            if (a.full_rows_unsupported && slice == 0 && threadIdx.x == 0) {
+                a.tokens[r] = -1;
+                if (a.stats) { a.stats[r] = vi_sample_stats{}; a.stats[r].flags = VI_FLAG_ERROR; }
+            }
+            return;
+        }
+        if (p.temperature > 0.0f) { K = p.top_k; inv_t = 1.0f / p.temperature; }
+        const int64_t hn = a.offsets ? a.offsets[r + 1] - a.offsets[r] : 0;
+        lookups = penalties_active(p) && hn > 0 && a.hash;
+        lookup_all = lookups && !penalties_lower_only(p);
+        if (lookups) table = a.hash + size_t(r) * size_t(a.hash_slots);
+        if (a.probs) {
+            float* pr = a.probs + size_t(r) * size_t(a.probs_stride);
+            for (int i = begin + threadIdx.x; i < end; i += kTopkThreads) pr[i] = 0.0f;
+        }
+    }
+
+    // ---- scan the slice
+    WaveList L;
+    uint32_t flags = 0, valid = 0;
+    float lse_m = -kInfF, lse_s = 0.0f;
+    const bool want_lse = MODE == kModeTopk && a.logprobs != nullptr;
+    scan_slice<DT, VEC, kTopkThreads>(row, begin, end, [&](uint32_t bits, int id, bool ok) {
+        const float x = Elem<DT>::decode(bits);
+        const bool finite = Elem<DT>::finite_bits(bits);
+        if constexpr (MODE == kModeTopk) {
+            if (ok && !finite) flags |= Elem<DT>::nan_bits(bits) ? (kSliceNan | kSliceNonfinite) : kSliceNonfinite;
+            const bool cand = ok && !Elem<DT>::nan_bits(bits);
+            if (want_lse && ok && finite) {
+                if (x > lse_m) { lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - x) * 1.4426950408889634f) + 1.0f; lse_m = x; }
+                else lse_s += __builtin_amdgcn_exp2f((x - lse_m) * 1.4426950408889634f);
+            }
+            list_offer(L, K, cand, x, id);
+        } else if constexpr (MODE == kModePacket) {
+            if (ok && !finite) flags |= kSliceNonfinite;
+            bool cand = ok && finite && better(x + slack, id, L.kv, L.ki);
+            float v = x;
+            if (cand && a.cfg.presence_penalty != 0.0f) {
+                bool seen = a.cfg.first_occurrence && a.cfg.first_occurrence[id] < key;
+                for (int j = 0; j < path_count && !seen; ++j) seen = path[j] == id;
+                if (seen) v = x - a.cfg.presence_penalty;
+            }
+            list_offer(L, K, cand, v, id);
+        } else if constexpr (MODE == kModeVerify) {
+            if (ok && !finite) flags |= kSliceNonfinite;
+            const float v = p.temperature > 0.0f ? x * inv_t : x;
+            const bool live = ok && finite && isfinite(v);
+            if (ok && finite && !live) flags |= kSliceNonfinite;
+            valid += live ? 1u : 0u;
+            list_offer(L, K, live, v, id);
+        } else {
+            if (ok && !finite) flags |= kSliceNonfinite;
+            bool live = ok && finite;
+            float v = p.temperature > 0.0f ? x * inv_t : x;
+            bool cand = live && better(v, id, L.kv, L.ki);
+            if (lookups && live && (cand || lookup_all || fabsf(x) >= overflow_guard<DT>() || !isfinite(v))) {
+                const uint32_t c = hash_count(table, a.hash_shift, a.hash_slots, id);
+                if (c) {
+                    const uint32_t pb = penalize_bits<DT>(bits, c, p);
+                    if (!Elem<DT>::finite_bits(pb)) { flags |= kSliceNonfinite; live = false; }
+                    else {
+                        float xp = Elem<DT>::decode(pb);
+                        if (xp == 0.0f) xp = 0.0f;
+                        v = p.temperature > 0.0f ? xp * inv_t : xp;
+                    }
+                }
+                if (live && p.temperature > 0.0f && !isfinite(v)) { flags |= kSliceNonfinite; live = false; }
+                cand = live && better(v, id, L.kv, L.ki);
+            } else if (live && p.temperature > 0.0f && !isfinite(v)) {
+                flags |= kSliceNonfinite; live = false; cand = false;
+            }
+            valid += live ? 1u : 0u;
+            list_offer(L, K, cand, v, id);
+        }
+    });
+
+    // ---- merge the wave lists in LDS
+    __shared__ float s_val[kTopkWaves][kMaxK];
+    __shared__ int s_idx[kTopkWaves][kMaxK];
+    __shared__ uint32_t s_flags[kTopkWaves], s_valid[kTopkWaves];
+    __shared__ float s_lm[kTopkWaves];
+    __shared__ double s_ls[kTopkWaves];
+    s_val[wave][lane] = L.v;
+    s_idx[wave][lane] = L.i;
+    // wave reductions of flags / valid / lse
+    {
+        uint32_t f = flags;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) f |= shfl_xor_u(f, o);
+        uint32_t c = valid;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) c += shfl_xor_u(c, o);
+        float m = lse_m;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
+        double s = (lse_m == -kInfF) ? 0.0 : double(lse_s) * exp(double(lse_m) - double(m));
+#pragma unroll
+        for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
+        if (lane == 0) { s_flags[wave] = f; s_valid[wave] = c; s_lm[wave] = m; s_ls[wave] = s; }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < kTopkWaves; ++w) list_offer(L, K, lane < K, s_val[w][lane], s_idx[w][lane]);
+    uint32_t f = 0, c = 0;
+    float m = -kInfF;
+    for (int w = 0; w < kTopkWaves; ++w) { f |= s_flags[w]; c += s_valid[w]; m = fmaxf(m, s_lm[w]); }
+    double s = 0.0;
+    for (int w = 0; w < kTopkWaves; ++w) if (s_lm[w] != -kInfF) s += s_ls[w] * exp(double(s_lm[w]) - double(m));
+
+    if (slices > 1) {
+        // ---- publish the slice, last arriver merges
+        const size_t at = (size_t(r) * slices + slice) * kMaxK;
+        if (lane < K) { a.pval[at + lane] = L.v; a.pidx[at + lane] = L.i; }
+        if (lane == 0) {
+            SliceHeader h;
+            h.flags = f; h.valid = c; h.lse_max = m; h.pad = 0.0f; h.lse_sum = s;
+            a.phdr[size_t(r) * slices + slice] = h;
+        }
+        __threadfence();
+        uint32_t arrived = 0;
+        if (lane == 0) arrived = atomicAdd(&a.arrivals[r], 1u);
+        if (readlane_i(int(arrived), 0) != slices - 1) return;
+        __threadfence();
+        L = WaveList{};
+        f = 0; c = 0; m = -kInfF;
+        for (int base = 0; base < slices * K; base += kWave) {
+            const int e = base + lane;
+            const bool ok = e < slices * K;
+            const int sl = ok ? e / K : 0, j = ok ? e % K : 0;
+            const size_t src = (size_t(r) * slices + sl) * kMaxK + j;
+            list_offer(L, K, ok, ok ? a.pval[src] : -kInfF, ok ? a.pidx[src] : kInvalidId);
+        }
+        for (int sl = 0; sl < slices; ++sl) {
+            const SliceHeader h = a.phdr[size_t(r) * slices + sl];
+            f |= h.flags; c += h.valid; m = fmaxf(m, h.lse_max);
+        }
+        s = 0.0;
+        for (int sl = 0; sl < slices; ++sl) {
+            const SliceHeader h = a.phdr[size_t(r) * slices + sl];
+            if (h.lse_max != -kInfF) s += h.lse_sum * exp(double(h.lse_max) - double(m));
+        }
+        if (lane == 0) a.arrivals[r] = 0u;
+    }
+
+    // ---- finish the row (wave 0 of the last workgroup)
+    s_val[0][lane] = L.v;
+    s_idx[0][lane] = L.i;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    if constexpr (MODE == kModeTopk) {
+        if (f & kSliceNan) {
+            if (lane == 0) {
+                float vals[kMaxK];
+                int idsl[kMaxK];
+                serial_topk_row<DT>(row, a.vocabulary, K, vals, idsl);
+                for (int j = 0; j < K; ++j) {
+                    a.ids[size_t(r) * K + j] = idsl[j];
+                    a.values[size_t(r) * K + j] = vals[j];
+                    if (a.logprobs) a.logprobs[size_t(r) * K + j] = __builtin_nanf("");
+                }
+            }
+        } else if (lane < K) {
+            a.ids[size_t(r) * K + lane] = L.i;
+            a.values[size_t(r) * K + lane] = L.v;
+            if (a.logprobs) {
+                const double lse = double(m) + log(s);
+                a.logprobs[size_t(r) * K + lane] = (f & kSliceNonfinite) ? __builtin_nanf("") : float(double(L.v) - lse);
+            }
+        }
+        if (lane == 0 && (f & kSliceNonfinite) && a.nonfinite_flag) atomicOr(a.nonfinite_flag, 1u);
+    } else if constexpr (MODE == kModePacket) {
+        if (lane == 0) {
+            const int sel = packet_draw(a.cfg, key, K, s_val[0], s_idx[0]);
+            a.out_rows[r].serial = a.serial;
+            a.out_rows[r].token = s_idx[0][sel];
+            a.out_rows[r].nonfinite = (f & kSliceNonfinite) ? 1u : 0u;
+        }
+    } else if constexpr (MODE == kModeVerify) {
+        if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
+        if (lane == 0) { a.lvalid[r] = c; a.lflags[r] = (f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u; }
+    } else {
+        if (lane == 0) {
+            uint32_t flags_out = 0;
+            if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
+            if (lookups) flags_out |= a.row_flags[r];
+            if (flags_out & VI_FLAG_ERROR) {
+                a.tokens[r] = -1;
+                if (a.uniforms) a.uniforms[r] = 0.0;
+                if (a.stats) { a.stats[r] = vi_sample_stats{}; a.stats[r].flags = flags_out; }
+                return;
+            }
+            const int cap = (p.temperature > 0.0f) ? min(K, int(c)) : 1;
+            float* pr = a.probs ? a.probs + size_t(r) * size_t(a.probs_stride) : nullptr;
+            sample_finish(p, cap, s_val[0], s_idx[0], a.vocabulary, &a.tokens[r],
+                          a.uniforms ? &a.uniforms[r] : nullptr, pr, a.stats ? &a.stats[r] : nullptr,
+                          flags_out, c);
+        }
+    }
+}
+
+// History hash builder: one workgroup per row; table cleared, then each history
+// token inserted with CAS (open addressing, linear probing).  row_flags[r]
+// receives VI_FLAG_BAD_HISTORY for out-of-range tokens and VI_FLAG_ERROR when
+// the history exceeds the workspace's max_history.
+__global__ __launch_bounds__(256) void history_hash_kernel(
+    const vi_row_params* params, const int32_t* histories, const int64_t* offsets, int vocabulary,
+    uint2* hash, int hash_shift, int hash_slots, uint32_t* row_flags, int64_t max_history) {
+    const int r = blockIdx.x;
+    const vi_row_params p = params[r];
+    if (!topk_route(p) || !penalties_active(p)) return;
+    const int64_t b = offsets[r], n = offsets[r + 1] - b;
+    __shared__ uint32_t s_flags;
+    if (threadIdx.x == 0) s_flags = 0;
+    uint2* table = hash + size_t(r) * size_t(hash_slots);
+    for (int i = threadIdx.x; i < hash_slots; i += blockDim.x) table[i] = make_uint2(0u, 0u);
+    __syncthreads();
+    if (n > max_history) {
+        if (threadIdx.x == 0) s_flags = VI_FLAG_ERROR;
+    } else {
+        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const int32_t t = histories[b + i];
+            if (t < 0 || t >= vocabulary) { atomicOr(&s_flags, uint32_t(VI_FLAG_BAD_HISTORY)); continue; }
+            uint32_t s = (uint32_t(t) * 0x9E3779B1u) >> hash_shift;
+            for (int probe = 0; probe < hash_slots; ++probe) {
+                const uint32_t old = atomicCAS(&table[s].x, 0u, uint32_t(t) + 1u);
+                if (old == 0u || old == uint32_t(t) + 1u) { atomicAdd(&table[s].y, 1u); break; }
+                s = (s + 1u) & uint32_t(hash_slots - 1);
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) row_flags[r] = s_flags;
+}
+
+template <int MODE>
+vi_status launch_mode(const TopkArgs& args, int dtype, bool vec, int rows, int slices, hipStream_t stream) {
+    const dim3 grid(slices, rows), block(kTopkThreads);
+#define VI_TOPK_LAUNCH(DT, V) hipLaunchKernelGGL((topk_kernel<DT, V, MODE>), grid, block, 0, stream, args)
+    switch (dtype) {
+        case VI_BF16: if (vec) VI_TOPK_LAUNCH(VI_BF16, true); else VI_TOPK_LAUNCH(VI_BF16, false); break;
+        case VI_F16: if (vec) VI_TOPK_LAUNCH(VI_F16, true); else VI_TOPK_LAUNCH(VI_F16, false); break;
+        default: if (vec) VI_TOPK_LAUNCH(VI_F32, true); else VI_TOPK_LAUNCH(VI_F32, false); break;
+    }
+#undef VI_TOPK_LAUNCH
+    return launch_status();
+}
+
+bool aligned16(const void* p, int64_t stride, int dtype) {
+    return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ((stride * elem_size(dtype)) % 16 == 0);
+}
+
+struct Partials {
+    float* pval;
+    int* pidx;
+    SliceHeader* phdr;
+    uint32_t* arrivals;
+};
+Partials carve_partials(Carver& c, int rows, int slices) {
+    Partials p{};
+    p.arrivals = c.take<uint32_t>(size_t(rows));
+    p.pval = c.take<float>(size_t(rows) * slices * kMaxK);
+    p.pidx = c.take<int>(size_t(rows) * slices * kMaxK);
+    p.phdr = c.take<SliceHeader>(size_t(rows) * slices);
+    return p;
+}
+
+}  // namespace
+
+TopkPlan topk_plan(int rows, int vocabulary) {
+    // >= 2048 workgroups (8 per CU) where the row count allows, slices >= 2048 logits.
+    int slices = rows >= 2048 ? 1 : (2048 + rows - 1) / rows;
+    slices = std::min(slices, std::max(1, vocabulary / 2048));
+    slices = std::max(1, std::min(slices, 64));
+    const int len = slice_len_for(vocabulary, slices);
+    slices = (vocabulary + len - 1) / len;
+    return {slices, len};
+}
+
+size_t topk_partials_bytes_slices(int rows, int slices) {
+    return align_up(size_t(rows) * 4, 256) + 2 * align_up(size_t(rows) * slices * kMaxK * 4, 256) +
+           align_up(size_t(rows) * slices * sizeof(SliceHeader), 256) + 256;
+}
+
+size_t topk_partials_bytes(int rows, int vocabulary) {
+    return topk_partials_bytes_slices(rows, topk_plan(rows, vocabulary).slices);
+}
+
+vi_status launch_topk_rows(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                           int k, int64_t* ids, float* values, float* logprobs,
+                           uint32_t* nonfinite_flag, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const TopkPlan plan = topk_plan(rows, vocabulary);
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, rows, plan.slices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    TopkArgs a{};
+    a.logits = logits; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
+    a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
+    a.k = k; a.ids = ids; a.values = values; a.logprobs = logprobs; a.nonfinite_flag = nonfinite_flag;
+    return launch_mode<kModeTopk>(a, dtype, aligned16(logits, stride, dtype), rows, plan.slices, stream);
+}
+
+vi_status launch_packet(const void* scores, int dtype, int rows, int vocabulary, int64_t stride,
+                        const vi_device_sampling& cfg, const PacketKeys& keys, uint64_t serial,
+                        vi_greedy_row* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const TopkPlan plan = topk_plan(rows, vocabulary);
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, rows, plan.slices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    TopkArgs a{};
+    a.logits = scores; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
+    a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
+    a.cfg = cfg; a.keys = keys; a.serial = serial; a.out_rows = out;
+    return launch_mode<kModePacket>(a, dtype, aligned16(scores, stride, dtype), rows, plan.slices, stream);
+}
+
+vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
+                              int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
+                              float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, void* ws,
+                              size_t ws_bytes, hipStream_t stream) {
+    // Partials carved for (layout_rows, layout_slices) so that launches over
+    // different row counts share one counter layout in one workspace.
+    const TopkPlan plan = topk_plan(rows, vocabulary);
+    if (rows > layout_rows || plan.slices > layout_slices) return VI_ERR_WORKSPACE;
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, layout_rows, layout_slices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    TopkArgs a{};
+    a.logits = logits; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
+    a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
+    a.params = params; a.params_div = params_div;
+    a.lval = lval; a.lidx = lidx; a.lvalid = lvalid; a.lflags = lflags;
+    return launch_mode<kModeVerify>(a, dtype, aligned16(logits, stride, dtype), rows, plan.slices, stream);
+}
+
+size_t history_hash_slots(int64_t max_history) {
+    size_t slots = 64;
+    while (slots < size_t(2 * std::max<int64_t>(max_history, 1))) slots <<= 1;
+    return slots;
+}
+
+size_t sample_workspace(int rows, int vocabulary, int64_t max_history) {
+    size_t bytes = topk_partials_bytes(rows, vocabulary);
+    bytes += align_up(size_t(rows) * 4, 256);
+    if (max_history > 0) bytes += align_up(size_t(rows) * history_hash_slots(max_history) * 8, 256);
+    bytes += full_workspace(rows);
+    return bytes + 1024;
+}
+
+vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const TopkPlan plan = topk_plan(s.rows, s.vocabulary);
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, s.rows, plan.slices);
+    uint2* hash = nullptr;
+    uint32_t* row_flags = c.take<uint32_t>(size_t(s.rows));
+    int slots = 0, shift = 0;
+    if (s.max_history > 0 && s.histories && s.offsets) {
+        slots = int(history_hash_slots(s.max_history));
+        shift = 32 - __builtin_ctz(unsigned(slots));
+        hash = c.take<uint2>(size_t(s.rows) * slots);
+    }
+    unsigned char* full_ws = c.take<unsigned char>(full_workspace(s.rows));
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    const bool run_topk = (s.route_mask & VI_ROUTE_TOPK) != 0;
+    const bool full_ok = full_supported(s.dtype, s.vocabulary, s.stride);
+    vi_status st = VI_OK;
+    if (run_topk) {
+        if (hash) {
+            hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(256), 0, stream, s.params, s.histories,
+                               s.offsets, s.vocabulary, hash, shift, slots, row_flags, s.max_history);
+            if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
+        }
+        TopkArgs a{};
+        a.logits = s.logits; a.vocabulary = s.vocabulary; a.stride = s.stride; a.slice_len = plan.slice_len;
+        a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
+        a.params = s.params; a.hash = hash; a.row_flags = row_flags; a.hash_shift = shift; a.hash_slots = slots;
+        a.offsets = s.offsets;
+        a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
+        a.stats = s.stats;
+        // fp32 logits / unaligned rows: full-route rows fail loudly in the top-k launch
+        a.full_rows_unsupported = (full_ok && (s.route_mask & VI_ROUTE_FULL)) ? 0 : (full_ok ? 0 : 1);
+        st = launch_mode<kModeSample>(a, s.dtype, aligned16(s.logits, s.stride, s.dtype), s.rows, plan.slices, stream);
+        if (st != VI_OK) return st;
+    }
+    if ((s.route_mask & VI_ROUTE_FULL) && full_ok) st = launch_full(s, full_ws, full_workspace(s.rows), stream);
+    else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) return VI_ERR_UNSUPPORTED;
+    return st;
+}
+
+}  // namespace vi

@@ -1,0 +1,200 @@
+// vi_device.h — device helpers shared by the gfx950 sampling kernels.
+//
+// Wave64 primitives (ballot / readlane / ds_bpermute), 16-byte row loads, the
+// 16-bit order-preserving logit keys, Philox4x32-10, the SplitMix64/Gumbel
+// noise of the coupled route, and the penalty arithmetic of the batched sampler.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/voidinfer_sampling.h"
+
+namespace vi {
+
+constexpr int kWave = 64;
+constexpr float kInfF = __builtin_huge_valf();
+
+// ------------------------------------------------------------------ wave ops
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+// Value of lane (lane - 1); lane 0 gets its own value.
+__device__ __forceinline__ float shift_up_f(float v) {
+    const int src = max(lane_id() - 1, 0) << 2;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ int shift_up_i(int v) {
+    const int src = max(lane_id() - 1, 0) << 2;
+    return __builtin_amdgcn_ds_bpermute(src, v);
+}
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xor(v, m, kWave); }
+
+// (value desc, id asc): exl3_sampled_better (sampled_select.cuh:55-57).
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// --------------------------------------------------------------- element decode
+template <int DT> struct Elem;
+template <> struct Elem<VI_BF16> {
+    using Bits = uint16_t;
+    static constexpr int kPerVec = 8;
+    __device__ static float decode(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+    __device__ static bool finite_bits(uint32_t b) { return (b & 0x7f80u) != 0x7f80u; }
+    __device__ static bool nan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7f80u; }
+    // Round to nearest even (the hardware conversion v_cvt_pk_bf16_f32).
+    __device__ static uint32_t round(float f) {
+        return uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
+    }
+};
+template <> struct Elem<VI_F16> {
+    using Bits = uint16_t;
+    static constexpr int kPerVec = 8;
+    __device__ static float decode(uint32_t b) {
+        return float(__builtin_bit_cast(_Float16, uint16_t(b)));
+    }
+    __device__ static bool finite_bits(uint32_t b) { return (b & 0x7c00u) != 0x7c00u; }
+    __device__ static bool nan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7c00u; }
+    __device__ static uint32_t round(float f) {
+        return uint32_t(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
+    }
+};
+template <> struct Elem<VI_F32> {
+    using Bits = uint32_t;
+    static constexpr int kPerVec = 4;
+    __device__ static float decode(uint32_t b) { return __builtin_bit_cast(float, b); }
+    __device__ static bool finite_bits(uint32_t b) { return (b & 0x7f800000u) != 0x7f800000u; }
+    __device__ static bool nan_bits(uint32_t b) { return (b & 0x7fffffffu) > 0x7f800000u; }
+    __device__ static uint32_t round(float f) { return __builtin_bit_cast(uint32_t, f); }
+};
+
+// Bits of element j (0..kPerVec-1) of a 16-byte vector.
+template <int DT>
+__device__ __forceinline__ uint32_t vec_bits(const uint4& v, int j) {
+    if constexpr (DT == VI_F32) {
+        return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+    } else {
+        const uint32_t w = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
+        return (j & 1) ? (w >> 16) : (w & 0xffffu);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t load_bits(const void* row, int64_t i) {
+    if constexpr (DT == VI_F32) return static_cast<const uint32_t*>(row)[i];
+    else return static_cast<const uint16_t*>(row)[i];
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Streaming 16-byte load (non-temporal hint: logits are read once).
+__device__ __forceinline__ uint4 load16(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16-bit order-preserving key of a sign-magnitude bf16 / fp16 pattern; -0 and
+// +0 share the key of +0.
+__device__ __forceinline__ uint32_t key16(uint32_t b) {
+    if (b == 0x8000u) b = 0;
+    return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t unkey16(uint32_t k) {
+    return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+}
+
+// ------------------------------------------------------------------ RNG
+// SplitMix64 finalizer (sampled_select.cuh:41-46).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+// Gumbel(0,1) of (seed, key, token) (sampled_select.cuh:47-54).
+__device__ __forceinline__ float gumbel(uint64_t seed, int key, int token) {
+    uint64_t h = splitmix64(seed ^ (uint64_t(uint32_t(key)) * 0xD1B54A32D192ED03ull));
+    h = splitmix64(h ^ (uint64_t(uint32_t(token)) * 0x2545F4914F6CDD1Dull));
+    const float u = (float(uint32_t(h >> 40)) + 0.5f) * (1.0f / 16777216.0f);
+    return -logf(-logf(u));
+}
+
+// Philox4x32-10 (Salmon et al., SC'11); word order as rocRAND's engine.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        const uint32_t lo0 = 0xD2511F53u * c.x, hi0 = __umulhi(0xD2511F53u, c.x);
+        const uint32_t lo1 = 0xCD9E8D57u * c.z, hi1 = __umulhi(0xCD9E8D57u, c.z);
+        c = make_uint4(hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0);
+    }
+    return c;
+}
+// 53-bit uniform in [0,1) of (seed, lane, position, purpose); counter
+// (position, 0, lane, purpose), key = seed.
+__device__ __forceinline__ double philox_uniform(uint64_t seed, uint32_t lane, int32_t position,
+                                                 uint32_t purpose) {
+    const uint4 o = philox4x32_10(make_uint4(uint32_t(position), 0u, lane, purpose), uint32_t(seed),
+                                  uint32_t(seed >> 32));
+    const uint64_t m = (uint64_t(o.x) << 21) | uint64_t(o.y >> 11);
+    return double(m) * 0x1p-53;
+}
+
+// ------------------------------------------------------------------ penalties
+// Penalty of a history token with `count` occurrences (HF repetition, then
+// OpenAI frequency and presence), fp32 without contraction, stored back in the
+// logits' dtype (round to nearest even).  Returns the penalized bits.
+template <int DT>
+__device__ __forceinline__ uint32_t penalize_bits(uint32_t bits, uint32_t count, const vi_row_params& p) {
+    float y = Elem<DT>::decode(bits);
+    if (p.repetition_penalty != 1.0f)
+        y = (y > 0.0f) ? __fdiv_rn(y, p.repetition_penalty) : __fmul_rn(y, p.repetition_penalty);
+    if (p.frequency_penalty != 0.0f) y = __fsub_rn(y, __fmul_rn(p.frequency_penalty, float(count)));
+    if (p.presence_penalty != 0.0f) y = __fsub_rn(y, p.presence_penalty);
+    return Elem<DT>::round(y);
+}
+__device__ __forceinline__ bool penalties_active(const vi_row_params& p) {
+    return p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
+}
+// Penalties can only lower a logit (so a raw value bounds the penalized one).
+__device__ __forceinline__ bool penalties_lower_only(const vi_row_params& p) {
+    return p.repetition_penalty >= 1.0f && p.presence_penalty >= 0.0f && p.frequency_penalty >= 0.0f;
+}
+// Rows served by the top-k kernel family: argmax rows and 1 <= top_k <= 64.
+__device__ __forceinline__ bool topk_route(const vi_row_params& p) {
+    return !(p.temperature > 0.0f) || (p.top_k >= 1 && p.top_k <= 64);
+}
+
+// ------------------------------------------------------------------ block scan
+// Exclusive prefix of a per-thread u32 over the block (blockDim.x = NT); `tmp`
+// holds NT/64 + 1 words.  Returns the exclusive prefix; *total gets the sum.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_t* tmp, uint32_t* total) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, kWave);
+        if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) tmp[wave] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t s = 0;
+        for (int w = 0; w < NT / kWave; ++w) { const uint32_t t = tmp[w]; tmp[w] = s; s += t; }
+        tmp[NT / kWave] = s;
+    }
+    __syncthreads();
+    const uint32_t r = tmp[wave] + x - v;
+    *total = tmp[NT / kWave];
+    __syncthreads();
+    return r;
+}
+
+}  // namespace vi

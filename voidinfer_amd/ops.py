@@ -1,0 +1,253 @@
+"""Torch-facing calls into libvoidinfer_sampling.so.
+
+PyTorch supplies device memory and the current stream; every computation is a
+HIP kernel of the library.  Function names follow the reference's launchers:
+
+=========================  ==========================================================
+``greedy_packet``           exl3_launch_greedy_packet (src/exl3/greedy_packet.cuh:256)
+``topk_rows``               dflash2_topk16_for_test (src/exl3/dflash2_draft.cu:2390)
+``sampled_packet``          exl3_launch_sampled_packet (src/exl3/sampled_select.cuh:362)
+``presence_*``              exl3_presence_reset/truncate/record (sampled_select.h:33-35)
+``sample_rows``             batched sampler (new entry; lanes x penalties x Philox)
+``verify_rows``             decide_exl3_outer_prefix / IndependentAcceptanceReference,
+                            on the device (exact_outer_reference.h:68,
+                            sampled_acceptance_reference.h:48)
+=========================  ==========================================================
+
+Workspaces: each entry point and shape owns a zero-initialised workspace (its
+arrival counters start at zero and the kernels leave them at zero), cached per
+device here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _abi
+from ._abi import (BF16, F16, F32, GREEDY_ROW, ROW_PARAMS, SAMPLE_STATS, DeviceSampling, check)
+
+_DTYPES = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
+_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def _lib():
+    return _abi.load()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def workspace(key: tuple, nbytes: int, device: torch.device) -> torch.Tensor:
+    """Zero-filled device workspace of at least `nbytes`, one per (key, device)."""
+    k = (key, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _workspaces.get(k)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[k] = ws
+    return ws
+
+
+def _logit_args(logits: torch.Tensor) -> tuple[int, int, int, int]:
+    if logits.dim() != 2:
+        raise ValueError("logits must be [rows, vocabulary]")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logit dtype {logits.dtype}")
+    if logits.stride(1) != 1:
+        raise ValueError("logit rows must be contiguous")
+    if not logits.is_cuda:
+        raise ValueError("logits must be on a HIP device")
+    rows, vocab = logits.shape
+    stride = logits.stride(0) if rows > 1 else max(vocab, logits.stride(0))
+    return _DTYPES[logits.dtype], rows, vocab, stride
+
+
+def _rows_view(logits: torch.Tensor, vocabulary: int | None) -> tuple[int, int, int, int]:
+    dtype, rows, width, stride = _logit_args(logits)
+    vocab = width if vocabulary is None else vocabulary
+    if vocab > width:
+        raise ValueError("vocabulary exceeds the row width")
+    return dtype, rows, vocab, stride
+
+
+def greedy_packet(logits: torch.Tensor, serial: int = 1, vocabulary: int | None = None) -> np.ndarray:
+    """Argmax rows -> structured array of vi_greedy_row (serial, token, nonfinite)."""
+    dtype, rows, vocab, stride = _rows_view(logits, vocabulary)
+    out = torch.empty(rows * GREEDY_ROW.itemsize, dtype=torch.uint8, device=logits.device)
+    nb = _lib().vi_greedy_workspace_bytes(rows, vocab)
+    ws = workspace(("greedy", rows, vocab), nb, logits.device)
+    check(_lib().vi_greedy_rows(logits.data_ptr(), dtype, rows, vocab, stride, serial, out.data_ptr(),
+                                ws.data_ptr(), ws.numel(), _stream()), "vi_greedy_rows")
+    return out.cpu().numpy().view(GREEDY_ROW)
+
+
+def greedy_rows_device(logits: torch.Tensor, out: torch.Tensor, serial: int = 1) -> None:
+    """Argmax into a caller-owned uint8 device buffer of rows * 16 bytes (no sync)."""
+    dtype, rows, vocab, stride = _rows_view(logits, None)
+    nb = _lib().vi_greedy_workspace_bytes(rows, vocab)
+    ws = workspace(("greedy", rows, vocab), nb, logits.device)
+    check(_lib().vi_greedy_rows(logits.data_ptr(), dtype, rows, vocab, stride, serial, out.data_ptr(),
+                                ws.data_ptr(), ws.numel(), _stream()), "vi_greedy_rows")
+
+
+def topk_rows(logits: torch.Tensor, k: int = 16, logprobs: bool = False, vocabulary: int | None = None,
+              nonfinite_flag: torch.Tensor | None = None):
+    """Exact top-k ids (int64), values (f32) and optional log-probs (f32)."""
+    dtype, rows, vocab, stride = _rows_view(logits, vocabulary)
+    dev = logits.device
+    ids = torch.empty(rows, k, dtype=torch.int64, device=dev)
+    vals = torch.empty(rows, k, dtype=torch.float32, device=dev)
+    lp = torch.empty(rows, k, dtype=torch.float32, device=dev) if logprobs else None
+    nb = _lib().vi_topk_workspace_bytes(rows, vocab, k)
+    ws = workspace(("topk", rows, vocab), nb, dev)
+    check(_lib().vi_topk_rows(logits.data_ptr(), dtype, rows, vocab, stride, k, ids.data_ptr(), vals.data_ptr(),
+                              _ptr(lp), _ptr(nonfinite_flag), ws.data_ptr(), ws.numel(), _stream()),
+          "vi_topk_rows")
+    return ids, vals, lp
+
+
+def sampled_packet(scores: torch.Tensor, temperature: float, top_k: int, top_p: float, min_p: float,
+                   seed: int, presence_penalty: float = 0.0, first_occurrence: torch.Tensor | None = None,
+                   first_key: int = 0, depths: Sequence[int] | None = None,
+                   inputs: Sequence[int] | None = None, serial: int = 1) -> np.ndarray:
+    """Coupled reference-semantics packet -> vi_greedy_row array."""
+    dtype, rows, vocab, stride = _rows_view(scores, None)
+    cfg = DeviceSampling(temperature, top_k, top_p, min_p, seed, presence_penalty, 0,
+                         first_occurrence.data_ptr() if first_occurrence is not None else None)
+    d = (C.c_int32 * rows)(*depths) if depths is not None else None
+    i = (C.c_int32 * rows)(*inputs) if inputs is not None else None
+    out = torch.empty(rows * GREEDY_ROW.itemsize, dtype=torch.uint8, device=scores.device)
+    nb = _lib().vi_sampled_packet_workspace_bytes(rows, vocab)
+    ws = workspace(("packet", rows, vocab), nb, scores.device)
+    check(_lib().vi_sampled_packet(scores.data_ptr(), dtype, rows, vocab, stride, C.byref(cfg), first_key,
+                                   C.cast(d, C.c_void_p) if d is not None else None,
+                                   len(depths) if depths is not None else 0,
+                                   C.cast(i, C.c_void_p) if i is not None else None,
+                                   len(inputs) if inputs is not None else 0, serial, out.data_ptr(),
+                                   ws.data_ptr(), ws.numel(), _stream()), "vi_sampled_packet")
+    return out.cpu().numpy().view(GREEDY_ROW)
+
+
+def presence_reset(table: torch.Tensor) -> None:
+    check(_lib().vi_presence_reset(table.data_ptr(), table.numel(), _stream()), "vi_presence_reset")
+
+
+def presence_truncate(table: torch.Tensor, start: int) -> None:
+    check(_lib().vi_presence_truncate(table.data_ptr(), table.numel(), start, _stream()), "vi_presence_truncate")
+
+
+def presence_record(table: torch.Tensor, first: int, tokens: torch.Tensor) -> None:
+    check(_lib().vi_presence_record(table.data_ptr(), table.numel(), first, tokens.data_ptr(), tokens.numel(),
+                                    _stream()), "vi_presence_record")
+
+
+def params_array(rows: int, **fields) -> np.ndarray:
+    """vi_row_params[rows] with neutral defaults; fields are scalars or arrays."""
+    p = np.zeros(rows, dtype=ROW_PARAMS)
+    p["temperature"] = 1.0
+    p["top_p"] = 1.0
+    p["repetition_penalty"] = 1.0
+    p["lane"] = np.arange(rows)
+    for k, v in fields.items():
+        p[k] = v
+    return p
+
+
+def to_device_bytes(arr: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).reshape(-1).copy()).to(device)
+
+
+class SampleOutputs:
+    def __init__(self, tokens, uniforms, probs, stats):
+        self.tokens, self.uniforms, self.probs, self.stats = tokens, uniforms, probs, stats
+
+
+def route_mask(params: np.ndarray) -> int:
+    """Kernels a batch needs: top-k route (T == 0 or 1 <= top_k <= 64) / full route."""
+    topk = (params["temperature"] <= 0) | ((params["top_k"] >= 1) & (params["top_k"] <= 64))
+    return (_abi.ROUTE_TOPK if topk.any() else 0) | (_abi.ROUTE_FULL if (~topk).any() else 0)
+
+
+def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor,
+                histories: torch.Tensor | None = None, offsets: torch.Tensor | None = None,
+                max_history: int = 0, want_probs: bool = False, want_stats: bool = True,
+                want_uniforms: bool = True, outputs: SampleOutputs | None = None,
+                routes: int | None = None) -> SampleOutputs:
+    """Batched sampler.  params: vi_row_params array (host numpy or device uint8);
+    with device params pass `routes` (default: run both kernel routes)."""
+    dtype, rows, vocab, stride = _rows_view(logits, None)
+    dev = logits.device
+    if routes is None:
+        routes = _abi.ROUTE_ALL if isinstance(params, torch.Tensor) else route_mask(params)
+    p_dev = params if isinstance(params, torch.Tensor) else to_device_bytes(params, dev)
+    if histories is not None:
+        if histories.dtype != torch.int32 or offsets is None or offsets.dtype != torch.int64:
+            raise ValueError("histories must be int32 with int64 offsets[rows + 1]")
+        if max_history <= 0:
+            raise ValueError("max_history must bound the longest history")
+    o = outputs
+    if o is None:
+        o = SampleOutputs(
+            torch.empty(rows, dtype=torch.int32, device=dev),
+            torch.empty(rows, dtype=torch.float64, device=dev) if want_uniforms else None,
+            torch.empty(rows, vocab, dtype=torch.float32, device=dev) if want_probs else None,
+            torch.empty(rows * SAMPLE_STATS.itemsize, dtype=torch.uint8, device=dev) if want_stats else None)
+    nb = _lib().vi_sample_workspace_bytes(rows, vocab, max_history)
+    ws = workspace(("sample", rows, vocab, max_history), nb, dev)
+    check(_lib().vi_sample_rows(logits.data_ptr(), dtype, rows, vocab, stride, p_dev.data_ptr(),
+                                _ptr(histories), _ptr(offsets), max_history, o.tokens.data_ptr(),
+                                _ptr(o.uniforms), _ptr(o.probs), vocab, _ptr(o.stats), routes, ws.data_ptr(),
+                                ws.numel(), _stream()), "vi_sample_rows")
+    return o
+
+
+def stats_numpy(stats: torch.Tensor) -> np.ndarray:
+    return stats.cpu().numpy().view(SAMPLE_STATS)
+
+
+def verify_rows(mode: int, target: torch.Tensor, drafted: torch.Tensor, lanes: int, drafts: int,
+                draft: torch.Tensor | None = None, params: np.ndarray | None = None,
+                terminal: Sequence[int] | None = None):
+    """Per-lane acceptance.  Returns (accepted[lanes], committed[lanes, drafts+1],
+    committed_count[lanes], lane_flags[lanes]) as numpy arrays."""
+    tdt, trows_total, vocab, tstride = _rows_view(target, None)
+    if trows_total % lanes:
+        raise ValueError("target rows must be lanes x target_rows")
+    trows = trows_total // lanes
+    dev = target.device
+    ddt, dstride, dptr = 0, 0, None
+    if draft is not None:
+        ddt, drows_total, dvocab, dstride = _rows_view(draft, None)
+        if dvocab != vocab or drows_total != lanes * drafts:
+            raise ValueError("draft must be [lanes * drafts, vocabulary]")
+        dptr = draft.data_ptr()
+    p_dev = to_device_bytes(params, dev) if params is not None else None
+    term = torch.tensor(list(terminal), dtype=torch.int64, device=dev) if terminal else None
+    acc = torch.empty(lanes, dtype=torch.int32, device=dev)
+    com = torch.empty(lanes, drafts + 1, dtype=torch.int32, device=dev)
+    cnt = torch.empty(lanes, dtype=torch.int32, device=dev)
+    flg = torch.empty(lanes, dtype=torch.int32, device=dev)
+    nb = _lib().vi_verify_workspace_bytes(lanes, drafts, vocab)
+    ws = workspace(("verify", lanes, drafts, vocab), nb, dev)
+    check(_lib().vi_verify_rows(mode, target.data_ptr(), tdt, tstride, trows, dptr, ddt, dstride, lanes, drafts,
+                                vocab, drafted.data_ptr(), _ptr(p_dev), _ptr(term), len(terminal or ()),
+                                acc.data_ptr(), com.data_ptr(), cnt.data_ptr(), flg.data_ptr(), ws.data_ptr(),
+                                ws.numel(), _stream()), "vi_verify_rows")
+    return acc.cpu().numpy(), com.cpu().numpy(), cnt.cpu().numpy(), flg.cpu().numpy().view(np.uint32)
+
+
+def probe_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    check(_lib().vi_probe_read(buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(), _stream()),
+          "vi_probe_read")
+
+
+def probe_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    check(_lib().vi_probe_copy(dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size(), _stream()),
+          "vi_probe_copy")

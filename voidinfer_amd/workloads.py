@@ -1,0 +1,148 @@
+"""Seeded synthetic inputs for the five BASELINE configurations (numpy, host side).
+
+Logits are N(0, s) — s read as the standard deviation — plus a Zipf(1.1) bias
+over a seeded random permutation of token ids, scaled so the largest bias is
+``zipf_max``.  Histories are uniform int32 token ids.  Every generator is keyed
+by (config, seed) so the GPU path, the CPU oracle and the benchmark see the same
+bits.  16-bit logits are returned as raw uint16 patterns (round to nearest
+even from float32).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+V_QWEN = 248_320
+V_CONFIG1 = 151_936
+ROW_PARAMS = np.dtype([
+    ("temperature", "<f4"), ("top_p", "<f4"), ("min_p", "<f4"),
+    ("repetition_penalty", "<f4"), ("presence_penalty", "<f4"), ("frequency_penalty", "<f4"),
+    ("top_k", "<i4"), ("lane", "<u4"), ("seed", "<u8"), ("position", "<i4"), ("reserved", "<u4"),
+])
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def to_f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def encode(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return to_bf16_bits(x)
+    if dtype == "f16":
+        return to_f16_bits(x)
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def zipf_bias(rng: np.random.Generator, vocab: int, s: float = 1.1, zipf_max: float = 8.0) -> np.ndarray:
+    ranks = rng.permutation(vocab).astype(np.float64) + 1.0
+    return (zipf_max / ranks ** s).astype(np.float32)
+
+
+def gaussian_zipf(rows: int, vocab: int, std: float, seed: int, zipf: bool = True,
+                  zipf_max: float = 8.0) -> np.ndarray:
+    """float32 [rows, vocab]: N(0, std) plus a per-row Zipf bias."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, vocab), dtype=np.float32) * np.float32(std)
+    if zipf:
+        for r in range(rows):
+            x[r] += zipf_bias(rng, vocab, zipf_max=zipf_max)
+    return x
+
+
+def histories(rows: int, length: int, vocab: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    rng = np.random.default_rng(seed ^ 0x5EED)
+    h = rng.integers(0, vocab, size=(rows, length), dtype=np.int32)
+    offsets = np.arange(rows + 1, dtype=np.int64) * length
+    return h.reshape(-1), offsets
+
+
+def lane_params(rows: int, seed: int, top_k_choices=(0, 20, 50), top_p_choices=(0.8, 0.95, 1.0),
+                min_p_choices=(0.0, 0.05), position: int = 4096) -> np.ndarray:
+    """Config-2 style per-lane parameters drawn from `seed`."""
+    rng = np.random.default_rng(seed ^ 0xC0FFEE)
+    p = np.zeros(rows, dtype=ROW_PARAMS)
+    p["temperature"] = rng.uniform(0.3, 1.2, rows)
+    p["top_k"] = rng.choice(np.asarray(top_k_choices, dtype=np.int32), rows)
+    p["top_p"] = rng.choice(np.asarray(top_p_choices, dtype=np.float32), rows)
+    p["min_p"] = rng.choice(np.asarray(min_p_choices, dtype=np.float32), rows)
+    p["repetition_penalty"] = rng.uniform(1.0, 1.1, rows)
+    p["presence_penalty"] = rng.uniform(0.0, 0.5, rows)
+    p["frequency_penalty"] = rng.uniform(0.0, 0.5, rows)
+    p["lane"] = np.arange(rows, dtype=np.uint32)
+    p["seed"] = rng.integers(1, 2**63, rows, dtype=np.uint64)
+    p["position"] = position
+    return p
+
+
+def config1(seed: int = 1):
+    """1 x fp32, V=151,936, N(0,2)+Zipf; greedy then T .7 / k 20 / p .8, rep 1.05 over 256 tokens."""
+    x = gaussian_zipf(1, V_CONFIG1, 2.0, seed)
+    h, off = histories(1, 256, V_CONFIG1, seed)
+    p = np.zeros(1, dtype=ROW_PARAMS)
+    p["temperature"], p["top_k"], p["top_p"], p["repetition_penalty"] = 0.7, 20, 0.8, 1.05
+    p["seed"], p["position"] = 0x1234_5678_9ABC_DEF0, 1024
+    return x, h, off, p
+
+
+def config2(seed: int = 2):
+    """8 lanes x bf16, V=248,320, mixed per-lane params, 4,096-token histories."""
+    x = gaussian_zipf(8, V_QWEN, 2.0, seed)
+    h, off = histories(8, 4096, V_QWEN, seed)
+    return to_bf16_bits(x), h, off, lane_params(8, seed)
+
+
+def config3(seed: int = 3, rows: int = 128):
+    """128 x fp16 draft rows, N(0,1.5), 8 planted peaks at +6..+10; top-8 + log-probs."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, V_QWEN), dtype=np.float32) * np.float32(1.5)
+    for r in range(rows):
+        pos = rng.choice(V_QWEN, 8, replace=False)
+        x[r, pos] = rng.uniform(6.0, 10.0, 8).astype(np.float32)
+    return to_f16_bits(x)
+
+
+def config5(seed: int = 5, rows: int = 128, history: int = 32768):
+    """128 x bf16 near-flat N(0,0.1), top_k off, top_p .95, 32,768-token histories."""
+    x = gaussian_zipf(rows, V_QWEN, 0.1, seed, zipf=False)
+    h, off = histories(rows, history, V_QWEN, seed)
+    p = lane_params(rows, seed, top_k_choices=(0,), top_p_choices=(0.95,), min_p_choices=(0.0,))
+    return to_bf16_bits(x), h, off, p
+
+
+def config4(seed: int = 4, lanes: int = 8, drafts: int = 16, bonus: bool = False, vocab: int = V_QWEN,
+            sample_fn=None):
+    """DFlash2 verification: draft fp16 rows, target bf16 = draft + N(0, 0.5).
+
+    Drafted ids: the draft rows' argmax when ``sample_fn`` is None, otherwise
+    ``sample_fn(draft_row_f32, lane, j) -> id`` (a draw from the filtered draft
+    distribution).  Returns target bits, draft bits, drafted int32 [lanes, drafts],
+    per-lane params (T .7, top_p .8, top_k 20)."""
+    rng = np.random.default_rng(seed)
+    d = gaussian_zipf(lanes * drafts, vocab, 2.0, seed)
+    trows = drafts + 1 if bonus else drafts
+    t = np.empty((lanes * trows, vocab), dtype=np.float32)
+    for l in range(lanes):
+        for j in range(trows):
+            src = d[l * drafts + min(j, drafts - 1)]
+            t[l * trows + j] = src + rng.standard_normal(vocab, dtype=np.float32) * np.float32(0.5)
+    d16 = to_f16_bits(d)
+    drafted = np.empty((lanes, drafts), dtype=np.int32)
+    for l in range(lanes):
+        for j in range(drafts):
+            row = d16[l * drafts + j].view(np.float16).astype(np.float32)
+            drafted[l, j] = int(np.argmax(row)) if sample_fn is None else sample_fn(row, l, j)
+    p = np.zeros(lanes, dtype=ROW_PARAMS)
+    p["temperature"], p["top_p"], p["top_k"], p["repetition_penalty"] = 0.7, 0.8, 20, 1.0
+    p["lane"] = np.arange(lanes)
+    p["seed"] = rng.integers(1, 2**62, lanes, dtype=np.uint64)
+    p["position"] = 5000
+    return to_bf16_bits(t), d16, drafted, p
