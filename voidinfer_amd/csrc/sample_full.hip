@@ -7,17 +7,19 @@
 // of the logit's 16-bit pattern.  The multiset of z over a row is therefore
 // exactly a 65,536-bin count histogram over order-preserving 16-bit keys, and
 // every truncation (top-k count, top-p mass, min-p ratio) and the draw reduce to
-// prefix sums over the occupied bins; the float work (one exp per bin, fp64) is
+// prefix sums over the occupied bins; the float work (one fp64 exp per bin) is
 // per distinct key, not per token.
 //
 // Shape: each row is owned by a PAIR of 1024-thread workgroups (one per half of
-// the vocabulary, placed on the same XCD), which keep their half of the row in
-// registers (16 x 16-byte vectors per thread):
+// the vocabulary, both on one XCD), which keep their half of the row in
+// registers (16 x 16-byte vectors per thread, plus <= 7 head / tail logits when
+// the half does not start 16-byte aligned):
 //   A. history -> LDS u8 occurrence counts of the half (saturating, exact side
 //      table), penalties applied to the register-resident logits in place;
 //   B. LDS u16 key histogram -> sorted (key, count) list published to HBM;
 //   C. one pair barrier; both workgroups merge the two lists (merge path) into
-//      cumulative counts / masses in LDS and take identical decisions;
+//      cumulative counts / masses in LDS and take identical decisions with
+//      wave-wide 64-ary searches;
 //   D. the half owning the drawn (key, rank) finds the token in its registers.
 // The pair barrier spins on an agent-scope counter with an iteration cap, so a
 // missing partner becomes VI_FLAG_ERROR, never a hang.  Roofline: HBM,
@@ -33,7 +35,7 @@ namespace {
 constexpr int kFT = 1024;                 // threads per workgroup
 constexpr int kFW = kFT / kWave;          // waves per workgroup
 constexpr int kFV = 16;                   // 16-byte vectors per thread
-constexpr int kHalfMax = kFT * kFV * 8;   // logits per half (131,072)
+constexpr int kVecMax = kFT * kFV;        // vectors per half
 constexpr int kListMax = 8192;            // merged (key, half) entries
 constexpr int kOvfMax = 512;              // history tokens with >= 255 occurrences per half
 constexpr uint32_t kSpinLimit = 1u << 22;
@@ -49,6 +51,13 @@ struct alignas(256) PairBarrier {
     uint32_t gen;
     uint32_t pad[62];
 };
+// What the probs kernel needs to rebuild the filtered distribution.
+struct alignas(16) RowBoundary {
+    double z0, s_n;
+    float inv_t;
+    int32_t pn_key, pn_half;
+    uint32_t pn_take, valid;
+};
 
 struct FullArgs {
     const void* logits;
@@ -59,28 +68,34 @@ struct FullArgs {
     const int64_t* offsets;
     int32_t* tokens;
     double* uniforms;
-    float* probs;
+    float* probs;            // optional; doubles as scratch for penalized bits
     int64_t probs_stride;
     vi_sample_stats* stats;
-    PairBarrier* barriers;   // [pairs]
+    PairBarrier* barriers;   // [rows]
     FullHeader* headers;     // [rows][2]
     uint32_t* lists;         // [rows][2][kListMax]
+    RowBoundary* bounds;     // [rows]
 };
 
 constexpr uint32_t kHdrNonfinite = 1u, kHdrBadHistory = 2u, kHdrError = 4u, kHdrOverflow = 8u;
 
 // LDS map (bytes).  Phase A: u8 counts [0, 128 KiB) + saturated side table.
-// Phase B: u16 histogram [0, 128 KiB).  Phase C: lists [0, 32 KiB), C u32
-// [32 KiB, 64 KiB + 4), W f64 [64 KiB + 256, 128 KiB + 264).
-constexpr int kLdsBytes = 131072 + 8 * kOvfMax + 1024;
-constexpr int kOffC = 32768, kOffW = 65536 + 256;
+// Phase B: u16 histogram [0, 128 KiB).  Phase C: lists A|B [0, 32 KiB) (then
+// cumulative counts C), merged entries M [32, 64 KiB), cumulative masses W
+// [64 KiB, 128 KiB + 8), half bits after.
+constexpr int kOffM = 4 * kListMax, kOffW = 8 * kListMax, kOffH = 16 * kListMax + 256;
+constexpr int kLdsBytes = 131072 + 8 * kOvfMax + 1280;
+static_assert(kOffH + kListMax / 8 <= kLdsBytes, "LDS map");
 
 struct Shared {
     uint32_t u[kFW + 1];
     double d[kFW + 1];
-    uint32_t ovf_n, flags, minp_pos, found;
-    int32_t sel_pos, sel_key, sel_half, sel_count;
-    double sel_w;
+    uint32_t ovf_n, flags, minp_pos;
+    // decisions (written by wave 0)
+    int32_t r_key, r_half, pn_key, pn_half;
+    uint32_t rank, pn_take, n_sup, slot, slot_rank;
+    double s_n, draw_u;
+    uint32_t slot_tot[kFV + 2];
 };
 
 template <int NT>
@@ -118,35 +133,59 @@ __device__ __forceinline__ float key_z(uint32_t key, float inv_t) {
     return Elem<DT>::decode(unkey16(key)) * inv_t;
 }
 
-// Sequential merge state of the two descending lists (half 0 first on ties).
-struct Merge {
-    const uint32_t* A;  // ascending in memory; read reversed
-    const uint32_t* B;
-    int n0, n1, i, j;
-    __device__ uint32_t a(int k) const { return A[n0 - 1 - k]; }
-    __device__ uint32_t b(int k) const { return B[n1 - 1 - k]; }
-    __device__ void seek(int d) {  // merge path: i + j = d
-        int lo = max(0, d - n1), hi = min(d, n0);
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if ((a(mid) >> 16) >= (b(d - 1 - mid) >> 16)) lo = mid + 1; else hi = mid;
+// Smallest i in [lo, hi) with pred(i) (pred monotone false -> true), or hi.
+// Wave-uniform call; 64 probes per round.
+template <class P>
+__device__ int wave_search(int lo, int hi, P pred) {
+    const int lane = lane_id();
+    while (hi > lo) {
+        const int n = hi - lo;
+        if (n <= kWave) {
+            const uint64_t m = ballot(lane < n && pred(lo + lane));
+            return m ? lo + __builtin_ctzll(m) : hi;
         }
-        i = lo; j = d - lo;
+        const int step = (n + kWave - 1) / kWave;
+        const int p = lo + lane * step;
+        const uint64_t valid = ballot(p < hi);
+        const uint64_t m = ballot(p < hi && pred(p));
+        if (!m) {
+            const int last = 63 - __builtin_clzll(valid);
+            lo = lo + last * step + 1;
+            continue;
+        }
+        const int f = __builtin_ctzll(m);
+        if (f == 0) return lo;
+        const int nlo = lo + (f - 1) * step + 1;
+        hi = lo + f * step;
+        lo = nlo;
+        if (lo == hi) return lo;
     }
-    // Next entry: (key << 16 | count) and its half.
-    __device__ uint32_t next(int& half) {
-        if (i < n0 && (j >= n1 || (a(i) >> 16) >= (b(j) >> 16))) { half = 0; return a(i++); }
-        half = 1;
-        return b(j++);
+    return lo;
+}
+
+// Element j (0..7) of a 16-byte vector held as two 64-bit halves.
+__device__ __forceinline__ uint32_t bits_of(uint64_t q0, uint64_t q1, int j) {
+    return uint32_t(((j < 4 ? q0 : q1) >> ((j & 3) * 16)) & 0xffffu);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t count_key8(const uint4& v, uint32_t key) {
+    uint32_t c = 0;
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+        c += (Elem<DT>::finite_bits(b) && key16(b) == key) ? 1u : 0u;
     }
-};
+    return c;
+}
 
 template <int DT>
 __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
     __shared__ Shared sh;
     uint32_t* lds32 = reinterpret_cast<uint32_t*>(lds);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     const int b = blockIdx.x, xcd = b & 7, slot = b >> 3, half = slot & 1;
     const int row = (slot >> 1) * 8 + xcd;
     if (row >= a.rows) return;
@@ -156,19 +195,29 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     const int V = a.vocabulary, H = a.half_len;
     const int h0 = half * H, h1 = min(V, h0 + H);
     const int n_el = max(0, h1 - h0);
-    const int nvec = n_el / 8, tail = n_el - nvec * 8;
-    const unsigned char* rowp = static_cast<const unsigned char*>(a.logits) + (size_t(row) * size_t(a.stride) + size_t(h0)) * 2;
+    const int64_t g0 = int64_t(row) * a.stride + h0;     // element offset of this half
+    const int head = min(n_el, int((8 - (g0 & 7)) & 7));
+    const int nvec = (n_el - head) / 8, tail = n_el - head - nvec * 8;
+    const uint16_t* base16 = static_cast<const uint16_t*>(a.logits) + g0;
+    const unsigned char* vbase = reinterpret_cast<const unsigned char*>(base16 + head);
+    const int vid0 = h0 + head;                          // token id of vector 0, element 0
 
     // ---- issue every load of this half up front (one HBM read of the row)
+    // Branch-free: out-of-range slots re-load the half's last vector (an L2
+    // hit) and are masked wherever the data is consumed (v < nvec).
     uint4 d[kFV];
+    const int vlast = max(nvec - 1, 0);
+    if (nvec > 0) {
 #pragma unroll
-    for (int i = 0; i < kFV; ++i) {
-        const int v = i * kFT + tid;
-        d[i] = v < nvec ? load16(rowp + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < kFV; ++i) d[i] = load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kFV; ++i) d[i] = make_uint4(0, 0, 0, 0);
     }
-    uint32_t tbits = tid < tail ? uint32_t(reinterpret_cast<const uint16_t*>(rowp)[nvec * 8 + tid]) : 0u;
+    uint32_t hbits = tid < head ? uint32_t(base16[tid]) : 0u;
+    uint32_t tbits = tid < tail ? uint32_t(base16[head + nvec * 8 + tid]) : 0u;
 
-    if (tid == 0) { sh.ovf_n = 0; sh.flags = 0; sh.minp_pos = 0xffffffffu; sh.found = 0; }
+    if (tid == 0) { sh.ovf_n = 0; sh.flags = 0; sh.minp_pos = 0xffffffffu; }
     const int64_t hb = a.offsets ? a.offsets[row] : 0;
     const int64_t hn = a.offsets ? a.offsets[row + 1] - hb : 0;
     const bool pen = penalties_active(p) && hn > 0 && a.histories;
@@ -213,7 +262,9 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             }
             __syncthreads();
         }
-        auto count_of = [&](int off, uint32_t c) -> uint32_t {
+        const unsigned char* cnt8 = lds;
+        auto count_at = [&](int off) -> uint32_t {   // occurrences of token h0 + off
+            const uint32_t c = cnt8[off];
             if (c != 255u) return c;
             for (uint32_t k = 0; k < n_ovf; ++k) if (ovf_tok[k] == uint32_t(h0 + off)) return ovf_cnt[k];
             return c;
@@ -222,29 +273,39 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         for (int i = 0; i < kFV; ++i) {
             const int v = i * kFT + tid;
             if (v < nvec) {
-                const uint2 cc = *reinterpret_cast<const uint2*>(lds + size_t(v) * 8);
-                if (cc.x | cc.y) {
-                    uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t c = ((j < 4 ? cc.x : cc.y) >> ((j & 3) * 8)) & 255u;
-                        if (c) {
-                            uint32_t& w = w4[j >> 1];
-                            const uint32_t bits = (j & 1) ? (w >> 16) : (w & 0xffffu);
-                            if (Elem<DT>::finite_bits(bits)) {
-                                const uint32_t nb = penalize_bits<DT>(bits, count_of(v * 8 + j, c), p) & 0xffffu;
-                                w = (j & 1) ? ((w & 0xffffu) | (nb << 16)) : ((w & 0xffff0000u) | nb);
-                            }
-                        }
+                const int off0 = head + v * 8;
+                // the 8 counts of this vector (two LDS words when the half starts aligned)
+                uint64_t cc = 0;
+                if ((head & 3) == 0) {
+                    const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cnt8 + off0);
+                    cc = uint64_t(c32[0]) | (uint64_t(c32[1]) << 32);
+                } else {
+                    for (int j = 0; j < 8; ++j) cc |= uint64_t(cnt8[off0 + j]) << (8 * j);
+                }
+                if (cc) {
+                    uint64_t q0 = uint64_t(d[i].x) | (uint64_t(d[i].y) << 32);
+                    uint64_t q1 = uint64_t(d[i].z) | (uint64_t(d[i].w) << 32);
+                    for (int j = 0; j < 8; ++j) {                     // rolled: low register use
+                        if (!((cc >> (8 * j)) & 255u)) continue;
+                        const uint32_t bits = bits_of(q0, q1, j);
+                        if (!Elem<DT>::finite_bits(bits)) continue;
+                        const uint64_t nb = penalize_bits<DT>(bits, count_at(off0 + j), p) & 0xffffu;
+                        const int s = (j & 3) * 16;
+                        if (j < 4) q0 = (q0 & ~(0xffffull << s)) | (nb << s);
+                        else q1 = (q1 & ~(0xffffull << s)) | (nb << s);
                     }
-                    d[i] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                    d[i] = make_uint4(uint32_t(q0), uint32_t(q0 >> 32), uint32_t(q1), uint32_t(q1 >> 32));
                 }
             }
         }
+        if (tid < head) {
+            const uint32_t c = count_at(tid);
+            if (c && Elem<DT>::finite_bits(hbits)) hbits = penalize_bits<DT>(hbits, c, p) & 0xffffu;
+        }
         if (tid < tail) {
-            const int off = nvec * 8 + tid;
-            const uint32_t c = (lds32[off >> 2] >> ((off & 3) * 8)) & 255u;
-            if (c && Elem<DT>::finite_bits(tbits)) tbits = penalize_bits<DT>(tbits, count_of(off, c), p) & 0xffffu;
+            const int off = head + nvec * 8 + tid;
+            const uint32_t c = count_at(off);
+            if (c && Elem<DT>::finite_bits(tbits)) tbits = penalize_bits<DT>(tbits, c, p) & 0xffffu;
         }
         __syncthreads();
     }
@@ -255,43 +316,43 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     bool nonfinite = false;
     for (int w = tid; w < 32768; w += kFT) lds32[w] = 0u;
     __syncthreads();
+    auto hist_add = [&](uint32_t bits) {
+        if (Elem<DT>::finite_bits(bits)) {
+            const uint32_t k = key16(bits);
+            atomicAdd(&lds32[k >> 1], (k & 1u) ? 0x10000u : 1u);
+            ++n_fin;
+        } else {
+            nonfinite = true;
+        }
+    };
 #pragma unroll
     for (int i = 0; i < kFV; ++i) {
         if (i * kFT + tid < nvec) {
             const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t bits = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                if (Elem<DT>::finite_bits(bits)) {
-                    const uint32_t k = key16(bits);
-                    atomicAdd(&lds32[k >> 1], (k & 1u) ? 0x10000u : 1u);
-                    ++n_fin;
-                } else {
-                    nonfinite = true;
-                }
-            }
+            for (int j = 0; j < 8; ++j) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
         }
     }
-    if (tid < tail) {
-        if (Elem<DT>::finite_bits(tbits)) { const uint32_t k = key16(tbits); atomicAdd(&lds32[k >> 1], (k & 1u) ? 0x10000u : 1u); ++n_fin; }
-        else nonfinite = true;
-    }
+    if (tid < head) hist_add(hbits);
+    if (tid < tail) hist_add(tbits);
     if (nonfinite) atomicOr(&sh.flags, kHdrNonfinite);
     __syncthreads();
     // thread t owns keys [64t, 64t + 64)
     uint32_t my_n = 0, my_sum = 0;
+#pragma unroll 2  // fully unrolled, the 32 LDS reads in flight spill the register-resident row
     for (int w = 0; w < 32; ++w) {
         const uint32_t x = lds32[tid * 32 + w];
         my_n += ((x & 0xffffu) != 0u) + ((x >> 16) != 0u);
         my_sum += (x & 0xffffu) + (x >> 16);
     }
     uint32_t n_list;
-    const uint32_t base = block_exclusive_scan_u32<kFT>(my_n, sh.u, &n_list);
+    const uint32_t lbase = block_exclusive_scan_u32<kFT>(my_n, sh.u, &n_list);
     const uint32_t tot_fin = block_sum_u32<kFT>(n_fin, sh.u);
     const uint32_t tot_sum = block_sum_u32<kFT>(my_sum, sh.u);
     uint32_t* my_list = a.lists + (size_t(row) * 2 + half) * kListMax;
     {
-        uint32_t at = base;
+        uint32_t at = lbase;
+#pragma unroll 2
         for (int w = 0; w < 32; ++w) {
             const uint32_t x = lds32[tid * 32 + w];
             const uint32_t k0 = uint32_t(tid * 64 + 2 * w);
@@ -321,7 +382,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         } else {
             uint32_t it = 0;
             while (__hip_atomic_load(&bar->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == gen) {
-                __builtin_amdgcn_s_sleep(2);
+                __builtin_amdgcn_s_sleep(1);
                 if (++it > kSpinLimit) { sh.flags |= kHdrError; break; }
             }
         }
@@ -331,12 +392,11 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     const FullHeader H0 = a.headers[size_t(row) * 2 + 0], H1 = a.headers[size_t(row) * 2 + 1];
     const uint32_t hflags = H0.flags | H1.flags | (sh.flags & kHdrError);
     const int n0 = int(H0.n_list), n1 = int(H1.n_list), n = n0 + n1;
-    const uint32_t N_f = H0.n_finite + H1.n_finite;
     uint32_t out_flags = 0;
     if (hflags & kHdrNonfinite) out_flags |= VI_FLAG_NONFINITE;
     if (hflags & kHdrBadHistory) out_flags |= VI_FLAG_BAD_HISTORY;
     const bool fail = (hflags & (kHdrError | kHdrOverflow)) || n > kListMax;
-    if (fail || N_f == 0) {
+    if (fail || H0.n_finite + H1.n_finite == 0) {
         if (half == 0 && tid == 0) {
             a.tokens[row] = fail ? -1 : V;
             if (a.uniforms) a.uniforms[row] = 0.0;
@@ -345,6 +405,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                 s.flags = out_flags | (fail ? VI_FLAG_ERROR : VI_FLAG_EMPTY);
                 a.stats[row] = s;
             }
+            if (a.bounds) a.bounds[row] = RowBoundary{0.0, 0.0, 0.0f, -1, 0, 0u, 0u};
         }
         if (a.probs) {
             float* pr = a.probs + size_t(row) * size_t(a.probs_stride);
@@ -353,108 +414,98 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         return;
     }
 
-    // ---- C'. merged cumulative counts / masses
+    // ---- C'. merge: M (entries, merged order), W (exclusive masses), C (counts)
     uint32_t* LA = lds32;
     uint32_t* LB = lds32 + n0;
-    uint32_t* C = reinterpret_cast<uint32_t*>(lds + kOffC);
+    uint32_t* M = reinterpret_cast<uint32_t*>(lds + kOffM);
     double* W = reinterpret_cast<double*>(lds + kOffW);
+    uint32_t* HB = reinterpret_cast<uint32_t*>(lds + kOffH);
+    uint32_t* C = lds32;   // reuses the list region after the merge
     {
-        const uint32_t* g0 = a.lists + (size_t(row) * 2 + 0) * kListMax;
-        const uint32_t* g1 = a.lists + (size_t(row) * 2 + 1) * kListMax;
-        for (int i = tid; i < n0; i += kFT) LA[i] = g0[i];
-        for (int i = tid; i < n1; i += kFT) LB[i] = g1[i];
+        const uint32_t* gl0 = a.lists + (size_t(row) * 2 + 0) * kListMax;
+        const uint32_t* gl1 = a.lists + (size_t(row) * 2 + 1) * kListMax;
+        for (int i = tid; i < n0; i += kFT) LA[i] = gl0[i];
+        for (int i = tid; i < n1; i += kFT) LB[i] = gl1[i];
+        for (int i = tid; i < (n + 31) / 32; i += kFT) HB[i] = 0u;
     }
     __syncthreads();
-    Merge M{LA, LB, n0, n1, 0, 0};
     const uint32_t top_key = max(n0 ? LA[n0 - 1] >> 16 : 0u, n1 ? LB[n1 - 1] >> 16 : 0u);
     const double z0 = double(key_z<DT>(top_key, inv_t));
     const int E = (n + kFT - 1) / kFT;
     const int d0 = min(tid * E, n), d1 = min(d0 + E, n);
     uint32_t lc = 0;
     double lw = 0.0;
-    M.seek(d0);
-    const int mi = M.i, mj = M.j;
-    for (int pos = d0; pos < d1; ++pos) {
-        int hh;
-        const uint32_t e = M.next(hh);
-        const float z = key_z<DT>(e >> 16, inv_t);
-        uint32_t cnt = e & 0xffffu;
-        double w = 0.0;
-        if (!isfinite(z)) { cnt = 0; atomicOr(&sh.flags, kHdrNonfinite); }
-        else w = exp(double(z) - z0);
-        if (p.min_p > 0.0f && w < double(p.min_p) && cnt) atomicMin(&sh.minp_pos, uint32_t(pos));
-        C[pos] = lc;
-        W[pos] = lw;
-        lc += cnt;
-        lw += double(cnt) * w;
+    {
+        // merge path over the two lists read in descending key order (half 0 first on ties)
+        auto A = [&](int k) { return LA[n0 - 1 - k]; };
+        auto B = [&](int k) { return LB[n1 - 1 - k]; };
+        int lo = max(0, d0 - n1), hi = min(d0, n0);
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((A(mid) >> 16) >= (B(d0 - 1 - mid) >> 16)) lo = mid + 1; else hi = mid;
+        }
+        int i = lo, j = d0 - lo;
+        for (int pos = d0; pos < d1; ++pos) {
+            uint32_t e;
+            if (i < n0 && (j >= n1 || (A(i) >> 16) >= (B(j) >> 16))) e = A(i++);
+            else { e = B(j++); atomicOr(&HB[pos >> 5], 1u << (pos & 31)); }
+            const float z = key_z<DT>(e >> 16, inv_t);
+            uint32_t cnt = e & 0xffffu;
+            double w = 0.0;
+            if (!isfinite(z) || !isfinite(z0)) { cnt = 0; atomicOr(&sh.flags, kHdrNonfinite); }
+            else w = exp(double(z) - z0);
+            if (p.min_p > 0.0f && cnt && w < double(p.min_p)) atomicMin(&sh.minp_pos, uint32_t(pos));
+            M[pos] = (e & 0xffff0000u) | cnt;
+            W[pos] = lw;
+            lc += cnt;
+            lw += double(cnt) * w;
+        }
     }
     uint32_t ctot;
     double wtot;
-    const uint32_t coff = block_exclusive_scan_u32<kFT>(lc, sh.u, &ctot);
+    const uint32_t coff = block_exclusive_scan_u32<kFT>(lc, sh.u, &ctot);   // (barriers inside: merge done)
     const double woff = block_exclusive_scan_f64<kFT>(lw, sh.d, &wtot);
-    for (int pos = d0; pos < d1; ++pos) { C[pos] += coff; W[pos] += woff; }
+    {
+        uint32_t c = coff;
+        for (int pos = d0; pos < d1; ++pos) {
+            W[pos] += woff;
+            C[pos] = c;
+            c += M[pos] & 0xffffu;
+        }
+    }
     if (tid == 0) { C[n] = ctot; W[n] = wtot; }
     __syncthreads();
     if (sh.flags & kHdrNonfinite) out_flags |= VI_FLAG_NONFINITE;
-    const uint32_t Nv = C[n];
 
-    // Parallel search: the first merged entry whose predicate holds; its
-    // (pos, key, half, count, w) land in sh.sel_*.  pred(pos, C[pos], W[pos],
-    // count, w) must be monotone in pos.
-    auto find_first = [&](auto pred) -> bool {
-        if (tid == 0) { sh.found = 0; sh.sel_pos = 0x7fffffff; }
-        __syncthreads();
-        Merge m2 = M;
-        m2.i = mi; m2.j = mj;
-        int hit = -1;
-        for (int pos = d0; pos < d1 && hit < 0; ++pos) {
-            int hh;
-            const uint32_t e = m2.next(hh);
-            const float z = key_z<DT>(e >> 16, inv_t);
-            const uint32_t cnt = isfinite(z) ? (e & 0xffffu) : 0u;
-            const double w = isfinite(z) ? exp(double(z) - z0) : 0.0;
-            if (pred(pos, C[pos], W[pos], cnt, w)) hit = pos;
+    // ---- decisions, identical in both workgroups (wave 0, 64-ary searches)
+    if (wave == 0) {
+        const uint32_t Nv = C[n];
+        auto wt = [&](int pos) -> double {
+            const float z = key_z<DT>(M[pos] >> 16, inv_t);
+            return isfinite(z) ? exp(double(z) - z0) : 0.0;
+        };
+        auto cnt = [&](int pos) -> uint32_t { return M[pos] & 0xffffu; };
+        const uint32_t cap = (p.top_k > 0 && uint32_t(p.top_k) < Nv) ? uint32_t(p.top_k) : Nv;
+        double s_cap = W[n];
+        if (cap < Nv) {
+            const int pk = wave_search(0, n, [&](int pos) { return C[pos + 1] >= cap; });
+            s_cap = W[pk] + double(cap - C[pk]) * wt(pk);
         }
-        if (hit >= 0) atomicMin(reinterpret_cast<unsigned*>(&sh.sel_pos), unsigned(hit));
-        __syncthreads();
-        if (hit >= 0 && hit == sh.sel_pos) {
-            Merge m3 = M;
-            m3.seek(hit);
-            int hh;
-            const uint32_t e = m3.next(hh);
-            const float z = key_z<DT>(e >> 16, inv_t);
-            sh.sel_key = int(e >> 16);
-            sh.sel_half = hh;
-            sh.sel_count = isfinite(z) ? int(e & 0xffffu) : 0;
-            sh.sel_w = isfinite(z) ? exp(double(z) - z0) : 0.0;
-            sh.found = 1;
-        }
-        __syncthreads();
-        return sh.found != 0;
-    };
-
-    // ---- decisions (identical in both workgroups)
-    const uint32_t cap = (p.top_k > 0 && uint32_t(p.top_k) < Nv) ? uint32_t(p.top_k) : Nv;
-    double s_cap = W[n];
-    if (cap < Nv) {
-        find_first([&](int, uint32_t c, double, uint32_t cnt, double) { return c + cnt >= cap; });
-        s_cap = W[sh.sel_pos] + double(cap - C[sh.sel_pos]) * sh.sel_w;
-    }
-    uint32_t n_sup = cap;
-    if (p.min_p > 0.0f && sh.minp_pos != 0xffffffffu) n_sup = min(n_sup, C[sh.minp_pos]);
-    if (p.top_p < 1.0f) {
-        const double target = double(p.top_p) * s_cap;
-        if (find_first([&](int, uint32_t c, double wc, uint32_t cnt, double w) {
+        uint32_t n_sup = cap;
+        if (p.min_p > 0.0f && sh.minp_pos != 0xffffffffu) n_sup = min(n_sup, C[sh.minp_pos]);
+        if (p.top_p < 1.0f) {
+            const double target = double(p.top_p) * s_cap;
+            const int pt = wave_search(0, n, [&](int pos) {
+                const uint32_t c = C[pos];
                 if (c >= cap) return true;
-                const uint32_t ce = min(cnt, cap - c);
-                return wc + double(ce) * w >= target;
-            })) {
-            const uint32_t c = C[sh.sel_pos];
-            if (c < cap) {
-                const double wc = W[sh.sel_pos], w = sh.sel_w;
-                const uint32_t ce = min(uint32_t(sh.sel_count), cap - c);
+                return W[pos] + double(min(cnt(pos), cap - c)) * wt(pos) >= target;
+            });
+            if (pt < n && C[pt] < cap) {
+                const uint32_t c = C[pt];
+                const double wc = W[pt], w = wt(pt);
+                const uint32_t ce = min(cnt(pt), cap - c);
                 // smallest i with wc + (i + 1) w >= target
-                double q = (target - wc) / w;
+                const double q = (target - wc) / w;
                 int i = q > 0.0 ? int(fmin(ceil(q), double(ce))) - 1 : 0;
                 i = max(0, min(i, int(ce) - 1));
                 while (i > 0 && wc + double(i) * w >= target) --i;
@@ -462,153 +513,180 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                 n_sup = min(n_sup, c + uint32_t(i) + 1u);
             }
         }
-    }
-    if (n_sup < 1u) n_sup = 1u;
-    // S_n: entry holding element n_sup
-    find_first([&](int, uint32_t c, double, uint32_t cnt, double) { return c + cnt >= n_sup; });
-    const double s_n = W[sh.sel_pos] + double(n_sup - C[sh.sel_pos]) * sh.sel_w;
-    const int pn_pos = sh.sel_pos, pn_key = sh.sel_key, pn_half = sh.sel_half;
-    const uint32_t pn_take = n_sup - C[pn_pos];
-    // draw
-    const double u = philox_uniform(p.seed, p.lane, p.position, 0u);
-    const double t = u * s_n;
-    int r_pos, r_key, r_half;
-    uint32_t rank;
-    const bool hit = find_first([&](int, uint32_t c, double wc, uint32_t cnt, double w) {
-        if (c >= n_sup) return true;
-        const uint32_t ce = min(cnt, n_sup - c);
-        return wc + double(ce) * w > t;
-    });
-    if (hit && C[sh.sel_pos] < n_sup) {
-        r_pos = sh.sel_pos; r_key = sh.sel_key; r_half = sh.sel_half;
-        const double wc = W[r_pos], w = sh.sel_w;
-        const uint32_t ce = min(uint32_t(sh.sel_count), n_sup - C[r_pos]);
-        // smallest i with wc + (i + 1) w > t
-        const double q = (t - wc) / w;
-        int i = q > 0.0 ? int(fmin(floor(q), double(ce - 1))) : 0;
-        i = max(0, min(i, int(ce) - 1));
-        while (i > 0 && wc + double(i) * w > t) --i;
-        while (i < int(ce) - 1 && wc + double(i + 1) * w <= t) ++i;
-        rank = uint32_t(i);
-    } else {
-        r_pos = pn_pos; r_key = pn_key; r_half = pn_half; rank = pn_take - 1u;
-    }
-
-    // ---- D. the owning half finds the rank-th logit of key r_key (id order)
-    auto count_key = [&](const uint4& v, int key) -> uint32_t {
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        uint32_t c = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t bits = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-            c += (Elem<DT>::finite_bits(bits) && key16(bits) == uint32_t(key)) ? 1u : 0u;
+        if (n_sup < 1u) n_sup = 1u;
+        const int pn = wave_search(0, n, [&](int pos) { return C[pos + 1] >= n_sup; });
+        const uint32_t pn_take = n_sup - C[pn];
+        const double w_pn = wt(pn);
+        const double s_n = W[pn] + double(pn_take) * w_pn;
+        const double u = philox_uniform(p.seed, p.lane, p.position, 0u);
+        const double t = u * s_n;
+        int ru = wave_search(0, pn + 1, [&](int pos) {
+            const uint32_t c = C[pos];
+            const uint32_t ce = pos == pn ? pn_take : cnt(pos);
+            return W[pos] + double(ce) * wt(pos) > t && c < n_sup;
+        });
+        uint32_t rank;
+        if (ru <= pn) {
+            const double wc = W[ru], w = wt(ru);
+            const uint32_t ce = ru == pn ? pn_take : cnt(ru);
+            // smallest i with wc + (i + 1) w > t
+            const double q = (t - wc) / w;
+            int i = q > 0.0 ? int(fmin(floor(q), double(ce - 1))) : 0;
+            i = max(0, min(i, int(ce) - 1));
+            while (i > 0 && wc + double(i) * w > t) --i;
+            while (i < int(ce) - 1 && wc + double(i + 1) * w <= t) ++i;
+            rank = uint32_t(i);
+        } else {
+            ru = pn;
+            rank = pn_take - 1u;
         }
-        return c;
-    };
-    // exclusive id-order rank, within this half, of the first logit of key `key`
-    // held by (vector i, this thread): per-vector totals, then one block scan.
-    uint32_t* vt = sh.u;  // reused: kFV + 1 <= kFW + 1 counters
+        if (lane == 0) {
+            sh.r_key = int(M[ru] >> 16);
+            sh.r_half = int((HB[ru >> 5] >> (ru & 31)) & 1u);
+            sh.rank = rank;
+            sh.pn_key = int(M[pn] >> 16);
+            sh.pn_half = int((HB[pn >> 5] >> (pn & 31)) & 1u);
+            sh.pn_take = pn_take;
+            sh.n_sup = n_sup;
+            sh.s_n = s_n;
+            sh.draw_u = u;
+            sh.slot = 0xffffffffu;
+        }
+    }
+    if (tid < kFV + 2) sh.slot_tot[tid] = 0u;
+    __syncthreads();
+    const int r_half = sh.r_half;
+    const uint32_t r_key = uint32_t(sh.r_key);
+
+    // ---- D. the owning half finds the rank-th logit of key r_key (id order:
+    // head slot, vector slots 0..15 (thread-major inside a slot), tail slot)
     if (half == r_half) {
-        if (tid <= kFV) vt[tid] = 0u;
-        __syncthreads();
-        uint32_t mine[kFV + 1];
+        // per-slot totals
+        uint32_t c_head = (tid < head && Elem<DT>::finite_bits(hbits) && key16(hbits) == r_key) ? 1u : 0u;
+        uint32_t c_tail = (tid < tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == r_key) ? 1u : 0u;
+        if (c_head) atomicAdd(&sh.slot_tot[0], 1u);
 #pragma unroll
         for (int i = 0; i < kFV; ++i) {
-            mine[i] = (i * kFT + tid < nvec) ? count_key(d[i], r_key) : 0u;
-            if (mine[i]) atomicAdd(&vt[i], mine[i]);
+            const uint32_t c = (i * kFT + tid < nvec) ? count_key8<DT>(d[i], r_key) : 0u;
+            if (c) atomicAdd(&sh.slot_tot[1 + i], c);
         }
-        mine[kFV] = (tid < tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == uint32_t(r_key)) ? 1u : 0u;
-        if (mine[kFV]) atomicAdd(&vt[kFV], 1u);
+        if (c_tail) atomicAdd(&sh.slot_tot[kFV + 1], 1u);
         __syncthreads();
-        int vi = kFV;
-        uint32_t before = 0;
-        {
+        if (tid == 0) {
             uint32_t acc = 0;
-            for (int i = 0; i <= kFV; ++i) {
-                if (rank < acc + vt[i]) { vi = i; before = acc; break; }
-                acc += vt[i];
+            for (int s = 0; s < kFV + 2; ++s) {
+                if (sh.rank < acc + sh.slot_tot[s]) { sh.slot = uint32_t(s); sh.slot_rank = sh.rank - acc; break; }
+                acc += sh.slot_tot[s];
             }
         }
-        uint32_t sel = 0;
+        __syncthreads();
+        const int s = int(sh.slot);
+        uint32_t mine = 0;
+        if (s == 0) mine = c_head;
+        else if (s == kFV + 1) mine = c_tail;
+        else {
 #pragma unroll
-        for (int i = 0; i <= kFV; ++i) if (i == vi) sel = mine[i];
+            for (int i = 0; i < kFV; ++i)
+                if (s == 1 + i && i * kFT + tid < nvec) mine = count_key8<DT>(d[i], r_key);
+        }
         uint32_t tot;
-        const uint32_t ex = block_exclusive_scan_u32<kFT>(sel, reinterpret_cast<uint32_t*>(sh.d), &tot);
-        const uint32_t want = rank - before;
-        if (sel && want >= ex && want < ex + sel) {
+        const uint32_t ex = block_exclusive_scan_u32<kFT>(mine, sh.u, &tot);
+        const uint32_t want = sh.slot_rank;
+        if (mine && want >= ex && want < ex + mine) {
             int32_t token = -1;
-            if (vi == kFV) {
-                token = h0 + nvec * 8 + tid;
-            } else {
+            if (s == 0) token = h0 + tid;
+            else if (s == kFV + 1) token = vid0 + nvec * 8 + tid;
+            else {
                 uint4 v = d[0];
 #pragma unroll
-                for (int i = 1; i < kFV; ++i) if (i == vi) v = d[i];
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                for (int i = 1; i < kFV; ++i) if (s == 1 + i) v = d[i];
+                const uint64_t q0 = uint64_t(v.x) | (uint64_t(v.y) << 32), q1 = uint64_t(v.z) | (uint64_t(v.w) << 32);
                 uint32_t k = want - ex;
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t bits = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                    if (Elem<DT>::finite_bits(bits) && key16(bits) == uint32_t(r_key)) {
-                        if (k == 0) { token = h0 + (vi * kFT + tid) * 8 + j; break; }
+                    const uint32_t bits = bits_of(q0, q1, j);
+                    if (Elem<DT>::finite_bits(bits) && key16(bits) == r_key) {
+                        if (k == 0) { token = vid0 + ((s - 1) * kFT + tid) * 8 + j; break; }
                         --k;
                     }
                 }
             }
             a.tokens[row] = token;
-            if (a.uniforms) a.uniforms[row] = u;
+            if (a.uniforms) a.uniforms[row] = sh.draw_u;
             if (a.stats) {
-                vi_sample_stats s{};
-                s.flags = out_flags; s.support = n_sup; s.finite = Nv; s.support_mass = s_n; s.uniform = u;
-                a.stats[row] = s;
+                vi_sample_stats st{};
+                st.flags = out_flags; st.support = sh.n_sup; st.finite = C[n]; st.support_mass = sh.s_n;
+                st.uniform = sh.draw_u;
+                a.stats[row] = st;
             }
         }
     }
 
-    // ---- optional filtered distribution of this half
+    // ---- optional: hand the penalized bits and the support boundary to the
+    // probs kernel (probs row = scratch for the bits until it overwrites them)
     if (a.probs) {
-        float* pr = a.probs + size_t(row) * size_t(a.probs_stride);
-        // rank of each boundary-key logit within this half, id order
-        const bool boundary_half = half == pn_half;
-        uint32_t running = 0;
-        for (int i = 0; i <= kFV; ++i) {
-            uint32_t c = 0;
-            if (boundary_half) {
+        uint32_t* pr = reinterpret_cast<uint32_t*>(a.probs + size_t(row) * size_t(a.probs_stride));
+        if (tid < head) pr[h0 + tid] = hbits;
+        if (tid < tail) pr[vid0 + nvec * 8 + tid] = tbits;
 #pragma unroll
-                for (int ii = 0; ii < kFV; ++ii) if (ii == i && i * kFT + tid < nvec) c = count_key(d[ii], pn_key);
-                if (i == kFV) c = (tid < tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == uint32_t(pn_key)) ? 1u : 0u;
-            }
-            uint32_t tot;
-            uint32_t ex = block_exclusive_scan_u32<kFT>(c, sh.u, &tot);
-            ex += running;
-            running += tot;
-            auto emit = [&](uint32_t bits, int id, uint32_t& k) {
-                float pv = 0.0f;
-                if (Elem<DT>::finite_bits(bits)) {
-                    const uint32_t key = key16(bits);
-                    bool in = key > uint32_t(pn_key);
-                    if (key == uint32_t(pn_key)) {
-                        if (half < pn_half) in = true;
-                        else if (half == pn_half) { in = k < pn_take; ++k; }
-                    }
-                    const float z = key_z<DT>(key, inv_t);
-                    if (in && isfinite(z)) pv = float(exp(double(z) - z0) / s_n);
-                }
-                pr[id] = pv;
-            };
-            uint32_t k = ex;
-            if (i < kFV) {
-                if (i * kFT + tid < nvec) {
-                    uint4 v = d[0];
+        for (int i = 0; i < kFV; ++i) {
+            const int v = i * kFT + tid;
+            if (v < nvec) {
+                const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
 #pragma unroll
-                    for (int ii = 1; ii < kFV; ++ii) if (ii == i) v = d[ii];
-                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t bits = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                        emit(bits, h0 + (i * kFT + tid) * 8 + j, k);
-                    }
-                }
-            } else if (tid < tail) {
-                emit(tbits, h0 + nvec * 8 + tid, k);
+                for (int j = 0; j < 8; ++j) pr[vid0 + v * 8 + j] = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
             }
+        }
+        if (half == 0 && tid == 0)
+            a.bounds[row] = RowBoundary{z0, sh.s_n, inv_t, sh.pn_key, sh.pn_half, sh.pn_take, 1u};
+    }
+}
+
+// Filtered distribution of the full-route rows: one workgroup per (half, row)
+// walks its half in id order, ranks the boundary-key logits with block scans
+// and writes w / S_n for the support (0 elsewhere).  Test / diagnostics path.
+template <int DT>
+__global__ __launch_bounds__(kFT) void full_probs_kernel(const vi_row_params* params, int rows, int vocabulary,
+                                                       int half_len, float* probs, int64_t probs_stride,
+                                                       const RowBoundary* bounds) {
+    __shared__ uint32_t tmp[kFW + 1];
+    const int half = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    if (row >= rows || topk_route(params[row])) return;
+    const RowBoundary bd = bounds[row];
+    const int h0 = half * half_len, h1 = min(vocabulary, h0 + half_len);
+    float* pr = probs + size_t(row) * size_t(probs_stride);
+    if (!bd.valid) {
+        for (int i = h0 + tid; i < h1; i += kFT) pr[i] = 0.0f;
+        return;
+    }
+    const uint32_t pkey = uint32_t(bd.pn_key);
+    uint32_t running = 0;
+    for (int c0 = h0; c0 < h1; c0 += kFT * 8) {
+        const int e0 = c0 + tid * 8;
+        uint32_t bits[8];
+        uint32_t mine = 0;
+        for (int j = 0; j < 8; ++j) {
+            const int e = e0 + j;
+            bits[j] = e < h1 ? reinterpret_cast<const uint32_t*>(pr)[e] : 0x7fffu;
+            if (e < h1 && half == bd.pn_half && Elem<DT>::finite_bits(bits[j]) && key16(bits[j]) == pkey) ++mine;
+        }
+        uint32_t tot;
+        uint32_t k = block_exclusive_scan_u32<kFT>(mine, tmp, &tot) + running;
+        running += tot;
+        for (int j = 0; j < 8; ++j) {
+            const int e = e0 + j;
+            if (e >= h1) break;
+            float pv = 0.0f;
+            if (Elem<DT>::finite_bits(bits[j])) {
+                const uint32_t key = key16(bits[j]);
+                bool in = key > pkey;
+                if (key == pkey) {
+                    if (half < bd.pn_half) in = true;
+                    else if (half == bd.pn_half) { in = k < bd.pn_take; ++k; }
+                }
+                const float z = Elem<DT>::decode(unkey16(key)) * bd.inv_t;
+                if (in && isfinite(z)) pv = float(exp(double(z) - bd.z0) / bd.s_n);
+            }
+            pr[e] = pv;
         }
     }
 }
@@ -618,13 +696,12 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 bool full_supported(int dtype, int vocabulary, int64_t stride) {
     if (dtype != VI_BF16 && dtype != VI_F16) return false;
     const int H = (((vocabulary + 1) / 2) + 63) / 64 * 64;
-    return H <= kHalfMax && (stride * 2) % 16 == 0;
+    return H <= kVecMax * 8 && stride >= vocabulary;
 }
 
 size_t full_workspace(int rows) {
-    const size_t pairs = size_t(rows);
-    return align_up(pairs * sizeof(PairBarrier), 256) + align_up(size_t(rows) * 2 * sizeof(FullHeader), 256) +
-           align_up(size_t(rows) * 2 * kListMax * 4, 256) + 256;
+    return align_up(size_t(rows) * sizeof(PairBarrier), 256) + align_up(size_t(rows) * 2 * sizeof(FullHeader), 256) +
+           align_up(size_t(rows) * 2 * kListMax * 4, 256) + align_up(size_t(rows) * sizeof(RowBoundary), 256) + 256;
 }
 
 vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream) {
@@ -634,6 +711,7 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.barriers = c.take<PairBarrier>(size_t(s.rows));
     a.headers = c.take<FullHeader>(size_t(s.rows) * 2);
     a.lists = c.take<uint32_t>(size_t(s.rows) * 2 * kListMax);
+    a.bounds = c.take<RowBoundary>(size_t(s.rows));
     if (!c.ok) return VI_ERR_WORKSPACE;
     a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary;
     a.half_len = (((s.vocabulary + 1) / 2) + 63) / 64 * 64;
@@ -644,6 +722,15 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     const dim3 grid(groups * 16), block(kFT);
     if (s.dtype == VI_BF16) hipLaunchKernelGGL(full_kernel<VI_BF16>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(full_kernel<VI_F16>, grid, block, 0, stream, a);
+    vi_status st = launch_status();
+    if (st != VI_OK || !s.probs) return st;
+    const dim3 pgrid(2, s.rows);
+    if (s.dtype == VI_BF16)
+        hipLaunchKernelGGL(full_probs_kernel<VI_BF16>, pgrid, block, 0, stream, s.params, s.rows, s.vocabulary,
+                           a.half_len, s.probs, s.probs_stride, a.bounds);
+    else
+        hipLaunchKernelGGL(full_probs_kernel<VI_F16>, pgrid, block, 0, stream, s.params, s.rows, s.vocabulary,
+                           a.half_len, s.probs, s.probs_stride, a.bounds);
     return launch_status();
 }
 
