@@ -12,7 +12,10 @@ from pathlib import Path
 
 import numpy as np
 
-LIB_PATH = Path(__file__).resolve().parent / "libvoidinfer_sampling.so"
+import os
+
+# VOIDINFER_AMD_LIB selects another build of the same library (e.g. an instrumented one).
+LIB_PATH = Path(os.environ.get("VOIDINFER_AMD_LIB", Path(__file__).resolve().parent / "libvoidinfer_sampling.so"))
 
 BF16, F16, F32 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_DEVICE = range(6)

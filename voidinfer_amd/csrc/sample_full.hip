@@ -38,6 +38,7 @@ constexpr int kFV = 16;                   // 16-byte vectors per thread
 constexpr int kVecMax = kFT * kFV;        // vectors per half
 constexpr int kListMax = 8192;            // merged (key, half) entries
 constexpr int kOvfMax = 512;              // history tokens with >= 255 occurrences per half
+constexpr int kHB = 8;                    // history entries per thread per load round
 constexpr uint32_t kSpinLimit = 1u << 22;
 
 struct FullHeader {
@@ -229,24 +230,34 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         const int32_t* hist = a.histories + hb;
         uint32_t* ovf_tok = lds32 + (131072 / 4);
         uint32_t* ovf_cnt = ovf_tok + kOvfMax;
-        for (int64_t i = tid; i < hn; i += kFT) {
-            const int32_t t = hist[i];
-            if (t < 0 || t >= V) { atomicOr(&sh.flags, kHdrBadHistory); continue; }
-            if (t < h0 || t >= h1) continue;
-            const int off = t - h0, word = off >> 2, sh8 = (off & 3) * 8;
-            uint32_t old = lds32[word];
-            for (;;) {
-                const uint32_t c = (old >> sh8) & 255u;
-                if (c == 255u) break;
-                const uint32_t prev = atomicCAS(&lds32[word], old, old + (1u << sh8));
-                if (prev == old) {
-                    if (c == 254u) {
-                        const uint32_t k = atomicAdd(&sh.ovf_n, 1u);
-                        if (k < uint32_t(kOvfMax)) ovf_tok[k] = uint32_t(t); else atomicOr(&sh.flags, kHdrError);
+        // kHB history entries per thread per round, all loads issued before any
+        // is consumed (clamped indices keep them branch-free).
+        const int64_t hlast = hn - 1;
+        for (int64_t base = 0; base < hn; base += int64_t(kFT) * kHB) {
+            int32_t t[kHB];
+#pragma unroll
+            for (int j = 0; j < kHB; ++j) t[j] = hist[min(base + int64_t(j) * kFT + tid, hlast)];
+#pragma unroll
+            for (int j = 0; j < kHB; ++j) {
+                if (base + int64_t(j) * kFT + tid > hlast) continue;
+                const int32_t tk = t[j];
+                if (tk < 0 || tk >= V) { atomicOr(&sh.flags, kHdrBadHistory); continue; }
+                if (tk < h0 || tk >= h1) continue;
+                const int off = tk - h0, word = off >> 2, sh8 = (off & 3) * 8;
+                uint32_t old = lds32[word];
+                for (;;) {
+                    const uint32_t c = (old >> sh8) & 255u;
+                    if (c == 255u) break;
+                    const uint32_t prev = atomicCAS(&lds32[word], old, old + (1u << sh8));
+                    if (prev == old) {
+                        if (c == 254u) {
+                            const uint32_t k = atomicAdd(&sh.ovf_n, 1u);
+                            if (k < uint32_t(kOvfMax)) ovf_tok[k] = uint32_t(tk); else atomicOr(&sh.flags, kHdrError);
+                        }
+                        break;
                     }
-                    break;
+                    old = prev;
                 }
-                old = prev;
             }
         }
         __syncthreads();
@@ -369,26 +380,32 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         a.headers[size_t(row) * 2 + half] = FullHeader{n_list, tot_fin, f, 0u};
     }
 
-    // ---- C. pair barrier (self-resetting; generation counter)
-    __threadfence();
+    // ---- C. pair barrier (self-resetting; generation counter).  Every wave
+    // drains its own list / header stores to L2 (s_waitcnt); one wave then
+    // publishes with a single agent-scope release (L2 write-back) and, after
+    // the partner arrived, takes a single agent-scope acquire (L1/L2
+    // invalidate) on behalf of the workgroup; the spin itself polls with
+    // relaxed loads so it does not invalidate caches each round.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
         PairBarrier* bar = &a.barriers[row];
-        const uint32_t gen = __hip_atomic_load(&bar->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const uint32_t gen = __hip_atomic_load(&bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (arrived == 1u) {
             __hip_atomic_store(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(&bar->gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&bar->gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             uint32_t it = 0;
-            while (__hip_atomic_load(&bar->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == gen) {
+            while (__hip_atomic_load(&bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
                 __builtin_amdgcn_s_sleep(1);
                 if (++it > kSpinLimit) { sh.flags |= kHdrError; break; }
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
-    __threadfence();
     const FullHeader H0 = a.headers[size_t(row) * 2 + 0], H1 = a.headers[size_t(row) * 2 + 1];
     const uint32_t hflags = H0.flags | H1.flags | (sh.flags & kHdrError);
     const int n0 = int(H0.n_list), n1 = int(H1.n_list), n = n0 + n1;
