@@ -13,14 +13,24 @@
 // Shape: each row is owned by a PAIR of 1024-thread workgroups (one per half of
 // the vocabulary, both on one XCD), which keep their half of the row in
 // registers (16 x 16-byte vectors per thread, plus <= 7 head / tail logits when
-// the half does not start 16-byte aligned):
-//   A. history -> LDS u8 occurrence counts of the half (saturating, exact side
-//      table), penalties applied to the register-resident logits in place;
+// the half does not start 16-byte aligned).
+//
+// Penalties (dense path, histories <= 32,768 tokens): the history is loaded
+// first and turned into a bitmap of the half's history tokens, a rank prefix
+// per bitmap word and a rank-ordered u16 count array; each thread takes 32
+// consecutive ranks, gathers those logits from the (cache-hot) row and keeps
+// (count, logit) in registers.  The streaming histogram then skips every
+// history token (one bitmap byte per 8 logits) and the dense pass penalizes the
+// gathered tokens, 32 per thread with no divergence, and adds them.  Longer
+// histories take the general path: a u8 occurrence table of the half and
+// penalties applied to the register-resident logits in place.
+//
 //   B. LDS u16 key histogram -> sorted (key, count) list published to HBM;
 //   C. one pair barrier; both workgroups merge the two lists (merge path) into
 //      cumulative counts / masses in LDS and take identical decisions with
 //      wave-wide 64-ary searches;
-//   D. the half owning the drawn (key, rank) finds the token in its registers.
+//   D. the half owning the drawn (key, rank) finds the token in its registers
+//      (history tokens: from the dense registers).
 // The pair barrier spins on an agent-scope counter with an iteration cap, so a
 // missing partner becomes VI_FLAG_ERROR, never a hang.  Roofline: HBM,
 // V x 2 + L x 4 bytes per row (logits once, history once per pair via L2).
@@ -36,16 +46,27 @@ constexpr int kFT = 1024;                 // threads per workgroup
 constexpr int kFW = kFT / kWave;          // waves per workgroup
 constexpr int kFV = 16;                   // 16-byte vectors per thread
 constexpr int kVecMax = kFT * kFV;        // vectors per half
-constexpr int kListMax = 8192;            // merged (key, half) entries
+constexpr int kListMax = 65536;           // list slots of one half: 16 wave segments of 4096 keys
+constexpr uint32_t kSpinLimit = 1u << 22;
+// general path
 constexpr int kOvfMax = 512;              // history tokens with >= 255 occurrences per half
 constexpr int kHB = 8;                    // history entries per thread per load round
-constexpr uint32_t kSpinLimit = 1u << 22;
+// dense path
+constexpr int kHistMax = 32768;           // history tokens per row
+constexpr int kHT = kHistMax / kFT;       // history tokens per thread
+constexpr int kDR = kHistMax / kFT;       // dense ranks (distinct history tokens) per thread
+constexpr int kBmapWords = kVecMax * 8 / 32;
 
-struct FullHeader {
-    uint32_t n_list;
-    uint32_t n_finite;
-    uint32_t flags;
-    uint32_t pad;
+constexpr int kCoarse = 256;              // coarse bins of 256 keys
+// What a half publishes for its partner: header, its sorted (key << 16 | count)
+// list's first index per coarse bin, and per coarse bin the count of valid
+// logits and their mass sum count * exp(z(key) - z(top_key)).
+struct alignas(16) HalfSummary {
+    uint32_t n_list, n_finite, flags, top_key;   // top_key: largest valid key, ~0u if none
+    uint32_t first[kCoarse], end[kCoarse];       // list slots of each coarse bin's entries
+    uint32_t ccnt[kCoarse];                      // valid logits of the bin
+    uint32_t bref[kCoarse];                      // the bin's largest valid key (its mass reference)
+    double cmass[kCoarse];                       // sum of count * exp(z(key) - z(bref))
 };
 struct alignas(256) PairBarrier {
     uint32_t count;
@@ -73,47 +94,67 @@ struct FullArgs {
     int64_t probs_stride;
     vi_sample_stats* stats;
     PairBarrier* barriers;   // [rows]
-    FullHeader* headers;     // [rows][2]
+    HalfSummary* summaries;  // [rows][2]
     uint32_t* lists;         // [rows][2][kListMax]
     RowBoundary* bounds;     // [rows]
 };
 
 constexpr uint32_t kHdrNonfinite = 1u, kHdrBadHistory = 2u, kHdrError = 4u, kHdrOverflow = 8u;
 
-// LDS map (bytes).  Phase A: u8 counts [0, 128 KiB) + saturated side table.
-// Phase B: u16 histogram [0, 128 KiB).  Phase C: lists A|B [0, 32 KiB) (then
-// cumulative counts C), merged entries M [32, 64 KiB), cumulative masses W
-// [64 KiB, 128 KiB + 8), half bits after.
-constexpr int kOffM = 4 * kListMax, kOffW = 8 * kListMax, kOffH = 16 * kListMax + 256;
-constexpr int kLdsBytes = 131072 + 8 * kOvfMax + 1280;
-static_assert(kOffH + kListMax / 8 <= kLdsBytes, "LDS map");
+// LDS map (bytes).  u16 key histogram [0, 128 KiB); merge: lists A|B (then
+// cumulative counts C) [0, 32 KiB), merged entries M [32, 64 KiB), exclusive
+// masses W [64, 128 KiB).  Dense path: u16 rank-ordered counts [0, 64 KiB)
+// before the histogram, history bitmap and rank prefix above 128 KiB for the
+// whole kernel.  General path: u8 occurrence table [0, 128 KiB) before the
+// histogram, saturated-token side table above it.
+// decisions (after the histogram): coarse tables of both halves, coarse
+// prefix, one 256-key window
+constexpr int kOffDM = 2048, kOffDF = kOffDM + 4096, kOffPC = kOffDF + 16 * kCoarse;
+constexpr int kOffPM = kOffPC + 4 * (kCoarse + 4), kOffWC = kOffPM + 8 * (kCoarse + 4);
+constexpr int kOffWW = kOffWC + 8 * kCoarse, kOffWN = kOffWW + 8 * kCoarse, kOffWM = kOffWN + 4 * (kCoarse + 4);
+constexpr int kOffDecEnd = kOffWM + 8 * (kCoarse + 4);
+constexpr int kOffBmap = 131072;
+constexpr int kOffPref = kOffBmap + 4 * (kBmapWords + 4);
+constexpr int kLdsDense = kOffPref + 2 * kBmapWords;
+constexpr int kOffP = 4 * kFT;            // D: penalized history bits by rank (u16), after fmask
+constexpr int kLdsGeneral = 131072 + 8 * kOvfMax;
+static_assert(kOffDecEnd <= 131072 && kOffDM % 8 == 0 && kOffPM % 8 == 0 && kOffWW % 8 == 0 && kOffWM % 8 == 0, "LDS map");
+static_assert(kHistMax / 2 * 4 <= 131072, "dense counts");
 
 struct Shared {
     uint32_t u[kFW + 1];
     double d[kFW + 1];
-    uint32_t ovf_n, flags, minp_pos;
+    uint32_t ovf_n, flags, top1, big_rank;
     // decisions (written by wave 0)
     int32_t r_key, r_half, pn_key, pn_half;
-    uint32_t rank, pn_take, n_sup, slot, slot_rank;
+    uint32_t rank, pn_take, n_sup, slot, slot_rank, ctot;
     double s_n, draw_u;
     uint32_t slot_tot[kFV + 2];
+    uint32_t n_sum, n_fin, wcount[kFW];
+    uint32_t first[kCoarse], bend[kCoarse];   // this half's list slots of each coarse bin
 };
+
+// Orders one wave's LDS accesses around an exchange between its lanes (a
+// wave's LDS operations execute in order; this keeps the compiler from moving
+// them across).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 template <int NT>
 __device__ __forceinline__ double block_exclusive_scan_f64(double v, double* tmp, double* total) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
-    double x = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const double y = __shfl_up(x, o, kWave);
-        if (lane >= o) x += y;
-    }
+    const double x = wave_incl_scan_f64(v);
     if (lane == kWave - 1) tmp[wave] = x;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        double s = 0;
-        for (int w = 0; w < NT / kWave; ++w) { const double t = tmp[w]; tmp[w] = s; s += t; }
-        tmp[NT / kWave] = s;
+    if (wave == 0) {   // scan of the wave totals in wave 0
+        const double t = lane < NT / kWave ? tmp[lane] : 0.0;
+        const double it = wave_incl_scan_f64(t);
+        const double ex = __shfl_up(it, 1, kWave);
+        if (lane < NT / kWave) tmp[lane] = lane == 0 ? 0.0 : ex;
+        if (lane == NT / kWave - 1) tmp[NT / kWave] = it;
     }
     __syncthreads();
     const double r = tmp[wave] + (x - v);
@@ -137,7 +178,7 @@ __device__ __forceinline__ float key_z(uint32_t key, float inv_t) {
 // Smallest i in [lo, hi) with pred(i) (pred monotone false -> true), or hi.
 // Wave-uniform call; 64 probes per round.
 template <class P>
-__device__ int wave_search(int lo, int hi, P pred) {
+__device__ __forceinline__ int wave_search(int lo, int hi, P pred) {
     const int lane = lane_id();
     while (hi > lo) {
         const int n = hi - lo;
@@ -169,21 +210,24 @@ __device__ __forceinline__ uint32_t bits_of(uint64_t q0, uint64_t q1, int j) {
     return uint32_t(((j < 4 ? q0 : q1) >> ((j & 3) * 16)) & 0xffffu);
 }
 
+// Bit j set: element j of the vector is finite and has order key `key`.
 template <int DT>
-__device__ __forceinline__ uint32_t count_key8(const uint4& v, uint32_t key) {
-    uint32_t c = 0;
+__device__ __forceinline__ uint32_t match_mask8(const uint4& v, uint32_t key) {
+    uint32_t m = 0;
     const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-        c += (Elem<DT>::finite_bits(b) && key16(b) == key) ? 1u : 0u;
+        m |= (Elem<DT>::finite_bits(b) && key16(b) == key) ? (1u << j) : 0u;
     }
-    return c;
+    return m;
 }
 
-template <int DT>
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT, bool kDense>
 __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kDense ? kLdsDense : kLdsGeneral];
     __shared__ Shared sh;
     uint32_t* lds32 = reinterpret_cast<uint32_t*>(lds);
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
@@ -203,122 +247,265 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     const unsigned char* vbase = reinterpret_cast<const unsigned char*>(base16 + head);
     const int vid0 = h0 + head;                          // token id of vector 0, element 0
 
-    // ---- issue every load of this half up front (one HBM read of the row)
-    // Branch-free: out-of-range slots re-load the half's last vector (an L2
-    // hit) and are masked wherever the data is consumed (v < nvec).
-    uint4 d[kFV];
-    const int vlast = max(nvec - 1, 0);
-    if (nvec > 0) {
-#pragma unroll
-        for (int i = 0; i < kFV; ++i) d[i] = load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16);
-    } else {
-#pragma unroll
-        for (int i = 0; i < kFV; ++i) d[i] = make_uint4(0, 0, 0, 0);
-    }
-    uint32_t hbits = tid < head ? uint32_t(base16[tid]) : 0u;
-    uint32_t tbits = tid < tail ? uint32_t(base16[head + nvec * 8 + tid]) : 0u;
-
-    if (tid == 0) { sh.ovf_n = 0; sh.flags = 0; sh.minp_pos = 0xffffffffu; }
+    if (tid == 0) { sh.ovf_n = 0; sh.flags = 0; sh.top1 = 0; sh.n_sum = 0; sh.n_fin = 0; }
     const int64_t hb = a.offsets ? a.offsets[row] : 0;
     const int64_t hn = a.offsets ? a.offsets[row + 1] - hb : 0;
     const bool pen = penalties_active(p) && hn > 0 && a.histories;
+    const int32_t* hist = pen ? a.histories + hb : nullptr;
 
-    // ---- A. occurrence counts of this half, penalties in place
-    if (pen) {
-        for (int w = tid; w < (H + 3) / 4; w += kFT) lds32[w] = 0u;
-        __syncthreads();
-        const int32_t* hist = a.histories + hb;
-        uint32_t* ovf_tok = lds32 + (131072 / 4);
-        uint32_t* ovf_cnt = ovf_tok + kOvfMax;
-        // kHB history entries per thread per round, all loads issued before any
-        // is consumed (clamped indices keep them branch-free).
-        const int64_t hlast = hn - 1;
-        for (int64_t base = 0; base < hn; base += int64_t(kFT) * kHB) {
-            int32_t t[kHB];
+    // ---- issue every load of this half up front (one HBM read of the row)
+    // Branch-free: out-of-range slots re-load the half's last vector (an L2
+    // hit) and are masked wherever the data is consumed (v < nvec).
+    // (dense path with a history: vectors kFV/2 .. kFV-1 are requested after
+    // the history work, which keeps the history and the row in registers together
+    // within the 128-VGPR budget)
+    uint4 d[kFV];
+    const int vlast = max(nvec - 1, 0);
+    auto load_vectors = [&](int i0, int i1) {
 #pragma unroll
-            for (int j = 0; j < kHB; ++j) t[j] = hist[min(base + int64_t(j) * kFT + tid, hlast)];
+        for (int i = 0; i < kFV; ++i)
+            if (i >= i0 && i < i1)
+                d[i] = nvec > 0 ? load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
+    };
+    load_vectors(0, kFV);
+    uint32_t hbits = tid < head ? uint32_t(base16[tid]) : 0u;
+    uint32_t tbits = tid < tail ? uint32_t(base16[head + nvec * 8 + tid]) : 0u;
+
+    // Flag bits of the half's tokens off0 .. off0 + 7 (bit j: token h0 + off0 + j
+    // is in the history), read from the LDS bitmap; dense path only.
+    auto flags8_lds = [&](int off0) -> uint32_t {
+        if constexpr (kDense) {
+            const uint32_t* bmap = reinterpret_cast<const uint32_t*>(lds + kOffBmap);
+            const int w = off0 >> 5, s = off0 & 31;
+            const uint64_t pr = uint64_t(bmap[w]) | (uint64_t(bmap[w + 1]) << 32);
+            return uint32_t(pr >> s) & 0xffu;
+        } else {
+            return 0u;
+        }
+    };
+    // the same for this thread's 16 vectors, kept in registers (8 bits each)
+    uint32_t vfl[kFV / 4] = {0u, 0u, 0u, 0u};
+    bool fl_head = false, fl_tail = false;
+    auto vflags = [&](int i) -> uint32_t { return (vfl[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+    // Vector slot i of this thread after the histogram: the dense path reads it
+    // again (an L2 / MALL hit; history tokens are taken from the dense ranks,
+    // so the raw bits are what is wanted), which frees the registers the row
+    // occupied while streaming; the general path kept it, penalized, in d[].
+    auto row_vec = [&](int i) -> uint4 {
+        if constexpr (kDense) return nvec > 0 ? load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
+        else return d[i];
+    };
+
+    // ---- A (dense). bitmap of the half's history tokens, exclusive rank
+    // prefix per bitmap word, rank-ordered entries (offset << 15 | count) in
+    // LDS; then the history tokens' logits are gathered (consecutive lanes take
+    // consecutive ranks: nearby tokens) and penalized into registers, rank
+    // k * kFT + tid in slot k.
+    uint32_t n_flag = 0;
+    uint32_t dpen[kDense ? kDR / 2 : 1];   // penalized bits, u16 pairs (slots 2q, 2q + 1)
 #pragma unroll
-            for (int j = 0; j < kHB; ++j) {
-                if (base + int64_t(j) * kFT + tid > hlast) continue;
-                const int32_t tk = t[j];
-                if (tk < 0 || tk >= V) { atomicOr(&sh.flags, kHdrBadHistory); continue; }
-                if (tk < h0 || tk >= h1) continue;
-                const int off = tk - h0, word = off >> 2, sh8 = (off & 3) * 8;
-                uint32_t old = lds32[word];
-                for (;;) {
-                    const uint32_t c = (old >> sh8) & 255u;
-                    if (c == 255u) break;
-                    const uint32_t prev = atomicCAS(&lds32[word], old, old + (1u << sh8));
-                    if (prev == old) {
-                        if (c == 254u) {
-                            const uint32_t k = atomicAdd(&sh.ovf_n, 1u);
-                            if (k < uint32_t(kOvfMax)) ovf_tok[k] = uint32_t(tk); else atomicOr(&sh.flags, kHdrError);
+    for (int q = 0; q < (kDense ? kDR / 2 : 1); ++q) dpen[q] = 0u;
+    auto dense_pen = [&](int k) -> uint32_t { return (dpen[k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+    // fn(rank, off) for every history token of this thread's 4 bitmap words
+    // (rows with penalties only: the bitmap is not built otherwise)
+    auto walk_words = [&](auto&& fn) {
+        if constexpr (kDense) {
+            if (!pen) return;
+            const uint32_t* bmap = reinterpret_cast<const uint32_t*>(lds + kOffBmap);
+            const uint16_t* pref = reinterpret_cast<const uint16_t*>(lds + kOffPref);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int w = 4 * tid + q;
+                uint32_t bits = bmap[w];
+                uint32_t rank = pref[w];
+                while (bits) {
+                    const int bpos = __builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    fn(rank++, w * 32 + bpos);
+                }
+            }
+        }
+    };
+    // fn(token) for each of the row's first kHistMax history tokens; the history
+    // is read in rounds of kHR tokens per thread (bounded registers)
+    auto for_history = [&](auto&& fn) {
+        constexpr int kHR = 16;
+        const int64_t hl = min(hn, int64_t(kHistMax));
+#pragma unroll
+        for (int r0 = 0; r0 < kHT; r0 += kHR) {
+            int32_t t[kHR];
+#pragma unroll
+            for (int j = 0; j < kHR; ++j) t[j] = hist[min(int64_t(r0 + j) * kFT + tid, hl - 1)];
+#pragma unroll
+            for (int j = 0; j < kHR; ++j)
+                if (int64_t(r0 + j) * kFT + tid < hl) fn(t[j]);
+        }
+    };
+    if constexpr (kDense) {
+        if (pen) {
+            uint32_t* bmap = reinterpret_cast<uint32_t*>(lds + kOffBmap);
+            uint16_t* pref = reinterpret_cast<uint16_t*>(lds + kOffPref);
+            for (int w = tid; w < kBmapWords + 4; w += kFT) bmap[w] = 0u;
+            if (tid == 0) sh.big_rank = 0xffffffffu;
+            __syncthreads();
+            if (tid == 0 && hn > kHistMax) atomicOr(&sh.flags, kHdrError);   // callers promise hn <= max_history
+            for_history([&](int32_t t) {
+                if (t < 0 || t >= V) { atomicOr(&sh.flags, kHdrBadHistory); return; }
+                if (t < h0 || t >= h1) return;
+                const int off = t - h0;
+                atomicOr(&bmap[off >> 5], 1u << (off & 31));
+            });
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kFV; ++i) {
+                const int v = i * kFT + tid;
+                if (v < nvec) vfl[i >> 2] |= flags8_lds(head + v * 8) << (8 * (i & 3));
+            }
+            fl_head = tid < head && (flags8_lds(tid) & 1u);
+            fl_tail = tid < tail && (flags8_lds(head + nvec * 8 + tid) & 1u);
+            // thread t owns bitmap words 4t .. 4t + 3
+            uint32_t c4[4], s4 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { c4[k] = __builtin_popcount(bmap[4 * tid + k]); s4 += c4[k]; }
+            uint32_t ex = block_exclusive_scan_u32<kFT>(s4, sh.u, &n_flag);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { pref[4 * tid + k] = uint16_t(ex); ex += c4[k]; }
+            __syncthreads();
+            walk_words([&](uint32_t rank, int off) { lds32[rank] = uint32_t(off) << 15; });
+            __syncthreads();
+            for_history([&](int32_t t) {   // (L2 hits now)
+                if (t < h0 || t >= h1) return;
+                const int off = t - h0, w = off >> 5;
+                const uint32_t rank = pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
+                // 15-bit count field: the 32,768th occurrence (a history of one
+                // repeated token) carries out of it; undo the carry and note the rank
+                const uint32_t old = atomicAdd(&lds32[rank], 1u);
+                if ((old & 0x7fffu) == 0x7fffu) { atomicSub(&lds32[rank], 1u); sh.big_rank = rank; }
+            });
+            __syncthreads();
+            const uint32_t big_rank = sh.big_rank;
+            // all gathers in flight at once (offsets from LDS), then the counts
+            uint32_t g[kDR];
+#pragma unroll
+            for (int k = 0; k < kDR; ++k) {   // unused slots load nothing (the half may be empty)
+                const uint32_t r = uint32_t(k) * kFT + tid;
+                g[k] = r < n_flag ? uint32_t(base16[lds32[r] >> 15]) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < kDR; ++k) {
+                const uint32_t r = uint32_t(k) * kFT + tid;
+                if (r < n_flag) {
+                    const uint32_t c = r == big_rank ? 32768u : (lds32[r] & 0x7fffu);
+                    const uint32_t pb = Elem<DT>::finite_bits(g[k]) ? penalize_bits<DT>(g[k], c, p) & 0xffffu : g[k];
+                    dpen[k >> 1] |= pb << (16 * (k & 1));
+                }
+            }
+            __syncthreads();   // entries read before the histogram overwrites them
+        }
+    }
+
+    // ---- A (general). occurrence counts of this half, penalties in place
+    if constexpr (!kDense) {
+        if (pen) {
+            for (int w = tid; w < (H + 3) / 4; w += kFT) lds32[w] = 0u;
+            __syncthreads();
+            uint32_t* ovf_tok = lds32 + (131072 / 4);
+            uint32_t* ovf_cnt = ovf_tok + kOvfMax;
+            // kHB history entries per thread per round, all loads issued before any
+            // is consumed (clamped indices keep them branch-free).
+            const int64_t hlast = hn - 1;
+            for (int64_t base = 0; base < hn; base += int64_t(kFT) * kHB) {
+                int32_t t[kHB];
+#pragma unroll
+                for (int j = 0; j < kHB; ++j) t[j] = hist[min(base + int64_t(j) * kFT + tid, hlast)];
+#pragma unroll
+                for (int j = 0; j < kHB; ++j) {
+                    if (base + int64_t(j) * kFT + tid > hlast) continue;
+                    const int32_t tk = t[j];
+                    if (tk < 0 || tk >= V) { atomicOr(&sh.flags, kHdrBadHistory); continue; }
+                    if (tk < h0 || tk >= h1) continue;
+                    const int off = tk - h0, word = off >> 2, sh8 = (off & 3) * 8;
+                    uint32_t old = lds32[word];
+                    for (;;) {
+                        const uint32_t c = (old >> sh8) & 255u;
+                        if (c == 255u) break;
+                        const uint32_t prev = atomicCAS(&lds32[word], old, old + (1u << sh8));
+                        if (prev == old) {
+                            if (c == 254u) {
+                                const uint32_t k = atomicAdd(&sh.ovf_n, 1u);
+                                if (k < uint32_t(kOvfMax)) ovf_tok[k] = uint32_t(tk); else atomicOr(&sh.flags, kHdrError);
+                            }
+                            break;
                         }
-                        break;
+                        old = prev;
                     }
-                    old = prev;
                 }
             }
-        }
-        __syncthreads();
-        const uint32_t n_ovf = min(sh.ovf_n, uint32_t(kOvfMax));
-        if (n_ovf) {
-            for (uint32_t k = tid; k < n_ovf; k += kFT) ovf_cnt[k] = 0u;
             __syncthreads();
-            for (int64_t i = tid; i < hn; i += kFT) {
-                const int32_t t = hist[i];
-                if (t < h0 || t >= h1) continue;
-                for (uint32_t k = 0; k < n_ovf; ++k)
-                    if (ovf_tok[k] == uint32_t(t)) { atomicAdd(&ovf_cnt[k], 1u); break; }
+            const uint32_t n_ovf = min(sh.ovf_n, uint32_t(kOvfMax));
+            if (n_ovf) {
+                for (uint32_t k = tid; k < n_ovf; k += kFT) ovf_cnt[k] = 0u;
+                __syncthreads();
+                for (int64_t i = tid; i < hn; i += kFT) {
+                    const int32_t t = hist[i];
+                    if (t < h0 || t >= h1) continue;
+                    for (uint32_t k = 0; k < n_ovf; ++k)
+                        if (ovf_tok[k] == uint32_t(t)) { atomicAdd(&ovf_cnt[k], 1u); break; }
+                }
+                __syncthreads();
             }
-            __syncthreads();
-        }
-        const unsigned char* cnt8 = lds;
-        auto count_at = [&](int off) -> uint32_t {   // occurrences of token h0 + off
-            const uint32_t c = cnt8[off];
-            if (c != 255u) return c;
-            for (uint32_t k = 0; k < n_ovf; ++k) if (ovf_tok[k] == uint32_t(h0 + off)) return ovf_cnt[k];
-            return c;
-        };
+            const unsigned char* cnt8 = lds;
+            auto count_at = [&](int off) -> uint32_t {   // occurrences of token h0 + off
+                const uint32_t c = cnt8[off];
+                if (c != 255u) return c;
+                for (uint32_t k = 0; k < n_ovf; ++k) if (ovf_tok[k] == uint32_t(h0 + off)) return ovf_cnt[k];
+                return c;
+            };
 #pragma unroll
-        for (int i = 0; i < kFV; ++i) {
-            const int v = i * kFT + tid;
-            if (v < nvec) {
-                const int off0 = head + v * 8;
-                // the 8 counts of this vector (two LDS words when the half starts aligned)
-                uint64_t cc = 0;
-                if ((head & 3) == 0) {
-                    const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cnt8 + off0);
-                    cc = uint64_t(c32[0]) | (uint64_t(c32[1]) << 32);
-                } else {
-                    for (int j = 0; j < 8; ++j) cc |= uint64_t(cnt8[off0 + j]) << (8 * j);
-                }
-                if (cc) {
-                    uint64_t q0 = uint64_t(d[i].x) | (uint64_t(d[i].y) << 32);
-                    uint64_t q1 = uint64_t(d[i].z) | (uint64_t(d[i].w) << 32);
-                    for (int j = 0; j < 8; ++j) {                     // rolled: low register use
-                        if (!((cc >> (8 * j)) & 255u)) continue;
-                        const uint32_t bits = bits_of(q0, q1, j);
-                        if (!Elem<DT>::finite_bits(bits)) continue;
-                        const uint64_t nb = penalize_bits<DT>(bits, count_at(off0 + j), p) & 0xffffu;
-                        const int s = (j & 3) * 16;
-                        if (j < 4) q0 = (q0 & ~(0xffffull << s)) | (nb << s);
-                        else q1 = (q1 & ~(0xffffull << s)) | (nb << s);
+            for (int i = 0; i < kFV; ++i) {
+                const int v = i * kFT + tid;
+                if (v < nvec) {
+                    const int off0 = head + v * 8;
+                    // the 8 counts of this vector (two LDS words when the half starts aligned)
+                    uint64_t cc = 0;
+                    if ((head & 3) == 0) {
+                        const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cnt8 + off0);
+                        cc = uint64_t(c32[0]) | (uint64_t(c32[1]) << 32);
+                    } else {
+                        for (int j = 0; j < 8; ++j) cc |= uint64_t(cnt8[off0 + j]) << (8 * j);
                     }
-                    d[i] = make_uint4(uint32_t(q0), uint32_t(q0 >> 32), uint32_t(q1), uint32_t(q1 >> 32));
+                    if (cc) {
+                        uint64_t q0 = uint64_t(d[i].x) | (uint64_t(d[i].y) << 32);
+                        uint64_t q1 = uint64_t(d[i].z) | (uint64_t(d[i].w) << 32);
+                        // visit only the elements with a count
+                        uint64_t nz = (cc | (cc >> 4)) & 0x0f0f0f0f0f0f0f0full;
+                        nz = (nz | (nz >> 2)) & 0x0303030303030303ull;
+                        nz = (nz | (nz >> 1)) & 0x0101010101010101ull;
+                        while (nz) {
+                            const int j = __builtin_ctzll(nz) >> 3;
+                            nz &= nz - 1u;
+                            const uint32_t bits = bits_of(q0, q1, j);
+                            if (!Elem<DT>::finite_bits(bits)) continue;
+                            const uint64_t nb = penalize_bits<DT>(bits, count_at(off0 + j), p) & 0xffffu;
+                            const int s = (j & 3) * 16;
+                            if (j < 4) q0 = (q0 & ~(0xffffull << s)) | (nb << s);
+                            else q1 = (q1 & ~(0xffffull << s)) | (nb << s);
+                        }
+                        d[i] = make_uint4(uint32_t(q0), uint32_t(q0 >> 32), uint32_t(q1), uint32_t(q1 >> 32));
+                    }
                 }
             }
+            if (tid < head) {
+                const uint32_t c = count_at(tid);
+                if (c && Elem<DT>::finite_bits(hbits)) hbits = penalize_bits<DT>(hbits, c, p) & 0xffffu;
+            }
+            if (tid < tail) {
+                const int off = head + nvec * 8 + tid;
+                const uint32_t c = count_at(off);
+                if (c && Elem<DT>::finite_bits(tbits)) tbits = penalize_bits<DT>(tbits, c, p) & 0xffffu;
+            }
+            __syncthreads();
         }
-        if (tid < head) {
-            const uint32_t c = count_at(tid);
-            if (c && Elem<DT>::finite_bits(hbits)) hbits = penalize_bits<DT>(hbits, c, p) & 0xffffu;
-        }
-        if (tid < tail) {
-            const int off = head + nvec * 8 + tid;
-            const uint32_t c = count_at(off);
-            if (c && Elem<DT>::finite_bits(tbits)) tbits = penalize_bits<DT>(tbits, c, p) & 0xffffu;
-        }
-        __syncthreads();
     }
 
     // ---- B. key histogram (u16 counts packed in pairs) and the sorted list
@@ -336,59 +523,145 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             nonfinite = true;
         }
     };
+    // history tokens (dense path) are skipped here and added by the dense pass
 #pragma unroll
     for (int i = 0; i < kFV; ++i) {
-        if (i * kFT + tid < nvec) {
+        const int v = i * kFT + tid;
+        if (v < nvec) {
+            const uint32_t fl = vflags(i);
             const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+            for (int j = 0; j < 8; ++j)
+                if (!((fl >> j) & 1u)) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
         }
     }
-    if (tid < head) hist_add(hbits);
-    if (tid < tail) hist_add(tbits);
+    if (tid < head && !fl_head) hist_add(hbits);
+    if (tid < tail && !fl_tail) hist_add(tbits);
+    if constexpr (kDense) {
+        // the history tokens, penalized
+#pragma unroll
+        for (int k = 0; k < kDR; ++k)
+            if (uint32_t(k) * kFT + tid < n_flag) hist_add(dense_pen(k));
+    }
     if (nonfinite) atomicOr(&sh.flags, kHdrNonfinite);
     __syncthreads();
-    // thread t owns keys [64t, 64t + 64)
-    uint32_t my_n = 0, my_sum = 0;
-#pragma unroll 2  // fully unrolled, the 32 LDS reads in flight spill the register-resident row
-    for (int w = 0; w < 32; ++w) {
-        const uint32_t x = lds32[tid * 32 + w];
-        my_n += ((x & 0xffffu) != 0u) + ((x >> 16) != 0u);
-        my_sum += (x & 0xffffu) + (x >> 16);
-    }
-    uint32_t n_list;
-    const uint32_t lbase = block_exclusive_scan_u32<kFT>(my_n, sh.u, &n_list);
-    const uint32_t tot_fin = block_sum_u32<kFT>(n_fin, sh.u);
-    const uint32_t tot_sum = block_sum_u32<kFT>(my_sum, sh.u);
+    // ---- B'. compaction and this half's summary.  Wave w owns the coarse bins
+    // w, w + 16, w + 32, ... (256 keys = 128 histogram words each; neighbouring
+    // bins go to different waves, which spreads a narrow key range over the
+    // block).  It reads a bin as two 64-word rows (lane = word: no bank
+    // conflicts), writes the bin's (key << 16 | count) entries in ascending key
+    // order to its own 4096-entry segment of the half's list (slots from
+    // ballots) and sums the bin's valid count and its mass relative to the
+    // bin's largest valid key (bref).  A listed key whose scaled logit
+    // z = x' / T is not finite is not valid: it is neither counted nor weighted
+    // (the reference drops such logits).
     uint32_t* my_list = a.lists + (size_t(row) * 2 + half) * kListMax;
+    HalfSummary* my_summary = a.summaries + size_t(row) * 2 + half;
     {
-        uint32_t at = lbase;
-#pragma unroll 2
-        for (int w = 0; w < 32; ++w) {
-            const uint32_t x = lds32[tid * 32 + w];
-            const uint32_t k0 = uint32_t(tid * 64 + 2 * w);
-            if ((x & 0xffffu) && at < uint32_t(kListMax)) my_list[at] = (k0 << 16) | (x & 0xffffu);
-            at += (x & 0xffffu) != 0u;
-            if ((x >> 16) && at < uint32_t(kListMax)) my_list[at] = ((k0 + 1u) << 16) | (x >> 16);
-            at += (x >> 16) != 0u;
+        uint32_t my_sum = 0;
+        uint32_t at = uint32_t(wave) * 4096u;                 // (wave-uniform) next list slot
+        uint32_t v_first = 0, v_end = 0, v_cnt = 0, v_ref = 0;   // lane b: bin b * 16 + wave
+        double v_mass = 0.0;
+        uint32_t wtop1 = 0;                                    // largest valid key + 1
+        bool bad_z = false;
+        constexpr int kBU = kDense ? 4 : 1;   // bins read ahead (the general path keeps its row live)
+#pragma unroll
+        for (int b0 = 0; b0 < kCoarse / kFW; b0 += kBU) {
+            uint32_t xs[2 * kBU];
+#pragma unroll
+            for (int u = 0; u < 2 * kBU; ++u) xs[u] = lds32[((b0 + u / 2) * kFW + wave) * 128 + (u & 1) * 64 + lane];
+#pragma unroll
+            for (int ub = 0; ub < kBU; ++ub) {
+                const int bb = b0 + ub, bin = bb * kFW + wave;
+                uint32_t cnt[4];   // keys kb + 2 lane + {0, 1} (row 0) and kb + 128 + 2 lane + {0, 1} (row 1)
+                cnt[0] = xs[2 * ub] & 0xffffu; cnt[1] = xs[2 * ub] >> 16;
+                cnt[2] = xs[2 * ub + 1] & 0xffffu; cnt[3] = xs[2 * ub + 1] >> 16;
+                my_sum += cnt[0] + cnt[1] + cnt[2] + cnt[3];
+                uint64_t bal[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bal[e] = ballot(cnt[e] != 0u);
+                const uint32_t first = at;
+                const uint32_t kb = uint32_t(bin * 256);
+                if (bal[0] | bal[1] | bal[2] | bal[3]) {
+                    // list slots: row 0's entries, then row 1's (ascending keys)
+                    const uint32_t r0 = at + __builtin_amdgcn_mbcnt_hi(uint32_t(bal[0] >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal[0]), 0u)) +
+                                        __builtin_amdgcn_mbcnt_hi(uint32_t(bal[1] >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal[1]), 0u));
+                    const uint32_t at1 = at + uint32_t(__builtin_popcountll(bal[0]) + __builtin_popcountll(bal[1]));
+                    const uint32_t r1 = at1 + __builtin_amdgcn_mbcnt_hi(uint32_t(bal[2] >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal[2]), 0u)) +
+                                        __builtin_amdgcn_mbcnt_hi(uint32_t(bal[3] >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal[3]), 0u));
+                    uint32_t key[4];
+                    key[0] = kb + 2u * uint32_t(lane); key[1] = key[0] + 1u;
+                    key[2] = key[0] + 128u; key[3] = key[0] + 129u;
+                    if (cnt[0]) my_list[r0] = (key[0] << 16) | cnt[0];
+                    if (cnt[1]) my_list[r0 + (cnt[0] != 0u)] = (key[1] << 16) | cnt[1];
+                    if (cnt[2]) my_list[r1] = (key[2] << 16) | cnt[2];
+                    if (cnt[3]) my_list[r1 + (cnt[2] != 0u)] = (key[3] << 16) | cnt[3];
+                    at = at1 + uint32_t(__builtin_popcountll(bal[2]) + __builtin_popcountll(bal[3]));
+                    // validity and the bin's reference key (largest valid key)
+                    float z[4];
+                    uint64_t vb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        z[e] = key_z<DT>(key[e], inv_t);
+                        const bool ok = cnt[e] != 0u && isfinite(z[e]);
+                        bad_z |= cnt[e] != 0u && !ok;
+                        if (!ok) cnt[e] = 0u;
+                        vb[e] = ballot(ok);
+                    }
+                    uint32_t ref1 = 0;   // largest valid key + 1 (0: none)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (vb[e]) ref1 = max(ref1, kb + 2u * uint32_t(63 - __builtin_clzll(vb[e])) + uint32_t(e & 1) + 128u * uint32_t(e >> 1) + 1u);
+                    if (ref1) {
+                        const double zr = double(key_z<DT>(ref1 - 1u, inv_t));
+                        double m = 0.0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (cnt[e]) m += double(cnt[e]) * exp(double(z[e]) - zr);
+                        const uint32_t bc = wave_sum_u32(cnt[0] + cnt[1] + cnt[2] + cnt[3]);
+                        const double bm = wave_sum_f64(m);
+                        if (lane == bb) { v_cnt = bc; v_mass = bm; v_ref = ref1 - 1u; }
+                        wtop1 = max(wtop1, ref1);
+                    }
+                }
+                if (lane == bb) { v_first = first; v_end = at; }
+            }
         }
-    }
-    if (tid == 0) {
-        uint32_t f = sh.flags;
-        if (tot_sum != tot_fin) f |= kHdrOverflow;  // a key held >= 65,536 logits of this half
-        if (n_list > uint32_t(kListMax)) f |= kHdrOverflow;
-        a.headers[size_t(row) * 2 + half] = FullHeader{n_list, tot_fin, f, 0u};
+        if (lane < kCoarse / kFW) {
+            const int bin = lane * kFW + wave;
+            my_summary->first[bin] = v_first;
+            my_summary->end[bin] = v_end;
+            my_summary->ccnt[bin] = v_cnt;
+            my_summary->bref[bin] = v_ref;
+            my_summary->cmass[bin] = v_mass;
+        }
+        const uint32_t wsum = wave_sum_u32(my_sum), wfin = wave_sum_u32(n_fin);
+        if (bad_z) atomicOr(&sh.flags, kHdrNonfinite);
+        if (lane == 0) {
+            sh.wcount[wave] = at - uint32_t(wave) * 4096u;
+            atomicAdd(&sh.n_sum, wsum);
+            atomicAdd(&sh.n_fin, wfin);
+            if (wtop1) atomicMax(&sh.top1, wtop1);
+        }
     }
 
     // ---- C. pair barrier (self-resetting; generation counter).  Every wave
-    // drains its own list / header stores to L2 (s_waitcnt); one wave then
-    // publishes with a single agent-scope release (L2 write-back) and, after
-    // the partner arrived, takes a single agent-scope acquire (L1/L2
-    // invalidate) on behalf of the workgroup; the spin itself polls with
-    // relaxed loads so it does not invalidate caches each round.
+    // drains its own list / summary stores to L2 (s_waitcnt); one wave then
+    // writes the header and publishes with a single agent-scope release and,
+    // after the partner arrived, takes a single agent-scope acquire on behalf
+    // of the workgroup; the spin polls with relaxed loads so it does not
+    // invalidate caches each round.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
+        uint32_t f = sh.flags;
+        if (sh.n_sum != sh.n_fin) f |= kHdrOverflow;  // a key held >= 65,536 logits of this half
+        uint32_t n_list = 0;
+        for (int w = 0; w < kFW; ++w) n_list += sh.wcount[w];
+        my_summary->n_list = n_list;
+        my_summary->n_finite = sh.n_fin;
+        my_summary->flags = f;
+        my_summary->top_key = sh.top1 ? sh.top1 - 1u : 0xffffffffu;
         PairBarrier* bar = &a.barriers[row];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t gen = __hip_atomic_load(&bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -406,14 +679,15 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
-    const FullHeader H0 = a.headers[size_t(row) * 2 + 0], H1 = a.headers[size_t(row) * 2 + 1];
-    const uint32_t hflags = H0.flags | H1.flags | (sh.flags & kHdrError);
-    const int n0 = int(H0.n_list), n1 = int(H1.n_list), n = n0 + n1;
+    const HalfSummary* S0 = a.summaries + size_t(row) * 2;
+    const HalfSummary* S1 = S0 + 1;
+    const uint32_t hflags = S0->flags | S1->flags | (sh.flags & kHdrError);
+    const uint32_t tk0 = S0->top_key, tk1 = S1->top_key;
     uint32_t out_flags = 0;
     if (hflags & kHdrNonfinite) out_flags |= VI_FLAG_NONFINITE;
     if (hflags & kHdrBadHistory) out_flags |= VI_FLAG_BAD_HISTORY;
-    const bool fail = (hflags & (kHdrError | kHdrOverflow)) || n > kListMax;
-    if (fail || H0.n_finite + H1.n_finite == 0) {
+    const bool fail = (hflags & (kHdrError | kHdrOverflow)) != 0u;
+    if (fail || (tk0 == 0xffffffffu && tk1 == 0xffffffffu)) {   // error, or no valid logit
         if (half == 0 && tid == 0) {
             a.tokens[row] = fail ? -1 : V;
             if (a.uniforms) a.uniforms[row] = 0.0;
@@ -431,163 +705,289 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         return;
     }
 
-    // ---- C'. merge: M (entries, merged order), W (exclusive masses), C (counts)
-    uint32_t* LA = lds32;
-    uint32_t* LB = lds32 + n0;
-    uint32_t* M = reinterpret_cast<uint32_t*>(lds + kOffM);
-    double* W = reinterpret_cast<double*>(lds + kOffW);
-    uint32_t* HB = reinterpret_cast<uint32_t*>(lds + kOffH);
-    uint32_t* C = lds32;   // reuses the list region after the merge
-    {
-        const uint32_t* gl0 = a.lists + (size_t(row) * 2 + 0) * kListMax;
-        const uint32_t* gl1 = a.lists + (size_t(row) * 2 + 1) * kListMax;
-        for (int i = tid; i < n0; i += kFT) LA[i] = gl0[i];
-        for (int i = tid; i < n1; i += kFT) LB[i] = gl1[i];
-        for (int i = tid; i < (n + 31) / 32; i += kFT) HB[i] = 0u;
+    // ---- C'. decisions, identical in both workgroups.  Coarse bins in
+    // descending key order (q = 255 - bin) carry merged counts and masses; a
+    // boundary is located on them, then resolved inside its bin on a 256-key
+    // window built from both halves' lists.
+    const uint32_t tkmax = (tk0 == 0xffffffffu) ? tk1 : (tk1 == 0xffffffffu ? tk0 : max(tk0, tk1));
+    const double z0 = double(key_z<DT>(tkmax, inv_t));
+    uint32_t* DC = lds32;                                             // [2][256] valid counts
+    double* DM = reinterpret_cast<double*>(lds + kOffDM);              // [2][256] masses (own reference)
+    uint32_t* DF = reinterpret_cast<uint32_t*>(lds + kOffDF);          // [2][first, end][256] list slots
+    uint32_t* PC = reinterpret_cast<uint32_t*>(lds + kOffPC);          // [257] count before q
+    double* PM = reinterpret_cast<double*>(lds + kOffPM);              // [257] mass before q
+    uint32_t* WC = reinterpret_cast<uint32_t*>(lds + kOffWC);          // [2][256] window counts by slot
+    double* WW = reinterpret_cast<double*>(lds + kOffWW);              // [256] slot weight
+    uint32_t* WN = reinterpret_cast<uint32_t*>(lds + kOffWN);          // [257] window count before slot
+    double* WM = reinterpret_cast<double*>(lds + kOffWM);              // [257] window mass before slot
+    for (int i = tid; i < 2 * kCoarse; i += kFT) {   // masses rescaled to z0
+        const HalfSummary* Sh = i < kCoarse ? S0 : S1;
+        const int c = i & (kCoarse - 1);
+        const uint32_t cc = Sh->ccnt[c];
+        DC[i] = cc;
+        DM[i] = cc ? Sh->cmass[c] * exp(double(key_z<DT>(Sh->bref[c], inv_t)) - z0) : 0.0;
+    }
+    for (int i = tid; i < 2 * kCoarse; i += kFT) {
+        const HalfSummary* Sh = i < kCoarse ? S0 : S1;
+        const int c = i & (kCoarse - 1);
+        DF[2 * (i & ~(kCoarse - 1)) + c] = Sh->first[c];
+        DF[2 * (i & ~(kCoarse - 1)) + kCoarse + c] = Sh->end[c];
     }
     __syncthreads();
-    const uint32_t top_key = max(n0 ? LA[n0 - 1] >> 16 : 0u, n1 ? LB[n1 - 1] >> 16 : 0u);
-    const double z0 = double(key_z<DT>(top_key, inv_t));
-    const int E = (n + kFT - 1) / kFT;
-    const int d0 = min(tid * E, n), d1 = min(d0 + E, n);
-    uint32_t lc = 0;
-    double lw = 0.0;
-    {
-        // merge path over the two lists read in descending key order (half 0 first on ties)
-        auto A = [&](int k) { return LA[n0 - 1 - k]; };
-        auto B = [&](int k) { return LB[n1 - 1 - k]; };
-        int lo = max(0, d0 - n1), hi = min(d0, n0);
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if ((A(mid) >> 16) >= (B(d0 - 1 - mid) >> 16)) lo = mid + 1; else hi = mid;
-        }
-        int i = lo, j = d0 - lo;
-        for (int pos = d0; pos < d1; ++pos) {
-            uint32_t e;
-            if (i < n0 && (j >= n1 || (A(i) >> 16) >= (B(j) >> 16))) e = A(i++);
-            else { e = B(j++); atomicOr(&HB[pos >> 5], 1u << (pos & 31)); }
-            const float z = key_z<DT>(e >> 16, inv_t);
-            uint32_t cnt = e & 0xffffu;
-            double w = 0.0;
-            if (!isfinite(z) || !isfinite(z0)) { cnt = 0; atomicOr(&sh.flags, kHdrNonfinite); }
-            else w = exp(double(z) - z0);
-            if (p.min_p > 0.0f && cnt && w < double(p.min_p)) atomicMin(&sh.minp_pos, uint32_t(pos));
-            M[pos] = (e & 0xffff0000u) | cnt;
-            W[pos] = lw;
-            lc += cnt;
-            lw += double(cnt) * w;
-        }
-    }
-    uint32_t ctot;
-    double wtot;
-    const uint32_t coff = block_exclusive_scan_u32<kFT>(lc, sh.u, &ctot);   // (barriers inside: merge done)
-    const double woff = block_exclusive_scan_f64<kFT>(lw, sh.d, &wtot);
-    {
-        uint32_t c = coff;
-        for (int pos = d0; pos < d1; ++pos) {
-            W[pos] += woff;
-            C[pos] = c;
-            c += M[pos] & 0xffffu;
-        }
-    }
-    if (tid == 0) { C[n] = ctot; W[n] = wtot; }
-    __syncthreads();
-    if (sh.flags & kHdrNonfinite) out_flags |= VI_FLAG_NONFINITE;
-
-    // ---- decisions, identical in both workgroups (wave 0, 64-ary searches)
     if (wave == 0) {
-        const uint32_t Nv = C[n];
-        auto wt = [&](int pos) -> double {
-            const float z = key_z<DT>(M[pos] >> 16, inv_t);
-            return isfinite(z) ? exp(double(z) - z0) : 0.0;
+        // merged coarse prefix: lane l owns q = 4l .. 4l + 3
+        {
+            uint32_t cq[4];
+            double mq[4];
+            uint32_t cs = 0;
+            double ms = 0.0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = kCoarse - 1 - (4 * lane + e);
+                cq[e] = DC[c] + DC[kCoarse + c];
+                mq[e] = DM[c] + DM[kCoarse + c];
+                cs += cq[e];
+                ms += mq[e];
+            }
+            const uint32_t cx = wave_incl_scan_u32(cs);
+            const double mx = wave_incl_scan_f64(ms);
+            uint32_t cb = cx - cs;
+            double mb = mx - ms;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                PC[4 * lane + e] = cb;
+                PM[4 * lane + e] = mb;
+                cb += cq[e];
+                mb += mq[e];
+            }
+            if (lane == kWave - 1) { PC[kCoarse] = cb; PM[kCoarse] = mb; }
+        }
+        wave_lds_sync();
+        const uint32_t Nv = PC[kCoarse];
+        const double S = PM[kCoarse];
+        // first q in [0, 256) with pred(q) (monotone), or 256
+        auto coarse_find = [&](auto pred) -> int {
+            uint32_t m4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m4 |= pred(4 * lane + e) ? (1u << e) : 0u;
+            const uint64_t b = ballot(m4 != 0u);
+            if (!b) return kCoarse;
+            const int l = __builtin_ctzll(b);
+            const uint32_t ml = uint32_t(__builtin_amdgcn_readlane(int(m4), l));
+            return 4 * l + __builtin_ctz(ml);
         };
-        auto cnt = [&](int pos) -> uint32_t { return M[pos] & 0xffffu; };
+        int win_q = -1;
+        // window of coarse position q: slot j <-> key (255 - q) * 256 + 255 - j
+        auto load_window = [&](int q) {
+            if (q == win_q) return;
+            win_q = q;
+            const int c = kCoarse - 1 - q;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { WC[4 * lane + e] = 0u; WC[kCoarse + 4 * lane + e] = 0u; }
+            wave_lds_sync();
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t* gl = a.lists + (size_t(row) * 2 + h) * kListMax;
+                const uint32_t f0 = DF[2 * kCoarse * h + c], f1 = DF[2 * kCoarse * h + kCoarse + c];
+                for (uint32_t i = f0 + lane; i < f1; i += kWave) {
+                    const uint32_t ent = gl[i];
+                    WC[h * kCoarse + (255u - ((ent >> 16) & 255u))] = ent & 0xffffu;
+                }
+            }
+            wave_lds_sync();
+            uint32_t cq[4];
+            double mq[4];
+            uint32_t cs = 0;
+            double ms = 0.0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 4 * lane + e;
+                const uint32_t key = uint32_t(c * 256 + 255 - j);
+                const float z = key_z<DT>(key, inv_t);
+                const bool ok = isfinite(z);
+                cq[e] = ok ? WC[j] + WC[kCoarse + j] : 0u;
+                if (!ok) { WC[j] = 0u; WC[kCoarse + j] = 0u; }
+                const double w = ok ? exp(double(z) - z0) : 0.0;
+                WW[j] = w;
+                mq[e] = double(cq[e]) * w;
+                cs += cq[e];
+                ms += mq[e];
+            }
+            const uint32_t cx = wave_incl_scan_u32(cs);
+            const double mx = wave_incl_scan_f64(ms);
+            uint32_t cb = cx - cs;
+            double mb = mx - ms;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                WN[4 * lane + e] = cb;
+                WM[4 * lane + e] = mb;
+                cb += cq[e];
+                mb += mq[e];
+            }
+            if (lane == kWave - 1) { WN[kCoarse] = cb; WM[kCoarse] = mb; }
+            wave_lds_sync();
+        };
+        auto slot_cnt = [&](int j) -> uint32_t { return WN[j + 1] - WN[j]; };
+        // position of the n-th element (1-based) in sorted order: coarse q, slot j, count before the slot
+        struct Pos { int q, j; uint32_t before; double mass_before; };
+        auto locate = [&](uint32_t nth) -> Pos {
+            const int q = coarse_find([&](int qq) { return PC[qq + 1] >= nth; });
+            load_window(q);
+            const int j = coarse_find([&](int jj) { return PC[q] + WN[jj + 1] >= nth; });
+            return Pos{q, j, PC[q] + WN[j], PM[q] + WM[j]};
+        };
         const uint32_t cap = (p.top_k > 0 && uint32_t(p.top_k) < Nv) ? uint32_t(p.top_k) : Nv;
-        double s_cap = W[n];
+        double s_cap = S;
         if (cap < Nv) {
-            const int pk = wave_search(0, n, [&](int pos) { return C[pos + 1] >= cap; });
-            s_cap = W[pk] + double(cap - C[pk]) * wt(pk);
+            const Pos ps = locate(cap);
+            s_cap = ps.mass_before + double(cap - ps.before) * WW[ps.j];
         }
         uint32_t n_sup = cap;
-        if (p.min_p > 0.0f && sh.minp_pos != 0xffffffffu) n_sup = min(n_sup, C[sh.minp_pos]);
+        if (p.min_p > 0.0f) {
+            // smallest key with w(key) >= min_p (w grows with the key); elements
+            // below it are cut (the reference cuts at the first w < min_p)
+            const double mp = double(p.min_p);
+            auto ok = [&](int key) {
+                const float z = key_z<DT>(uint32_t(key), inv_t);
+                return isfinite(z) && exp(double(z) - z0) >= mp;
+            };
+            const int km = wave_search(0, int(tkmax) + 1, [&](int key) { return ok(key); });
+            uint32_t n_minp = 0;
+            if (km <= int(tkmax)) {
+                const int q = kCoarse - 1 - (km >> 8);
+                load_window(q);
+                n_minp = PC[q] + WN[255 - (km & 255) + 1];
+            }
+            n_sup = min(n_sup, n_minp);
+        }
         if (p.top_p < 1.0f) {
             const double target = double(p.top_p) * s_cap;
-            const int pt = wave_search(0, n, [&](int pos) {
-                const uint32_t c = C[pos];
-                if (c >= cap) return true;
-                return W[pos] + double(min(cnt(pos), cap - c)) * wt(pos) >= target;
-            });
-            if (pt < n && C[pt] < cap) {
-                const uint32_t c = C[pt];
-                const double wc = W[pt], w = wt(pt);
-                const uint32_t ce = min(cnt(pt), cap - c);
-                // smallest i with wc + (i + 1) w >= target
-                const double q = (target - wc) / w;
-                int i = q > 0.0 ? int(fmin(ceil(q), double(ce))) - 1 : 0;
-                i = max(0, min(i, int(ce) - 1));
-                while (i > 0 && wc + double(i) * w >= target) --i;
-                while (i < int(ce) - 1 && wc + double(i + 1) * w < target) ++i;
-                n_sup = min(n_sup, c + uint32_t(i) + 1u);
+            const int q = coarse_find([&](int qq) { return PM[qq + 1] >= target || PC[qq + 1] >= cap; });
+            if (q < kCoarse) {
+                load_window(q);
+                const int j = coarse_find([&](int jj) { return PM[q] + WM[jj + 1] >= target || PC[q] + WN[jj + 1] >= cap; });
+                const uint32_t c = PC[q] + WN[j];
+                if (j < kCoarse && c < cap) {
+                    const double wc = PM[q] + WM[j], w = WW[j];
+                    const uint32_t ce = min(slot_cnt(j), cap - c);
+                    if (wc + double(ce) * w >= target) {
+                        // smallest i with wc + (i + 1) w >= target
+                        const double qq = (target - wc) / w;
+                        int i = qq > 0.0 ? int(fmin(ceil(qq), double(ce))) - 1 : 0;
+                        i = max(0, min(i, int(ce) - 1));
+                        while (i > 0 && wc + double(i) * w >= target) --i;
+                        while (i < int(ce) - 1 && wc + double(i + 1) * w < target) ++i;
+                        n_sup = min(n_sup, c + uint32_t(i) + 1u);
+                    }
+                }
             }
         }
         if (n_sup < 1u) n_sup = 1u;
-        const int pn = wave_search(0, n, [&](int pos) { return C[pos + 1] >= n_sup; });
-        const uint32_t pn_take = n_sup - C[pn];
-        const double w_pn = wt(pn);
-        const double s_n = W[pn] + double(pn_take) * w_pn;
+        const Pos pn = locate(n_sup);
+        const uint32_t pn_take = n_sup - pn.before;
+        const double s_n = pn.mass_before + double(pn_take) * WW[pn.j];
+        const uint32_t pn_key = uint32_t((kCoarse - 1 - pn.q) * 256 + 255 - pn.j);
+        const uint32_t pn_c0 = WC[pn.j];
         const double u = philox_uniform(p.seed, p.lane, p.position, 0u);
         const double t = u * s_n;
-        int ru = wave_search(0, pn + 1, [&](int pos) {
-            const uint32_t c = C[pos];
-            const uint32_t ce = pos == pn ? pn_take : cnt(pos);
-            return W[pos] + double(ce) * wt(pos) > t && c < n_sup;
-        });
+        // draw: first position (among the first n_sup) whose cumulative mass exceeds t
+        int rq = coarse_find([&](int qq) { return PM[qq + 1] > t || PC[qq + 1] >= n_sup; });
+        if (rq > pn.q) rq = pn.q;
+        load_window(rq);
+        int rj = coarse_find([&](int jj) { return PM[rq] + WM[jj + 1] > t || PC[rq] + WN[jj + 1] >= n_sup; });
         uint32_t rank;
-        if (ru <= pn) {
-            const double wc = W[ru], w = wt(ru);
-            const uint32_t ce = ru == pn ? pn_take : cnt(ru);
-            // smallest i with wc + (i + 1) w > t
-            const double q = (t - wc) / w;
-            int i = q > 0.0 ? int(fmin(floor(q), double(ce - 1))) : 0;
-            i = max(0, min(i, int(ce) - 1));
-            while (i > 0 && wc + double(i) * w > t) --i;
-            while (i < int(ce) - 1 && wc + double(i + 1) * w <= t) ++i;
-            rank = uint32_t(i);
-        } else {
-            ru = pn;
-            rank = pn_take - 1u;
+        {
+            const bool at_pn = rq == pn.q && rj >= pn.j;
+            if (at_pn) rj = pn.j;
+            const double wc = PM[rq] + WM[rj], w = WW[rj];
+            const uint32_t ce = at_pn ? pn_take : slot_cnt(rj);
+            if (wc + double(ce) * w > t) {
+                // smallest i with wc + (i + 1) w > t
+                const double qq = (t - wc) / w;
+                int i = qq > 0.0 ? int(fmin(floor(qq), double(ce - 1))) : 0;
+                i = max(0, min(i, int(ce) - 1));
+                while (i > 0 && wc + double(i) * w > t) --i;
+                while (i < int(ce) - 1 && wc + double(i + 1) * w <= t) ++i;
+                rank = uint32_t(i);
+            } else {   // rounding left t beyond the support: its last element
+                rank = ce - 1u;
+            }
         }
+        const uint32_t r_c0 = WC[rj];
         if (lane == 0) {
-            sh.r_key = int(M[ru] >> 16);
-            sh.r_half = int((HB[ru >> 5] >> (ru & 31)) & 1u);
-            sh.rank = rank;
-            sh.pn_key = int(M[pn] >> 16);
-            sh.pn_half = int((HB[pn >> 5] >> (pn & 31)) & 1u);
-            sh.pn_take = pn_take;
+            sh.r_key = int((kCoarse - 1 - rq) * 256 + 255 - rj);
+            sh.r_half = rank < r_c0 ? 0 : 1;
+            sh.rank = rank < r_c0 ? rank : rank - r_c0;
+            sh.pn_key = int(pn_key);
+            sh.pn_half = pn_take <= pn_c0 ? 0 : 1;
+            sh.pn_take = pn_take <= pn_c0 ? pn_take : pn_take - pn_c0;
             sh.n_sup = n_sup;
             sh.s_n = s_n;
             sh.draw_u = u;
+            sh.ctot = Nv;
             sh.slot = 0xffffffffu;
         }
     }
     if (tid < kFV + 2) sh.slot_tot[tid] = 0u;
     __syncthreads();
+    // dense path: penalized history bits by rank into LDS (the merge region is free)
+    uint16_t* P = reinterpret_cast<uint16_t*>(lds + kOffP);
+    if constexpr (kDense) {
+        if (pen) {
+#pragma unroll
+            for (int k = 0; k < kDR; ++k) {
+                const uint32_t r = uint32_t(k) * kFT + tid;
+                if (r < n_flag) P[r] = uint16_t(dense_pen(k));
+            }
+            __syncthreads();
+        }
+    }
     const int r_half = sh.r_half;
     const uint32_t r_key = uint32_t(sh.r_key);
 
     // ---- D. the owning half finds the rank-th logit of key r_key (id order:
     // head slot, vector slots 0..15 (thread-major inside a slot), tail slot)
     if (half == r_half) {
-        // per-slot totals
-        uint32_t c_head = (tid < head && Elem<DT>::finite_bits(hbits) && key16(hbits) == r_key) ? 1u : 0u;
-        uint32_t c_tail = (tid < tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == r_key) ? 1u : 0u;
-        if (c_head) atomicAdd(&sh.slot_tot[0], 1u);
+        uint32_t* fmask = lds32;   // [kFT] history-token candidates per owning thread
+        fmask[tid] = 0u;
+        const uint32_t c_head = (tid < head && !fl_head && Elem<DT>::finite_bits(hbits) && key16(hbits) == r_key);
+        const uint32_t c_tail = (tid < tail && !fl_tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == r_key);
+        // per-slot counts summed over the wave with shuffles: one LDS atomic
+        // per wave and slot instead of one per thread
+        auto wave_add = [&](int s2, uint32_t c) {
+            c = wave_sum_u32(c);
+            if (lane == 0 && c) atomicAdd(&sh.slot_tot[s2], c);
+        };
+        auto vec_match = [&](int i) -> uint32_t {   // candidates of vector slot i outside the history
+            const int v = i * kFT + tid;
+            return v < nvec ? match_mask8<DT>(row_vec(i), r_key) & ~vflags(i) : 0u;
+        };
+        wave_add(0, c_head);
+        uint32_t vm[kFV / 4] = {0u, 0u, 0u, 0u};   // candidate masks of the 16 vector slots
 #pragma unroll
         for (int i = 0; i < kFV; ++i) {
-            const uint32_t c = (i * kFT + tid < nvec) ? count_key8<DT>(d[i], r_key) : 0u;
-            if (c) atomicAdd(&sh.slot_tot[1 + i], c);
+            const uint32_t m = vec_match(i);
+            vm[i >> 2] |= m << (8 * (i & 3));
+            wave_add(1 + i, __builtin_popcount(m));
         }
-        if (c_tail) atomicAdd(&sh.slot_tot[kFV + 1], 1u);
+        wave_add(kFV + 1, c_tail);
+        // slot, owning thread and element index of the half's token h0 + off
+        auto place = [&](int off, int* owner, int* j) -> int {
+            if (off < head) { *owner = off; *j = 0; return 0; }
+            const int rel = off - head;
+            if (rel >= nvec * 8) { *owner = rel - nvec * 8; *j = 0; return kFV + 1; }
+            const int v = rel >> 3;
+            *owner = v & (kFT - 1);
+            *j = rel & 7;
+            return 1 + v / kFT;
+        };
+        walk_words([&](uint32_t rank, int off) {
+            const uint32_t pb = P[rank];
+            if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key) {
+                int o, j;
+                atomicAdd(&sh.slot_tot[place(off, &o, &j)], 1u);
+            }
+        });
         __syncthreads();
         if (tid == 0) {
             uint32_t acc = 0;
@@ -598,40 +998,47 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
         __syncthreads();
         const int s = int(sh.slot);
-        uint32_t mine = 0;
-        if (s == 0) mine = c_head;
-        else if (s == kFV + 1) mine = c_tail;
+        walk_words([&](uint32_t rank, int off) {
+            const uint32_t pb = P[rank];
+            int o, j;
+            if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key && place(off, &o, &j) == s) atomicOr(&fmask[o], 1u << j);
+        });
+        __syncthreads();
+        uint32_t cm = fmask[tid];   // candidate bits (element j of this thread's group in slot s)
+        if (s == 0) cm |= c_head;
+        else if (s == kFV + 1) cm |= c_tail;
         else {
 #pragma unroll
             for (int i = 0; i < kFV; ++i)
-                if (s == 1 + i && i * kFT + tid < nvec) mine = count_key8<DT>(d[i], r_key);
+                if (s == 1 + i) cm |= (vm[i >> 2] >> (8 * (i & 3))) & 0xffu;
         }
+        const uint32_t mine = __builtin_popcount(cm);
         uint32_t tot;
         const uint32_t ex = block_exclusive_scan_u32<kFT>(mine, sh.u, &tot);
         const uint32_t want = sh.slot_rank;
-        if (mine && want >= ex && want < ex + mine) {
-            int32_t token = -1;
-            if (s == 0) token = h0 + tid;
-            else if (s == kFV + 1) token = vid0 + nvec * 8 + tid;
-            else {
-                uint4 v = d[0];
-#pragma unroll
-                for (int i = 1; i < kFV; ++i) if (s == 1 + i) v = d[i];
-                const uint64_t q0 = uint64_t(v.x) | (uint64_t(v.y) << 32), q1 = uint64_t(v.z) | (uint64_t(v.w) << 32);
-                uint32_t k = want - ex;
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t bits = bits_of(q0, q1, j);
-                    if (Elem<DT>::finite_bits(bits) && key16(bits) == r_key) {
-                        if (k == 0) { token = vid0 + ((s - 1) * kFT + tid) * 8 + j; break; }
-                        --k;
-                    }
+        if (s < 0 || s > kFV + 1) {
+            if (tid == 0) {   // counts disagree with the histogram: cannot happen for consistent inputs
+                a.tokens[row] = -1;
+                if (a.uniforms) a.uniforms[row] = sh.draw_u;
+                if (a.stats) {
+                    vi_sample_stats st{};
+                    st.flags = out_flags | VI_FLAG_ERROR;
+                    a.stats[row] = st;
                 }
             }
+        } else if (mine && want >= ex && want < ex + mine) {
+            uint32_t m = cm;
+            for (uint32_t k = want - ex; k > 0; --k) m &= m - 1u;
+            const int j = __builtin_ctz(m);
+            int32_t token;
+            if (s == 0) token = h0 + tid;
+            else if (s == kFV + 1) token = vid0 + nvec * 8 + tid;
+            else token = vid0 + ((s - 1) * kFT + tid) * 8 + j;
             a.tokens[row] = token;
             if (a.uniforms) a.uniforms[row] = sh.draw_u;
             if (a.stats) {
                 vi_sample_stats st{};
-                st.flags = out_flags; st.support = sh.n_sup; st.finite = C[n]; st.support_mass = sh.s_n;
+                st.flags = out_flags; st.support = sh.n_sup; st.finite = sh.ctot; st.support_mass = sh.s_n;
                 st.uniform = sh.draw_u;
                 a.stats[row] = st;
             }
@@ -642,17 +1049,21 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // probs kernel (probs row = scratch for the bits until it overwrites them)
     if (a.probs) {
         uint32_t* pr = reinterpret_cast<uint32_t*>(a.probs + size_t(row) * size_t(a.probs_stride));
-        if (tid < head) pr[h0 + tid] = hbits;
-        if (tid < tail) pr[vid0 + nvec * 8 + tid] = tbits;
+        if (tid < head && !fl_head) pr[h0 + tid] = hbits;
+        if (tid < tail && !fl_tail) pr[vid0 + nvec * 8 + tid] = tbits;
 #pragma unroll
         for (int i = 0; i < kFV; ++i) {
             const int v = i * kFT + tid;
             if (v < nvec) {
-                const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
+                const uint32_t fl = vflags(i);
+                const uint4 dv = row_vec(i);
+                const uint32_t w4[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) pr[vid0 + v * 8 + j] = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                for (int j = 0; j < 8; ++j)
+                    if (!((fl >> j) & 1u)) pr[vid0 + v * 8 + j] = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
             }
         }
+        walk_words([&](uint32_t rank, int off) { pr[h0 + off] = P[rank]; });
         if (half == 0 && tid == 0)
             a.bounds[row] = RowBoundary{z0, sh.s_n, inv_t, sh.pn_key, sh.pn_half, sh.pn_take, 1u};
     }
@@ -708,6 +1119,12 @@ __global__ __launch_bounds__(kFT) void full_probs_kernel(const vi_row_params* pa
     }
 }
 
+template <int DT>
+void launch_full_dt(const FullArgs& a, bool dense, dim3 grid, hipStream_t stream) {
+    if (dense) hipLaunchKernelGGL((full_kernel<DT, true>), grid, dim3(kFT), 0, stream, a);
+    else hipLaunchKernelGGL((full_kernel<DT, false>), grid, dim3(kFT), 0, stream, a);
+}
+
 }  // namespace
 
 bool full_supported(int dtype, int vocabulary, int64_t stride) {
@@ -717,7 +1134,7 @@ bool full_supported(int dtype, int vocabulary, int64_t stride) {
 }
 
 size_t full_workspace(int rows) {
-    return align_up(size_t(rows) * sizeof(PairBarrier), 256) + align_up(size_t(rows) * 2 * sizeof(FullHeader), 256) +
+    return align_up(size_t(rows) * sizeof(PairBarrier), 256) + align_up(size_t(rows) * 2 * sizeof(HalfSummary), 256) +
            align_up(size_t(rows) * 2 * kListMax * 4, 256) + align_up(size_t(rows) * sizeof(RowBoundary), 256) + 256;
 }
 
@@ -726,7 +1143,7 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     Carver c(ws, ws_bytes);
     FullArgs a{};
     a.barriers = c.take<PairBarrier>(size_t(s.rows));
-    a.headers = c.take<FullHeader>(size_t(s.rows) * 2);
+    a.summaries = c.take<HalfSummary>(size_t(s.rows) * 2);
     a.lists = c.take<uint32_t>(size_t(s.rows) * 2 * kListMax);
     a.bounds = c.take<RowBoundary>(size_t(s.rows));
     if (!c.ok) return VI_ERR_WORKSPACE;
@@ -736,12 +1153,14 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
     a.stats = s.stats;
     const int groups = (s.rows + 7) / 8;
-    const dim3 grid(groups * 16), block(kFT);
-    if (s.dtype == VI_BF16) hipLaunchKernelGGL(full_kernel<VI_BF16>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(full_kernel<VI_F16>, grid, block, 0, stream, a);
+    const dim3 grid(groups * 16);
+    // histories up to kHistMax tokens: dense penalty path; longer: general path
+    const bool dense = s.max_history <= kHistMax;
+    if (s.dtype == VI_BF16) launch_full_dt<VI_BF16>(a, dense, grid, stream);
+    else launch_full_dt<VI_F16>(a, dense, grid, stream);
     vi_status st = launch_status();
     if (st != VI_OK || !s.probs) return st;
-    const dim3 pgrid(2, s.rows);
+    const dim3 pgrid(2, s.rows), block(kFT);
     if (s.dtype == VI_BF16)
         hipLaunchKernelGGL(full_probs_kernel<VI_BF16>, pgrid, block, 0, stream, s.params, s.rows, s.vocabulary,
                            a.half_len, s.probs, s.probs_stride, a.bounds);

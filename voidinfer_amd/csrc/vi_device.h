@@ -171,24 +171,64 @@ __device__ __forceinline__ bool topk_route(const vi_row_params& p) {
     return !(p.temperature > 0.0f) || (p.top_k >= 1 && p.top_k <= 64);
 }
 
+// ------------------------------------------------------------ DPP wave scans
+// Inclusive prefix sums over the 64 lanes of a wave with DPP moves: row shifts
+// 1, 2, 4, 8 inside each 16-lane row, then the row_bcast:15 / row_bcast:31
+// carries between rows.  VALU-latency data movement, no LDS crossbar.
+template <int kCtrl, int kRowMask, bool kBound>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kCtrl, kRowMask, 0xf, kBound));
+}
+template <int kCtrl, int kRowMask, bool kBound>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = uint64_t(dpp_u32<kCtrl, kRowMask, kBound>(uint32_t(b))) |
+                       (uint64_t(dpp_u32<kCtrl, kRowMask, kBound>(uint32_t(b >> 32))) << 32);
+    return __builtin_bit_cast(double, r);
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+    x += dpp_u32<0x111, 0xf, true>(x);    // row_shr:1
+    x += dpp_u32<0x112, 0xf, true>(x);    // row_shr:2
+    x += dpp_u32<0x114, 0xf, true>(x);    // row_shr:4
+    x += dpp_u32<0x118, 0xf, true>(x);    // row_shr:8
+    x += dpp_u32<0x142, 0xa, false>(x);   // row_bcast:15 -> rows 1, 3
+    x += dpp_u32<0x143, 0xc, false>(x);   // row_bcast:31 -> rows 2, 3
+    return x;
+}
+__device__ __forceinline__ double wave_incl_scan_f64(double x) {
+    x += dpp_f64<0x111, 0xf, true>(x);
+    x += dpp_f64<0x112, 0xf, true>(x);
+    x += dpp_f64<0x114, 0xf, true>(x);
+    x += dpp_f64<0x118, 0xf, true>(x);
+    x += dpp_f64<0x142, 0xa, false>(x);
+    x += dpp_f64<0x143, 0xc, false>(x);
+    return x;
+}
+// Sum over the wave, returned in every lane.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
+    return uint32_t(__builtin_amdgcn_readlane(int(wave_incl_scan_u32(x)), kWave - 1));
+}
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, wave_incl_scan_f64(x));
+    const uint64_t r = uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), kWave - 1))) |
+                       (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), kWave - 1))) << 32);
+    return __builtin_bit_cast(double, r);
+}
+
 // ------------------------------------------------------------------ block scan
 // Exclusive prefix of a per-thread u32 over the block (blockDim.x = NT); `tmp`
 // holds NT/64 + 1 words.  Returns the exclusive prefix; *total gets the sum.
 template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_t* tmp, uint32_t* total) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
-    uint32_t x = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = __shfl_up(x, o, kWave);
-        if (lane >= o) x += y;
-    }
+    const uint32_t x = wave_incl_scan_u32(v);
     if (lane == kWave - 1) tmp[wave] = x;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t s = 0;
-        for (int w = 0; w < NT / kWave; ++w) { const uint32_t t = tmp[w]; tmp[w] = s; s += t; }
-        tmp[NT / kWave] = s;
+    if (wave == 0) {   // scan of the wave totals in wave 0
+        const uint32_t t = lane < NT / kWave ? tmp[lane] : 0u;
+        const uint32_t it = wave_incl_scan_u32(t);
+        if (lane < NT / kWave) tmp[lane] = it - t;
+        if (lane == NT / kWave - 1) tmp[NT / kWave] = it;
     }
     __syncthreads();
     const uint32_t r = tmp[wave] + x - v;
