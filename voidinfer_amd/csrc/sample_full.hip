@@ -58,6 +58,7 @@ constexpr int kDR = kHistMax / kFT;       // dense ranks (distinct history token
 constexpr int kBmapWords = kVecMax * 8 / 32;
 
 constexpr int kCoarse = 256;              // coarse bins of 256 keys
+constexpr int kNfBins = 4;                // coarse bins at each end holding non-finite keys
 // What a half publishes for its partner: header, its sorted (key << 16 | count)
 // list's first index per coarse bin, and per coarse bin the count of valid
 // logits and their mass sum count * exp(z(key) - z(top_key)).
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // fn(token) for each of the row's first kHistMax history tokens; the history
     // is read in rounds of kHR tokens per thread (bounded registers)
     auto for_history = [&](auto&& fn) {
-        constexpr int kHR = 16;
+        constexpr int kHR = 8;
         const int64_t hl = min(hn, int64_t(kHistMax));
 #pragma unroll
         for (int r0 = 0; r0 < kHT; r0 += kHR) {
@@ -384,20 +385,27 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             });
             __syncthreads();
             const uint32_t big_rank = sh.big_rank;
-            // all gathers in flight at once (offsets from LDS), then the counts
-            uint32_t g[kDR];
+            // gathers in batches of kGB ranks per thread (offsets from LDS), then
+            // the counts; batches past the last rank are skipped (n_flag is uniform)
+            constexpr int kGB = 8;
 #pragma unroll
-            for (int k = 0; k < kDR; ++k) {   // unused slots load nothing (the half may be empty)
-                const uint32_t r = uint32_t(k) * kFT + tid;
-                g[k] = r < n_flag ? uint32_t(base16[lds32[r] >> 15]) : 0u;
-            }
+            for (int bt = 0; bt < kDR; bt += kGB) {
+                if (uint32_t(bt) * kFT >= n_flag) break;
+                uint32_t g[kGB];
 #pragma unroll
-            for (int k = 0; k < kDR; ++k) {
-                const uint32_t r = uint32_t(k) * kFT + tid;
-                if (r < n_flag) {
-                    const uint32_t c = r == big_rank ? 32768u : (lds32[r] & 0x7fffu);
-                    const uint32_t pb = Elem<DT>::finite_bits(g[k]) ? penalize_bits<DT>(g[k], c, p) & 0xffffu : g[k];
-                    dpen[k >> 1] |= pb << (16 * (k & 1));
+                for (int u = 0; u < kGB; ++u) {   // unused slots load nothing (the half may be empty)
+                    const uint32_t r = uint32_t(bt + u) * kFT + tid;
+                    g[u] = r < n_flag ? uint32_t(base16[lds32[r] >> 15]) : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < kGB; ++u) {
+                    const int k = bt + u;
+                    const uint32_t r = uint32_t(k) * kFT + tid;
+                    if (r < n_flag) {
+                        const uint32_t c = r == big_rank ? 32768u : (lds32[r] & 0x7fffu);
+                        const uint32_t pb = Elem<DT>::finite_bits(g[u]) ? penalize_bits<DT>(g[u], c, p) & 0xffffu : g[u];
+                        dpen[k >> 1] |= pb << (16 * (k & 1));
+                    }
                 }
             }
             __syncthreads();   // entries read before the histogram overwrites them
@@ -508,42 +516,49 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
     }
 
-    // ---- B. key histogram (u16 counts packed in pairs) and the sorted list
+    // ---- B. key histogram (u16 counts packed in pairs, key k in word k >> 1).
+    // Every logit is counted under its order key, non-finite ones included (their
+    // keys form the ends of the key range and are split off at compaction);
+    // history tokens (dense path) count 0 here and are added by the dense pass.
     const float inv_t = 1.0f / p.temperature;
-    uint32_t n_fin = 0;
-    bool nonfinite = false;
     for (int w = tid; w < 32768; w += kFT) lds32[w] = 0u;
     __syncthreads();
-    auto hist_add = [&](uint32_t bits) {
-        if (Elem<DT>::finite_bits(bits)) {
-            const uint32_t k = key16(bits);
-            atomicAdd(&lds32[k >> 1], (k & 1u) ? 0x10000u : 1u);
-            ++n_fin;
-        } else {
-            nonfinite = true;
-        }
+    auto hist_key = [&](uint32_t k, bool skip) {
+        atomicAdd(&lds32[k >> 1], skip ? 0u : ((k & 1u) ? 0x10000u : 1u));
     };
-    // history tokens (dense path) are skipped here and added by the dense pass
+    // both logits of a 32-bit word: key16 on the two halves at once (without
+    // key16's -0 -> +0 fold: -0 lands on key 0x7fff, folded into 0x8000 below)
+    auto hist_word = [&](uint32_t w, uint32_t skip2) {
+        const uint32_t s2 = (w >> 15) & 0x00010001u;
+        const uint32_t k2 = w ^ ((s2 * 0x7fffu) | 0x80008000u);
+        hist_key(k2 & 0xffffu, skip2 & 1u);
+        hist_key(k2 >> 16, skip2 & 2u);
+    };
 #pragma unroll
     for (int i = 0; i < kFV; ++i) {
         const int v = i * kFT + tid;
         if (v < nvec) {
             const uint32_t fl = vflags(i);
-            const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (!((fl >> j) & 1u)) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+            hist_word(d[i].x, fl);
+            hist_word(d[i].y, fl >> 2);
+            hist_word(d[i].z, fl >> 4);
+            hist_word(d[i].w, fl >> 6);
         }
     }
-    if (tid < head && !fl_head) hist_add(hbits);
-    if (tid < tail && !fl_tail) hist_add(tbits);
+    if (tid < head) hist_key(key16(hbits), fl_head);
+    if (tid < tail) hist_key(key16(tbits), fl_tail);
     if constexpr (kDense) {
         // the history tokens, penalized
 #pragma unroll
         for (int k = 0; k < kDR; ++k)
-            if (uint32_t(k) * kFT + tid < n_flag) hist_add(dense_pen(k));
+            if (uint32_t(k) * kFT + tid < n_flag) hist_key(key16(dense_pen(k)), false);
     }
-    if (nonfinite) atomicOr(&sh.flags, kHdrNonfinite);
+    __syncthreads();
+    if (tid == 0) {   // -0 counts as +0 (key 0x7fff is only ever -0)
+        const uint32_t x = lds32[0x7fff >> 1];
+        lds32[0x7fff >> 1] = x & 0xffffu;
+        lds32[0x8000 >> 1] += x >> 16;
+    }
     __syncthreads();
     // ---- B'. compaction and this half's summary.  Wave w owns the coarse bins
     // w, w + 16, w + 32, ... (256 keys = 128 histogram words each; neighbouring
@@ -558,7 +573,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     uint32_t* my_list = a.lists + (size_t(row) * 2 + half) * kListMax;
     HalfSummary* my_summary = a.summaries + size_t(row) * 2 + half;
     {
-        uint32_t my_sum = 0;
+        uint32_t my_sum = 0, my_nf = 0;
         uint32_t at = uint32_t(wave) * 4096u;                 // (wave-uniform) next list slot
         uint32_t v_first = 0, v_end = 0, v_cnt = 0, v_ref = 0;   // lane b: bin b * 16 + wave
         double v_mass = 0.0;
@@ -577,6 +592,13 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                 cnt[0] = xs[2 * ub] & 0xffffu; cnt[1] = xs[2 * ub] >> 16;
                 cnt[2] = xs[2 * ub + 1] & 0xffffu; cnt[3] = xs[2 * ub + 1] >> 16;
                 my_sum += cnt[0] + cnt[1] + cnt[2] + cnt[3];
+                if (bin < kNfBins || bin >= kCoarse - kNfBins) {   // the non-finite logits' keys
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t k = uint32_t(bin * 256) + 2u * uint32_t(lane) + uint32_t(e & 1) + 128u * uint32_t(e >> 1);
+                        if (Elem<DT>::nonfinite_key(k)) { my_nf += cnt[e]; cnt[e] = 0u; }
+                    }
+                }
                 uint64_t bal[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) bal[e] = ballot(cnt[e] != 0u);
@@ -635,8 +657,9 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             my_summary->bref[bin] = v_ref;
             my_summary->cmass[bin] = v_mass;
         }
-        const uint32_t wsum = wave_sum_u32(my_sum), wfin = wave_sum_u32(n_fin);
-        if (bad_z) atomicOr(&sh.flags, kHdrNonfinite);
+        const uint32_t wsum = wave_sum_u32(my_sum), wnf = wave_sum_u32(my_nf);
+        const uint32_t wfin = wsum - wnf;
+        if (bad_z || wnf) atomicOr(&sh.flags, kHdrNonfinite);
         if (lane == 0) {
             sh.wcount[wave] = at - uint32_t(wave) * 4096u;
             atomicAdd(&sh.n_sum, wsum);
@@ -655,7 +678,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     __syncthreads();
     if (tid == 0) {
         uint32_t f = sh.flags;
-        if (sh.n_sum != sh.n_fin) f |= kHdrOverflow;  // a key held >= 65,536 logits of this half
+        if (sh.n_sum != uint32_t(n_el)) f |= kHdrOverflow;  // a key held >= 65,536 logits of this half
         uint32_t n_list = 0;
         for (int w = 0; w < kFW; ++w) n_list += sh.wcount[w];
         my_summary->n_list = n_list;
@@ -958,17 +981,20 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             c = wave_sum_u32(c);
             if (lane == 0 && c) atomicAdd(&sh.slot_tot[s2], c);
         };
-        auto vec_match = [&](int i) -> uint32_t {   // candidates of vector slot i outside the history
-            const int v = i * kFT + tid;
-            return v < nvec ? match_mask8<DT>(row_vec(i), r_key) & ~vflags(i) : 0u;
-        };
         wave_add(0, c_head);
         uint32_t vm[kFV / 4] = {0u, 0u, 0u, 0u};   // candidate masks of the 16 vector slots
 #pragma unroll
-        for (int i = 0; i < kFV; ++i) {
-            const uint32_t m = vec_match(i);
-            vm[i >> 2] |= m << (8 * (i & 3));
-            wave_add(1 + i, __builtin_popcount(m));
+        for (int i0 = 0; i0 < kFV; i0 += kFV / 2) {   // 8 vectors in flight
+            uint4 rv[kFV / 2];
+#pragma unroll
+            for (int u = 0; u < kFV / 2; ++u) rv[u] = row_vec(i0 + u);
+#pragma unroll
+            for (int u = 0; u < kFV / 2; ++u) {
+                const int i = i0 + u;
+                const uint32_t m = i * kFT + tid < nvec ? match_mask8<DT>(rv[u], r_key) & ~vflags(i) : 0u;
+                vm[i >> 2] |= m << (8 * (i & 3));
+                wave_add(1 + i, __builtin_popcount(m));
+            }
         }
         wave_add(kFV + 1, c_tail);
         // slot, owning thread and element index of the half's token h0 + off

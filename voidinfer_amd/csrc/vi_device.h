@@ -49,6 +49,8 @@ template <> struct Elem<VI_BF16> {
     __device__ static float decode(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
     __device__ static bool finite_bits(uint32_t b) { return (b & 0x7f80u) != 0x7f80u; }
     __device__ static bool nan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7f80u; }
+    // order keys (key16) of the non-finite patterns: the 128 lowest and highest
+    __device__ static bool nonfinite_key(uint32_t k) { return k < 0x80u || k >= 0xff80u; }
     // Round to nearest even (the hardware conversion v_cvt_pk_bf16_f32).
     __device__ static uint32_t round(float f) {
         return uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
@@ -62,6 +64,8 @@ template <> struct Elem<VI_F16> {
     }
     __device__ static bool finite_bits(uint32_t b) { return (b & 0x7c00u) != 0x7c00u; }
     __device__ static bool nan_bits(uint32_t b) { return (b & 0x7fffu) > 0x7c00u; }
+    // order keys (key16) of the non-finite patterns: the 1024 lowest and highest
+    __device__ static bool nonfinite_key(uint32_t k) { return k < 0x400u || k >= 0xfc00u; }
     __device__ static uint32_t round(float f) {
         return uint32_t(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
     }
