@@ -21,9 +21,12 @@ LIB = PKG / "libvoidinfer_sampling.so"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
-# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation.
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation (some of their forms have
+# given wrong results on these GPUs).  -ffp-contract=off: every float operation is
+# rounded as written, as in the CPU reference (fused multiply-adds only where the
+# source calls fmaf).
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-ffp-contract=fast",
+    "--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     "-I", str(ROOT / "include"),

@@ -156,11 +156,16 @@ __device__ __forceinline__ double philox_uniform(uint64_t seed, uint32_t lane, i
 // logits' dtype (round to nearest even).  Returns the penalized bits.
 template <int DT>
 __device__ __forceinline__ uint32_t penalize_bits(uint32_t bits, uint32_t count, const vi_row_params& p) {
+    // Separate roundings, as in the reference's CPU path: the library is built
+    // with -ffp-contract=off, and the product and the difference stay apart.
+#pragma clang fp contract(off)
     float y = Elem<DT>::decode(bits);
-    if (p.repetition_penalty != 1.0f)
-        y = (y > 0.0f) ? __fdiv_rn(y, p.repetition_penalty) : __fmul_rn(y, p.repetition_penalty);
-    if (p.frequency_penalty != 0.0f) y = __fsub_rn(y, __fmul_rn(p.frequency_penalty, float(count)));
-    if (p.presence_penalty != 0.0f) y = __fsub_rn(y, p.presence_penalty);
+    if (p.repetition_penalty != 1.0f) y = (y > 0.0f) ? y / p.repetition_penalty : y * p.repetition_penalty;
+    if (p.frequency_penalty != 0.0f) {
+        const float t = p.frequency_penalty * float(count);
+        y = y - t;
+    }
+    if (p.presence_penalty != 0.0f) y = y - p.presence_penalty;
     return Elem<DT>::round(y);
 }
 __device__ __forceinline__ bool penalties_active(const vi_row_params& p) {
