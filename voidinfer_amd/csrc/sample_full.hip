@@ -98,6 +98,7 @@ struct FullArgs {
     HalfSummary* summaries;  // [rows][2]
     uint32_t* lists;         // [rows][2][kListMax]
     RowBoundary* bounds;     // [rows]
+    uint16_t* dense;         // [rows][2][kHistMax] penalized history-token logits by rank
 };
 
 constexpr uint32_t kHdrNonfinite = 1u, kHdrBadHistory = 2u, kHdrError = 4u, kHdrOverflow = 8u;
@@ -125,7 +126,7 @@ static_assert(kHistMax / 2 * 4 <= 131072, "dense counts");
 struct Shared {
     uint32_t u[kFW + 1];
     double d[kFW + 1];
-    uint32_t ovf_n, flags, top1, big_rank;
+    uint32_t ovf_n, flags, top1;
     // decisions (written by wave 0)
     int32_t r_key, r_half, pn_key, pn_half;
     uint32_t rank, pn_take, n_sup, slot, slot_rank, ctot;
@@ -303,10 +304,9 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // consecutive ranks: nearby tokens) and penalized into registers, rank
     // k * kFT + tid in slot k.
     uint32_t n_flag = 0;
-    uint32_t dpen[kDense ? kDR / 2 : 1];   // penalized bits, u16 pairs (slots 2q, 2q + 1)
-#pragma unroll
-    for (int q = 0; q < (kDense ? kDR / 2 : 1); ++q) dpen[q] = 0u;
-    auto dense_pen = [&](int k) -> uint32_t { return (dpen[k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+    // the history tokens' penalized logits by rank: this half's slice of the
+    // workspace (written once, read back from L2; not kept in registers)
+    uint16_t* dpen = kDense ? a.dense + (size_t(row) * 2 + half) * kHistMax : nullptr;
     // fn(rank, off) for every history token of this thread's 4 bitmap words
     // (rows with penalties only: the bitmap is not built otherwise)
     auto walk_words = [&](auto&& fn) {
@@ -331,15 +331,16 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // is read in rounds of kHR tokens per thread (bounded registers)
     auto for_history = [&](auto&& fn) {
         constexpr int kHR = 8;
-        const int64_t hl = min(hn, int64_t(kHistMax));
+        const int hl = int(min(hn, int64_t(kHistMax)));   // (32-bit offsets: one VGPR per load)
 #pragma unroll
         for (int r0 = 0; r0 < kHT; r0 += kHR) {
+            if (r0 * kFT >= hl) break;   // (uniform)
             int32_t t[kHR];
 #pragma unroll
-            for (int j = 0; j < kHR; ++j) t[j] = hist[min(int64_t(r0 + j) * kFT + tid, hl - 1)];
+            for (int j = 0; j < kHR; ++j) t[j] = hist[min((r0 + j) * kFT + tid, hl - 1)];
 #pragma unroll
             for (int j = 0; j < kHR; ++j)
-                if (int64_t(r0 + j) * kFT + tid < hl) fn(t[j]);
+                if ((r0 + j) * kFT + tid < hl) fn(t[j]);
         }
     };
     if constexpr (kDense) {
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             uint32_t* bmap = reinterpret_cast<uint32_t*>(lds + kOffBmap);
             uint16_t* pref = reinterpret_cast<uint16_t*>(lds + kOffPref);
             for (int w = tid; w < kBmapWords + 4; w += kFT) bmap[w] = 0u;
-            if (tid == 0) sh.big_rank = 0xffffffffu;
+            for (int w = tid; w < kHistMax / 2; w += kFT) lds32[w] = 0u;   // C16
             __syncthreads();
             if (tid == 0 && hn > kHistMax) atomicOr(&sh.flags, kHdrError);   // callers promise hn <= max_history
             for_history([&](int32_t t) {
@@ -372,40 +373,48 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) { pref[4 * tid + k] = uint16_t(ex); ex += c4[k]; }
             __syncthreads();
-            walk_words([&](uint32_t rank, int off) { lds32[rank] = uint32_t(off) << 15; });
-            __syncthreads();
+            // u16 occurrence counts by rank, C16 = [0, 64 KiB) (a count reaches at
+            // most kHistMax = 32,768: no carry between the packed halves)
             for_history([&](int32_t t) {   // (L2 hits now)
                 if (t < h0 || t >= h1) return;
                 const int off = t - h0, w = off >> 5;
                 const uint32_t rank = pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
-                // 15-bit count field: the 32,768th occurrence (a history of one
-                // repeated token) carries out of it; undo the carry and note the rank
-                const uint32_t old = atomicAdd(&lds32[rank], 1u);
-                if ((old & 0x7fffu) == 0x7fffu) { atomicSub(&lds32[rank], 1u); sh.big_rank = rank; }
+                atomicAdd(&lds32[rank >> 1], (rank & 1u) ? 0x10000u : 1u);
             });
-            __syncthreads();
-            const uint32_t big_rank = sh.big_rank;
-            // gathers in batches of kGB ranks per thread (offsets from LDS), then
-            // the counts; batches past the last rank are skipped (n_flag is uniform)
-            constexpr int kGB = 8;
+            // the history tokens' logits by rank, P16 = [64 KiB, 128 KiB), written by
+            // the threads holding them (a vector's history tokens have consecutive ranks)
+            uint16_t* P16 = reinterpret_cast<uint16_t*>(lds + 65536);
+            auto rank_of = [&](int off) -> uint32_t {
+                const int w = off >> 5;
+                return pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
+            };
 #pragma unroll
-            for (int bt = 0; bt < kDR; bt += kGB) {
-                if (uint32_t(bt) * kFT >= n_flag) break;
-                uint32_t g[kGB];
+            for (int i = 0; i < kFV; ++i) {
+                const uint32_t fl = vflags(i);
+                if (fl) {
+                    const uint32_t r0 = rank_of(head + (i * kFT + tid) * 8);
+                    const uint32_t w4[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
 #pragma unroll
-                for (int u = 0; u < kGB; ++u) {   // unused slots load nothing (the half may be empty)
-                    const uint32_t r = uint32_t(bt + u) * kFT + tid;
-                    g[u] = r < n_flag ? uint32_t(base16[lds32[r] >> 15]) : 0u;
+                    for (int j = 0; j < 8; ++j)
+                        if ((fl >> j) & 1u)
+                            P16[r0 + __builtin_popcount(fl & ((1u << j) - 1u))] =
+                                uint16_t((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
                 }
+            }
+            if (fl_head) P16[rank_of(tid)] = uint16_t(hbits);
+            if (fl_tail) P16[rank_of(head + nvec * 8 + tid)] = uint16_t(tbits);
+            __syncthreads();
+            // penalized, rank k * kFT + tid into slot k (ranks past n_flag skipped:
+            // n_flag is uniform)
 #pragma unroll
-                for (int u = 0; u < kGB; ++u) {
-                    const int k = bt + u;
-                    const uint32_t r = uint32_t(k) * kFT + tid;
-                    if (r < n_flag) {
-                        const uint32_t c = r == big_rank ? 32768u : (lds32[r] & 0x7fffu);
-                        const uint32_t pb = Elem<DT>::finite_bits(g[u]) ? penalize_bits<DT>(g[u], c, p) & 0xffffu : g[u];
-                        dpen[k >> 1] |= pb << (16 * (k & 1));
-                    }
+            for (int k = 0; k < kDR; ++k) {
+                const uint32_t r = uint32_t(k) * kFT + tid;
+                if (uint32_t(k) * kFT >= n_flag) break;
+                if (r < n_flag) {
+                    const uint32_t bits = P16[r];
+                    const uint32_t c = (lds32[r >> 1] >> (16 * (r & 1u))) & 0xffffu;
+                    const uint32_t pb = Elem<DT>::finite_bits(bits) ? penalize_bits<DT>(bits, c, p) & 0xffffu : bits;
+                    dpen[r] = uint16_t(pb);
                 }
             }
             __syncthreads();   // entries read before the histogram overwrites them
@@ -421,14 +430,16 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             uint32_t* ovf_cnt = ovf_tok + kOvfMax;
             // kHB history entries per thread per round, all loads issued before any
             // is consumed (clamped indices keep them branch-free).
-            const int64_t hlast = hn - 1;
-            for (int64_t base = 0; base < hn; base += int64_t(kFT) * kHB) {
+            // (32-bit offsets, one VGPR per load; a row's history is < 2^31 tokens)
+            const int hlast = int(min(hn, int64_t(0x7fffffff))) - 1;
+            if (tid == 0 && hn > 0x7fffffff) atomicOr(&sh.flags, kHdrError);
+            for (int base = 0; base <= hlast; base += kFT * kHB) {
                 int32_t t[kHB];
 #pragma unroll
-                for (int j = 0; j < kHB; ++j) t[j] = hist[min(base + int64_t(j) * kFT + tid, hlast)];
+                for (int j = 0; j < kHB; ++j) t[j] = hist[min(base + j * kFT + tid, hlast)];
 #pragma unroll
                 for (int j = 0; j < kHB; ++j) {
-                    if (base + int64_t(j) * kFT + tid > hlast) continue;
+                    if (base + j * kFT + tid > hlast) continue;
                     const int32_t tk = t[j];
                     if (tk < 0 || tk >= V) { atomicOr(&sh.flags, kHdrBadHistory); continue; }
                     if (tk < h0 || tk >= h1) continue;
@@ -454,7 +465,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             if (n_ovf) {
                 for (uint32_t k = tid; k < n_ovf; k += kFT) ovf_cnt[k] = 0u;
                 __syncthreads();
-                for (int64_t i = tid; i < hn; i += kFT) {
+                for (int i = tid; i <= hlast; i += kFT) {
                     const int32_t t = hist[i];
                     if (t < h0 || t >= h1) continue;
                     for (uint32_t k = 0; k < n_ovf; ++k)
@@ -549,9 +560,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     if (tid < tail) hist_key(key16(tbits), fl_tail);
     if constexpr (kDense) {
         // the history tokens, penalized
-#pragma unroll
-        for (int k = 0; k < kDR; ++k)
-            if (uint32_t(k) * kFT + tid < n_flag) hist_key(key16(dense_pen(k)), false);
+        for (uint32_t r = tid; r < n_flag; r += kFT) hist_key(key16(dpen[r]), false);
     }
     __syncthreads();
     if (tid == 0) {   // -0 counts as +0 (key 0x7fff is only ever -0)
@@ -957,11 +966,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     uint16_t* P = reinterpret_cast<uint16_t*>(lds + kOffP);
     if constexpr (kDense) {
         if (pen) {
-#pragma unroll
-            for (int k = 0; k < kDR; ++k) {
-                const uint32_t r = uint32_t(k) * kFT + tid;
-                if (r < n_flag) P[r] = uint16_t(dense_pen(k));
-            }
+            for (uint32_t r = tid; r < n_flag; r += kFT) P[r] = dpen[r];
             __syncthreads();
         }
     }
@@ -1161,7 +1166,8 @@ bool full_supported(int dtype, int vocabulary, int64_t stride) {
 
 size_t full_workspace(int rows) {
     return align_up(size_t(rows) * sizeof(PairBarrier), 256) + align_up(size_t(rows) * 2 * sizeof(HalfSummary), 256) +
-           align_up(size_t(rows) * 2 * kListMax * 4, 256) + align_up(size_t(rows) * sizeof(RowBoundary), 256) + 256;
+           align_up(size_t(rows) * 2 * kListMax * 4, 256) + align_up(size_t(rows) * sizeof(RowBoundary), 256) +
+           align_up(size_t(rows) * 2 * kHistMax * 2, 256) + 256;
 }
 
 vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream) {
@@ -1172,6 +1178,7 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.summaries = c.take<HalfSummary>(size_t(s.rows) * 2);
     a.lists = c.take<uint32_t>(size_t(s.rows) * 2 * kListMax);
     a.bounds = c.take<RowBoundary>(size_t(s.rows));
+    a.dense = c.take<uint16_t>(size_t(s.rows) * 2 * kHistMax);
     if (!c.ok) return VI_ERR_WORKSPACE;
     a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary;
     a.half_len = (((s.vocabulary + 1) / 2) + 63) / 64 * 64;
