@@ -119,6 +119,9 @@ constexpr int kOffBmap = 131072;
 constexpr int kOffPref = kOffBmap + 4 * (kBmapWords + 4);
 constexpr int kLdsDense = kOffPref + 2 * kBmapWords;
 constexpr int kOffP = 4 * kFT;            // D: penalized history bits by rank (u16), after fmask
+constexpr int kOffML = kOffP + 2 * kHistMax;   // D: history tokens matching the drawn key
+constexpr int kMatchMax = 2048;
+static_assert(kOffML + 4 * kMatchMax <= 131072, "owner LDS");
 constexpr int kLdsGeneral = 131072 + 8 * kOvfMax;
 static_assert(kOffDecEnd <= 131072 && kOffDM % 8 == 0 && kOffPM % 8 == 0 && kOffWW % 8 == 0 && kOffWM % 8 == 0, "LDS map");
 static_assert(kHistMax / 2 * 4 <= 131072, "dense counts");
@@ -132,7 +135,7 @@ struct Shared {
     uint32_t rank, pn_take, n_sup, slot, slot_rank, ctot;
     double s_n, draw_u;
     uint32_t slot_tot[kFV + 2];
-    uint32_t n_sum, n_fin, wcount[kFW];
+    uint32_t n_sum, n_fin, n_match, wcount[kFW];
     uint32_t first[kCoarse], bend[kCoarse];   // this half's list slots of each coarse bin
 };
 
@@ -267,7 +270,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
         for (int i = 0; i < kFV; ++i)
             if (i >= i0 && i < i1)
-                d[i] = nvec > 0 ? load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
+                d[i] = nvec > 0 ? load16_cached(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
     };
     load_vectors(0, kFV);
     uint32_t hbits = tid < head ? uint32_t(base16[tid]) : 0u;
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // so the raw bits are what is wanted), which frees the registers the row
     // occupied while streaming; the general path kept it, penalized, in d[].
     auto row_vec = [&](int i) -> uint4 {
-        if constexpr (kDense) return nvec > 0 ? load16(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
+        if constexpr (kDense) return nvec > 0 ? load16_cached(vbase + size_t(min(i * kFT + tid, vlast)) * 16) : make_uint4(0, 0, 0, 0);
         else return d[i];
     };
 
@@ -961,6 +964,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
     }
     if (tid < kFV + 2) sh.slot_tot[tid] = 0u;
+    if (tid == 0) sh.n_match = 0u;
     __syncthreads();
     // dense path: penalized history bits by rank into LDS (the merge region is free)
     uint16_t* P = reinterpret_cast<uint16_t*>(lds + kOffP);
@@ -989,12 +993,12 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         wave_add(0, c_head);
         uint32_t vm[kFV / 4] = {0u, 0u, 0u, 0u};   // candidate masks of the 16 vector slots
 #pragma unroll
-        for (int i0 = 0; i0 < kFV; i0 += kFV / 2) {   // 8 vectors in flight
-            uint4 rv[kFV / 2];
+        for (int i0 = 0; i0 < kFV; i0 += kFV) {   // all 16 vectors in flight
+            uint4 rv[kFV];
 #pragma unroll
-            for (int u = 0; u < kFV / 2; ++u) rv[u] = row_vec(i0 + u);
+            for (int u = 0; u < kFV; ++u) rv[u] = row_vec(i0 + u);
 #pragma unroll
-            for (int u = 0; u < kFV / 2; ++u) {
+            for (int u = 0; u < kFV; ++u) {
                 const int i = i0 + u;
                 const uint32_t m = i * kFT + tid < nvec ? match_mask8<DT>(rv[u], r_key) & ~vflags(i) : 0u;
                 vm[i >> 2] |= m << (8 * (i & 3));
@@ -1012,13 +1016,33 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             *j = rel & 7;
             return 1 + v / kFT;
         };
-        walk_words([&](uint32_t rank, int off) {
-            const uint32_t pb = P[rank];
-            if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key) {
-                int o, j;
-                atomicAdd(&sh.slot_tot[place(off, &o, &j)], 1u);
+        // history tokens with key r_key: a scan of the rank-ordered penalized
+        // logits (their token offsets found by rank only for the rare matches),
+        // kept in a short list for the second step
+        uint32_t* ML = reinterpret_cast<uint32_t*>(lds + kOffML);
+        if constexpr (kDense) {
+            if (pen) {
+                const uint32_t* bmap = reinterpret_cast<const uint32_t*>(lds + kOffBmap);
+                const uint16_t* pref = reinterpret_cast<const uint16_t*>(lds + kOffPref);
+                for (uint32_t r = tid; r < n_flag; r += kFT) {
+                    const uint32_t pb = P[r];
+                    if (!(Elem<DT>::finite_bits(pb) && key16(pb) == r_key)) continue;
+                    int lo = 0, hi = kBmapWords;             // last word with pref <= r
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (uint32_t(pref[mid]) <= r) lo = mid + 1; else hi = mid;
+                    }
+                    const int w = lo - 1;
+                    uint32_t bits = bmap[w];
+                    for (uint32_t k = r - pref[w]; k > 0; --k) bits &= bits - 1u;
+                    const int off = w * 32 + __builtin_ctz(bits);
+                    int o, j;
+                    atomicAdd(&sh.slot_tot[place(off, &o, &j)], 1u);
+                    const uint32_t at = atomicAdd(&sh.n_match, 1u);
+                    if (at < uint32_t(kMatchMax)) ML[at] = uint32_t(off);
+                }
             }
-        });
+        }
         __syncthreads();
         if (tid == 0) {
             uint32_t acc = 0;
@@ -1029,11 +1053,18 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
         __syncthreads();
         const int s = int(sh.slot);
-        walk_words([&](uint32_t rank, int off) {
-            const uint32_t pb = P[rank];
-            int o, j;
-            if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key && place(off, &o, &j) == s) atomicOr(&fmask[o], 1u << j);
-        });
+        if (sh.n_match <= uint32_t(kMatchMax)) {
+            for (uint32_t m = tid; m < sh.n_match; m += kFT) {
+                int o, j;
+                if (place(int(ML[m]), &o, &j) == s) atomicOr(&fmask[o], 1u << j);
+            }
+        } else {   // (a list overflow: walk the bitmap)
+            walk_words([&](uint32_t rank, int off) {
+                const uint32_t pb = P[rank];
+                int o, j;
+                if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key && place(off, &o, &j) == s) atomicOr(&fmask[o], 1u << j);
+            });
+        }
         __syncthreads();
         uint32_t cm = fmask[tid];   // candidate bits (element j of this thread's group in slot s)
         if (s == 0) cm |= c_head;

@@ -102,6 +102,11 @@ __device__ __forceinline__ uint4 load16(const void* p) {
     const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Ordinary (cached) 16-byte load.
+__device__ __forceinline__ uint4 load16_cached(const void* p) {
+    const u32x4_t v = *static_cast<const u32x4_t*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // 16-bit order-preserving key of a sign-magnitude bf16 / fp16 pattern; -0 and
 // +0 share the key of +0.
