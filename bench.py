@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark: batched token sampling on one MI355X.
 
-Workload (the metric's shape): 128 rows x 248,320 bf16 logits,
+Workload (configuration 5, the headline metric's shape): 128 rows x 248,320 bf16 logits,
 near-flat N(0, 0.1), top_k off, top_p 0.95, repetition / presence / frequency
 penalties over 32,768-token int32 histories, an independent Philox stream per row.
 One step = one ``vi_sample_rows`` call over all 128 rows (all rows take the
@@ -85,7 +85,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}); rows are independent, "
-              "so N GPUs would run N copies of this step (see DESIGN.md, 'More than one GPU').", file=sys.stderr)
+              "so N GPUs would run N independent copies of this step.", file=sys.stderr)
         sys.exit(2)
 
     if args.calibrate_copy:

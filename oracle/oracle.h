@@ -7,7 +7,7 @@
  * reference file:line whose behaviour it restates.  Semantic extensions that the
  * reference does not implement (full-vocabulary filtering, repetition and
  * frequency penalties, Philox inverse-CDF draws, log-probs, device verification)
- * are marked EXTENSION; their pins are listed in DESIGN.md.
+ * are marked EXTENSION; the tests under tests/ name what pins each of them.
  */
 #ifndef VOIDINFER_ORACLE_H
 #define VOIDINFER_ORACLE_H

@@ -1,6 +1,8 @@
 """Test helpers: move numpy logit patterns to the device, compare against the oracle."""
 from __future__ import annotations
 
+import functools
+
 import numpy as np
 import torch
 
@@ -46,19 +48,23 @@ def xorshift_topk_case(rows: int, vocab: int, pattern: int) -> np.ndarray:
     return out.reshape(rows, vocab)
 
 
-def xorshift_topk_case_fast(rows: int, vocab: int, pattern: int) -> np.ndarray:
-    """Vectorised version of xorshift_topk_case (same bits); used for large vocabularies."""
-    n = rows * vocab
+@functools.lru_cache(maxsize=4)
+def xorshift_states(n: int) -> np.ndarray:
+    """The first n states of the reference generator's xorshift32 (seed 0x12345678)."""
     states = np.empty(n, dtype=np.uint32)
-    s = np.uint32(0x12345678)
-    # the sequence is inherently serial; generate in chunks with numpy scalars
-    st = int(s)
-    buf = states
-    for i in range(n):
+    st = 0x12345678
+    for i in range(n):  # inherently serial
         st ^= (st << 13) & 0xFFFFFFFF
         st ^= st >> 17
         st ^= (st << 5) & 0xFFFFFFFF
-        buf[i] = st
+        states[i] = st
+    states.setflags(write=False)
+    return states
+
+
+def xorshift_topk_case_fast(rows: int, vocab: int, pattern: int) -> np.ndarray:
+    """Vectorised version of xorshift_topk_case (same bits); used for large vocabularies."""
+    states = xorshift_states(rows * vocab)
     c = np.tile(np.arange(vocab), rows)
     bits = (states & 0x8000) | (states % 0x7C00)
     if pattern == 1:
@@ -83,3 +89,32 @@ def exempt_draw(margins_row: np.ndarray, tol: float = 1e-6) -> bool:
     """Token mismatch allowed when the drawn uniform or a truncation cut lies
     within `tol` of a cumulative-mass boundary."""
     return bool(margins_row[0] < tol or margins_row[1] < tol or margins_row[2] < tol)
+
+
+def greedy_reference_patterns(rows: int, vocab: int):
+    """The authored binary16 greedy patterns of the reference's device test
+    (test_exl3_greedy_device.cu:47-97): stride V + 7 padded with NaN, near-equal
+    pairs at the row ends and lane boundary 256, signed zeros, +-Inf / NaN."""
+    stride = vocab + 7
+    base = np.full((rows, stride), 0x7E00, dtype=np.uint16)
+    base[:, :vocab] = 0xBC00
+    yield base.copy()
+    for a, b in [(0x3C00, 0x3C01), (0x0001, 0x0002), (0x03FF, 0x0400), (0xFBFF, 0xFBFE), (0x7BFE, 0x7BFF)]:
+        near = base.copy()
+        near[:, :vocab] = a
+        near[:, vocab - 1] = b
+        if vocab > 256:
+            near[:, 256] = b
+        yield near
+    x = base.copy()
+    x[:, vocab - 1] = 0x0000
+    x[:, 0] = 0x8000
+    yield x.copy()
+    x[:, vocab - 1] = 0x3C00
+    if vocab > 256:
+        x[:, 256] = 0x3C00
+    yield x.copy()
+    for bad in (0x7C00, 0xFC00, 0x7E01):
+        inv = x.copy()
+        inv[rows - 1, vocab - 1] = bad
+        yield inv

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import to_dev
+from helpers import greedy_reference_patterns as reference_patterns, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -36,32 +36,6 @@ def check(orc, dev, bits: np.ndarray, dtype: int, vocab: int):
         if fin.any():
             masked = np.where(fin, vals[r], -np.inf)
             assert want["token"][r] == int(np.argmax(masked)) or (masked[want["token"][r]] == masked.max())
-
-
-def reference_patterns(rows: int, vocab: int):
-    stride = vocab + 7
-    base = np.full((rows, stride), 0x7E00, dtype=np.uint16)
-    base[:, :vocab] = 0xBC00
-    yield base.copy()
-    for a, b in [(0x3C00, 0x3C01), (0x0001, 0x0002), (0x03FF, 0x0400), (0xFBFF, 0xFBFE), (0x7BFE, 0x7BFF)]:
-        near = base.copy()
-        near[:, :vocab] = a
-        near[:, vocab - 1] = b
-        if vocab > 256:
-            near[:, 256] = b
-        yield near
-    x = base.copy()
-    x[:, vocab - 1] = 0x0000
-    x[:, 0] = 0x8000
-    yield x.copy()
-    x[:, vocab - 1] = 0x3C00
-    if vocab > 256:
-        x[:, 256] = 0x3C00
-    yield x.copy()
-    for bad in (0x7C00, 0xFC00, 0x7E01):
-        inv = x.copy()
-        inv[rows - 1, vocab - 1] = bad
-        yield inv
 
 
 @pytest.mark.parametrize("rows", [1, 8, 16])

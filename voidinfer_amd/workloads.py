@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the five BASELINE configurations (numpy, host side).
+"""Seeded synthetic inputs for the five benchmark configurations (numpy, host side).
 
 Logits are N(0, s) — s read as the standard deviation — plus a Zipf(1.1) bias
 over a seeded random permutation of token ids, scaled so the largest bias is
