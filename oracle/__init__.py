@@ -17,6 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 REF_LIB_PATH = HERE / "_ref" / "libvoidinfer_ref.so"
+REF_DIFF_PATH = HERE / "_ref" / "ref_diff"
 
 BF16, F16, F32 = 0, 1, 2
 
@@ -64,7 +65,7 @@ def build_ref() -> Path | None:
     ref = Path(os.environ.get("VOIDINFER_REFERENCE", "/root/reference"))
     if not (ref / "src" / "exl3" / "sampling_policy.h").exists():
         return None
-    subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF={ref}"], check=True)
+    subprocess.run(["make", "-s", "-C", str(HERE), "ref", "diff", f"REF={ref}"], check=True)
     return REF_LIB_PATH
 
 
