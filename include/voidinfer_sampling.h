@@ -163,6 +163,32 @@ vi_status vi_presence_truncate(int32_t* table, int vocabulary, int from, void* s
 vi_status vi_presence_record(int32_t* table, int vocabulary, int first,
                              const int64_t* tokens, size_t count, void* stream);
 
+/* ---- VeriCache row scores -----------------------------------------------------
+ * Scoring of a verified block: per row r, the exact choice and the gap, in
+ * logit units, by which the drafted token next[r] trails it (next < 0: gap 0).
+ *
+ * vi_row_scores replaces exact_row_score_kernel (src/exl3/text_model.cu:11393-11420):
+ * greedy[r] = argmax over values greater than -Inf (NaN and -Inf never win, +Inf
+ * can; lowest id on ties; vocabulary if none); gap[r] = max - logit(next[r]) for
+ * next in [0, vocabulary) other than the argmax, else 0.
+ *
+ * vi_sampled_scores replaces exl3_sampled_score_kernel
+ * (src/exl3/sampled_select.cuh:300-360): chosen[r] = the coupled draw of row r
+ * at key first_key + r (no drafted path); gap[r] = T x the perturbed-value gap
+ * when next[r] is in the support; outside it, infinite unless raising next's
+ * logit by `tolerance` (>= 0) brings it into the support, then measured against
+ * the best other support entry; temperature 0: max(0, best - penalized
+ * logit(next)).  next[r] >= vocabulary gives an infinite gap.  Rows unbounded. */
+size_t vi_row_scores_workspace_bytes(int rows, int vocabulary);
+vi_status vi_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                        const int64_t* next, int64_t* greedy, float* gap,
+                        void* workspace, size_t workspace_bytes, void* stream);
+size_t vi_sampled_scores_workspace_bytes(int rows, int vocabulary);
+vi_status vi_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
+                            const vi_device_sampling* cfg, int first_key, float tolerance,
+                            const int64_t* next, int64_t* chosen, float* gap,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- batched sampler (extended semantics) ----------------------------------
  * New batched entry for many lanes (the reference's packet stops at 16 rows,
  * sampled_select.cuh:200-216): per-row temperature, top-k, top-p, min-p,

@@ -88,6 +88,8 @@ def lib() -> C.CDLL:
             "or_cpu_greedy": ([vp, i64], i64),
             "or_topk_rows": ([vp, i, i, i, i64, i, vp, vp, vp, vp], i),
             "or_sampled_packet": ([vp, i, i, i, i64, C.POINTER(DeviceSampling), i, vp, i, vp, i, u64, vp, vp], i),
+            "or_sampled_scores": ([vp, i, i, i, i64, C.POINTER(DeviceSampling), i, C.c_float, vp, vp, vp], i),
+            "or_row_scores": ([vp, i, i, i, i64, vp, vp, vp], i),
             "or_sample_rows": ([vp, i, i, i, i64, vp, vp, vp, vp, vp, vp, i64, vp, vp, i], i),
             "or_accept": ([vp, vp, i64, u32, d, d, C.POINTER(AcceptOutcome), vp], i),
             "or_outer_prefix": ([vp, vp, i, vp, i, vp, vp, vp, vp, vp], i),
@@ -184,6 +186,37 @@ def sampled_packet(scores: np.ndarray, dtype: int, temperature: float, top_k: in
     if st:
         raise ValueError("oracle packet: invalid arguments")
     return out, detail
+
+
+def sampled_scores(scores: np.ndarray, dtype: int, temperature: float, top_k: int, top_p: float, min_p: float,
+                   seed: int, next_tokens, first_key: int = 0, tolerance: float = 0.0, presence_penalty: float = 0.0,
+                   first_occurrence: np.ndarray | None = None):
+    """VeriCache sampled row scores: (chosen int64[rows], gap float32[rows])."""
+    rows, width = scores.shape
+    fo = None if first_occurrence is None else np.ascontiguousarray(first_occurrence, dtype=np.int32)
+    cfg = DeviceSampling(temperature, top_k, top_p, min_p, seed, presence_penalty, 0,
+                         fo.ctypes.data if fo is not None else None)
+    nxt = np.ascontiguousarray(next_tokens, dtype=np.int64)
+    chosen = np.zeros(rows, dtype=np.int64)
+    gap = np.zeros(rows, dtype=np.float32)
+    st = lib().or_sampled_scores(_p(np.ascontiguousarray(scores)), dtype, rows, width, width, C.byref(cfg),
+                                 first_key, tolerance, _p(nxt), _p(chosen), _p(gap))
+    if st:
+        raise ValueError("oracle sampled scores: invalid arguments")
+    return chosen, gap
+
+
+def row_scores(logits: np.ndarray, dtype: int, next_tokens):
+    """VeriCache exact row scores: (greedy int64[rows], gap float32[rows])."""
+    rows, width = logits.shape
+    nxt = np.ascontiguousarray(next_tokens, dtype=np.int64)
+    greedy = np.zeros(rows, dtype=np.int64)
+    gap = np.zeros(rows, dtype=np.float32)
+    st = lib().or_row_scores(_p(np.ascontiguousarray(logits)), dtype, rows, width, width, _p(nxt), _p(greedy),
+                             _p(gap))
+    if st:
+        raise ValueError("oracle row scores: invalid arguments")
+    return greedy, gap
 
 
 def sample_rows(logits: np.ndarray, dtype: int, params: np.ndarray, histories: np.ndarray | None = None,

@@ -373,10 +373,90 @@ int or_topk_rows(const void* logits, int dtype, int rows, int vocabulary, int64_
     return VI_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// One row of the coupled sampler (sampled_select.cuh:79-116, 121-193): the
+// presence-penalized top-cap candidates, the truncated support and the
+// perturbed values.  The reference compiles with nvcc's default --fmad=true;
+// the two multiply-add expressions of the draw (cand*inv_temp - m,
+// cand*inv_temp + G) are therefore fused, as here.
+struct PacketRow {
+    int cap = 0, support = 1, selected = 0;
+    float val[20], value[20] = {}, prob[20] = {}, sum = 0.0f;
+    int idx[20];
+    uint32_t bad = 0;
+};
+
+int packet_cap(const vi_device_sampling& cfg) {
+    int cap = 20;
+    if (cfg.top_k > 0 && cfg.top_k < cap) cap = cfg.top_k;
+    return cap;
+}
+
+bool packet_seen(const vi_device_sampling& cfg, int key, const int* path, int path_count, int v) {
+    bool seen = cfg.first_occurrence && cfg.first_occurrence[v] < key;
+    for (int i = 0; i < path_count && !seen; ++i) seen = path[i] == v;
+    return seen;
+}
+
+// exl3_sampled_support (sampled_select.cuh:283-298).
+int packet_support(const float* value, int cap, const vi_device_sampling& cfg, float* prob, float* sum_out) {
+    const float inv_temp = 1.0f / cfg.temperature;
+    const float m = value[0] * inv_temp;
+    float sum = 0.0f;
+    for (int j = 0; j < cap; ++j) { prob[j] = std::exp(std::fmaf(value[j], inv_temp, -m)); sum += prob[j]; }
+    const float min_p_thresh = cfg.min_p > 0.0f ? cfg.min_p * prob[0] : -1.0f;
+    const bool top_p_active = cfg.top_p < 1.0f;
+    const float top_p_target = cfg.top_p * sum;
+    float cum = 0.0f; int support = 0;
+    for (int j = 0; j < cap; ++j) {
+        if (min_p_thresh >= 0.0f && prob[j] < min_p_thresh) break;
+        cum += prob[j]; support = j + 1;
+        if (top_p_active && cum >= top_p_target) break;
+    }
+    if (sum_out) *sum_out = sum;
+    return support < 1 ? 1 : support;
+}
+
+void packet_row(const void* row, int dtype, int vocabulary, const vi_device_sampling& cfg, int key,
+                const int* path, int path_count, PacketRow& o) {
+    o = PacketRow{};
+    o.cap = std::min(packet_cap(cfg), vocabulary);
+    for (int j = 0; j < 20; ++j) { o.val[j] = -kInf; o.idx[j] = 0x7fffffff; }
+    const int cap = o.cap;
+    for (int v = 0; v < vocabulary; ++v) {
+        float x = element(row, dtype, v);
+        if (!std::isfinite(x)) { o.bad = 1; continue; }
+        if (cfg.presence_penalty != 0.0f && packet_seen(cfg, key, path, path_count, v)) x -= cfg.presence_penalty;
+        if (!better(x, v, o.val[cap - 1], o.idx[cap - 1])) continue;
+        int pos = cap - 1;
+        while (pos > 0 && better(x, v, o.val[pos - 1], o.idx[pos - 1])) {
+            o.val[pos] = o.val[pos - 1]; o.idx[pos] = o.idx[pos - 1]; --pos;
+        }
+        o.val[pos] = x; o.idx[pos] = v;
+    }
+    if (!(cfg.temperature > 0.0f)) {
+        o.value[0] = o.val[0];
+        return;
+    }
+    const float inv_temp = 1.0f / cfg.temperature;
+    o.support = packet_support(o.val, cap, cfg, o.prob, &o.sum);
+    int best = 0;
+    for (int j = 0; j < o.support; ++j) {
+        o.value[j] = std::fmaf(o.val[j], inv_temp, or_gumbel(cfg.seed, key, o.idx[j]));
+        if (o.value[j] > o.value[best]) best = j;
+    }
+    o.selected = best;
+}
+
+}  // namespace
+
+extern "C" {
+
 // exl3_launch_sampled_packet with one-CTA semantics (sampled_select.cuh:79-116,
-// 121-193, 218-225, 283-298, 362-377).  The reference compiles with nvcc's
-// default --fmad=true; the two multiply-add expressions of the draw
-// (cand*inv_temp - m, cand*inv_temp + G) are therefore fused, as here.
+// 121-193, 218-225, 283-298, 362-377).
 int or_sampled_packet(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
                       const vi_device_sampling* cfg, int first_key, const int32_t* depths,
                       int n_depths, const int32_t* inputs, int n_inputs, uint64_t serial,
@@ -386,64 +466,104 @@ int or_sampled_packet(const void* scores, int dtype, int rows, int vocabulary, i
     const bool tree = n_depths == rows && depths;
     for (int r = 0; r < rows; ++r) depth[r] = tree ? depths[r] : r;
     if (n_inputs == rows && inputs) { input_count = rows; for (int r = 0; r < rows; ++r) input[r] = inputs[r]; }
-    int cap = 20;
-    if (cfg->top_k > 0 && cfg->top_k < cap) cap = cfg->top_k;
-    if (vocabulary < cap) cap = vocabulary;
     for (int r = 0; r < rows; ++r) {
-        const void* row = row_ptr(scores, dtype, r, row_stride);
         const int key = first_key + depth[r];
         int path[17]; int path_count = 0;
         if (input_count > r) {
             for (int j = 0; j < depth[r] && j < input_count; ++j) path[path_count++] = input[j];
             path[path_count++] = input[r];
         }
-        float val[20]; int idx[20];
-        for (int j = 0; j < 20; ++j) { val[j] = -kInf; idx[j] = 0x7fffffff; }
-        uint32_t bad = 0;
-        for (int v = 0; v < vocabulary; ++v) {
-            float x = element(row, dtype, v);
-            if (!std::isfinite(x)) { bad = 1; continue; }
-            if (cfg->presence_penalty != 0.0f) {
-                bool seen = cfg->first_occurrence && cfg->first_occurrence[v] < key;
-                for (int i = 0; i < path_count && !seen; ++i) seen = path[i] == v;
-                if (seen) x -= cfg->presence_penalty;
-            }
-            if (!better(x, v, val[cap - 1], idx[cap - 1])) continue;
-            int pos = cap - 1;
-            while (pos > 0 && better(x, v, val[pos - 1], idx[pos - 1])) { val[pos] = val[pos - 1]; idx[pos] = idx[pos - 1]; --pos; }
-            val[pos] = x; idx[pos] = v;
-        }
-        float value[20] = {}, prob[20] = {}; float sum = 0.0f;
-        int support = 1, selected = 0;
-        if (!(cfg->temperature > 0.0f)) {
-            value[0] = val[0];
-        } else {
-            const float inv_temp = 1.0f / cfg->temperature;
-            const float m = val[0] * inv_temp;
-            for (int j = 0; j < cap; ++j) { prob[j] = std::exp(std::fmaf(val[j], inv_temp, -m)); sum += prob[j]; }
-            const float min_p_thresh = cfg->min_p > 0.0f ? cfg->min_p * prob[0] : -1.0f;
-            const bool top_p_active = cfg->top_p < 1.0f;
-            const float top_p_target = cfg->top_p * sum;
-            float cum = 0.0f; support = 0;
-            for (int j = 0; j < cap; ++j) {
-                if (min_p_thresh >= 0.0f && prob[j] < min_p_thresh) break;
-                cum += prob[j]; support = j + 1;
-                if (top_p_active && cum >= top_p_target) break;
-            }
-            if (support < 1) support = 1;
-            int best = 0;
-            for (int j = 0; j < support; ++j) {
-                value[j] = std::fmaf(val[j], inv_temp, or_gumbel(cfg->seed, key, idx[j]));
-                if (value[j] > value[best]) best = j;
-            }
-            selected = best;
-        }
-        out[r].serial = serial; out[r].token = idx[selected]; out[r].nonfinite = bad;
+        PacketRow o;
+        packet_row(row_ptr(scores, dtype, r, row_stride), dtype, vocabulary, *cfg, key, path, path_count, o);
+        out[r].serial = serial; out[r].token = o.idx[o.selected]; out[r].nonfinite = o.bad;
         if (detail) {
             or_packet_detail& d = detail[r];
-            d.cap = cap; d.support = support; d.selected = selected; d.key = key; d.sum = sum;
-            for (int j = 0; j < 20; ++j) { d.cand_val[j] = val[j]; d.cand_idx[j] = idx[j]; d.value[j] = value[j]; d.prob[j] = prob[j]; }
+            d.cap = o.cap; d.support = o.support; d.selected = o.selected; d.key = key; d.sum = o.sum;
+            for (int j = 0; j < 20; ++j) {
+                d.cand_val[j] = o.val[j]; d.cand_idx[j] = o.idx[j]; d.value[j] = o.value[j]; d.prob[j] = o.prob[j];
+            }
         }
+    }
+    return VI_OK;
+}
+
+// exl3_sampled_score_kernel (sampled_select.cuh:300-360): row r chooses key
+// first_key + r with no drafted path; gap in logit units by which next[r]
+// trails the choice.  A next[r] outside [0, vocabulary) gets an infinite gap
+// (the reference reads past the row there).
+int or_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
+                      const vi_device_sampling* cfg, int first_key, float tolerance, const int64_t* next,
+                      int64_t* chosen, float* gap) {
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !cfg || !next || !chosen || !gap)
+        return VI_ERR_INVALID;
+    for (int r = 0; r < rows; ++r) {
+        const void* row = row_ptr(scores, dtype, r, row_stride);
+        const int key = first_key + r;
+        PacketRow o;
+        packet_row(row, dtype, vocabulary, *cfg, key, nullptr, 0, o);
+        const int token = o.idx[o.selected];
+        chosen[r] = token;
+        const int64_t want = next[r];
+        float g = 0.0f;
+        if (want >= vocabulary && want != token) {
+            g = kInf;
+        } else if (want >= 0 && want != token && !(cfg->temperature > 0.0f)) {
+            float own = element(row, dtype, int(want));
+            if (cfg->presence_penalty != 0.0f && packet_seen(*cfg, key, nullptr, 0, int(want)))
+                own -= cfg->presence_penalty;
+            g = std::fmax(0.0f, o.val[o.selected] - own);
+        } else if (want >= 0 && want != token) {
+            g = kInf;
+            const int cap = packet_cap(*cfg);
+            int rank = -1;
+            for (int j = 0; j < cap; ++j) if (o.idx[j] == want) { rank = j; break; }
+            if (rank >= 0 && rank < o.support) {
+                g = (o.value[o.selected] - o.value[rank]) * cfg->temperature;
+            } else if (rank >= 0 && tolerance > 0.0f) {
+                float value[20]; int index[20];
+                const float boosted = o.val[rank] + tolerance;
+                int at = 0;
+                for (int j = 0; j < cap; ++j) {
+                    if (j == rank) continue;
+                    value[at] = o.val[j]; index[at] = o.idx[j]; ++at;
+                }
+                int pos = at;
+                while (pos > 0 && boosted > value[pos - 1]) { value[pos] = value[pos - 1]; index[pos] = index[pos - 1]; --pos; }
+                value[pos] = boosted; index[pos] = int(want);
+                float prob[20];
+                const int support = packet_support(value, cap, *cfg, prob, nullptr);
+                if (pos < support) {
+                    const float inv_temp = 1.0f / cfg->temperature;
+                    float best = -kInf;
+                    for (int j = 0; j < support; ++j)
+                        if (j != pos) best = std::fmax(best, std::fmaf(value[j], inv_temp, or_gumbel(cfg->seed, key, index[j])));
+                    const float own = std::fmaf(o.val[rank], inv_temp, or_gumbel(cfg->seed, key, int(want)));
+                    g = std::fmax(0.0f, (best - own) * cfg->temperature);
+                }
+            }
+        }
+        gap[r] = g;
+    }
+    return VI_OK;
+}
+
+// exact_row_score_kernel (text_model.cu:11393-11420): argmax over the values
+// that compare greater than -Inf (NaN and -Inf never win, +Inf can), lowest
+// index on ties, index = vocabulary when none; gap = max - logit(next) for a
+// next in [0, vocabulary) other than the argmax, else 0.
+int or_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                  const int64_t* next, int64_t* greedy, float* gap) {
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !next || !greedy || !gap) return VI_ERR_INVALID;
+    for (int r = 0; r < rows; ++r) {
+        const void* row = row_ptr(logits, dtype, r, row_stride);
+        float value = -kInf; int index = vocabulary;
+        for (int i = 0; i < vocabulary; ++i) {
+            const float v = element(row, dtype, i);
+            if (v > value) { value = v; index = i; }
+        }
+        greedy[r] = index;
+        const int64_t t = next[r];
+        gap[r] = (t >= 0 && t < vocabulary && t != index) ? value - element(row, dtype, int(t)) : 0.0f;
     }
     return VI_OK;
 }

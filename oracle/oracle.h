@@ -68,6 +68,16 @@ int or_sampled_packet(const void* scores, int dtype, int rows, int vocabulary, i
                       int n_depths, const int32_t* inputs, int n_inputs, uint64_t serial,
                       vi_greedy_row* out, or_packet_detail* detail);
 
+/* VeriCache sampled row scores (exl3_sampled_score_kernel,
+ * sampled_select.cuh:300-360): chosen token and gap of next[r] in logit units;
+ * row r uses key first_key + r.  cfg->first_occurrence is a HOST pointer. */
+int or_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
+                      const vi_device_sampling* cfg, int first_key, float tolerance, const int64_t* next,
+                      int64_t* chosen, float* gap);
+/* VeriCache exact row scores (exact_row_score_kernel, text_model.cu:11393-11420). */
+int or_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                  const int64_t* next, int64_t* greedy, float* gap);
+
 /* EXTENSION: batched sampler.  margins (optional, 4 doubles per row):
  * [0] draw margin  |cum - u*S_n| / S_n at the chosen token's boundaries,
  * [1] top-p margin |cum - top_p*S_cap| / S_cap at the cut,

@@ -505,3 +505,117 @@ def test_verify_sampled_preserves_target_law(orc):
     assert np.all(flg & 4 == 0)
     counts = np.bincount(com[:, 0], minlength=v)
     assert chi2_pvalue(counts, p) > 1e-4
+
+
+# ---------------------------------------------------------------- VeriCache row scores
+
+def test_row_scores_closed_form(orc):
+    """exact_row_score_kernel: argmax over values greater than -Inf (NaN and -Inf
+    never win, +Inf can), lowest index; gap = max - logit(next)."""
+    rng = np.random.default_rng(61)
+    for dtype in (BF16, F16, F32):
+        v = 777
+        bits = random_bits(rng, (8, v), dtype, 2.0)
+        inf_, ninf, nan = {F32: (np.float32(np.inf), np.float32(-np.inf), np.float32(np.nan)),
+                           F16: (0x7C00, 0xFC00, 0x7E00), BF16: (0x7F80, 0xFF80, 0x7FC0)}[dtype]
+        bits[1, [5, 300]] = inf_               # +Inf wins, first one
+        bits[2, ::3] = nan                     # NaN never wins
+        bits[3, :] = ninf                      # nothing beats -Inf: index V
+        bits[4, :] = nan
+        x = decode(bits, dtype)
+        nxt = np.array([-1, 300, 7, 3, 4, v, 0, 0], dtype=np.int64)
+        cand = x > -np.inf
+        masked = np.where(cand, x, -np.inf)
+        want_idx = np.where(cand.any(axis=1), masked.argmax(axis=1), v)
+        nxt[6] = want_idx[6]                    # next == argmax: gap 0
+        nxt[7] = (want_idx[7] + 1) % v
+        greedy, gap = orc.row_scores(bits, dtype, nxt)
+        assert np.array_equal(greedy, want_idx)
+        with np.errstate(invalid="ignore"):
+            for r in range(8):
+                t = nxt[r]
+                best = masked[r, want_idx[r]] if want_idx[r] < v else np.float32(-np.inf)
+                exp = np.float32(best) - x[r, t] if (0 <= t < v and t != want_idx[r]) else np.float32(0)
+                assert (np.isnan(exp) and np.isnan(gap[r])) or gap[r] == exp, (dtype, r, gap[r], exp)
+
+
+def fma32(a, b, c):
+    """fp32 fused multiply-add through fp64 (a*b is exact in fp64)."""
+    return np.float32(np.float64(np.float32(a)) * np.float64(np.float32(b)) + np.float64(np.float32(c)))
+
+
+def test_sampled_scores_trivial_and_greedy_cases(orc):
+    rng = np.random.default_rng(67)
+    rows, v = 6, 400
+    bits = random_bits(rng, (rows, v), F16, 1.0)
+    x = decode(bits, F16)
+    # temperature 0 with presence: chosen = penalized argmax, gap = best - penalized logit
+    fo = np.full(v, 2**31 - 1, dtype=np.int32)
+    fo[np.argmax(x, axis=1)] = 2                       # seen before keys >= 3
+    nxt = np.argsort(-x, axis=1)[:, 3].astype(np.int64)
+    fo[nxt[::2]] = 0                                   # some next tokens carry the penalty too
+    chosen, gap = orc.sampled_scores(bits, F16, 0.0, 0, 1.0, 0.0, 9, nxt, first_key=1, presence_penalty=0.7,
+                                     first_occurrence=fo)
+    for r in range(rows):
+        key = 1 + r
+        pen = np.where(fo < key, x[r] - np.float32(0.7), x[r]).astype(np.float32)
+        assert chosen[r] == np.argmax(pen)
+        assert gap[r] == max(np.float32(0), pen[chosen[r]] - pen[nxt[r]])
+    # next == chosen or -1: gap 0; next >= V: infinite
+    chosen, _ = orc.sampled_scores(bits, F16, 0.8, 0, 0.9, 0.0, 9, np.zeros(rows), first_key=5)
+    _, gap = orc.sampled_scores(bits, F16, 0.8, 0, 0.9, 0.0, 9, chosen, first_key=5)
+    assert np.all(gap == 0)
+    _, gap = orc.sampled_scores(bits, F16, 0.8, 0, 0.9, 0.0, 9, np.full(rows, -1), first_key=5)
+    assert np.all(gap == 0)
+    _, gap = orc.sampled_scores(bits, F16, 0.8, 0, 0.9, 0.0, 9, np.full(rows, v), first_key=5)
+    assert np.all(np.isinf(gap))
+
+
+@pytest.mark.parametrize("tolerance", [0.0, 0.05, 0.5, 3.0])
+def test_sampled_scores_against_the_packet_and_a_boosted_row(orc, tolerance):
+    """In-support next: T times the perturbed-value gap of the coupled draw.
+    Just outside the support: re-running the coupled sampler on the row with
+    next's logit raised by `tolerance` decides admission, and the gap is
+    measured against the best other support entry of that run."""
+    rng = np.random.default_rng(71)
+    v, temperature, top_p, min_p, seed = 300, 0.8, 0.85, 0.02, 1234
+    checked_out, checked_in = 0, 0
+    for trial in range(40):
+        x = (rng.standard_normal((1, v)) * 1.5).astype(np.float32)
+        key = 10 + trial
+        out, det = orc.sampled_packet(x, F32, temperature, 0, top_p, min_p, seed=seed, first_key=key)
+        d = det[0]
+        sup, cap = int(d["support"]), int(d["cap"])
+        sel = int(d["selected"])
+        for rank in range(cap):
+            want = int(d["cand_idx"][rank])
+            chosen, gap = orc.sampled_scores(x, F32, temperature, 0, top_p, min_p, seed, [want], first_key=key,
+                                             tolerance=tolerance)
+            assert chosen[0] == out["token"][0]
+            if rank == sel:
+                assert gap[0] == 0
+            elif rank < sup:
+                exp = (np.float32(d["value"][sel]) - np.float32(d["value"][rank])) * np.float32(temperature)
+                assert gap[0] == np.float32(exp) and gap[0] >= 0
+                checked_in += 1
+            elif tolerance == 0.0:
+                assert np.isinf(gap[0])
+            else:
+                xb = x.copy()
+                xb[0, want] = np.float32(x[0, want] + np.float32(tolerance))
+                _, db = orc.sampled_packet(xb, F32, temperature, 0, top_p, min_p, seed=seed, first_key=key)
+                db = db[0]
+                ids = list(db["cand_idx"][: int(db["support"])])
+                if want not in ids:
+                    assert np.isinf(gap[0])
+                    continue
+                others = [db["value"][j] for j in range(int(db["support"])) if db["cand_idx"][j] != want]
+                best = max(others) if others else np.float32(-np.inf)
+                inv = np.float32(1.0) / np.float32(temperature)
+                own = fma32(x[0, want], inv, orc.gumbel(seed, key, want))
+                exp = max(np.float32(0), (np.float32(best) - own) * np.float32(temperature))
+                assert gap[0] == np.float32(exp), (trial, rank, gap[0], exp)
+                checked_out += 1
+    assert checked_in > 20
+    if tolerance > 0:
+        assert checked_out > 10

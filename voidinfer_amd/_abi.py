@@ -62,6 +62,11 @@ SIGNATURES = {
     "vi_sampled_packet_workspace_bytes": ([_i, _i], _sz),
     "vi_sampled_packet": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, _vp, _i, _vp, _i, _u64,
                            _vp, _vp, _sz, _vp], _i),
+    "vi_row_scores_workspace_bytes": ([_i, _i], _sz),
+    "vi_row_scores": ([_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _vp, _sz, _vp], _i),
+    "vi_sampled_scores_workspace_bytes": ([_i, _i], _sz),
+    "vi_sampled_scores": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, C.c_float, _vp, _vp, _vp, _vp,
+                           _sz, _vp], _i),
     "vi_presence_reset": ([_vp, _i, _vp], _i),
     "vi_presence_truncate": ([_vp, _i, _i, _vp], _i),
     "vi_presence_record": ([_vp, _i, _i, _vp, _sz, _vp], _i),
@@ -84,11 +89,15 @@ def load() -> C.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise ImportError(
-                f"{LIB_PATH} is missing: build it with `python -m voidinfer_amd.build` "
+                f"{LIB_PATH} is missing: build it with `python voidinfer_amd/build.py` "
                 "(there is no CPU fallback)")
         lib = C.CDLL(str(LIB_PATH))
         for name, (args, res) in SIGNATURES.items():
-            fn = getattr(lib, name)
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as e:
+                raise ImportError(f"{LIB_PATH} lacks {name}: it is older than its sources, rebuild it with "
+                                  "`python voidinfer_amd/build.py`") from e
             fn.argtypes = args
             fn.restype = res
         _lib = lib

@@ -1,8 +1,9 @@
 """Build the gfx950 sampling library in-tree.
 
-``python -m voidinfer_amd.build`` (or ``build()``) compiles every HIP source
+``python voidinfer_amd/build.py`` (or ``build()``) compiles every HIP source
 under ``voidinfer_amd/csrc`` with hipcc for gfx950 and links
-``voidinfer_amd/libvoidinfer_sampling.so``.  Objects go to ``_build/``.
+``voidinfer_amd/libvoidinfer_sampling.so``.  Objects go to ``_build/``.  Run it as a
+script (not ``-m``): importing the package loads the library this builds.
 """
 from __future__ import annotations
 

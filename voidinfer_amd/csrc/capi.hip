@@ -93,6 +93,38 @@ vi_status vi_sampled_packet(const void* scores, int dtype, int rows, int vocabul
                          workspace_bytes, as_stream(stream));
 }
 
+size_t vi_row_scores_workspace_bytes(int rows, int vocabulary) {
+    if (rows <= 0 || vocabulary <= 0) return 0;
+    return greedy_workspace(rows, vocabulary);
+}
+
+vi_status vi_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                        const int64_t* next, int64_t* greedy, float* gap, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    if (rows == 0) return VI_OK;
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !dtype_ok(dtype) || !logits || !next || !greedy ||
+        !gap)
+        return VI_ERR_INVALID;
+    return launch_row_scores(logits, dtype, rows, vocabulary, row_stride, next, greedy, gap, workspace,
+                             workspace_bytes, as_stream(stream));
+}
+
+size_t vi_sampled_scores_workspace_bytes(int rows, int vocabulary) {
+    if (rows <= 0 || vocabulary <= 0) return 0;
+    return topk_partials_bytes(rows, vocabulary);
+}
+
+vi_status vi_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
+                            const vi_device_sampling* cfg, int first_key, float tolerance, const int64_t* next,
+                            int64_t* chosen, float* gap, void* workspace, size_t workspace_bytes, void* stream) {
+    if (rows == 0) return VI_OK;
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !dtype_ok(dtype) || !scores || !cfg || !next ||
+        !chosen || !gap || !(tolerance >= 0.0f))
+        return VI_ERR_INVALID;
+    return launch_sampled_scores(scores, dtype, rows, vocabulary, row_stride, *cfg, first_key, tolerance, next, chosen,
+                                 gap, workspace, workspace_bytes, as_stream(stream));
+}
+
 vi_status vi_presence_reset(int32_t* table, int vocabulary, void* stream) {
     if (!table || vocabulary <= 0) return VI_ERR_INVALID;
     return launch_presence_reset(table, vocabulary, as_stream(stream));

@@ -11,6 +11,12 @@
 // with more than one slice the last workgroup of a row to arrive (self-resetting
 // arrival counter, as greedy_packet.cuh:139-246) reduces the slice partials in
 // slice order.  Roofline: HBM, V x sizeof(logit) bytes per row.
+//
+// Row-score variant (SCORE = true; exact_row_score_kernel,
+// src/exl3/text_model.cu:11393-11420, the VeriCache exact route): candidates
+// are the values that compare greater than -Inf (NaN and -Inf never win, +Inf
+// can), nothing is flagged, and the row's writer also emits the gap
+// max - logit(next[r]) for a next in [0, V) other than the argmax (else 0).
 #include "row_scan.h"
 #include "vi_internal.h"
 
@@ -30,10 +36,28 @@ __device__ __forceinline__ void greedy_combine(float& best, int& index, float ob
     if (ob > best || (ob == best && oi < index)) { best = ob; index = oi; }
 }
 
-template <int DT, bool VEC>
+// Writes row r's result (one thread).
+template <int DT, bool SCORE>
+__device__ __forceinline__ void greedy_write(const void* row, int r, int vocabulary, float best, int index, bool bad,
+                                             uint64_t serial, vi_greedy_row* out, const int64_t* next,
+                                             int64_t* greedy, float* gap) {
+    if constexpr (SCORE) {
+        greedy[r] = index;
+        const int64_t t = next[r];
+        float g = 0.0f;
+        if (t >= 0 && t < vocabulary && t != index)
+            g = best - Elem<DT>::decode(static_cast<const typename Elem<DT>::Bits*>(row)[t]);
+        gap[r] = g;
+    } else {
+        out[r].serial = serial; out[r].token = index; out[r].nonfinite = bad ? 1u : 0u;
+    }
+}
+
+template <int DT, bool VEC, bool SCORE>
 __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     const void* logits, int vocabulary, int64_t stride, int slice_len, uint64_t serial,
-    vi_greedy_row* out, GreedyPartial* partials, uint32_t* arrivals) {
+    vi_greedy_row* out, GreedyPartial* partials, uint32_t* arrivals, const int64_t* next, int64_t* greedy,
+    float* gap) {
     const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
     const void* row = static_cast<const unsigned char*>(logits) + size_t(r) * size_t(stride) * sizeof(typename Elem<DT>::Bits);
     const int begin = slice * slice_len, end = min(vocabulary, begin + slice_len);
@@ -43,7 +67,11 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     scan_slice<DT, VEC, kGreedyThreads>(row, begin, end, [&](uint32_t bits, int id, bool ok) {
         if (!ok) return;
         const float x = Elem<DT>::decode(bits);
-        if (!Elem<DT>::finite_bits(bits)) { bad = true; return; }
+        if constexpr (SCORE) {
+            if (!(x > -kInfF)) return;
+        } else {
+            if (!Elem<DT>::finite_bits(bits)) { bad = true; return; }
+        }
         if (x > best || (x == best && id < index)) { best = x; index = id; }
     });
 #pragma unroll
@@ -60,7 +88,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
         uint32_t b = 0;
         for (int w = 0; w < kGreedyThreads / kWave; ++w) { greedy_combine(best, index, s_best[w], s_index[w]); b |= s_bad[w]; }
         if (slices == 1) {
-            out[r].serial = serial; out[r].token = index; out[r].nonfinite = b;
+            greedy_write<DT, SCORE>(row, r, vocabulary, best, index, b != 0, serial, out, next, greedy, gap);
             return;
         }
         GreedyPartial& p = partials[size_t(r) * slices + slice];
@@ -84,7 +112,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     const bool any_bad = ballot(b != 0) != 0;
     if (lane == 0) {
         arrivals[r] = 0u;
-        out[r].serial = serial; out[r].token = index; out[r].nonfinite = any_bad ? 1u : 0u;
+        greedy_write<DT, SCORE>(row, r, vocabulary, best, index, any_bad, serial, out, next, greedy, gap);
     }
 }
 
@@ -106,9 +134,12 @@ size_t greedy_workspace(int rows, int vocabulary) {
     return align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256) + align_up(size_t(rows) * 4, 256);
 }
 
-vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
-                        uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
-                        hipStream_t stream) {
+namespace {
+
+template <bool SCORE>
+vi_status launch_greedy_kind(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                             uint64_t serial, vi_greedy_row* out, const int64_t* next, int64_t* greedy, float* gap,
+                             void* ws, size_t ws_bytes, hipStream_t stream) {
     const GreedyPlan p = greedy_plan(rows, vocabulary);
     GreedyPartial* partials = nullptr;
     uint32_t* arrivals = nullptr;
@@ -120,8 +151,9 @@ vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary,
     }
     const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && ((stride * elem_size(dtype)) % 16 == 0);
     const dim3 grid(p.slices, rows), block(kGreedyThreads);
-#define VI_GREEDY_LAUNCH(DT, V) \
-    hipLaunchKernelGGL((greedy_kernel<DT, V>), grid, block, 0, stream, logits, vocabulary, stride, p.slice_len, serial, out, partials, arrivals)
+#define VI_GREEDY_LAUNCH(DT, V)                                                                          \
+    hipLaunchKernelGGL((greedy_kernel<DT, V, SCORE>), grid, block, 0, stream, logits, vocabulary, stride, \
+                       p.slice_len, serial, out, partials, arrivals, next, greedy, gap)
     switch (dtype) {
         case VI_BF16: if (vec) VI_GREEDY_LAUNCH(VI_BF16, true); else VI_GREEDY_LAUNCH(VI_BF16, false); break;
         case VI_F16: if (vec) VI_GREEDY_LAUNCH(VI_F16, true); else VI_GREEDY_LAUNCH(VI_F16, false); break;
@@ -129,6 +161,22 @@ vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary,
     }
 #undef VI_GREEDY_LAUNCH
     return launch_status();
+}
+
+}  // namespace
+
+vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                        uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
+                        hipStream_t stream) {
+    return launch_greedy_kind<false>(logits, dtype, rows, vocabulary, stride, serial, out, nullptr, nullptr, nullptr,
+                                     ws, ws_bytes, stream);
+}
+
+vi_status launch_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                            const int64_t* next, int64_t* greedy, float* gap, void* ws, size_t ws_bytes,
+                            hipStream_t stream) {
+    return launch_greedy_kind<true>(logits, dtype, rows, vocabulary, stride, 0, nullptr, next, greedy, gap, ws,
+                                    ws_bytes, stream);
 }
 
 }  // namespace vi

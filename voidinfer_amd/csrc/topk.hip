@@ -60,6 +60,11 @@ struct TopkArgs {
     PacketKeys keys;
     uint64_t serial;
     vi_greedy_row* out_rows;
+    int score;              // VeriCache sampled scores instead of packet rows
+    float tolerance;
+    const int64_t* next;
+    int64_t* chosen;
+    float* score_gap;
     // kModeSample
     const vi_row_params* params;
     const uint2* hash;      // [rows][hash_slots] (token+1, count)
@@ -152,16 +157,16 @@ __device__ void serial_topk_row(const void* row, int vocabulary, int k, float* v
 }
 
 // ------------------------------------------------------------- finishing steps
-// Coupled draw over the sorted candidates (sampled_select.cuh:79-116); nvcc's
-// default contraction fuses the two multiply-adds, restated with fmaf.
-__device__ int packet_draw(const vi_device_sampling& cfg, int key, int cap, const float* cand_val,
-                           const int* cand_idx) {
-    if (!(cfg.temperature > 0.0f)) return 0;
+// Support size of candidates sorted by value (exl3_sampled_support,
+// sampled_select.cuh:283-298).  nvcc's default contraction fuses the
+// multiply-adds of the coupled sampler; they are restated with fmaf.
+// Tail work of one lane: its arrays live in LDS (`prob`, `v2`, `i2`) rather than
+// in per-lane scratch.
+__device__ __forceinline__ int packet_support(const vi_device_sampling& cfg, int cap, const float* value, float* prob) {
     const float inv_temp = 1.0f / cfg.temperature;
-    const float m = cand_val[0] * inv_temp;
-    float prob[20];
+    const float m = value[0] * inv_temp;
     float sum = 0.0f;
-    for (int j = 0; j < cap; ++j) { prob[j] = expf(fmaf(cand_val[j], inv_temp, -m)); sum += prob[j]; }
+    for (int j = 0; j < cap; ++j) { prob[j] = expf(fmaf(value[j], inv_temp, -m)); sum += prob[j]; }
     const float min_p_thresh = cfg.min_p > 0.0f ? cfg.min_p * prob[0] : -1.0f;
     const bool top_p_active = cfg.top_p < 1.0f;
     const float top_p_target = cfg.top_p * sum;
@@ -173,21 +178,82 @@ __device__ int packet_draw(const vi_device_sampling& cfg, int key, int cap, cons
         support = j + 1;
         if (top_p_active && cum >= top_p_target) break;
     }
-    if (support < 1) support = 1;
-    int best = 0;
-    float best_value = -kInfF;
-    for (int j = 0; j < support; ++j) {
-        const float value = fmaf(cand_val[j], inv_temp, gumbel(cfg.seed, key, cand_idx[j]));
-        if (j == 0 || value > best_value) { best_value = value; best = j; }
+    return support < 1 ? 1 : support;
+}
+
+// Coupled draw over the sorted candidates (sampled_select.cuh:79-116): the
+// selected index; value[0..support) receives the perturbed values l/T + G.
+__device__ __forceinline__ int packet_draw(const vi_device_sampling& cfg, int key, int cap, const float* cand_val,
+                           const int* cand_idx, float* value, float* prob, int* support_out) {
+    if (!(cfg.temperature > 0.0f)) {
+        value[0] = cand_val[0];
+        *support_out = 1;
+        return 0;
     }
+    const float inv_temp = 1.0f / cfg.temperature;
+    const int support = packet_support(cfg, cap, cand_val, prob);
+    int best = 0;
+    for (int j = 0; j < support; ++j) {
+        value[j] = fmaf(cand_val[j], inv_temp, gumbel(cfg.seed, key, cand_idx[j]));
+        if (j > 0 && value[j] > value[best]) best = j;
+    }
+    *support_out = support;
     return best;
+}
+
+// VeriCache sampled gap (exl3_sampled_score_kernel, sampled_select.cuh:300-360):
+// how far, in logit units, next trails the selected token.  In the support:
+// T times the perturbed-value gap.  Outside it: infinite, unless raising next's
+// logit by `tolerance` re-ranks it into the support of the same sampler; then
+// the gap is taken against the best other support entry.  A next at or past
+// the vocabulary end is infinite.
+template <int DT>
+__device__ __forceinline__ float sampled_gap(const vi_device_sampling& cfg, int key, const void* row, int vocabulary,
+                             float tolerance, int64_t want, int selected, int support, const float* cand_val,
+                             const int* cand_idx, const float* value, float* prob, float* v2, int* i2) {
+    const int token = cand_idx[selected];
+    if (want < 0 || want == token) return 0.0f;
+    if (want >= vocabulary) return kInfF;
+    if (!(cfg.temperature > 0.0f)) {
+        float own = Elem<DT>::decode(static_cast<const typename Elem<DT>::Bits*>(row)[want]);
+        if (cfg.presence_penalty != 0.0f && cfg.first_occurrence && cfg.first_occurrence[want] < key)
+            own -= cfg.presence_penalty;
+        return fmaxf(0.0f, cand_val[selected] - own);
+    }
+    int cap = 20;
+    if (cfg.top_k > 0 && cfg.top_k < cap) cap = cfg.top_k;
+    int rank = -1;
+    for (int j = 0; j < cap; ++j)
+        if (cand_idx[j] == want) { rank = j; break; }
+    if (rank >= 0 && rank < support) return (value[selected] - value[rank]) * cfg.temperature;
+    if (rank < 0 || !(tolerance > 0.0f)) return kInfF;
+    const float boosted = cand_val[rank] + tolerance;
+    int at = 0;
+    for (int j = 0; j < cap; ++j) {
+        if (j == rank) continue;
+        v2[at] = cand_val[j];
+        i2[at] = cand_idx[j];
+        ++at;
+    }
+    int pos = at;
+    while (pos > 0 && boosted > v2[pos - 1]) { v2[pos] = v2[pos - 1]; i2[pos] = i2[pos - 1]; --pos; }
+    v2[pos] = boosted;
+    i2[pos] = int(want);
+    const int s2 = packet_support(cfg, cap, v2, prob);
+    if (pos >= s2) return kInfF;
+    const float inv_temp = 1.0f / cfg.temperature;
+    float best = -kInfF;
+    for (int j = 0; j < s2; ++j)
+        if (j != pos) best = fmaxf(best, fmaf(v2[j], inv_temp, gumbel(cfg.seed, key, i2[j])));
+    const float own = fmaf(cand_val[rank], inv_temp, gumbel(cfg.seed, key, int(want)));
+    return fmaxf(0.0f, (best - own) * cfg.temperature);
 }
 
 // Extended sampler finish over the sorted top-`cap` list (fp64 weights,
 // min_p / top_p prefix cuts, Philox inverse CDF in sorted order).
-__device__ void sample_finish(const vi_row_params& p, int cap, const float* z, const int* ids,
+__device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, const float* z, const int* ids,
                               int vocabulary, int32_t* token_out, double* uniform_out, float* probs_row,
-                              vi_sample_stats* stats_out, uint32_t flags, uint32_t valid) {
+                              vi_sample_stats* stats_out, uint32_t flags, uint32_t valid, double* w) {
     int32_t token = vocabulary;
     double u = 0.0, sn = 0.0;
     int support = 0;
@@ -197,7 +263,6 @@ __device__ void sample_finish(const vi_row_params& p, int cap, const float* z, c
         token = ids[0]; support = 1; sn = 1.0;
         if (probs_row) probs_row[token] = 1.0f;
     } else {
-        double w[kMaxK];
         const double z0 = double(z[0]);
         double s = 0.0;
         for (int j = 0; j < cap; ++j) { w[j] = exp(double(z[j]) - z0); s += w[j]; }
@@ -257,8 +322,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         K = 20;
         if (a.cfg.top_k > 0 && a.cfg.top_k < K) K = a.cfg.top_k;
         if (a.vocabulary < K) K = a.vocabulary;
-        key = a.keys.first + a.keys.depth[r];
-        if (a.keys.inputs > r) {
+        key = a.keys.first + (a.score ? r : a.keys.depth[r]);
+        if (!a.score && a.keys.inputs > r) {
             for (int j = 0; j < a.keys.depth[r] && j < a.keys.inputs; ++j) path[path_count++] = a.keys.input[j];
             path[path_count++] = a.keys.input[r];
         }
@@ -421,8 +486,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     if constexpr (MODE == kModeTopk) {
         if (f & kSliceNan) {
             if (lane == 0) {
-                float vals[kMaxK];
-                int idsl[kMaxK];
+                // the other waves' merged lists are dead here: their LDS holds the serial list
+                float* vals = s_val[1];
+                int* idsl = s_idx[1];
                 serial_topk_row<DT>(row, a.vocabulary, K, vals, idsl);
                 for (int j = 0; j < K; ++j) {
                     a.ids[size_t(r) * K + j] = idsl[j];
@@ -440,11 +506,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         if (lane == 0 && (f & kSliceNonfinite) && a.nonfinite_flag) atomicOr(a.nonfinite_flag, 1u);
     } else if constexpr (MODE == kModePacket) {
+        __shared__ float s_tail[3][20];
+        __shared__ int s_tail_i[20];
         if (lane == 0) {
-            const int sel = packet_draw(a.cfg, key, K, s_val[0], s_idx[0]);
-            a.out_rows[r].serial = a.serial;
-            a.out_rows[r].token = s_idx[0][sel];
-            a.out_rows[r].nonfinite = (f & kSliceNonfinite) ? 1u : 0u;
+            int support = 1;
+            const int sel = packet_draw(a.cfg, key, K, s_val[0], s_idx[0], s_tail[0], s_tail[1], &support);
+            if (a.score) {
+                a.chosen[r] = s_idx[0][sel];
+                a.score_gap[r] = sampled_gap<DT>(a.cfg, key, row, a.vocabulary, a.tolerance, a.next[r], sel, support,
+                                                 s_val[0], s_idx[0], s_tail[0], s_tail[1], s_tail[2], s_tail_i);
+            } else {
+                a.out_rows[r].serial = a.serial;
+                a.out_rows[r].token = s_idx[0][sel];
+                a.out_rows[r].nonfinite = (f & kSliceNonfinite) ? 1u : 0u;
+            }
         }
     } else if constexpr (MODE == kModeVerify) {
         if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
@@ -461,10 +536,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 return;
             }
             const int cap = (p.temperature > 0.0f) ? min(K, int(c)) : 1;
+            __shared__ double s_w[kMaxK];   // the weights live in LDS, not per-lane scratch
             float* pr = a.probs ? a.probs + size_t(r) * size_t(a.probs_stride) : nullptr;
             sample_finish(p, cap, s_val[0], s_idx[0], a.vocabulary, &a.tokens[r],
                           a.uniforms ? &a.uniforms[r] : nullptr, pr, a.stats ? &a.stats[r] : nullptr,
-                          flags_out, c);
+                          flags_out, c, s_w);
         }
     }
 }
@@ -581,6 +657,22 @@ vi_status launch_packet(const void* scores, int dtype, int rows, int vocabulary,
     a.logits = scores; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
     a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
     a.cfg = cfg; a.keys = keys; a.serial = serial; a.out_rows = out;
+    return launch_mode<kModePacket>(a, dtype, aligned16(scores, stride, dtype), rows, plan.slices, stream);
+}
+
+vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t stride,
+                                const vi_device_sampling& cfg, int first_key, float tolerance,
+                                const int64_t* next, int64_t* chosen, float* gap, void* ws, size_t ws_bytes,
+                                hipStream_t stream) {
+    const TopkPlan plan = topk_plan(rows, vocabulary);
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, rows, plan.slices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    TopkArgs a{};
+    a.logits = scores; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
+    a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
+    a.cfg = cfg; a.keys.first = first_key; a.score = 1; a.tolerance = tolerance;
+    a.next = next; a.chosen = chosen; a.score_gap = gap;
     return launch_mode<kModePacket>(a, dtype, aligned16(scores, stride, dtype), rows, plan.slices, stream);
 }
 

@@ -36,6 +36,10 @@ size_t greedy_workspace(int rows, int vocabulary);
 vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                         uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
                         hipStream_t stream);
+// VeriCache exact row scores (argmax + gap of next[r]); workspace as greedy.
+vi_status launch_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                            const int64_t* next, int64_t* greedy, float* gap, void* ws, size_t ws_bytes,
+                            hipStream_t stream);
 
 // ---- top-k family -------------------------------------------------------------
 enum TopkMode { kModeTopk = 0, kModePacket = 1, kModeSample = 2, kModeVerify = 3 };
@@ -61,6 +65,12 @@ vi_status launch_topk_rows(const void* logits, int dtype, int rows, int vocabula
 vi_status launch_packet(const void* scores, int dtype, int rows, int vocabulary, int64_t stride,
                         const vi_device_sampling& cfg, const PacketKeys& keys, uint64_t serial,
                         vi_greedy_row* out, void* ws, size_t ws_bytes, hipStream_t stream);
+// VeriCache sampled row scores: the coupled draw of row r at key first_key + r
+// (no drafted path) and the gap of next[r].
+vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t stride,
+                                const vi_device_sampling& cfg, int first_key, float tolerance,
+                                const int64_t* next, int64_t* chosen, float* gap, void* ws, size_t ws_bytes,
+                                hipStream_t stream);
 
 // Sorted, filtered top-k lists (z values, ids) of verification rows.
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,

@@ -135,6 +135,37 @@ def sampled_packet(scores: torch.Tensor, temperature: float, top_k: int, top_p: 
     return out.cpu().numpy().view(GREEDY_ROW)
 
 
+def row_scores(logits: torch.Tensor, next_tokens: torch.Tensor):
+    """VeriCache exact row scores -> (greedy int64 [rows], gap f32 [rows]) on the device."""
+    dtype, rows, vocab, stride = _rows_view(logits, None)
+    nxt = next_tokens.to(device=logits.device, dtype=torch.int64).contiguous()
+    greedy = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    gap = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    nb = _lib().vi_row_scores_workspace_bytes(rows, vocab)
+    ws = workspace(("greedy", rows, vocab), nb, logits.device)
+    check(_lib().vi_row_scores(logits.data_ptr(), dtype, rows, vocab, stride, nxt.data_ptr(), greedy.data_ptr(),
+                               gap.data_ptr(), ws.data_ptr(), ws.numel(), _stream()), "vi_row_scores")
+    return greedy, gap
+
+
+def sampled_scores(scores: torch.Tensor, next_tokens: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                   min_p: float, seed: int, first_key: int = 0, tolerance: float = 0.0,
+                   presence_penalty: float = 0.0, first_occurrence: torch.Tensor | None = None):
+    """VeriCache sampled row scores -> (chosen int64 [rows], gap f32 [rows]) on the device."""
+    dtype, rows, vocab, stride = _rows_view(scores, None)
+    cfg = DeviceSampling(temperature, top_k, top_p, min_p, seed, presence_penalty, 0,
+                         first_occurrence.data_ptr() if first_occurrence is not None else None)
+    nxt = next_tokens.to(device=scores.device, dtype=torch.int64).contiguous()
+    chosen = torch.empty(rows, dtype=torch.int64, device=scores.device)
+    gap = torch.empty(rows, dtype=torch.float32, device=scores.device)
+    nb = _lib().vi_sampled_scores_workspace_bytes(rows, vocab)
+    ws = workspace(("packet", rows, vocab), nb, scores.device)
+    check(_lib().vi_sampled_scores(scores.data_ptr(), dtype, rows, vocab, stride, C.byref(cfg), first_key, tolerance,
+                                   nxt.data_ptr(), chosen.data_ptr(), gap.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   _stream()), "vi_sampled_scores")
+    return chosen, gap
+
+
 def presence_reset(table: torch.Tensor) -> None:
     check(_lib().vi_presence_reset(table.data_ptr(), table.numel(), _stream()), "vi_presence_reset")
 
