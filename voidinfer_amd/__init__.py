@@ -13,5 +13,6 @@ from ._abi import (ABSENT_OCCURRENCE, BF16, F16, F32, FLAG_BAD_HISTORY, FLAG_EMP
 load()
 
 from .ops import (greedy_packet, params_array, presence_record, presence_reset, presence_truncate,  # noqa: E402,F401
-                  probe_copy, probe_read, route_mask, sample_rows, sampled_packet, stats_numpy, to_device_bytes, topk_rows,
+                  probe_copy, probe_read, route_mask, row_scores, sample_rows, sampled_packet, sampled_scores, stats_numpy,
+                  to_device_bytes, topk_rows,
                   verify_rows, workspace)
