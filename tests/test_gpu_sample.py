@@ -160,6 +160,26 @@ def test_full_route_penalties_and_saturation(orc, dev, rng, dtype):
     compare(*run_both(orc, dev, bits, dtype, p, hist, offs), p, "full-pen")
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_full_route_repeated_history_tokens(orc, dev, rng, dtype):
+    """Tokens seen 2..7 times per history: the counts come from the first- and
+    second-occurrence bitmaps plus the short list of further occurrences (a
+    few hundred entries per half), without a second history pass."""
+    rows, vocab = 8, 248_320
+    bits = make_rows(rng, rows, vocab, std=0.5, dtype=dtype)
+    p = params(rows, rng, temperature=rng.uniform(0.5, 1.2, rows), top_k=0, top_p=rng.choice([0.9, 0.95], rows),
+               repetition_penalty=rng.uniform(1.0, 1.3, rows), presence_penalty=rng.uniform(0, 0.5, rows),
+               frequency_penalty=rng.uniform(0.05, 0.3, rows))
+    rows_h = []
+    for r in range(rows):
+        pool = rng.choice(vocab, 400, replace=False)
+        reps = np.concatenate([np.repeat(pool[:300], 2 + r % 3), np.repeat(pool[300:], 7)])
+        h = np.concatenate([rng.integers(0, vocab, 3000), reps, [vocab // 2 - 1] * 4, [vocab // 2] * 5])
+        rows_h.append(rng.permutation(h).astype(np.int32))
+    offs = np.concatenate([[0], np.cumsum([len(h) for h in rows_h])]).astype(np.int64)
+    compare(*run_both(orc, dev, bits, dtype, p, np.concatenate(rows_h), offs), p, "full-rep")
+
+
 def test_full_route_nonfinite_and_ties(orc, dev, rng):
     rows, vocab = 6, 9_000
     bits = make_rows(rng, rows, vocab, std=1.0)

@@ -53,6 +53,11 @@ constexpr int kOvfMax = 512;              // history tokens with >= 255 occurren
 constexpr int kHB = 8;                    // history entries per thread per load round
 // dense path
 constexpr int kHistMax = 32768;           // history tokens per row
+// one-pass history counting: a second-occurrence bitmap and a list of the
+// offsets of further occurrences, in the P16 region [64 KiB, 128 KiB) until the
+// exchange overwrites it
+constexpr int kList3 = 4096;              // list capacity; a longer list takes a second pass
+constexpr int kOffB2 = 65536, kOffL3 = kOffB2 + 4 * 4096;
 constexpr int kHT = kHistMax / kFT;       // history tokens per thread
 constexpr int kDR = kHistMax / kFT;       // dense ranks (distinct history tokens) per thread
 constexpr int kBmapWords = kVecMax * 8 / 32;
@@ -125,6 +130,7 @@ static_assert(kOffML + 4 * kMatchMax <= 131072, "owner LDS");
 constexpr int kLdsGeneral = 131072 + 8 * kOvfMax;
 static_assert(kOffDecEnd <= 131072 && kOffDM % 8 == 0 && kOffPM % 8 == 0 && kOffWW % 8 == 0 && kOffWM % 8 == 0, "LDS map");
 static_assert(kHistMax / 2 * 4 <= 131072, "dense counts");
+static_assert(kOffL3 + 4 * kList3 <= 131072 && kHistMax * 2 <= kOffB2, "one-pass history counting");
 
 struct Shared {
     uint32_t u[kFW + 1];
@@ -135,7 +141,7 @@ struct Shared {
     uint32_t rank, pn_take, n_sup, slot, slot_rank, ctot;
     double s_n, draw_u;
     uint32_t slot_tot[kFV + 2];
-    uint32_t n_sum, n_fin, n_match, wcount[kFW];
+    uint32_t n_sum, n_fin, n_match, n3, wcount[kFW];
     uint32_t first[kCoarse], bend[kCoarse];   // this half's list slots of each coarse bin
 };
 
@@ -307,6 +313,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     // consecutive ranks: nearby tokens) and penalized into registers, rank
     // k * kFT + tid in slot k.
     uint32_t n_flag = 0;
+    uint32_t dkeep[kDR / 2] = {};   // dense path: penalized bits of ranks k * kFT + tid, two per register
     // the history tokens' penalized logits by rank: this half's slice of the
     // workspace (written once, read back from L2; not kept in registers)
     uint16_t* dpen = kDense ? a.dense + (size_t(row) * 2 + half) * kHistMax : nullptr;
@@ -350,16 +357,60 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         if (pen) {
             uint32_t* bmap = reinterpret_cast<uint32_t*>(lds + kOffBmap);
             uint16_t* pref = reinterpret_cast<uint16_t*>(lds + kOffPref);
+            // One history pass: a bitmap of first occurrences, a second bitmap of
+            // second occurrences and a short list of the offsets of all further
+            // occurrences, in the P16 region (free until the exchange); a long list
+            // falls back to a second pass over the history.
+            uint32_t* bmap2 = lds32 + kOffB2 / 4;
+            uint32_t* list3 = lds32 + kOffL3 / 4;
             for (int w = tid; w < kBmapWords + 4; w += kFT) bmap[w] = 0u;
-            for (int w = tid; w < kHistMax / 2; w += kFT) lds32[w] = 0u;   // C16
+            for (int w = tid; w < kBmapWords; w += kFT) bmap2[w] = 0u;
+            if (tid == 0) sh.n3 = 0u;
             __syncthreads();
             if (tid == 0 && hn > kHistMax) atomicOr(&sh.flags, kHdrError);   // callers promise hn <= max_history
-            for_history([&](int32_t t) {
-                if (t < 0 || t >= V) { atomicOr(&sh.flags, kHdrBadHistory); return; }
-                if (t < h0 || t >= h1) return;
-                const int off = t - h0;
-                atomicOr(&bmap[off >> 5], 1u << (off & 31));
-            });
+            {
+                // rounds of kHR tokens per thread; each stage's LDS atomics of a
+                // round are issued together (their results are awaited once)
+                constexpr int kHR = 8;
+                const int hl = int(min(hn, int64_t(kHistMax)));
+#pragma unroll
+                for (int r0 = 0; r0 < kHT; r0 += kHR) {
+                    if (r0 * kFT >= hl) break;   // (uniform)
+                    int32_t t[kHR];
+#pragma unroll
+                    for (int j = 0; j < kHR; ++j) t[j] = hist[min((r0 + j) * kFT + tid, hl - 1)];
+                    uint32_t in = 0, dup = 0, dup2 = 0;
+#pragma unroll
+                    for (int j = 0; j < kHR; ++j) {
+                        if ((r0 + j) * kFT + tid >= hl) continue;
+                        if (t[j] < 0 || t[j] >= V) atomicOr(&sh.flags, kHdrBadHistory);
+                        else if (t[j] >= h0 && t[j] < h1) in |= 1u << j;
+                    }
+                    uint32_t old[kHR];
+#pragma unroll
+                    for (int j = 0; j < kHR; ++j) {
+                        const int off = t[j] - h0;
+                        old[j] = ((in >> j) & 1u) ? atomicOr(&bmap[off >> 5], 1u << (off & 31)) : 0u;
+                    }
+#pragma unroll
+                    for (int j = 0; j < kHR; ++j) dup |= ((old[j] >> ((t[j] - h0) & 31)) & ((in >> j) & 1u)) << j;
+                    if (dup) {
+#pragma unroll
+                        for (int j = 0; j < kHR; ++j) {
+                            const int off = t[j] - h0;
+                            old[j] = ((dup >> j) & 1u) ? atomicOr(&bmap2[off >> 5], 1u << (off & 31)) : 0u;
+                        }
+#pragma unroll
+                        for (int j = 0; j < kHR; ++j) dup2 |= ((old[j] >> ((t[j] - h0) & 31)) & ((dup >> j) & 1u)) << j;
+                        while (dup2) {
+                            const int j = __builtin_ctz(dup2);
+                            dup2 &= dup2 - 1u;
+                            const uint32_t k = atomicAdd(&sh.n3, 1u);
+                            if (k < uint32_t(kList3)) list3[k] = uint32_t(t[j] - h0);
+                        }
+                    }
+                }
+            }
             __syncthreads();
 #pragma unroll
             for (int i = 0; i < kFV; ++i) {
@@ -378,12 +429,27 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             __syncthreads();
             // u16 occurrence counts by rank, C16 = [0, 64 KiB) (a count reaches at
             // most kHistMax = 32,768: no carry between the packed halves)
-            for_history([&](int32_t t) {   // (L2 hits now)
-                if (t < h0 || t >= h1) return;
-                const int off = t - h0, w = off >> 5;
-                const uint32_t rank = pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
-                atomicAdd(&lds32[rank >> 1], (rank & 1u) ? 0x10000u : 1u);
-            });
+            const uint32_t n3 = sh.n3;
+            if (n3 <= uint32_t(kList3)) {   // (uniform) counts from the bitmaps, then the list, by rank
+                uint16_t* c16 = reinterpret_cast<uint16_t*>(lds);
+                walk_words([&](uint32_t rank, int off) { c16[rank] = uint16_t(1u + ((bmap2[off >> 5] >> (off & 31)) & 1u)); });
+                __syncthreads();
+                for (uint32_t k = tid; k < n3; k += kFT) {
+                    const int off = int(list3[k]), w = off >> 5;
+                    const uint32_t rank = pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
+                    atomicAdd(&lds32[rank >> 1], (rank & 1u) ? 0x10000u : 1u);
+                }
+            } else {   // a second pass over the history (L2 hits now)
+                for (int w = tid; w < kHistMax / 2; w += kFT) lds32[w] = 0u;
+                __syncthreads();
+                for_history([&](int32_t t) {
+                    if (t < h0 || t >= h1) return;
+                    const int off = t - h0, w = off >> 5;
+                    const uint32_t rank = pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u));
+                    atomicAdd(&lds32[rank >> 1], (rank & 1u) ? 0x10000u : 1u);
+                });
+            }
+            __syncthreads();   // the bitmaps and the list are read before the exchange overwrites them
             // the history tokens' logits by rank, P16 = [64 KiB, 128 KiB), written by
             // the threads holding them (a vector's history tokens have consecutive ranks)
             uint16_t* P16 = reinterpret_cast<uint16_t*>(lds + 65536);
@@ -418,6 +484,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                     const uint32_t c = (lds32[r >> 1] >> (16 * (r & 1u))) & 0xffffu;
                     const uint32_t pb = Elem<DT>::finite_bits(bits) ? penalize_bits<DT>(bits, c, p) & 0xffffu : bits;
                     dpen[r] = uint16_t(pb);
+                    dkeep[k >> 1] |= pb << (16 * (k & 1));
                 }
             }
             __syncthreads();   // entries read before the histogram overwrites them
@@ -562,8 +629,12 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     if (tid < head) hist_key(key16(hbits), fl_head);
     if (tid < tail) hist_key(key16(tbits), fl_tail);
     if constexpr (kDense) {
-        // the history tokens, penalized
-        for (uint32_t r = tid; r < n_flag; r += kFT) hist_key(key16(dpen[r]), false);
+        // the history tokens, penalized (ranks k * kFT + tid, kept in registers)
+#pragma unroll
+        for (int k = 0; k < kDR; ++k) {
+            if (uint32_t(k) * kFT >= n_flag) break;
+            if (uint32_t(k) * kFT + tid < n_flag) hist_key(key16((dkeep[k >> 1] >> (16 * (k & 1))) & 0xffffu), false);
+        }
     }
     __syncthreads();
     if (tid == 0) {   // -0 counts as +0 (key 0x7fff is only ever -0)
@@ -820,15 +891,21 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) { WC[4 * lane + e] = 0u; WC[kCoarse + 4 * lane + e] = 0u; }
             wave_lds_sync();
+            // both halves' entries of the bin (<= 256 each): all loads in flight at once
+            uint32_t ent[8];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t* gl = a.lists + (size_t(row) * 2 + h) * kListMax;
                 const uint32_t f0 = DF[2 * kCoarse * h + c], f1 = DF[2 * kCoarse * h + kCoarse + c];
-                for (uint32_t i = f0 + lane; i < f1; i += kWave) {
-                    const uint32_t ent = gl[i];
-                    WC[h * kCoarse + (255u - ((ent >> 16) & 255u))] = ent & 0xffffu;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t i = f0 + uint32_t(lane + k * kWave);
+                    ent[h * 4 + k] = i < f1 ? gl[i] : 0u;
                 }
             }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (ent[u]) WC[(u >> 2) * kCoarse + (255u - ((ent[u] >> 16) & 255u))] = ent[u] & 0xffffu;
             wave_lds_sync();
             uint32_t cq[4];
             double mq[4];
