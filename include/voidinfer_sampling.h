@@ -189,6 +189,33 @@ vi_status vi_sampled_scores(const void* scores, int dtype, int rows, int vocabul
                             const int64_t* next, int64_t* chosen, float* gap,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- DFlash2 draft coupled proposal ---------------------------------------------
+ * Replaces dflash_sampled_choice with DraftSelectSampling
+ * (src/exl3/dflash2_draft.cu:2554-2610) for many lanes: per lane, draft positions
+ * 0..positions-1 in order, position p choosing among its 16 candidates.  With
+ * inv_temperature > 0: candidates equal to the lane's seed token, generated
+ * before key = key_base + p (first_occurrence[token] < key) or proposed at an
+ * earlier position lose presence_penalty; the penalized scores are ordered
+ * (stable, descending), capped at top_k, cut by min_p / top_p over
+ * exp(score/T - max) and the argmax of score/T + Gumbel(seed, key, token) over
+ * that support is proposed.  Otherwise the first maximum of the scores wins (the
+ * reference feeds its selector scores there).  scores: f32 [lanes][positions][16];
+ * candidates: int64 [lanes][positions][16]; seed_tokens: int64 [lanes] (or
+ * NULL); sampling: one record per lane (device memory); proposals: int64
+ * [lanes][positions].  first_occurrence lookups are bounded by `vocabulary`. */
+typedef struct vi_draft_sampling {   /* field-for-field DraftSelectSampling */
+    float inv_temperature, top_p, min_p;
+    int32_t top_k;
+    uint64_t seed;
+    int32_t key_base, reserved;
+    float presence_penalty;
+    int32_t reserved2;
+    const int32_t* first_occurrence;   /* device int32[vocabulary] or NULL */
+} vi_draft_sampling;
+vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float* scores,
+                          const int64_t* candidates, const int64_t* seed_tokens,
+                          const vi_draft_sampling* sampling, int64_t* proposals, void* stream);
+
 /* ---- batched sampler (extended semantics) ----------------------------------
  * New batched entry for many lanes (the reference's packet stops at 16 rows,
  * sampled_select.cuh:200-216): per-row temperature, top-k, top-p, min-p,

@@ -1180,6 +1180,30 @@ inline void exl3_presence_record(std::int32_t* table, int first, const std::int6
     detail::check(vi_presence_record(table, vocabulary, first, tokens, count, stream), "presence record");
 }
 
+// DFlash2 draft proposal configuration — src/exl3/dflash2_draft.cu:2562-2572
+// (the 48-byte layout of vi_draft_sampling).
+struct DraftSelectSampling {
+    float inv_temperature = 0.0F, top_p = 1.0F, min_p = 0.0F;
+    int top_k = 0;
+    unsigned long long seed = 0;
+    int key_base = 0, pad = 0;
+    float presence_penalty = 0.0F;
+    const std::int32_t* first_occurrence = nullptr;
+};
+static_assert(sizeof(DraftSelectSampling) == sizeof(vi_draft_sampling) && sizeof(DraftSelectSampling) == 48);
+static_assert(offsetof(DraftSelectSampling, first_occurrence) == offsetof(vi_draft_sampling, first_occurrence));
+
+// dflash_sampled_choice (dflash2_draft.cu:2574-2610) for every position of every
+// lane: `sampling` is a device array of one DraftSelectSampling per lane.
+inline void dflash_sampled_choices(int lanes, int positions, const float* scores, const std::int64_t* candidates,
+                                   const std::int64_t* seed_tokens, const DraftSelectSampling* sampling,
+                                   std::int64_t* proposals, void* stream,
+                                   int vocabulary = int(kDefaultVocabulary)) {
+    detail::check(vi_draft_choice(lanes, positions, vocabulary, scores, candidates, seed_tokens,
+                                  reinterpret_cast<const vi_draft_sampling*>(sampling), proposals, stream),
+                  "draft sampled choice");
+}
+
 // Scratch of the top-k route (the reference's qualification entry allocates
 // none; this library's slices need vi_topk_workspace_bytes).
 struct Exl3TopkScratch {

@@ -90,6 +90,7 @@ def lib() -> C.CDLL:
             "or_sampled_packet": ([vp, i, i, i, i64, C.POINTER(DeviceSampling), i, vp, i, vp, i, u64, vp, vp], i),
             "or_sampled_scores": ([vp, i, i, i, i64, C.POINTER(DeviceSampling), i, C.c_float, vp, vp, vp], i),
             "or_row_scores": ([vp, i, i, i, i64, vp, vp, vp], i),
+            "or_draft_choice": ([i, i, i, vp, vp, vp, vp, vp], i),
             "or_sample_rows": ([vp, i, i, i, i64, vp, vp, vp, vp, vp, vp, i64, vp, vp, i], i),
             "or_accept": ([vp, vp, i64, u32, d, d, C.POINTER(AcceptOutcome), vp], i),
             "or_outer_prefix": ([vp, vp, i, vp, i, vp, vp, vp, vp, vp], i),
@@ -204,6 +205,29 @@ def sampled_scores(scores: np.ndarray, dtype: int, temperature: float, top_k: in
     if st:
         raise ValueError("oracle sampled scores: invalid arguments")
     return chosen, gap
+
+
+DRAFT_SAMPLING = np.dtype([
+    ("inv_temperature", "<f4"), ("top_p", "<f4"), ("min_p", "<f4"), ("top_k", "<i4"), ("seed", "<u8"),
+    ("key_base", "<i4"), ("reserved", "<i4"), ("presence_penalty", "<f4"), ("reserved2", "<i4"),
+    ("first_occurrence", "<u8"),
+])
+
+
+def draft_choice(scores: np.ndarray, candidates: np.ndarray, sampling: np.ndarray, seed_tokens=None,
+                 vocabulary: int = 248320) -> np.ndarray:
+    """DFlash2 coupled proposals: scores f32 [lanes, positions, 16], candidates int64
+    [lanes, positions, 16], sampling DRAFT_SAMPLING [lanes] (first_occurrence = host
+    address or 0) -> proposals int64 [lanes, positions]."""
+    lanes, positions, _ = scores.shape
+    sc = np.ascontiguousarray(scores, dtype=np.float32)
+    cd = np.ascontiguousarray(candidates, dtype=np.int64)
+    st = None if seed_tokens is None else np.ascontiguousarray(seed_tokens, dtype=np.int64)
+    smp = np.ascontiguousarray(sampling, dtype=DRAFT_SAMPLING)
+    out = np.zeros((lanes, positions), dtype=np.int64)
+    if lib().or_draft_choice(lanes, positions, vocabulary, _p(sc), _p(cd), _p(st), _p(smp), _p(out)):
+        raise ValueError("oracle draft choice: invalid arguments")
+    return out
 
 
 def row_scores(logits: np.ndarray, dtype: int, next_tokens):

@@ -547,6 +547,74 @@ int or_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, i
     return VI_OK;
 }
 
+// dflash_sampled_choice with DraftSelectSampling (dflash2_draft.cu:2554-2610),
+// applied to every position of every lane in position order; the inv_temperature
+// <= 0 branch is the first maximum of the given scores (the reference's selector
+// argmax).  As in the reference build, the two multiply-adds are fused.
+int or_draft_choice(int lanes, int positions, int vocabulary, const float* scores, const int64_t* candidates,
+                    const int64_t* seed_tokens, const vi_draft_sampling* sampling, int64_t* proposals) {
+    if (lanes < 0 || positions < 0 || vocabulary <= 0 || !scores || !candidates || !sampling || !proposals)
+        return VI_ERR_INVALID;
+    constexpr int K = 16;
+    for (int l = 0; l < lanes; ++l) {
+        const vi_draft_sampling& s = sampling[l];
+        const int64_t seed_token = seed_tokens ? seed_tokens[l] : -1;
+        int64_t* out = proposals + size_t(l) * positions;
+        for (int pos = 0; pos < positions; ++pos) {
+            const size_t at = (size_t(l) * positions + pos) * K;
+            const float* sc = scores + at;
+            const int64_t* cd = candidates + at;
+            int best = 0;
+            if (!(s.inv_temperature > 0.0f)) {
+                for (int c = 1; c < K; ++c) if (sc[c] > sc[best]) best = c;
+            } else {
+                const int key = s.key_base + pos;
+                float v[K];
+                int order[K];
+                for (int c = 0; c < K; ++c) {
+                    v[c] = sc[c];
+                    order[c] = c;
+                    if (s.presence_penalty == 0.0f) continue;
+                    const int64_t token = cd[c];
+                    bool seen = token == seed_token ||
+                                (s.first_occurrence && token >= 0 && token < vocabulary && s.first_occurrence[token] < key);
+                    for (int i = 0; i < pos && !seen; ++i) seen = out[i] == token;
+                    if (seen) v[c] -= s.presence_penalty;
+                }
+                for (int i = 1; i < K; ++i) {
+                    const int o = order[i];
+                    int j = i;
+                    while (j > 0 && v[o] > v[order[j - 1]]) { order[j] = order[j - 1]; --j; }
+                    order[j] = o;
+                }
+                int cap = K;
+                if (s.top_k > 0 && s.top_k < cap) cap = s.top_k;
+                const float m = v[order[0]] * s.inv_temperature;
+                float prob[K], sum = 0.0f;
+                for (int j = 0; j < cap; ++j) { prob[j] = std::exp(std::fmaf(v[order[j]], s.inv_temperature, -m)); sum += prob[j]; }
+                const float thresh = s.min_p > 0.0f ? s.min_p * prob[0] : -1.0f;
+                float cum = 0.0f;
+                int support = 0;
+                for (int j = 0; j < cap; ++j) {
+                    if (thresh >= 0.0f && prob[j] < thresh) break;
+                    cum += prob[j]; support = j + 1;
+                    if (s.top_p < 1.0f && cum >= s.top_p * sum) break;
+                }
+                if (support < 1) support = 1;
+                best = order[0];
+                float best_value = -kInf;
+                for (int j = 0; j < support; ++j) {
+                    const int c = order[j];
+                    const float val = std::fmaf(v[c], s.inv_temperature, or_gumbel(s.seed, key, int32_t(cd[c])));
+                    if (val > best_value) { best_value = val; best = c; }
+                }
+            }
+            out[pos] = cd[best];
+        }
+    }
+    return VI_OK;
+}
+
 // exact_row_score_kernel (text_model.cu:11393-11420): argmax over the values
 // that compare greater than -Inf (NaN and -Inf never win, +Inf can), lowest
 // index on ties, index = vocabulary when none; gap = max - logit(next) for a

@@ -74,6 +74,10 @@ int or_sampled_packet(const void* scores, int dtype, int rows, int vocabulary, i
 int or_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, int64_t row_stride,
                       const vi_device_sampling* cfg, int first_key, float tolerance, const int64_t* next,
                       int64_t* chosen, float* gap);
+/* DFlash2 draft coupled proposal (dflash_sampled_choice, dflash2_draft.cu:2554-2610);
+ * host pointers (first_occurrence included), layouts as vi_draft_choice. */
+int or_draft_choice(int lanes, int positions, int vocabulary, const float* scores, const int64_t* candidates,
+                    const int64_t* seed_tokens, const vi_draft_sampling* sampling, int64_t* proposals);
 /* VeriCache exact row scores (exact_row_score_kernel, text_model.cu:11393-11420). */
 int or_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
                   const int64_t* next, int64_t* greedy, float* gap);

@@ -1,0 +1,78 @@
+"""GPU DFlash2 draft coupled proposals (vi_draft_choice) vs the CPU oracle
+(dflash_sampled_choice, dflash2_draft.cu:2554-2610).
+
+Proposals equal position by position; a lane may differ only where the
+oracle's decision sat within float rounding of a boundary (the two best
+perturbed values within 1e-5, or a top-p / min-p cut within 1e-5 relative),
+and is not compared past such a position (later positions depend on it
+through the presence penalty).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def near_boundary(orc, scores, cands, s, key):
+    x = scores.astype(np.float64)
+    inv = float(s["inv_temperature"])
+    order = np.argsort(-x, kind="stable")
+    cap = int(s["top_k"]) if 0 < int(s["top_k"]) < 16 else 16
+    w = np.exp((x[order[:cap]] - x[order[0]]) * inv)
+    near = False
+    if float(s["top_p"]) < 1:
+        near |= bool(np.any(np.abs(np.cumsum(w) - float(s["top_p"]) * w.sum()) <= 1e-5 * w.sum()))
+    if float(s["min_p"]) > 0:
+        near |= bool(np.any(np.abs(w - float(s["min_p"])) <= 1e-5))
+    g = np.array([orc.gumbel(int(s["seed"]), key, int(c)) for c in cands[order[:cap]]])
+    v = np.sort(x[order[:cap]] * inv + g)[::-1]
+    near |= bool(len(v) > 1 and abs(v[0] - v[1]) <= 1e-5 * (1 + abs(v[0])))
+    return near
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_draft_choice_vs_oracle(orc, dev, case):
+    import voidinfer_amd as vi
+    rng = np.random.default_rng(500 + case)
+    lanes, pos, vocab = 96, 8, 50_000
+    scores = (rng.standard_normal((lanes, pos, 16)) * 1.5).astype(np.float32)
+    cands = np.stack([np.stack([rng.choice(vocab, 16, replace=False) for _ in range(pos)]) for _ in range(lanes)])
+    cands[:, 1:, 0] = cands[:, :1, 0]                      # a repeated top candidate exercises the chain penalty
+    scores[:, :, 0] += 2.0
+    smp = np.zeros(lanes, dtype=vi.DRAFT_SAMPLING)
+    smp["inv_temperature"] = [0.0, 1.4, 0.9, 2.5][case] if case else 0.0
+    smp["top_k"] = rng.choice([0, 4, 12], lanes)
+    smp["top_p"] = rng.choice([1.0, 0.9, 0.7], lanes)
+    smp["min_p"] = rng.choice([0.0, 0.05], lanes)
+    smp["seed"] = rng.integers(1, 2**62, lanes)
+    smp["key_base"] = rng.integers(0, 100_000, lanes)
+    smp["presence_penalty"] = [0.0, 0.0, 1.5, -0.5][case]
+    fo = np.full(vocab, 0x7F7F7F7F, dtype=np.int32)
+    fo[cands[:, 0, 1]] = 3
+    seeds = cands[:, 0, 2].copy()
+    fo_dev = torch.from_numpy(fo).to(dev)
+    smp_dev = smp.copy()
+    smp_host = smp.copy()
+    if case >= 2:
+        smp_dev["first_occurrence"] = fo_dev.data_ptr()
+        smp_host["first_occurrence"] = fo.ctypes.data
+    got = vi.draft_choice(torch.from_numpy(scores).to(dev), torch.from_numpy(cands).to(dev), smp_dev,
+                          torch.from_numpy(seeds).to(dev), vocabulary=vocab)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    want = orc.draft_choice(scores, cands, smp_host, seed_tokens=seeds, vocabulary=vocab)
+    for l in range(lanes):
+        for p in range(pos):
+            if got[l, p] != want[l, p]:
+                assert near_boundary(orc, scores[l, p], cands[l, p], smp[l], int(smp["key_base"][l]) + p), (l, p)
+                break
+
+
+def test_draft_choice_rejects_invalid(dev):
+    import ctypes as C
+    from voidinfer_amd import _abi
+    lib = _abi.load()
+    assert lib.vi_draft_choice(0, 4, 100, None, None, None, None, None, None) == 0      # nothing to do
+    assert lib.vi_draft_choice(2, 4, 100, None, None, None, None, None, None) == 1      # null arrays
+    assert lib.vi_draft_choice(-1, 4, 100, None, None, None, None, None, None) == 1

@@ -619,3 +619,97 @@ def test_sampled_scores_against_the_packet_and_a_boosted_row(orc, tolerance):
     assert checked_in > 20
     if tolerance > 0:
         assert checked_out > 10
+
+
+# ---------------------------------------------------------------- DFlash2 draft coupled proposal
+
+def draft_sampling(n, **kw):
+    import oracle
+    s = np.zeros(n, dtype=oracle.DRAFT_SAMPLING)
+    s["top_p"] = 1.0
+    for k, v in kw.items():
+        s[k] = v
+    return s
+
+
+def test_draft_choice_greedy_is_first_maximum(orc):
+    rng = np.random.default_rng(81)
+    lanes, pos = 5, 4
+    sc = rng.standard_normal((lanes, pos, 16)).astype(np.float32)
+    sc[0, 0, [3, 9]] = 9.0                                   # tie: the first wins
+    cd = rng.integers(0, 1000, (lanes, pos, 16))
+    out = orc.draft_choice(sc, cd, draft_sampling(lanes, inv_temperature=0.0), vocabulary=1000)
+    want = np.take_along_axis(cd, sc.argmax(axis=2)[..., None], axis=2)[..., 0]
+    assert np.array_equal(out, want) and out[0, 0] == cd[0, 0, 3]
+
+
+def test_draft_choice_presence_covers_seed_history_and_chain(orc):
+    """The top candidate is penalized when it is the seed token, was generated
+    before the key, or was proposed at an earlier position of the chain."""
+    lanes, pos, v = 4, 3, 100
+    sc = np.tile(np.linspace(3.0, 0.0, 16, dtype=np.float32), (lanes, pos, 1))
+    cd = np.tile(np.arange(16, dtype=np.int64), (lanes, pos, 1))
+    fo = np.full(v, 2**31 - 1, dtype=np.int32)
+    fo[0] = 5                                                 # token 0 generated at index 5
+    smp = draft_sampling(lanes, inv_temperature=1.0, top_k=1, presence_penalty=100.0, seed=3)
+    smp["key_base"] = [0, 0, 10, 0]
+    smp["first_occurrence"][2] = fo.ctypes.data
+    out = orc.draft_choice(sc, cd, smp, seed_tokens=[50, 0, 50, 50], vocabulary=v)
+    # lane 0: nothing seen -> 0, then 0 is in the chain -> 1, then 2
+    assert out[0].tolist() == [0, 1, 2]
+    # lane 1: the seed token is 0 -> 1, 2, 3
+    assert out[1].tolist() == [1, 2, 3]
+    # lane 2: key 10 > first occurrence 5 of token 0 -> 1, 2, 3
+    assert out[2].tolist() == [1, 2, 3]
+    # lane 3: keys 0..2 < 5 would not see token 0 even with the table
+    smp["first_occurrence"][3] = fo.ctypes.data
+    assert orc.draft_choice(sc, cd, smp, seed_tokens=[50, 0, 50, 50], vocabulary=v)[3].tolist() == [0, 1, 2]
+
+
+@pytest.mark.parametrize("params", [(1.25, 0, 0.9, 0.02), (0.8, 6, 1.0, 0.0), (2.0, 0, 0.7, 0.1)])
+def test_draft_choice_gumbel_max_law(orc, params):
+    """Over seeds, the proposal follows softmax(score/T) over the truncated support."""
+    inv_t, top_k, top_p, min_p = params
+    rng = np.random.default_rng(83)
+    x = rng.standard_normal(16).astype(np.float32)
+    cand = rng.choice(5000, 16, replace=False).astype(np.int64)
+    order = np.lexsort((np.arange(16), -x.astype(np.float64)))
+    cap = top_k if 0 < top_k < 16 else 16
+    w = np.exp((x[order[:cap]].astype(np.float64) - x[order[0]]) * inv_t)
+    keep = np.ones(cap, bool)
+    if min_p > 0:
+        keep &= np.cumprod(w >= min_p).astype(bool)
+    if top_p < 1:
+        keep &= np.concatenate([[0.0], np.cumsum(w)[:-1]]) < top_p * w.sum()
+    n = max(1, int(keep.sum()))
+    probs = w[:n] / w[:n].sum()
+    seeds = np.arange(1, 6001, dtype=np.uint64)
+    smp = draft_sampling(len(seeds), inv_temperature=inv_t, top_k=top_k, top_p=top_p, min_p=min_p)
+    smp["seed"] = seeds
+    smp["key_base"] = np.arange(len(seeds)) % 97
+    out = orc.draft_choice(np.tile(x, (len(seeds), 1, 1)), np.tile(cand, (len(seeds), 1, 1)), smp, vocabulary=5000)
+    pos = {int(cand[order[j]]): j for j in range(n)}
+    counts = np.zeros(n, dtype=np.int64)
+    for t in out[:, 0]:
+        counts[pos[int(t)]] += 1
+    assert chi2_pvalue(counts, probs) > 1e-4
+
+
+def test_draft_choice_couples_with_the_target_packet(orc):
+    """Same candidates, scores and key as the target's coupled sampler: the draft
+    proposes exactly the token the target packet draws (the coupling the
+    reference relies on: key = absolute index of the proposed token)."""
+    rng = np.random.default_rng(89)
+    agree = 0
+    for trial in range(200):
+        bits = random_bits(rng, (1, 16), F16, 1.0)
+        x = decode(bits, F16)[0]
+        key = int(rng.integers(0, 10_000))
+        seed = int(rng.integers(1, 2**62))
+        temperature, top_k, top_p, min_p = 0.8, int(rng.choice([0, 5, 12])), 0.9, 0.02
+        out, _ = orc.sampled_packet(bits, F16, temperature, top_k, top_p, min_p, seed=seed, first_key=key)
+        smp = draft_sampling(1, inv_temperature=np.float32(1.0) / np.float32(temperature), top_k=top_k,
+                             top_p=top_p, min_p=min_p, seed=seed, key_base=key)
+        prop = orc.draft_choice(x.reshape(1, 1, 16), np.arange(16).reshape(1, 1, 16), smp, vocabulary=16)
+        agree += int(prop[0, 0] == out["token"][0])
+    assert agree == 200

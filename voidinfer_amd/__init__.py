@@ -8,11 +8,11 @@ falls back to a CPU implementation.
 from ._abi import (ABSENT_OCCURRENCE, BF16, F16, F32, FLAG_BAD_HISTORY, FLAG_EMPTY, FLAG_ERROR,  # noqa: F401
                    FLAG_NO_RESIDUAL, FLAG_NONFINITE, FLAG_ZERO_Q, GREEDY_ROW, LIB_PATH, ROUTE_ALL, ROUTE_FULL,
                    ROUTE_TOPK, ROW_PARAMS,
-                   SAMPLE_STATS, VERIFY_GREEDY, VERIFY_SAMPLED, DeviceSampling, VIError, load)
+                   SAMPLE_STATS, VERIFY_GREEDY, VERIFY_SAMPLED, DRAFT_SAMPLING, DeviceSampling, VIError, load)
 
 load()
 
-from .ops import (greedy_packet, params_array, presence_record, presence_reset, presence_truncate,  # noqa: E402,F401
+from .ops import (draft_choice, greedy_packet, params_array, presence_record, presence_reset, presence_truncate,  # noqa: E402,F401
                   probe_copy, probe_read, route_mask, row_scores, sample_rows, sampled_packet, sampled_scores, stats_numpy,
                   to_device_bytes, topk_rows,
                   verify_rows, workspace)

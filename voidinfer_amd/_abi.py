@@ -38,6 +38,14 @@ SAMPLE_STATS = np.dtype([
 assert GREEDY_ROW.itemsize == 16 and ROW_PARAMS.itemsize == 48 and SAMPLE_STATS.itemsize == 32
 
 
+DRAFT_SAMPLING = np.dtype([   # vi_draft_sampling == DraftSelectSampling (dflash2_draft.cu:2562-2572)
+    ("inv_temperature", "<f4"), ("top_p", "<f4"), ("min_p", "<f4"), ("top_k", "<i4"), ("seed", "<u8"),
+    ("key_base", "<i4"), ("reserved", "<i4"), ("presence_penalty", "<f4"), ("reserved2", "<i4"),
+    ("first_occurrence", "<u8"),
+])
+assert DRAFT_SAMPLING.itemsize == 48
+
+
 class DeviceSampling(C.Structure):
     """vi_device_sampling == Exl3DeviceSampling (src/exl3/sampled_select.h:17-28)."""
     _fields_ = [
@@ -67,6 +75,7 @@ SIGNATURES = {
     "vi_sampled_scores_workspace_bytes": ([_i, _i], _sz),
     "vi_sampled_scores": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, C.c_float, _vp, _vp, _vp, _vp,
                            _sz, _vp], _i),
+    "vi_draft_choice": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "vi_presence_reset": ([_vp, _i, _vp], _i),
     "vi_presence_truncate": ([_vp, _i, _i, _vp], _i),
     "vi_presence_record": ([_vp, _i, _i, _vp, _sz, _vp], _i),

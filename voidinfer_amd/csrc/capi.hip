@@ -125,6 +125,16 @@ vi_status vi_sampled_scores(const void* scores, int dtype, int rows, int vocabul
                                  gap, workspace, workspace_bytes, as_stream(stream));
 }
 
+vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float* scores, const int64_t* candidates,
+                          const int64_t* seed_tokens, const vi_draft_sampling* sampling, int64_t* proposals,
+                          void* stream) {
+    if (lanes == 0 || positions == 0) return VI_OK;
+    if (lanes < 0 || positions < 0 || vocabulary <= 0 || !scores || !candidates || !sampling || !proposals)
+        return VI_ERR_INVALID;
+    return launch_draft_choice(lanes, positions, vocabulary, scores, candidates, seed_tokens, sampling, proposals,
+                               as_stream(stream));
+}
+
 vi_status vi_presence_reset(int32_t* table, int vocabulary, void* stream) {
     if (!table || vocabulary <= 0) return VI_ERR_INVALID;
     return launch_presence_reset(table, vocabulary, as_stream(stream));

@@ -166,6 +166,25 @@ def sampled_scores(scores: torch.Tensor, next_tokens: torch.Tensor, temperature:
     return chosen, gap
 
 
+def draft_choice(scores: torch.Tensor, candidates: torch.Tensor, sampling: np.ndarray,
+                 seed_tokens: torch.Tensor | None = None, vocabulary: int = 248320) -> torch.Tensor:
+    """DFlash2 coupled proposals for every lane: scores f32 [lanes, positions, 16],
+    candidates int64 [lanes, positions, 16], sampling DRAFT_SAMPLING [lanes] (its
+    first_occurrence field a device address or 0) -> int64 [lanes, positions]."""
+    if scores.dim() != 3 or scores.shape[2] != 16 or candidates.shape != scores.shape:
+        raise ValueError("scores / candidates must be [lanes, positions, 16]")
+    lanes, positions, _ = scores.shape
+    dev = scores.device
+    sc = scores.to(torch.float32).contiguous()
+    cd = candidates.to(device=dev, dtype=torch.int64).contiguous()
+    st = None if seed_tokens is None else seed_tokens.to(device=dev, dtype=torch.int64).contiguous()
+    smp = to_device_bytes(np.ascontiguousarray(sampling, dtype=_abi.DRAFT_SAMPLING), dev)
+    out = torch.empty(lanes, positions, dtype=torch.int64, device=dev)
+    check(_lib().vi_draft_choice(lanes, positions, vocabulary, sc.data_ptr(), cd.data_ptr(), _ptr(st),
+                                 smp.data_ptr(), out.data_ptr(), _stream()), "vi_draft_choice")
+    return out
+
+
 def presence_reset(table: torch.Tensor) -> None:
     check(_lib().vi_presence_reset(table.data_ptr(), table.numel(), _stream()), "vi_presence_reset")
 
