@@ -216,6 +216,21 @@ vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float*
                           const int64_t* candidates, const int64_t* seed_tokens,
                           const vi_draft_sampling* sampling, int64_t* proposals, void* stream);
 
+/* ---- verification tree (host function, no device work) ---------------------
+ * Replaces exl3_build_verification_tree (src/exl3/verification_tree.h:44-112):
+ * a chain prefix of the drafts plus sibling leaves chosen to maximise
+ * (1 + expected accepted tokens) / (1 + row_cost * rows) from the draft's
+ * top-16 unary softmax.  Host pointers: drafts int64[depth]; candidate_ids
+ * int64[depth][16] and candidate_unary float[depth][16] in unary order (the
+ * top-16 output of vi_topk_rows after D2H); budget = verifier rows besides
+ * the anchor.  Outputs: *chain_drafts, and *sibling_count (<= budget) leaves
+ * in sibling_tokens / sibling_offsets (capacity `budget` each).  row_cost:
+ * the reference default is 0.0141 (0 for batched multi-agent rounds). */
+vi_status vi_build_verification_tree(const int64_t* drafts, int depth, const int64_t* candidate_ids,
+                                     const float* candidate_unary, int budget, int max_siblings, float row_cost,
+                                     int32_t* chain_drafts, int64_t* sibling_tokens, int32_t* sibling_offsets,
+                                     int32_t* sibling_count);
+
 /* ---- batched sampler (extended semantics) ----------------------------------
  * New batched entry for many lanes (the reference's packet stops at 16 rows,
  * sampled_select.cuh:200-216): per-row temperature, top-k, top-p, min-p,

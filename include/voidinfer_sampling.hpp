@@ -715,6 +715,125 @@ inline int exl3_promote_sibling(Exl3OuterDecision& decision, std::span<const std
     return -1;
 }
 
+// =====================================================================
+// Verification tree of a DFlash2 round — src/exl3/verification_tree.h:27-112.
+// A chain prefix of the drafts plus sibling leaves (the draft's next-best
+// candidates at each depth), chosen to maximise the expected committed tokens
+// per verifier round time (1 + E[accepted]) / (1 + row_cost * rows).  Node
+// acceptance comes from the draft's top-16 unary softmax: a chain token's hit
+// rate by its probability decile, a sibling's by its unary rank (1..3 among
+// the non-chain candidates) and decile, from the reference's measured tables.
+// =====================================================================
+
+struct Exl3VerificationTree {
+    int chain_drafts = 0;                   // chain rows 1..chain_drafts
+    std::vector<std::int64_t> sibling_tokens;
+    std::vector<int> sibling_offsets;       // logical offset (depth) of each leaf
+};
+
+// Row cost relative to the fixed verifier round, and the empirical hit-rate
+// tables (verification_tree.h:33-40; the values are the reference's data).
+inline constexpr float kExl3TreeRowCost = 0.0141f;
+inline constexpr std::array<float, 10> kExl3TreeChainHit{
+    0.32f, 0.38f, 0.35f, 0.44f, 0.42f, 0.49f, 0.57f, 0.67f, 0.78f, 0.97f};
+inline constexpr std::array<std::array<float, 10>, 3> kExl3TreeSiblingHit{{
+    {0.04f, 0.13f, 0.18f, 0.23f, 0.26f, 0.27f, 0.13f, 0.09f, 0.06f, 0.07f},
+    {0.03f, 0.10f, 0.15f, 0.09f, 0.12f, 0.12f, 0.12f, 0.12f, 0.12f, 0.12f},
+    {0.03f, 0.10f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f},
+}};
+
+// drafts: chain proposals at depths 1..D; candidate_ids / candidate_unary:
+// [D][16] in unary order (the draft's top-16); budget: verifier rows besides
+// the anchor.  The float arithmetic, the scan order over (rows, chain) and the
+// partial selection of the leaf pool follow the reference step for step: the
+// chosen tree, ties included, is part of the contract.  Candidate arrays
+// shorter than D x 16 are refused (std::invalid_argument).
+inline Exl3VerificationTree exl3_build_verification_tree(std::span<const std::int64_t> drafts,
+                                                         std::span<const std::int64_t> candidate_ids,
+                                                         std::span<const float> candidate_unary, int budget,
+                                                         int max_siblings, float row_cost = kExl3TreeRowCost) {
+    constexpr int kTop = 16, kRanks = 3;
+    const int depth = std::min(static_cast<int>(drafts.size()), budget);
+    if (depth > 0 && (candidate_ids.size() < std::size_t(depth) * kTop ||
+                      candidate_unary.size() < std::size_t(depth) * kTop))
+        throw std::invalid_argument("verification tree candidate extent");
+    struct Leaf {
+        float value;
+        int offset;
+        std::int64_t token;
+    };
+    const auto decile = [](float pr) { return std::clamp(static_cast<int>(pr * 10.0f), 0, 9); };
+    // per depth: the chain token's hit rate and up to three sibling leaves
+    std::vector<float> hit(std::size_t(std::max(depth, 0)));
+    std::vector<std::array<Leaf, kRanks>> leaf(std::size_t(std::max(depth, 0)));
+    for (int d = 0; d < depth; ++d) {
+        const std::int64_t* id = candidate_ids.data() + std::size_t(d) * kTop;
+        const float* un = candidate_unary.data() + std::size_t(d) * kTop;
+        const std::int64_t chain_token = drafts[std::size_t(d)];
+        const float top = *std::max_element(un, un + kTop);
+        std::array<float, kTop> w{};
+        float total = 0.0f;
+        for (int c = 0; c < kTop; ++c) total += w[std::size_t(c)] = std::exp(un[c] - top);
+        float chain_pr = 0.0f;   // (the last candidate carrying the chain token)
+        for (int c = 0; c < kTop; ++c)
+            if (id[c] == chain_token) chain_pr = w[std::size_t(c)] / total;
+        hit[std::size_t(d)] = kExl3TreeChainHit[std::size_t(decile(chain_pr))];
+        std::array<int, kTop> rank_order{};
+        for (int c = 0; c < kTop; ++c) rank_order[std::size_t(c)] = c;
+        std::stable_sort(rank_order.begin(), rank_order.end(), [&](int x, int y) { return un[x] > un[y]; });
+        int r = 0;
+        for (int i = 0; i < kTop && r < kRanks; ++i) {
+            const int c = rank_order[std::size_t(i)];
+            if (id[c] == chain_token) continue;
+            leaf[std::size_t(d)][std::size_t(r)] = {
+                kExl3TreeSiblingHit[std::size_t(r)][std::size_t(decile(w[std::size_t(c)] / total))], d + 1, id[c]};
+            ++r;
+        }
+        for (; r < kRanks; ++r) leaf[std::size_t(d)][std::size_t(r)] = {0.0f, d + 1, -1};
+    }
+    // per chain length: its expected accepted chain length and its leaf pool
+    // (each leaf weighted by the chain's survival down to its parent)
+    std::vector<float> chain_value(std::size_t(std::max(depth, 0)) + 1, 0.0f);
+    std::vector<std::vector<Leaf>> pool(std::size_t(std::max(depth, 0)) + 1);
+    for (int chain = 1; chain <= depth; ++chain) {
+        float survive = 1.0f, value = 0.0f;
+        auto& pl = pool[std::size_t(chain)];
+        for (int d = 0; d < chain; ++d) {
+            for (const Leaf& l : leaf[std::size_t(d)])
+                if (l.token >= 0) pl.push_back({survive * l.value, l.offset, l.token});
+            survive *= hit[std::size_t(d)];
+            value += survive;
+        }
+        chain_value[std::size_t(chain)] = value;
+    }
+    Exl3VerificationTree best;
+    float best_rate = -1.0f;
+    std::vector<Leaf> scratch;
+    for (int nodes = 1; nodes <= budget; ++nodes) {
+        for (int chain = std::max(1, nodes - std::max(0, max_siblings)); chain <= std::min(depth, nodes); ++chain) {
+            const int count = nodes - chain;
+            if (count > static_cast<int>(pool[std::size_t(chain)].size())) continue;
+            scratch = pool[std::size_t(chain)];
+            std::partial_sort(scratch.begin(), scratch.begin() + count, scratch.end(),
+                              [](const Leaf& x, const Leaf& y) { return x.value > y.value; });
+            float value = chain_value[std::size_t(chain)];
+            for (int i = 0; i < count; ++i) value += scratch[std::size_t(i)].value;
+            const float rate = (1.0f + value) / (1.0f + row_cost * static_cast<float>(nodes));
+            if (rate > best_rate) {
+                best_rate = rate;
+                best.chain_drafts = chain;
+                best.sibling_tokens.clear();
+                best.sibling_offsets.clear();
+                for (int i = 0; i < count; ++i) {
+                    best.sibling_tokens.push_back(scratch[std::size_t(i)].token);
+                    best.sibling_offsets.push_back(scratch[std::size_t(i)].offset);
+                }
+            }
+        }
+    }
+    return best;
+}
+
 // FP64 rejection sampling of one speculative position —
 // src/exl3/sampled_acceptance_reference.h:15-89.
 struct Exl3SampledAcceptanceOutcome {

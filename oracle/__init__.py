@@ -96,6 +96,7 @@ def lib() -> C.CDLL:
             "or_outer_prefix": ([vp, vp, i, vp, i, vp, vp, vp, vp, vp], i),
             "or_verify_rows": ([i, vp, i, i64, i, vp, i, i64, i, i, i, vp, vp, vp, i, vp, vp, vp, vp, vp, i], i),
             "or_row_distribution": ([vp, i, i, vp, vp, vp], i),
+            "or_build_verification_tree": ([vp, i, vp, vp, i, i, C.c_float, vp, vp, vp, vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -314,3 +315,46 @@ def verify_rows(mode: int, target: np.ndarray, tdtype: int, draft: np.ndarray | 
     if st:
         raise ValueError("oracle verify: invalid arguments")
     return acc, com, cnt, flg, margins
+
+
+def _tree_call(fn, drafts, candidate_ids, candidate_unary, budget: int, max_siblings: int, row_cost: float):
+    d = np.ascontiguousarray(drafts, dtype=np.int64)
+    ids = np.ascontiguousarray(candidate_ids, dtype=np.int64).reshape(-1)
+    un = np.ascontiguousarray(candidate_unary, dtype=np.float32).reshape(-1)
+    if ids.size < 16 * d.size or un.size < 16 * d.size:
+        raise ValueError("verification tree candidate extent")
+    cap = max(1, budget)
+    toks = np.zeros(cap, dtype=np.int64)
+    offs = np.zeros(cap, dtype=np.int32)
+    chain, n = np.zeros(1, dtype=np.int32), np.zeros(1, dtype=np.int32)
+    st = fn(_p(d), d.size, _p(ids), _p(un), budget, max_siblings, C.c_float(row_cost), _p(chain), _p(toks),
+            _p(offs), _p(n))
+    if st:
+        raise ValueError(f"verification tree status {st}")
+    return int(chain[0]), [int(t) for t in toks[: n[0]]], [int(o) for o in offs[: n[0]]]
+
+
+ROW_COST = 0.0141   # kExl3TreeRowCost (verification_tree.h:33)
+
+
+def build_verification_tree(drafts, candidate_ids, candidate_unary, budget: int, max_siblings: int,
+                            row_cost: float = ROW_COST):
+    """(chain_drafts, sibling_tokens, sibling_offsets) of the DFlash2 verification
+    tree (verification_tree.h:44-112)."""
+    return _tree_call(lib().or_build_verification_tree, drafts, candidate_ids, candidate_unary, budget,
+                      max_siblings, row_cost)
+
+
+def ref_build_verification_tree(drafts, candidate_ids, candidate_unary, budget: int, max_siblings: int,
+                                row_cost: float = ROW_COST):
+    """The same through the reference's own header compiled into oracle/_ref
+    (None when that library is not built)."""
+    if not REF_LIB_PATH.exists():
+        return None
+    ref = C.CDLL(str(REF_LIB_PATH))
+    fn = ref.ref_build_verification_tree
+    vp, i = C.c_void_p, C.c_int
+    fn.argtypes = [vp, i, vp, vp, i, i, C.c_float, vp, vp, vp, vp]
+    fn.restype = i
+    return _tree_call(fn, drafts, candidate_ids, candidate_unary, budget, max_siblings, row_cost)
+

@@ -759,6 +759,83 @@ int or_outer_prefix(const int64_t* target_path, const int64_t* tentative, int n,
 // batched sampler (no penalties).  Greedy mode = decide_exl3_outer_prefix over the
 // target rows' greedy packets; sampled mode = the FP64 acceptance rule above with
 // p, q the filtered distributions, the residual resampled in token-id order.
+// exl3_build_verification_tree (verification_tree.h:44-112), restated in the
+// reference's own loop shape: per depth the top-16 softmax in float, the chain
+// token's hit rate by decile (:53-68), up to three sibling leaves in stable
+// unary order skipping the chain token (:69-77); then every (rows, chain) pair
+// in order, the leaf pool rebuilt and partially sorted each time (:81-97), and
+// the first strict maximum of (1 + value) / (1 + row_cost * rows) kept (:99-109).
+int or_build_verification_tree(const int64_t* drafts, int depth_in, const int64_t* candidate_ids,
+                               const float* candidate_unary, int budget, int max_siblings, float row_cost,
+                               int* chain_drafts, int64_t* sibling_tokens, int* sibling_offsets, int* n_siblings) {
+    static const float kChainHit[10] = {0.32f, 0.38f, 0.35f, 0.44f, 0.42f, 0.49f, 0.57f, 0.67f, 0.78f, 0.97f};
+    static const float kSiblingHit[3][10] = {
+        {0.04f, 0.13f, 0.18f, 0.23f, 0.26f, 0.27f, 0.13f, 0.09f, 0.06f, 0.07f},
+        {0.03f, 0.10f, 0.15f, 0.09f, 0.12f, 0.12f, 0.12f, 0.12f, 0.12f, 0.12f},
+        {0.03f, 0.10f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f}};
+    if (depth_in < 0 || budget < 0) return 1;
+    const int depth = std::min(depth_in, budget);
+    struct Leaf { float value; int offset; int64_t token; };
+    auto decile = [](float pr) { int k = int(pr * 10.0f); return k < 0 ? 0 : (k > 9 ? 9 : k); };
+    std::vector<float> chain_hit(static_cast<size_t>(depth));
+    std::vector<Leaf> leaves(static_cast<size_t>(depth) * 3);
+    for (int d = 0; d < depth; ++d) {
+        const int64_t* ids = candidate_ids + size_t(d) * 16;
+        const float* un = candidate_unary + size_t(d) * 16;
+        float top = un[0];
+        for (int c = 1; c < 16; ++c) if (un[c] > top) top = un[c];
+        float p[16], sum = 0.0f;
+        for (int c = 0; c < 16; ++c) { p[c] = std::exp(un[c] - top); sum += p[c]; }
+        int order[16];
+        for (int c = 0; c < 16; ++c) order[c] = c;
+        std::stable_sort(order, order + 16, [&](int a, int b) { return un[a] > un[b]; });
+        float chain_p = 0.0f;
+        for (int c = 0; c < 16; ++c) if (ids[c] == drafts[d]) chain_p = p[c] / sum;
+        chain_hit[size_t(d)] = kChainHit[decile(chain_p)];
+        int rank = 0;
+        for (int i = 0; i < 16 && rank < 3; ++i) {
+            const int c = order[i];
+            if (ids[c] == drafts[d]) continue;
+            leaves[size_t(d) * 3 + size_t(rank)] = {kSiblingHit[rank][decile(p[c] / sum)], d + 1, ids[c]};
+            ++rank;
+        }
+        for (; rank < 3; ++rank) leaves[size_t(d) * 3 + size_t(rank)] = {0.0f, d + 1, -1};
+    }
+    float best_rate = -1.0f;
+    *chain_drafts = 0;
+    *n_siblings = 0;
+    for (int nodes = 1; nodes <= budget; ++nodes) {
+        for (int chain = std::max(1, nodes - std::max(0, max_siblings)); chain <= std::min(depth, nodes); ++chain) {
+            float survive = 1.0f, value = 0.0f;
+            std::vector<Leaf> pool;
+            for (int d = 0; d < chain; ++d) {
+                for (int r = 0; r < 3; ++r) {
+                    const Leaf& l = leaves[size_t(d) * 3 + size_t(r)];
+                    if (l.token >= 0) pool.push_back({survive * l.value, l.offset, l.token});
+                }
+                survive *= chain_hit[size_t(d)];
+                value += survive;
+            }
+            const int count = nodes - chain;
+            if (count > int(pool.size())) continue;
+            std::partial_sort(pool.begin(), pool.begin() + count, pool.end(),
+                              [](const Leaf& a, const Leaf& b) { return a.value > b.value; });
+            for (int i = 0; i < count; ++i) value += pool[size_t(i)].value;
+            const float rate = (1.0f + value) / (1.0f + row_cost * float(nodes));
+            if (rate > best_rate) {
+                best_rate = rate;
+                *chain_drafts = chain;
+                *n_siblings = count;
+                for (int i = 0; i < count; ++i) {
+                    sibling_tokens[i] = pool[size_t(i)].token;
+                    sibling_offsets[i] = pool[size_t(i)].offset;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
 int or_verify_rows(int mode, const void* target, int target_dtype, int64_t target_stride,
                    int target_rows, const void* draft, int draft_dtype, int64_t draft_stride,
                    int lanes, int drafts, int vocabulary, const int32_t* drafted,

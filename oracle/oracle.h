@@ -111,6 +111,12 @@ int or_outer_prefix(const int64_t* target_path, const int64_t* tentative, int n,
                     const int64_t* terminal, int n_terminal, int64_t* committed,
                     int* n_committed, int* accepted, int* rejected, int* stopped);
 
+/* DFlash2 verification tree (verification_tree.h:44-112): chain length and
+ * sibling leaves (tokens, offsets; *n_siblings of them, capacity `budget`). */
+int or_build_verification_tree(const int64_t* drafts, int depth, const int64_t* candidate_ids,
+                               const float* candidate_unary, int budget, int max_siblings, float row_cost,
+                               int* chain_drafts, int64_t* sibling_tokens, int* sibling_offsets, int* n_siblings);
+
 /* EXTENSION: lane verification (greedy prefix / sampled rejection with the
  * target distribution computed from logits), same arguments as
  * vi_verify_rows but host pointers. */

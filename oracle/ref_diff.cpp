@@ -14,6 +14,7 @@
 #include "exl3/sampling_policy.h"
 #include "exl3/sampling_window_transaction.h"
 #include "exl3/sampling_workspace_reservation.h"
+#include "exl3/verification_tree.h"
 #include "runtime/contract/sampling.h"
 
 #include "../include/voidinfer_sampling.hpp"
@@ -462,6 +463,33 @@ void diff_admission(Rng& g, long n) {
 
 }  // namespace
 
+// Verification trees: random top-16 candidate sets with planted ties (equal
+// unary values, repeated probability deciles), chain tokens inside or outside
+// the candidates, budgets 0..12, sibling caps -1..5, the default and zero row
+// costs.
+void diff_trees(Rng& g, long n) {
+    for (long i = 0; i < n; ++i) {
+        const int depth = g.below(9);
+        std::vector<std::int64_t> drafts(static_cast<std::size_t>(depth)), ids(static_cast<std::size_t>(depth) * 16);
+        std::vector<float> unary(static_cast<std::size_t>(depth) * 16);
+        for (int d = 0; d < depth; ++d) {
+            const int spread = 1 + g.below(4);
+            for (int c = 0; c < 16; ++c) {
+                ids[std::size_t(d) * 16 + std::size_t(c)] = 1000 + g.below(40);
+                unary[std::size_t(d) * 16 + std::size_t(c)] = g.coin(30) ? float(g.below(3)) : float(g.unit() * 6.0 * spread);
+            }
+            drafts[std::size_t(d)] = g.coin(80) ? ids[std::size_t(d) * 16 + std::size_t(g.below(16))] : 5;
+        }
+        const int budget = g.below(13), max_sib = g.below(7) - 1;
+        const float cost = g.coin(25) ? 0.0f : (g.coin(50) ? M::kExl3TreeRowCost : float(g.unit() * 0.2));
+        const auto a = M::exl3_build_verification_tree(drafts, ids, unary, budget, max_sib, cost);
+        const auto b = R::exl3_build_verification_tree(drafts, ids, unary, budget, max_sib, cost);
+        same(a.chain_drafts == b.chain_drafts, "tree chain", i);
+        same(a.sibling_tokens == b.sibling_tokens, "tree sibling tokens", i);
+        same(a.sibling_offsets == b.sibling_offsets, "tree sibling offsets", i);
+    }
+}
+
 int main(int argc, char** argv) {
     const long n = argc > 1 ? std::atol(argv[1]) : 20000;
     Rng g{0x5eed5eedULL};
@@ -471,6 +499,7 @@ int main(int argc, char** argv) {
     diff_windows(g, n / 20);
     diff_packets(g, n);
     diff_admission(g, n / 2);
+    diff_trees(g, n / 2);
     std::printf("ref_diff checks=%ld mismatches=%d\n", checks, mismatches);
     return mismatches ? 1 : 0;
 }

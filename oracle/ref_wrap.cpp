@@ -7,6 +7,7 @@
 #include "exl3/sampled_acceptance_reference.h"
 #include "exl3/sampling_policy.h"
 #include "exl3/sampling_window_transaction.h"
+#include "exl3/verification_tree.h"
 #include "runtime/contract/sampling.h"
 
 #include <cstdint>
@@ -146,6 +147,27 @@ int ref_window_script(uint64_t seed, const char* ops, size_t published, uint64_t
         *committed_prefix = s.committed_prefix();
         return 0;
     } catch (...) { return classify(); }
+}
+
+// exl3_build_verification_tree (verification_tree.h:44-112).
+int ref_build_verification_tree(const int64_t* drafts, int depth, const int64_t* ids, const float* unary,
+                                int budget, int max_siblings, float row_cost, int* chain_drafts,
+                                int64_t* sibling_tokens, int* sibling_offsets, int* n_siblings) {
+    try {
+        const size_t n = size_t(depth);
+        const Exl3VerificationTree t = exl3_build_verification_tree(
+            std::span<const std::int64_t>(drafts, n), std::span<const std::int64_t>(ids, n * 16),
+            std::span<const float>(unary, n * 16), budget, max_siblings, row_cost);
+        *chain_drafts = t.chain_drafts;
+        *n_siblings = int(t.sibling_tokens.size());
+        for (size_t i = 0; i < t.sibling_tokens.size(); ++i) {
+            sibling_tokens[i] = t.sibling_tokens[i];
+            sibling_offsets[i] = t.sibling_offsets[i];
+        }
+        return 0;
+    } catch (...) {
+        return classify();
+    }
 }
 
 }  // extern "C"

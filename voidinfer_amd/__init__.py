@@ -15,4 +15,4 @@ load()
 from .ops import (draft_choice, greedy_packet, params_array, presence_record, presence_reset, presence_truncate,  # noqa: E402,F401
                   probe_copy, probe_read, route_mask, row_scores, sample_rows, sampled_packet, sampled_scores, stats_numpy,
                   to_device_bytes, topk_rows,
-                  verify_rows, workspace)
+                  verification_tree, verify_rows, workspace)

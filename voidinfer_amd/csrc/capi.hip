@@ -1,9 +1,11 @@
 // capi.hip — the extern "C" boundary (include/voidinfer_sampling.h): argument
 // validation, workspace sizing and dispatch to the kernel translation units.
-// No exceptions cross it and nothing here allocates or synchronizes.
+// No exceptions cross it, and nothing here allocates device memory or
+// synchronizes.
 #include <string.h>
 
 #include "vi_internal.h"
+#include "../../include/voidinfer_sampling.hpp"
 
 using namespace vi;
 
@@ -133,6 +135,32 @@ vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float*
         return VI_ERR_INVALID;
     return launch_draft_choice(lanes, positions, vocabulary, scores, candidates, seed_tokens, sampling, proposals,
                                as_stream(stream));
+}
+
+vi_status vi_build_verification_tree(const int64_t* drafts, int depth, const int64_t* candidate_ids,
+                                     const float* candidate_unary, int budget, int max_siblings, float row_cost,
+                                     int32_t* chain_drafts, int64_t* sibling_tokens, int32_t* sibling_offsets,
+                                     int32_t* sibling_count) {
+    if (depth < 0 || budget < 0 || !chain_drafts || !sibling_count || (depth > 0 && (!drafts || !candidate_ids ||
+        !candidate_unary)) || (budget > 0 && (!sibling_tokens || !sibling_offsets)) || !std::isfinite(row_cost))
+        return VI_ERR_INVALID;
+    try {   // (the host layer's implementation; nothing throws across the ABI)
+        const std::size_t n = std::size_t(depth);
+        const voidinfer_amd::Exl3VerificationTree t = voidinfer_amd::exl3_build_verification_tree(
+            std::span<const int64_t>(drafts, n), std::span<const int64_t>(candidate_ids, n * 16),
+            std::span<const float>(candidate_unary, n * 16), budget, max_siblings, row_cost);
+        *chain_drafts = t.chain_drafts;
+        *sibling_count = int32_t(t.sibling_tokens.size());
+        for (std::size_t i = 0; i < t.sibling_tokens.size(); ++i) {
+            sibling_tokens[i] = t.sibling_tokens[i];
+            sibling_offsets[i] = t.sibling_offsets[i];
+        }
+        return VI_OK;
+    } catch (const std::invalid_argument&) {
+        return VI_ERR_INVALID;
+    } catch (...) {
+        return VI_ERR_UNSUPPORTED;
+    }
 }
 
 vi_status vi_presence_reset(int32_t* table, int vocabulary, void* stream) {

@@ -12,6 +12,8 @@ HIP kernel of the library.  Function names follow the reference's launchers:
 ``verify_rows``             decide_exl3_outer_prefix / IndependentAcceptanceReference,
                             on the device (exact_outer_reference.h:68,
                             sampled_acceptance_reference.h:48)
+``verification_tree``       exl3_build_verification_tree (src/exl3/verification_tree.h:44),
+                            a host function of the library
 =========================  ==========================================================
 
 Workspaces: each entry point and shape owns a zero-initialised workspace (its
@@ -301,3 +303,25 @@ def probe_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
 def probe_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
     check(_lib().vi_probe_copy(dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size(), _stream()),
           "vi_probe_copy")
+
+
+def verification_tree(drafts: Sequence[int], candidate_ids, candidate_unary, budget: int, max_siblings: int,
+                      row_cost: float = 0.0141):
+    """DFlash2 verification tree from the draft's top-16 (host arrays): chain
+    length, sibling tokens and their offsets (depths).  candidate_ids /
+    candidate_unary: [depth, 16] in unary order (vi_topk_rows' output)."""
+    d = np.ascontiguousarray(drafts, dtype=np.int64)
+    ids = np.ascontiguousarray(candidate_ids, dtype=np.int64).reshape(-1)
+    un = np.ascontiguousarray(candidate_unary, dtype=np.float32).reshape(-1)
+    if ids.size < 16 * d.size or un.size < 16 * d.size:
+        raise ValueError("candidate arrays must be [depth, 16]")
+    cap = max(1, int(budget))
+    toks = np.zeros(cap, dtype=np.int64)
+    offs = np.zeros(cap, dtype=np.int32)
+    chain, n = np.zeros(1, dtype=np.int32), np.zeros(1, dtype=np.int32)
+    vp = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    check(_lib().vi_build_verification_tree(vp(d), d.size, vp(ids), vp(un), int(budget), int(max_siblings),
+                                            C.c_float(row_cost), vp(chain), vp(toks), vp(offs), vp(n)),
+          "vi_build_verification_tree")
+    return int(chain[0]), [int(t) for t in toks[: n[0]]], [int(o) for o in offs[: n[0]]]
+
