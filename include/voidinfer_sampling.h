@@ -256,6 +256,47 @@ vi_status vi_sample_rows(const void* logits, int dtype, int rows, int vocabulary
                          int64_t probs_stride, vi_sample_stats* stats, uint32_t route_mask,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- per-lane penalty state --------------------------------------------------
+ * Occurrence counts of each lane's generated tokens, kept current on the device
+ * so that the sampler reads them instead of scanning the lane's history at
+ * every step.  Generalizes the reference's incremental first-occurrence table
+ * (exl3_presence_reset / _truncate / _record, src/exl3/sampled_select.h:33-35,
+ * src/exl3/text_model.cu:12139-12173, driven by PresenceTrack::sync,
+ * src/exl3/exl3_engine_core.cpp:106-133) from presence to counts, which the
+ * repetition and frequency penalties need.
+ *
+ * One lane's state is vi_penalty_state_bytes(vocabulary, slots) bytes; `states`
+ * holds `lanes` of them back to back (lane l at l * bytes), in device memory.
+ * slots: power of two >= 64, at least twice the distinct tokens a lane records
+ * between resets (a removed token keeps its slot).  reset: every lane empty.
+ * update: sign +1 records, -1 removes, per lane the tokens
+ * tokens[offsets[l] .. offsets[l+1]) (device int32 / int64 arrays), or, with
+ * offsets NULL, the single token tokens[l] (a negative one is skipped: the
+ * sampler's output of a failed row).  Recording a token outside
+ * [0, vocabulary) sets VI_FLAG_BAD_HISTORY on the lane (the token is ignored,
+ * as in a history); a full table or removing a token that is not there sets
+ * VI_FLAG_ERROR.  Both flags stay until reset and are reported by every row
+ * that takes penalties from the lane (such a row fails on ERROR).  Calls on one set of
+ * states run in stream order; vocabulary and slots must be the same in every
+ * call on a state, the sampler's included. */
+size_t vi_penalty_state_bytes(int vocabulary, int slots);
+vi_status vi_penalty_state_reset(void* states, int lanes, int vocabulary, int slots, void* stream);
+vi_status vi_penalty_state_update(void* states, int lanes, int vocabulary, int slots, const int32_t* tokens,
+                                  const int64_t* offsets, int sign, void* stream);
+/* vi_sample_rows with the penalties taken from the lanes' penalty states (row r
+ * uses lane r's state) instead of histories: results are those of vi_sample_rows
+ * over any history with the same occurrence counts.  record = 1 also appends
+ * each row's sampled token (when it is in [0, vocabulary)) to its lane's state,
+ * in the same launch: a decode step is then one call.  Workspace:
+ * vi_sample_workspace_bytes(rows, vocabulary, 0).  A full-route row with
+ * penalties fails (token -1, VI_FLAG_ERROR) when its lane holds more than
+ * 32,768 distinct recorded tokens in one half of the vocabulary or a count
+ * above 65,535 there; top-k-route rows have neither limit. */
+vi_status vi_sample_rows_state(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                               const vi_row_params* params, void* states, int slots, int record, int32_t* tokens,
+                               double* uniforms, float* probs, int64_t probs_stride, vi_sample_stats* stats,
+                               uint32_t route_mask, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- DFlash2 verification ---------------------------------------------------
  * Replaces the host decisions decide_exl3_outer_prefix
  * (src/exl3/exact_outer_reference.h:68-82) in greedy mode and

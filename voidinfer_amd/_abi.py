@@ -77,6 +77,11 @@ SIGNATURES = {
                            _sz, _vp], _i),
     "vi_draft_choice": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "vi_build_verification_tree": ([_vp, _i, _vp, _vp, _i, _i, C.c_float, _vp, _vp, _vp, _vp], _i),
+    "vi_penalty_state_bytes": ([_i, _i], _sz),
+    "vi_penalty_state_reset": ([_vp, _i, _i, _i, _vp], _i),
+    "vi_penalty_state_update": ([_vp, _i, _i, _i, _vp, _vp, _i, _vp], _i),
+    "vi_sample_rows_state": ([_vp, _i, _i, _i, _i64, _vp, _vp, _i, _i, _vp, _vp, _vp, _i64, _vp, _u32, _vp, _sz,
+                              _vp], _i),
     "vi_presence_reset": ([_vp, _i, _vp], _i),
     "vi_presence_truncate": ([_vp, _i, _i, _vp], _i),
     "vi_presence_record": ([_vp, _i, _i, _vp, _sz, _vp], _i),

@@ -199,6 +199,44 @@ vi_status vi_sample_rows(const void* logits, int dtype, int rows, int vocabulary
     return launch_sample(a, workspace, workspace_bytes, as_stream(stream));
 }
 
+size_t vi_penalty_state_bytes(int vocabulary, int slots) {
+    if (vocabulary <= 0 || !penalty_slots_ok(slots)) return 0;
+    return penalty_layout(vocabulary, slots).lane_bytes;
+}
+
+vi_status vi_penalty_state_reset(void* states, int lanes, int vocabulary, int slots, void* stream) {
+    if (lanes == 0) return VI_OK;
+    if (lanes < 0 || !states || vocabulary <= 0 || !penalty_slots_ok(slots)) return VI_ERR_INVALID;
+    return launch_penalty_reset(states, lanes, penalty_layout(vocabulary, slots), as_stream(stream));
+}
+
+vi_status vi_penalty_state_update(void* states, int lanes, int vocabulary, int slots, const int32_t* tokens,
+                                  const int64_t* offsets, int sign, void* stream) {
+    if (lanes == 0) return VI_OK;
+    if (lanes < 0 || !states || !tokens || vocabulary <= 0 || !penalty_slots_ok(slots) || (sign != 1 && sign != -1))
+        return VI_ERR_INVALID;
+    return launch_penalty_update(states, lanes, vocabulary, penalty_layout(vocabulary, slots), tokens, offsets, sign,
+                                 as_stream(stream));
+}
+
+vi_status vi_sample_rows_state(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                               const vi_row_params* params, void* states, int slots, int record, int32_t* tokens,
+                               double* uniforms, float* probs, int64_t probs_stride, vi_sample_stats* stats,
+                               uint32_t route_mask, void* workspace, size_t workspace_bytes, void* stream) {
+    if (rows == 0) return VI_OK;
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !dtype_ok(dtype) || !logits || !params ||
+        !tokens || !states || !penalty_slots_ok(slots) || (probs && probs_stride < vocabulary) ||
+        (record != 0 && record != 1))
+        return VI_ERR_INVALID;
+    SampleArgs a{};
+    a.logits = logits; a.dtype = dtype; a.rows = rows; a.vocabulary = vocabulary; a.stride = row_stride;
+    a.params = params; a.pstate = static_cast<unsigned char*>(states);
+    a.playout = penalty_layout(vocabulary, slots); a.record = record;
+    a.tokens = tokens; a.uniforms = uniforms; a.probs = probs; a.probs_stride = probs_stride; a.stats = stats;
+    a.route_mask = route_mask == 0 ? uint32_t(VI_ROUTE_ALL) : route_mask;
+    return launch_sample(a, workspace, workspace_bytes, as_stream(stream));
+}
+
 size_t vi_verify_workspace_bytes(int lanes, int drafts, int vocabulary) {
     if (lanes <= 0 || drafts <= 0 || vocabulary <= 0) return 0;
     return verify_workspace(lanes, drafts, vocabulary);

@@ -36,6 +36,7 @@
 // V x 2 + L x 4 bytes per row (logits once, history once per pair via L2).
 #include <math.h>
 
+#include "penalty_state.h"
 #include "vi_device.h"
 #include "vi_internal.h"
 
@@ -59,6 +60,9 @@ constexpr int kHistMax = 32768;           // history tokens per row
 constexpr int kList3 = 4096;              // list capacity; a longer list takes a second pass
 constexpr int kOffB2 = 65536, kOffL3 = kOffB2 + 4 * 4096;
 constexpr int kHT = kHistMax / kFT;       // history tokens per thread
+// state route: the first kStage repeat-list entries are staged in LDS [64, 96) KiB
+// (the one-pass counting's region, unused on this route) before the row arrives
+constexpr int kStage = 4096, kOffStage = kOffB2;
 constexpr int kDR = kHistMax / kFT;       // dense ranks (distinct history tokens) per thread
 constexpr int kBmapWords = kVecMax * 8 / 32;
 
@@ -94,6 +98,9 @@ struct FullArgs {
     const vi_row_params* params;
     const int32_t* histories;
     const int64_t* offsets;
+    unsigned char* pstate;   // per-lane penalty states instead of histories (or null)
+    PenaltyLayout pl;
+    int record;              // append the sampled token to the lane's state
     int32_t* tokens;
     double* uniforms;
     float* probs;            // optional; doubles as scratch for penalized bits
@@ -236,6 +243,12 @@ __device__ __forceinline__ uint32_t match_mask8(const uint4& v, uint32_t key) {
 
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
+// A lane state's sticky flags as this kernel's header bits.
+__device__ __forceinline__ uint32_t state_flags(const unsigned char* lstate) {
+    const uint32_t f = reinterpret_cast<const PenaltyHeader*>(lstate)->flags;
+    return ((f & VI_FLAG_BAD_HISTORY) ? kHdrBadHistory : 0u) | ((f & VI_FLAG_ERROR) ? kHdrError : 0u);
+}
+
 template <int DT, bool kDense>
 __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kDense ? kLdsDense : kLdsGeneral];
@@ -259,10 +272,35 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     const int vid0 = h0 + head;                          // token id of vector 0, element 0
 
     if (tid == 0) { sh.ovf_n = 0; sh.flags = 0; sh.top1 = 0; sh.n_sum = 0; sh.n_fin = 0; }
-    const int64_t hb = a.offsets ? a.offsets[row] : 0;
-    const int64_t hn = a.offsets ? a.offsets[row + 1] - hb : 0;
-    const bool pen = penalties_active(p) && hn > 0 && a.histories;
-    const int32_t* hist = pen ? a.histories + hb : nullptr;
+    // penalties from the lane's penalty state (bitmaps and hash) or from its history
+    const unsigned char* lstate = a.pstate ? a.pstate + size_t(row) * a.pl.lane_bytes : nullptr;
+    const int64_t hb = (!lstate && a.offsets) ? a.offsets[row] : 0;
+    const int64_t hn = (!lstate && a.offsets) ? a.offsets[row + 1] - hb : 0;
+    const bool pen = penalties_active(p) && (lstate || (hn > 0 && a.histories));
+    const int32_t* hist = (pen && !lstate) ? a.histories + hb : nullptr;
+    // state route: this half's presence bitmap words 4 * tid .. 4 * tid + 3 and
+    // repeat-list entries q * kFT + tid (the first kStage, zero past the list's
+    // end), requested before the row: they are consumed first, and a wave's
+    // loads complete in the order they were issued
+    uint32_t sb1[4] = {0u, 0u, 0u, 0u};
+    uint2 le[kStage / kFT];
+    if constexpr (kDense) {
+        if (pen && lstate) {
+            const uint32_t* b1 = reinterpret_cast<const uint32_t*>(lstate + a.pl.off_b1) + (h0 >> 5);
+            const uint2* list = reinterpret_cast<const uint2*>(lstate + a.pl.off_list);
+            const int nw = (n_el + 31) >> 5;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int w = 4 * tid + q;
+                if (w < nw) sb1[q] = b1[w];
+            }
+#pragma unroll
+            for (int q = 0; q < kStage / kFT; ++q) {
+                const int k = q * kFT + tid;
+                le[q] = k < a.pl.slots ? list[k] : make_uint2(0u, 0u);
+            }
+        }
+    }
 
     // ---- issue every load of this half up front (one HBM read of the row)
     // Branch-free: out-of-range slots re-load the half's last vector (an L2
@@ -363,12 +401,27 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             // falls back to a second pass over the history.
             uint32_t* bmap2 = lds32 + kOffB2 / 4;
             uint32_t* list3 = lds32 + kOffL3 / 4;
-            for (int w = tid; w < kBmapWords + 4; w += kFT) bmap[w] = 0u;
-            for (int w = tid; w < kBmapWords; w += kFT) bmap2[w] = 0u;
             if (tid == 0) sh.n3 = 0u;
+            if (lstate) {   // the state's bitmap (the last word masked to the half), the staged list
+                const int nw = (n_el + 31) >> 5;
+                const uint32_t lastm = (n_el & 31) ? (1u << (n_el & 31)) - 1u : ~0u;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int w = 4 * tid + q;
+                    bmap[w] = sb1[q] & (w == nw - 1 ? lastm : ~0u);
+                }
+                if (tid < 4) bmap[kBmapWords + tid] = 0u;
+                uint2* stage = reinterpret_cast<uint2*>(lds + kOffStage);
+#pragma unroll
+                for (int q = 0; q < kStage / kFT; ++q) stage[q * kFT + tid] = le[q];
+                if (tid == 0) atomicOr(&sh.flags, state_flags(lstate));
+            } else {
+                for (int w = tid; w < kBmapWords + 4; w += kFT) bmap[w] = 0u;
+                for (int w = tid; w < kBmapWords; w += kFT) bmap2[w] = 0u;
+            }
             __syncthreads();
             if (tid == 0 && hn > kHistMax) atomicOr(&sh.flags, kHdrError);   // callers promise hn <= max_history
-            {
+            if (!lstate) {
                 // rounds of kHR tokens per thread; each stage's LDS atomics of a
                 // round are issued together (their results are awaited once)
                 constexpr int kHR = 8;
@@ -424,6 +477,17 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) { c4[k] = __builtin_popcount(bmap[4 * tid + k]); s4 += c4[k]; }
             uint32_t ex = block_exclusive_scan_u32<kFT>(s4, sh.u, &n_flag);
+            if (n_flag > uint32_t(kHistMax)) {   // (uniform; state route only) more distinct tokens than
+                // the dense ranks hold: the row fails, and the rest runs as if without history
+                if (tid == 0) atomicOr(&sh.flags, kHdrError);
+                n_flag = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { bmap[4 * tid + k] = 0u; c4[k] = 0; }
+#pragma unroll
+                for (int k = 0; k < kFV / 4; ++k) vfl[k] = 0u;
+                fl_head = fl_tail = false;
+                ex = 0;
+            }
 #pragma unroll
             for (int k = 0; k < 4; ++k) { pref[4 * tid + k] = uint16_t(ex); ex += c4[k]; }
             __syncthreads();
@@ -432,7 +496,27 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             const uint32_t n3 = sh.n3;
             if (n3 <= uint32_t(kList3)) {   // (uniform) counts from the bitmaps, then the list, by rank
                 uint16_t* c16 = reinterpret_cast<uint16_t*>(lds);
-                walk_words([&](uint32_t rank, int off) { c16[rank] = uint16_t(1u + ((bmap2[off >> 5] >> (off & 31)) & 1u)); });
+                if (lstate) {   // count 1 by rank, then the repeat list's counts (>= 2) of this half's tokens
+                    walk_words([&](uint32_t rank, int off) { c16[rank] = uint16_t(1u); });
+                    __syncthreads();
+                    auto put = [&](uint2 e) {
+                        const int off = int(e.x) - h0;
+                        if (e.y < 2u || off < 0 || off >= n_el) return;
+                        const int w = off >> 5;
+                        if (!((bmap[w] >> (off & 31)) & 1u) || e.y > 0xffffu) {   // inconsistent / too many
+                            atomicOr(&sh.flags, kHdrError);
+                            return;
+                        }
+                        c16[pref[w] + __builtin_popcount(bmap[w] & ((1u << (off & 31)) - 1u))] = uint16_t(e.y);
+                    };
+                    const uint2* stage = reinterpret_cast<const uint2*>(lds + kOffStage);
+                    for (int k = tid; k < kStage; k += kFT) put(stage[k]);
+                    const int nrep = int(min(reinterpret_cast<const PenaltyHeader*>(lstate)->nrep, uint32_t(a.pl.slots)));
+                    const uint2* list = reinterpret_cast<const uint2*>(lstate + a.pl.off_list);
+                    for (int k = kStage + tid; k < nrep; k += kFT) put(list[k]);
+                } else {
+                    walk_words([&](uint32_t rank, int off) { c16[rank] = uint16_t(1u + ((bmap2[off >> 5] >> (off & 31)) & 1u)); });
+                }
                 __syncthreads();
                 for (uint32_t k = tid; k < n3; k += kFT) {
                     const int off = int(list3[k]), w = off >> 5;
@@ -1174,6 +1258,10 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             else if (s == kFV + 1) token = vid0 + nvec * 8 + tid;
             else token = vid0 + ((s - 1) * kFT + tid) * 8 + j;
             a.tokens[row] = token;
+            if (a.record) {   // both halves have read the state (they passed the pair barrier)
+                const LaneState ls = lane_state(a.pstate + size_t(row) * a.pl.lane_bytes, a.pl);
+                state_publish(ls, state_apply(ls, a.pl, V, token, 1));
+            }
             if (a.uniforms) a.uniforms[row] = sh.draw_u;
             if (a.stats) {
                 vi_sample_stats st{};
@@ -1291,12 +1379,15 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary;
     a.half_len = (((s.vocabulary + 1) / 2) + 63) / 64 * 64;
     a.stride = s.stride; a.params = s.params; a.histories = s.histories; a.offsets = s.offsets;
+    if (s.pstate) {
+        a.pstate = s.pstate; a.pl = s.playout; a.record = s.record;
+    }
     a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
     a.stats = s.stats;
     const int groups = (s.rows + 7) / 8;
     const dim3 grid(groups * 16);
     // histories up to kHistMax tokens: dense penalty path; longer: general path
-    const bool dense = s.max_history <= kHistMax;
+    const bool dense = s.pstate || s.max_history <= kHistMax;
     if (s.dtype == VI_BF16) launch_full_dt<VI_BF16>(a, dense, grid, stream);
     else launch_full_dt<VI_F16>(a, dense, grid, stream);
     vi_status st = launch_status();

@@ -20,6 +20,7 @@
 // per row; the per-element work is a compare and a ballot.
 #include <math.h>
 
+#include "penalty_state.h"
 #include "row_scan.h"
 #include "vi_internal.h"
 
@@ -72,6 +73,9 @@ struct TopkArgs {
     int hash_shift;         // 32 - log2(hash_slots)
     int hash_slots;
     const int64_t* offsets;
+    unsigned char* pstate;   // per-lane penalty states (hash and flags) instead of the above
+    PenaltyLayout pl;
+    int record;              // append each row's sampled token to its lane's state
     int32_t* tokens;
     double* uniforms;
     float* probs;
@@ -117,18 +121,6 @@ __device__ __forceinline__ void list_offer(WaveList& L, int K, bool ok, float v,
         const int ci = readlane_i(id, src);
         if (better(cv, ci, L.kv, L.ki)) list_insert(L, K, cv, ci);
     }
-}
-
-// Count of `token` in the row's history hash (0 if absent).
-__device__ __forceinline__ uint32_t hash_count(const uint2* table, int shift, int slots, int token) {
-    uint32_t s = (uint32_t(token) * 0x9E3779B1u) >> shift;
-    for (int probe = 0; probe < slots; ++probe) {
-        const uint2 e = table[s];
-        if (e.x == uint32_t(token) + 1u) return e.y;
-        if (e.x == 0u) return 0u;
-        s = (s + 1u) & uint32_t(slots - 1);
-    }
-    return 0u;
 }
 
 // Largest finite magnitude a penalty could push past the dtype's range.
@@ -341,10 +333,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             return;
         }
         if (p.temperature > 0.0f) { K = p.top_k; inv_t = 1.0f / p.temperature; }
-        const int64_t hn = a.offsets ? a.offsets[r + 1] - a.offsets[r] : 0;
-        lookups = penalties_active(p) && hn > 0 && a.hash;
+        if (a.pstate) {
+            lookups = penalties_active(p);
+            if (lookups) table = reinterpret_cast<const uint2*>(a.pstate + size_t(r) * a.pl.lane_bytes + a.pl.off_hash);
+        } else {
+            const int64_t hn = a.offsets ? a.offsets[r + 1] - a.offsets[r] : 0;
+            lookups = penalties_active(p) && hn > 0 && a.hash;
+            if (lookups) table = a.hash + size_t(r) * size_t(a.hash_slots);
+        }
         lookup_all = lookups && !penalties_lower_only(p);
-        if (lookups) table = a.hash + size_t(r) * size_t(a.hash_slots);
         if (a.probs) {
             float* pr = a.probs + size_t(r) * size_t(a.probs_stride);
             for (int i = begin + threadIdx.x; i < end; i += kTopkThreads) pr[i] = 0.0f;
@@ -528,7 +525,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         if (lane == 0) {
             uint32_t flags_out = 0;
             if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
-            if (lookups) flags_out |= a.row_flags[r];
+            if (lookups)
+                flags_out |= a.pstate ? reinterpret_cast<const PenaltyHeader*>(a.pstate + size_t(r) * a.pl.lane_bytes)->flags
+                                      : a.row_flags[r];
             if (flags_out & VI_FLAG_ERROR) {
                 a.tokens[r] = -1;
                 if (a.uniforms) a.uniforms[r] = 0.0;
@@ -541,6 +540,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             sample_finish(p, cap, s_val[0], s_idx[0], a.vocabulary, &a.tokens[r],
                           a.uniforms ? &a.uniforms[r] : nullptr, pr, a.stats ? &a.stats[r] : nullptr,
                           flags_out, c, s_w);
+            if (a.record) {   // every slice of this row has finished reading the state (last arriver)
+                const int32_t t = a.tokens[r];
+                if (t >= 0 && t < a.vocabulary) {
+                    const LaneState ls = lane_state(a.pstate + size_t(r) * a.pl.lane_bytes, a.pl);
+                    state_publish(ls, state_apply(ls, a.pl, a.vocabulary, t, 1));
+                }
+            }
         }
     }
 }
@@ -716,7 +722,10 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
     uint2* hash = nullptr;
     uint32_t* row_flags = c.take<uint32_t>(size_t(s.rows));
     int slots = 0, shift = 0;
-    if (s.max_history > 0 && s.histories && s.offsets) {
+    if (s.pstate) {   // the lanes' own hashes
+        slots = s.playout.slots;
+        shift = s.playout.shift;
+    } else if (s.max_history > 0 && s.histories && s.offsets) {
         slots = int(history_hash_slots(s.max_history));
         shift = 32 - __builtin_ctz(unsigned(slots));
         hash = c.take<uint2>(size_t(s.rows) * slots);
@@ -737,6 +746,7 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
         a.params = s.params; a.hash = hash; a.row_flags = row_flags; a.hash_shift = shift; a.hash_slots = slots;
         a.offsets = s.offsets;
+        a.pstate = s.pstate; a.pl = s.playout; a.record = s.record;
         a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
         a.stats = s.stats;
         // fp32 logits / unaligned rows: full-route rows fail loudly in the top-k launch

@@ -180,6 +180,18 @@ __device__ __forceinline__ bool penalties_active(const vi_row_params& p) {
 __device__ __forceinline__ bool penalties_lower_only(const vi_row_params& p) {
     return p.repetition_penalty >= 1.0f && p.presence_penalty >= 0.0f && p.frequency_penalty >= 0.0f;
 }
+// Count of `token` in a (token + 1, count) open-addressing hash with linear
+// probing from (token * 0x9E3779B1) >> shift (0 if absent).
+__device__ __forceinline__ uint32_t hash_count(const uint2* table, int shift, int slots, int token) {
+    uint32_t s = (uint32_t(token) * 0x9E3779B1u) >> shift;
+    for (int probe = 0; probe < slots; ++probe) {
+        const uint2 e = table[s];
+        if (e.x == uint32_t(token) + 1u) return e.y;
+        if (e.x == 0u) return 0u;
+        s = (s + 1u) & uint32_t(slots - 1);
+    }
+    return 0u;
+}
 // Rows served by the top-k kernel family: argmax rows and 1 <= top_k <= 64.
 __device__ __forceinline__ bool topk_route(const vi_row_params& p) {
     return !(p.temperature > 0.0f) || (p.top_k >= 1 && p.top_k <= 64);

@@ -82,6 +82,48 @@ size_t topk_partials_bytes_slices(int rows, int slices);
 // History hash (token -> count) per row for the top-k sampler route.
 size_t history_hash_slots(int64_t max_history);
 
+// ---- per-lane penalty state --------------------------------------------------
+// One lane's state, at lane * lane_bytes: a 64-byte header (flags as VI_FLAG_*
+// bits, sticky until reset; keys = hash slots holding a token; total = tokens
+// recorded minus tokens removed; nrep = repeat-list entries), a presence
+// bitmap of ceil(V / 32) words (rounded up to 16 bytes), an open-addressing
+// hash of (token + 1, count) pairs with linear probing from
+// (token * 0x9E3779B1) >> (32 - log2 slots), per slot the 1-based index of the
+// slot's token in the repeat list (0: none), and the repeat list: one
+// (token, count) entry per token that has reached count 2 since the reset, in
+// the order they did, holding the token's current count (an entry whose count
+// fell below 2 is kept and ignored).  A removed token keeps its slot (count 0),
+// so probe chains stay intact.
+struct PenaltyHeader {
+    uint32_t flags, keys;
+    uint64_t total;
+    uint32_t nrep;
+    uint32_t pad[11];
+};
+static_assert(sizeof(PenaltyHeader) == 64, "penalty header");
+struct PenaltyLayout {
+    size_t lane_bytes, off_b1, off_hash, off_ridx, off_list;
+    int words, slots, shift;
+};
+inline bool penalty_slots_ok(int slots) {
+    return slots >= 64 && slots <= (1 << 26) && (slots & (slots - 1)) == 0;
+}
+inline PenaltyLayout penalty_layout(int vocabulary, int slots) {
+    PenaltyLayout l{};
+    l.words = int(align_up((size_t(vocabulary) + 31) / 32, 4));
+    l.slots = slots;
+    l.shift = 32 - __builtin_ctz(unsigned(slots));
+    l.off_b1 = sizeof(PenaltyHeader);
+    l.off_hash = align_up(l.off_b1 + 4 * size_t(l.words), 64);
+    l.off_ridx = l.off_hash + 8 * size_t(slots);
+    l.off_list = l.off_ridx + 4 * size_t(slots);
+    l.lane_bytes = align_up(l.off_list + 8 * size_t(slots), 256);
+    return l;
+}
+vi_status launch_penalty_reset(void* states, int lanes, const PenaltyLayout& l, hipStream_t stream);
+vi_status launch_penalty_update(void* states, int lanes, int vocabulary, const PenaltyLayout& l,
+                                const int32_t* tokens, const int64_t* offsets, int sign, hipStream_t stream);
+
 struct SampleArgs {
     const void* logits;
     int dtype, rows, vocabulary;
@@ -90,6 +132,9 @@ struct SampleArgs {
     const int32_t* histories;
     const int64_t* offsets;
     int64_t max_history;
+    unsigned char* pstate;   // per-lane penalty states instead of histories (or null)
+    PenaltyLayout playout;
+    int record;              // append each row's sampled token to its lane's state
     int32_t* tokens;
     double* uniforms;
     float* probs;

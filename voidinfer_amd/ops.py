@@ -260,6 +260,68 @@ def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor,
     return o
 
 
+class PenaltyState:
+    """Per-lane occurrence counts on the device (vi_penalty_state_*): lane l's
+    state is bytes [l * lane_bytes, (l + 1) * lane_bytes) of one uint8 tensor."""
+
+    def __init__(self, lanes: int, vocabulary: int, slots: int = 65536, device="cuda"):
+        self.lanes, self.vocabulary, self.slots = lanes, vocabulary, slots
+        self.lane_bytes = _lib().vi_penalty_state_bytes(vocabulary, slots)
+        if self.lane_bytes == 0:
+            raise ValueError("slots must be a power of two >= 64")
+        self.buf = torch.empty(lanes * self.lane_bytes, dtype=torch.uint8, device=device)
+        self.reset()
+
+    def reset(self) -> None:
+        check(_lib().vi_penalty_state_reset(self.buf.data_ptr(), self.lanes, self.vocabulary, self.slots,
+                                            _stream()), "vi_penalty_state_reset")
+
+    def update(self, tokens: torch.Tensor, offsets: torch.Tensor | None = None, sign: int = 1) -> None:
+        """Record (sign +1) or remove (-1) tokens[offsets[l]:offsets[l+1]] per lane,
+        or tokens[l] per lane without offsets (negative tokens skipped)."""
+        if tokens.dtype != torch.int32 or (offsets is not None and offsets.dtype != torch.int64):
+            raise ValueError("tokens must be int32 (offsets int64)")
+        check(_lib().vi_penalty_state_update(self.buf.data_ptr(), self.lanes, self.vocabulary, self.slots,
+                                             tokens.data_ptr(), _ptr(offsets), sign, _stream()),
+              "vi_penalty_state_update")
+
+    def header(self) -> np.ndarray:
+        """(flags, keys, total) per lane."""
+        h = self.buf.view(self.lanes, self.lane_bytes)[:, :16].cpu().numpy()
+        return np.stack([h[:, 0:4].copy().view(np.uint32)[:, 0], h[:, 4:8].copy().view(np.uint32)[:, 0],
+                         h[:, 8:16].copy().view(np.uint64)[:, 0].astype(np.int64)], axis=1)
+
+
+def sample_rows_state(logits: torch.Tensor, params: np.ndarray | torch.Tensor, state: PenaltyState,
+                      record: bool = False, want_probs: bool = False, want_stats: bool = True,
+                      want_uniforms: bool = True, outputs: SampleOutputs | None = None,
+                      routes: int | None = None) -> SampleOutputs:
+    """The batched sampler with penalties from `state` (row r uses lane r); with
+    `record`, each row's sampled token is also recorded in its lane's state."""
+    dtype, rows, vocab, stride = _rows_view(logits, None)
+    if rows > state.lanes or vocab != state.vocabulary:
+        raise ValueError("penalty state has too few lanes or another vocabulary")
+    dev = logits.device
+    if routes is None:
+        routes = _abi.ROUTE_ALL if isinstance(params, torch.Tensor) else route_mask(params)
+    p_dev = params if isinstance(params, torch.Tensor) else to_device_bytes(params, dev)
+    o = outputs
+    if o is None:
+        o = SampleOutputs(
+            torch.empty(rows, dtype=torch.int32, device=dev),
+            torch.empty(rows, dtype=torch.float64, device=dev) if want_uniforms else None,
+            torch.empty(rows, vocab, dtype=torch.float32, device=dev) if want_probs else None,
+            torch.empty(rows * SAMPLE_STATS.itemsize, dtype=torch.uint8, device=dev) if want_stats else None)
+    nb = _lib().vi_sample_workspace_bytes(rows, vocab, 0)
+    ws = workspace(("sample", rows, vocab, 0), nb, dev)
+    check(_lib().vi_sample_rows_state(logits.data_ptr(), dtype, rows, vocab, stride, p_dev.data_ptr(),
+                                      state.buf.data_ptr(), state.slots, int(record), o.tokens.data_ptr(),
+                                      _ptr(o.uniforms),
+                                      _ptr(o.probs), vocab, _ptr(o.stats), routes, ws.data_ptr(), ws.numel(),
+                                      _stream()), "vi_sample_rows_state")
+    return o
+
+
 def stats_numpy(stats: torch.Tensor) -> np.ndarray:
     return stats.cpu().numpy().view(SAMPLE_STATS)
 
