@@ -4,13 +4,24 @@
 Workload (configuration 5, the headline metric's shape): 128 rows x 248,320 bf16 logits,
 near-flat N(0, 0.1), top_k off, top_p 0.95, repetition / presence / frequency
 penalties over 32,768-token int32 histories, an independent Philox stream per row.
-One step = one ``vi_sample_rows`` call over all 128 rows (all rows take the
-full-vocabulary route: exactly one kernel launch).  Five distinct input sets
-(~402 MB) rotate across steps so the 256 MB Infinity Cache cannot serve repeats.
+Five distinct input sets (~402 MB of logits) rotate across steps so the 256 MB
+Infinity Cache cannot serve repeats.
 
-Prints ONE JSON line: rows/s (whole job), achieved HBM GB/s of the kernel against
-MI355X's 8 TB/s peak (per-launch HIP events on the launch stream), the oracle's
-CPU rate on the same inputs, and a GPU-vs-oracle parity count for one step.
+One step is one decode step of all 128 lanes, a single kernel launch (every row
+takes the full-vocabulary route):
+
+* ``--route state`` (default): ``vi_sample_rows_state`` with record = 1.  Each
+  lane's penalties come from its device penalty state (presence bitmap, count
+  hash, repeat list), built from the lane's 32,768-token history before timing,
+  as the histories themselves are; every step also records the sampled token in
+  the state, so the lane's history grows by one token per step as in decoding.
+* ``--route history``: ``vi_sample_rows`` over the int32 histories.
+
+With the state route, the history route is also timed (``--compare-steps``) and
+reported beside it.  Prints ONE JSON line: rows/s (whole job), achieved HBM GB/s
+of the kernel against MI355X's 8 TB/s peak (per-launch HIP events on the launch
+stream), the oracle's CPU rate on the same inputs, and a GPU-vs-oracle parity
+count for one step.
 """
 from __future__ import annotations
 
@@ -27,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "sampled rows/sec + achieved HBM GB/s (% peak) at 128×248,320 bf16 logits"
 PEAK_GBPS = 8000.0
 ROWS, VOCAB, HISTORY, SETS = 128, 248_320, 32_768, 5
+SLOTS = 65_536   # penalty-state hash slots per lane (>= 2 x distinct tokens)
 
 
 def parse():
@@ -35,6 +47,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--rows", type=int, default=ROWS)
+    ap.add_argument("--route", choices=("state", "history"), default="state")
+    ap.add_argument("--compare-steps", type=int, default=200,
+                    help="steps of the history route timed beside the state route (0: none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
@@ -68,10 +83,10 @@ def calibrate_copy():
                                       "vi_probe_copy": {"bytes_written_per_launch": 1 << 28, "launches": 5}}}))
 
 
-def traffic_from_profiles() -> float | None:
-    """HBM bytes per launch of the full-vocabulary kernel, from the rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes recorded in profiles/ (None if absent)."""
-    f = ROOT / "profiles" / "full_kernel_config5_traffic.md"
+def traffic_from_profiles(route: str) -> float | None:
+    """HBM bytes per launch of the full-vocabulary kernel on `route`, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/ (None if absent)."""
+    f = ROOT / "profiles" / f"full_kernel_config5_{route}_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -119,41 +134,86 @@ def main():
     lib = vi.load()
     tokens = torch.empty(rows, dtype=torch.int32, device=dev)
     stats = torch.empty(rows * 32, dtype=torch.uint8, device=dev)
-    nb = lib.vi_sample_workspace_bytes(rows, VOCAB, HISTORY)
-    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     sptr = stream.cuda_stream
-    calls = []
-    for logits, hist, offs, _, p_dev in sets:
-        calls.append((logits.data_ptr(), 0, rows, VOCAB, VOCAB, p_dev.data_ptr(), hist.data_ptr(), offs.data_ptr(),
-                      HISTORY, tokens.data_ptr(), None, None, VOCAB, stats.data_ptr(), routes, ws.data_ptr(), nb,
-                      sptr))
-    fn = lib.vi_sample_rows
+    nb_h = lib.vi_sample_workspace_bytes(rows, VOCAB, HISTORY)
+    ws_h = torch.zeros(nb_h, dtype=torch.uint8, device=dev)
+    hist_calls = [(lg.data_ptr(), 0, rows, VOCAB, VOCAB, pd.data_ptr(), h.data_ptr(), o.data_ptr(), HISTORY,
+                   tokens.data_ptr(), None, None, VOCAB, stats.data_ptr(), routes, ws_h.data_ptr(), nb_h, sptr)
+                  for lg, h, o, _, pd in sets]
 
-    for i in range(args.warmup):
-        st = fn(*calls[i % SETS])
-        assert st == 0, st
+    def hist_step(i):
+        return lib.vi_sample_rows(*hist_calls[i % SETS])
+
+    state_info = None
+    if args.route == "state":
+        print("[bench] building the lanes' penalty states from the histories", file=sys.stderr, flush=True)
+        states = []
+        for _, h, o, _, _ in sets:
+            st = vi.PenaltyState(rows, VOCAB, SLOTS, device=dev)
+            st.update(h, o)
+            states.append(st)
+        hdr = states[0].header()
+        assert (hdr[:, 0] == 0).all() and (hdr[:, 2] == HISTORY).all(), hdr[:4]
+        nrep = int(np.frombuffer(states[0].buf.view(rows, states[0].lane_bytes)[:, 16:20].cpu().numpy().tobytes(),
+                                 dtype=np.uint32).mean())
+        nb_s = lib.vi_sample_workspace_bytes(rows, VOCAB, 0)
+        ws_s = torch.zeros(nb_s, dtype=torch.uint8, device=dev)
+
+        def state_args(i, record):
+            lg, _, _, _, pd = sets[i % SETS]
+            return (lg.data_ptr(), 0, rows, VOCAB, VOCAB, pd.data_ptr(), states[i % SETS].buf.data_ptr(), SLOTS,
+                    record, tokens.data_ptr(), None, None, VOCAB, stats.data_ptr(), routes, ws_s.data_ptr(), nb_s,
+                    sptr)
+        state_calls = [state_args(i, 1) for i in range(SETS)]
+
+        def step(i):
+            return lib.vi_sample_rows_state(*state_calls[i % SETS])
+        # bytes per launch: the logits, the presence bitmap and the repeat list (8 B per entry)
+        bytes_per_row = VOCAB * 2 + (VOCAB + 31) // 32 * 4 + 8 * nrep
+        state_info = {"slots": SLOTS, "lane_bytes": states[0].lane_bytes, "repeat_list_mean": nrep,
+                      "record": "each step records its sampled tokens in the lanes' states (same launch)"}
+        # parity input: set 0's states before anything is recorded
+        assert lib.vi_sample_rows_state(*state_args(0, 0)) == 0
+    else:
+        step = hist_step
+        bytes_per_row = VOCAB * 2 + HISTORY * 4
+        assert hist_step(0) == 0
     torch.cuda.synchronize()
+    gpu_tok = tokens.cpu().numpy().copy()
+
+    def timed(fn, K, warmup):
+        for i in range(warmup):
+            st = fn(i)
+            assert st == 0, st
+        torch.cuda.synchronize()
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(K):
+            starts[i].record(stream)
+            fn(i)
+            ends[i].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per_launch = np.array([starts[i].elapsed_time(ends[i]) for i in range(K)])
+        return starts[0].elapsed_time(ends[-1]) / K, per_launch, wall
 
     K = args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-    print(f"[bench] timing {K} steps", file=sys.stderr, flush=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(K):
-        starts[i].record(stream)
-        fn(*calls[i % SETS])
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_launch_ms = np.array([starts[i].elapsed_time(ends[i]) for i in range(K)])
-    total_ms = starts[0].elapsed_time(ends[-1])
-    ms_per_step = total_ms / K
-    rows_per_s = rows * K / (total_ms / 1e3)
+    print(f"[bench] timing {K} steps ({args.route} route)", file=sys.stderr, flush=True)
+    ms_per_step, per_launch_ms, wall = timed(step, K, args.warmup)
+    rows_per_s = rows / (ms_per_step / 1e3)
     kernel_ms = float(per_launch_ms.mean())
-    bytes_per_launch = rows * (VOCAB * 2 + HISTORY * 4)
+    bytes_per_launch = rows * bytes_per_row
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
+    history_route = None
+    if args.route == "state" and args.compare_steps > 0:
+        print(f"[bench] timing {args.compare_steps} steps of the history route", file=sys.stderr, flush=True)
+        h_ms, h_launch, _ = timed(hist_step, args.compare_steps, 20)
+        history_route = {"ms_per_step": h_ms, "rows_per_s": rows / (h_ms / 1e3),
+                         "kernel_ms": float(h_launch.mean()),
+                         "bytes_per_launch": rows * (VOCAB * 2 + HISTORY * 4), "steps": args.compare_steps}
 
     # stream-read probe (measured HBM read rate) over a 1 GiB buffer
     probe = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -170,11 +230,9 @@ def main():
     probe_gbps = (1 << 30) * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9
     del probe
 
-    # parity of one step against the CPU oracle, and the CPU baseline on the same inputs
+    # parity of the first step (set 0, before any recording) against the CPU
+    # oracle, and the CPU baseline on the same inputs
     logits0, hist0, offs0, p0, p0_dev = sets[0]
-    fn(*calls[0])
-    torch.cuda.synchronize()
-    gpu_tok = tokens.cpu().numpy().copy()
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -215,12 +273,14 @@ def main():
         "config": {"workload": "config5: 128 lanes x 248,320 bf16 logits N(0,0.1), top_k off, top_p 0.95, "
                                "rep/presence/frequency penalties over 32,768-token histories, Philox per row",
                    "rows": rows, "vocabulary": VOCAB, "history": HISTORY, "input_sets": SETS,
+                   "route": args.route, "penalty_state": state_info,
                    "kernel": "full_kernel<bf16> (voidinfer_amd/csrc/sample_full.hip)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / PEAK_GBPS, "traffic": traffic_from_profiles(),
+                     "frac": achieved / PEAK_GBPS, "traffic": traffic_from_profiles(args.route),
                      "bytes_per_launch": bytes_per_launch, "kernel_ms": kernel_ms,
                      "kernel_ms_p50": float(np.median(per_launch_ms)),
                      "probe_read_gbps": probe_gbps, "frac_of_probe": achieved / probe_gbps},
+        "history_route": history_route,
         "cpu_baseline": cpu,
         "parity": parity,
         "host_wall_s": wall,
