@@ -216,6 +216,23 @@ vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float*
                           const int64_t* candidates, const int64_t* seed_tokens,
                           const vi_draft_sampling* sampling, int64_t* proposals, void* stream);
 
+/* Fused selector chain; replaces dflash_selector_fused_chain_kernel
+ * (src/exl3/dflash2_draft.cu:2615-2678), batched over lanes.  Lane l's anchor
+ * starts at anchors[l]; at each position p the score of candidate c is
+ * unary[l][p][c] + sum over r < 256 of pred[anchor][r] * hidden[l][p][r] *
+ * succ[candidates[l][p][c]][r] (fp16 codebooks pred / succ [vocabulary][256],
+ * fp16 hidden [lanes][positions][256], fp32 arithmetic reduced in the
+ * reference's order), the first maximum is proposed and becomes the anchor.  A
+ * lane whose sampling record has inv_temperature > 0 (sampling may be NULL: all
+ * greedy) proposes by the coupled sampled choice over the unary scores instead,
+ * as vi_draft_choice does, with anchors[l] as its seed token.  An anchor or a
+ * candidate outside [0, vocabulary) ends the lane's chain: that position and
+ * every later one get -1.  All pointers are device memory. */
+vi_status vi_selector_chain(int lanes, int positions, int vocabulary, const int64_t* anchors,
+                            const int64_t* candidates, const float* unary, const void* hidden,
+                            const void* pred_codebook, const void* succ_codebook,
+                            const vi_draft_sampling* sampling, int64_t* proposals, void* stream);
+
 /* ---- verification tree (host function, no device work) ---------------------
  * Replaces exl3_build_verification_tree (src/exl3/verification_tree.h:44-112):
  * a chain prefix of the drafts plus sibling leaves chosen to maximise

@@ -91,6 +91,7 @@ def lib() -> C.CDLL:
             "or_sampled_scores": ([vp, i, i, i, i64, C.POINTER(DeviceSampling), i, C.c_float, vp, vp, vp], i),
             "or_row_scores": ([vp, i, i, i, i64, vp, vp, vp], i),
             "or_draft_choice": ([i, i, i, vp, vp, vp, vp, vp], i),
+            "or_selector_chain": ([i, i, i, vp, vp, vp, vp, vp, vp, vp, vp], i),
             "or_sample_rows": ([vp, i, i, i, i64, vp, vp, vp, vp, vp, vp, i64, vp, vp, i], i),
             "or_accept": ([vp, vp, i64, u32, d, d, C.POINTER(AcceptOutcome), vp], i),
             "or_outer_prefix": ([vp, vp, i, vp, i, vp, vp, vp, vp, vp], i),
@@ -228,6 +229,28 @@ def draft_choice(scores: np.ndarray, candidates: np.ndarray, sampling: np.ndarra
     out = np.zeros((lanes, positions), dtype=np.int64)
     if lib().or_draft_choice(lanes, positions, vocabulary, _p(sc), _p(cd), _p(st), _p(smp), _p(out)):
         raise ValueError("oracle draft choice: invalid arguments")
+    return out
+
+
+def selector_chain(anchors, candidates, unary, hidden, pred_codebook, succ_codebook, sampling=None,
+                   vocabulary: int | None = None) -> np.ndarray:
+    """Fused selector chain: anchors int64 [lanes], candidates int64 / unary f32
+    [lanes, positions, 16], hidden fp16 bits [lanes, positions, 256], codebooks fp16
+    bits [vocabulary, 256], sampling DRAFT_SAMPLING [lanes] or None -> int64
+    [lanes, positions]."""
+    lanes, positions, _ = candidates.shape
+    vocabulary = pred_codebook.shape[0] if vocabulary is None else vocabulary
+    an = np.ascontiguousarray(anchors, dtype=np.int64)
+    cd = np.ascontiguousarray(candidates, dtype=np.int64)
+    un = np.ascontiguousarray(unary, dtype=np.float32)
+    hd = np.ascontiguousarray(hidden, dtype=np.uint16)
+    pc = np.ascontiguousarray(pred_codebook, dtype=np.uint16)
+    sc = np.ascontiguousarray(succ_codebook, dtype=np.uint16)
+    smp = None if sampling is None else np.ascontiguousarray(sampling, dtype=DRAFT_SAMPLING)
+    out = np.zeros((lanes, positions), dtype=np.int64)
+    if lib().or_selector_chain(lanes, positions, vocabulary, _p(an), _p(cd), _p(un), _p(hd), _p(pc), _p(sc),
+                               _p(smp), _p(out)):
+        raise ValueError("oracle selector chain: invalid arguments")
     return out
 
 

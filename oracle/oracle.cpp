@@ -615,6 +615,68 @@ int or_draft_choice(int lanes, int positions, int vocabulary, const float* score
     return VI_OK;
 }
 
+// dflash_selector_fused_chain_kernel (src/exl3/dflash2_draft.cu:2615-2678):
+// candidate c's selector value is reduced as 32 lanes of 8 products each
+// (lane `sub` holds ranks sub + 32k), r[k] += r[k+4], r[k] += r[k+2],
+// r[0] + r[1] per lane (:2640-2651), then a shuffle-down tree over offsets
+// 16 .. 1 (:2652-2653); score = unary + value (:2655-2656); the first maximum
+// is proposed and becomes the anchor (:2659-2673).  A sampled lane takes
+// dflash_sampled_choice over the unary scores (:2661-2666), which is
+// or_draft_choice with those scores and the initial anchor as seed token.
+int or_selector_chain(int lanes, int positions, int vocabulary, const int64_t* anchors, const int64_t* candidates,
+                      const float* unary, const uint16_t* hidden, const uint16_t* pred_codebook,
+                      const uint16_t* succ_codebook, const vi_draft_sampling* sampling, int64_t* proposals) {
+    if (lanes < 0 || positions < 0 || vocabulary <= 0 || !anchors || !candidates || !unary || !hidden ||
+        !pred_codebook || !succ_codebook || !proposals)
+        return VI_ERR_INVALID;
+    constexpr int K = 16, R = 256;
+    for (int l = 0; l < lanes; ++l) {
+        int64_t* out = proposals + size_t(l) * positions;
+        int64_t anchor = anchors[l];
+        bool bad = anchor < 0 || anchor >= vocabulary;
+        const bool sampled = sampling && sampling[l].inv_temperature > 0.0f;
+        std::vector<int64_t> chain(size_t(positions), 0);
+        if (sampled && !bad) {
+            // the sampled proposals do not depend on the anchors; the chain ends at
+            // the first position holding an invalid candidate
+            or_draft_choice(1, positions, vocabulary, unary + size_t(l) * positions * K,
+                            candidates + size_t(l) * positions * K, &anchors[l], &sampling[l], chain.data());
+        }
+        for (int pos = 0; pos < positions; ++pos) {
+            const size_t at = size_t(l) * positions + pos;
+            const int64_t* cd = candidates + at * K;
+            for (int c = 0; c < K; ++c) bad = bad || cd[c] < 0 || cd[c] >= vocabulary;
+            if (bad) { out[pos] = -1; continue; }
+            if (sampled) { out[pos] = chain[size_t(pos)]; continue; }
+            float score[K];
+            for (int c = 0; c < K; ++c) {
+                float lane_v[32];
+                for (int sub = 0; sub < 32; ++sub) {
+                    float r[8];
+                    for (int k = 0; k < 8; ++k) {
+                        const int rank = sub + 32 * k;
+                        const float a = or_decode(VI_F16, pred_codebook[size_t(anchor) * R + rank]);
+                        const float h = or_decode(VI_F16, hidden[at * R + rank]);
+                        const float b = or_decode(VI_F16, succ_codebook[size_t(cd[c]) * R + rank]);
+                        r[k] = a * h * b;
+                    }
+                    for (int k = 0; k < 4; ++k) r[k] += r[k + 4];
+                    for (int k = 0; k < 2; ++k) r[k] += r[k + 2];
+                    lane_v[sub] = r[0] + r[1];
+                }
+                for (int off = 16; off > 0; off >>= 1)
+                    for (int sub = 0; sub < off; ++sub) lane_v[sub] += lane_v[sub + off];
+                score[c] = unary[at * K + c] + lane_v[0];
+            }
+            int best = 0;
+            for (int c = 1; c < K; ++c) if (score[c] > score[best]) best = c;
+            out[pos] = cd[best];
+            anchor = cd[best];
+        }
+    }
+    return VI_OK;
+}
+
 // exact_row_score_kernel (text_model.cu:11393-11420): argmax over the values
 // that compare greater than -Inf (NaN and -Inf never win, +Inf can), lowest
 // index on ties, index = vocabulary when none; gap = max - logit(next) for a

@@ -76,6 +76,11 @@ int or_sampled_scores(const void* scores, int dtype, int rows, int vocabulary, i
                       int64_t* chosen, float* gap);
 /* DFlash2 draft coupled proposal (dflash_sampled_choice, dflash2_draft.cu:2554-2610);
  * host pointers (first_occurrence included), layouts as vi_draft_choice. */
+/* Fused selector chain (dflash_selector_fused_chain_kernel, dflash2_draft.cu:2615-2678), layouts as
+ * vi_selector_chain; fp16 arrays as uint16 bit patterns; sampling may be NULL. */
+int or_selector_chain(int lanes, int positions, int vocabulary, const int64_t* anchors, const int64_t* candidates,
+                      const float* unary, const uint16_t* hidden, const uint16_t* pred_codebook,
+                      const uint16_t* succ_codebook, const vi_draft_sampling* sampling, int64_t* proposals);
 int or_draft_choice(int lanes, int positions, int vocabulary, const float* scores, const int64_t* candidates,
                     const int64_t* seed_tokens, const vi_draft_sampling* sampling, int64_t* proposals);
 /* VeriCache exact row scores (exact_row_score_kernel, text_model.cu:11393-11420). */

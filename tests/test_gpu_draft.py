@@ -1,5 +1,6 @@
-"""GPU DFlash2 draft coupled proposals (vi_draft_choice) vs the CPU oracle
-(dflash_sampled_choice, dflash2_draft.cu:2554-2610).
+"""GPU DFlash2 draft coupled proposals (vi_draft_choice) and the fused selector
+chain (vi_selector_chain) vs the CPU oracle (dflash_sampled_choice,
+dflash2_draft.cu:2554-2610; dflash_selector_fused_chain_kernel, :2615-2678).
 
 Proposals equal position by position; a lane may differ only where the
 oracle's decision sat within float rounding of a boundary (the two best
@@ -76,3 +77,61 @@ def test_draft_choice_rejects_invalid(dev):
     assert lib.vi_draft_choice(0, 4, 100, None, None, None, None, None, None) == 0      # nothing to do
     assert lib.vi_draft_choice(2, 4, 100, None, None, None, None, None, None) == 1      # null arrays
     assert lib.vi_draft_choice(-1, 4, 100, None, None, None, None, None, None) == 1
+
+
+def _chain_case(rng, lanes, positions, vocab):
+    anchors = rng.integers(0, vocab, lanes).astype(np.int64)
+    cands = np.stack([np.stack([rng.choice(vocab, 16, replace=False) for _ in range(positions)])
+                      for _ in range(lanes)]).astype(np.int64)
+    unary = (rng.standard_normal((lanes, positions, 16)) * 2).astype(np.float32)
+    f16 = lambda shape: rng.standard_normal(shape).astype(np.float16)   # noqa: E731
+    return anchors, cands, unary, f16((lanes, positions, 256)), f16((vocab, 256)), f16((vocab, 256))
+
+
+def _run_chain(dev, anchors, cands, unary, hidden, pred, succ, smp=None):
+    import voidinfer_amd as vi
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)   # noqa: E731
+    got = vi.selector_chain(t(anchors), t(cands), t(unary), t(hidden), t(pred), t(succ), smp)
+    torch.cuda.synchronize()
+    return got.cpu().numpy()
+
+
+def test_selector_chain_vs_oracle(orc, dev):
+    """Greedy lanes bit-exact (the reference's reduction order on both sides);
+    sampled lanes equal up to a position within rounding of a boundary; invalid
+    ids end a lane's chain."""
+    import voidinfer_amd as vi
+    rng = np.random.default_rng(77)
+    lanes, positions, vocab = 24, 16, 30_000
+    anchors, cands, unary, hidden, pred, succ = _chain_case(rng, lanes, positions, vocab)
+    anchors[5] = -1
+    cands[3, 9, 4] = vocab
+    cands[:, 1:, 2] = anchors[:, None]          # the seed token keeps coming back (presence penalty)
+    smp = np.zeros(lanes, dtype=vi.DRAFT_SAMPLING)
+    sampled = np.arange(lanes) % 3 == 0
+    smp["inv_temperature"] = np.where(sampled, 1 / 0.8, 0.0)
+    smp["top_k"], smp["top_p"], smp["min_p"] = 10, 0.9, 0.0
+    smp["seed"] = rng.integers(1, 2**62, lanes)
+    smp["key_base"] = rng.integers(0, 100_000, lanes)
+    smp["presence_penalty"] = 0.5
+    hb, pb, sb = hidden.view(np.uint16), pred.view(np.uint16), succ.view(np.uint16)
+    got = _run_chain(dev, anchors, cands, unary, hidden, pred, succ, smp)
+    want = orc.selector_chain(anchors, cands, unary, hb, pb, sb, smp)
+    assert (want[5] == -1).all() and (want[3, 9:] == -1).all()
+    for l in range(lanes):
+        if not sampled[l]:
+            assert np.array_equal(got[l], want[l]), l
+            continue
+        for p in range(positions):
+            if got[l, p] != want[l, p]:
+                assert near_boundary(orc, unary[l, p], cands[l, p], smp[l], int(smp["key_base"][l]) + p), (l, p)
+                break
+
+
+def test_selector_chain_full_vocabulary_greedy(orc, dev):
+    rng = np.random.default_rng(78)
+    anchors, cands, unary, hidden, pred, succ = _chain_case(rng, 4, 16, 248_320)
+    got = _run_chain(dev, anchors, cands, unary, hidden, pred, succ)
+    want = orc.selector_chain(anchors, cands, unary, hidden.view(np.uint16), pred.view(np.uint16),
+                              succ.view(np.uint16))
+    assert np.array_equal(got, want)

@@ -14,6 +14,6 @@ load()
 
 from .ops import (PenaltyState, draft_choice, greedy_packet, params_array, presence_record, presence_reset,  # noqa: E402,F401
                   presence_truncate, probe_copy, probe_read, route_mask, row_scores, sample_rows, sample_rows_state,
-                  sampled_packet, sampled_scores, stats_numpy,
+                  sampled_packet, sampled_scores, selector_chain, stats_numpy,
                   to_device_bytes, topk_rows,
                   verification_tree, verify_rows, workspace)

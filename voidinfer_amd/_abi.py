@@ -76,6 +76,7 @@ SIGNATURES = {
     "vi_sampled_scores": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, C.c_float, _vp, _vp, _vp, _vp,
                            _sz, _vp], _i),
     "vi_draft_choice": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "vi_selector_chain": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "vi_build_verification_tree": ([_vp, _i, _vp, _vp, _i, _i, C.c_float, _vp, _vp, _vp, _vp], _i),
     "vi_penalty_state_bytes": ([_i, _i], _sz),
     "vi_penalty_state_reset": ([_vp, _i, _i, _i, _vp], _i),

@@ -137,6 +137,18 @@ vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float*
                                as_stream(stream));
 }
 
+vi_status vi_selector_chain(int lanes, int positions, int vocabulary, const int64_t* anchors,
+                            const int64_t* candidates, const float* unary, const void* hidden,
+                            const void* pred_codebook, const void* succ_codebook,
+                            const vi_draft_sampling* sampling, int64_t* proposals, void* stream) {
+    if (lanes == 0 || positions == 0) return VI_OK;
+    if (lanes < 0 || positions < 0 || vocabulary <= 0 || !anchors || !candidates || !unary || !hidden ||
+        !pred_codebook || !succ_codebook || !proposals)
+        return VI_ERR_INVALID;
+    return launch_selector_chain(lanes, positions, vocabulary, anchors, candidates, unary, hidden, pred_codebook,
+                                 succ_codebook, sampling, proposals, as_stream(stream));
+}
+
 vi_status vi_build_verification_tree(const int64_t* drafts, int depth, const int64_t* candidate_ids,
                                      const float* candidate_unary, int budget, int max_siblings, float row_cost,
                                      int32_t* chain_drafts, int64_t* sibling_tokens, int32_t* sibling_offsets,

@@ -179,6 +179,10 @@ vi_status launch_probe_copy(void* dst, const void* src, size_t bytes, hipStream_
 vi_status launch_draft_choice(int lanes, int positions, int vocabulary, const float* scores,
                               const int64_t* candidates, const int64_t* seed_tokens,
                               const vi_draft_sampling* sampling, int64_t* proposals, hipStream_t stream);
+vi_status launch_selector_chain(int lanes, int positions, int vocabulary, const int64_t* anchors,
+                                const int64_t* candidates, const float* unary, const void* hidden,
+                                const void* pred_codebook, const void* succ_codebook,
+                                const vi_draft_sampling* sampling, int64_t* proposals, hipStream_t stream);
 vi_status launch_presence_reset(int32_t* table, int vocabulary, hipStream_t stream);
 vi_status launch_presence_truncate(int32_t* table, int vocabulary, int from, hipStream_t stream);
 vi_status launch_presence_record(int32_t* table, int vocabulary, int first, const int64_t* tokens,

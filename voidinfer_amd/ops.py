@@ -187,6 +187,35 @@ def draft_choice(scores: torch.Tensor, candidates: torch.Tensor, sampling: np.nd
     return out
 
 
+def selector_chain(anchors: torch.Tensor, candidates: torch.Tensor, unary: torch.Tensor, hidden: torch.Tensor,
+                   pred_codebook: torch.Tensor, succ_codebook: torch.Tensor, sampling: np.ndarray | None = None,
+                   vocabulary: int | None = None) -> torch.Tensor:
+    """Fused selector chain (vi_selector_chain): anchors int64 [lanes], candidates
+    int64 / unary f32 [lanes, positions, 16], hidden fp16 [lanes, positions, 256],
+    codebooks fp16 [vocabulary, 256], sampling DRAFT_SAMPLING [lanes] or None ->
+    proposals int64 [lanes, positions]."""
+    if candidates.dim() != 3 or candidates.shape[2] != 16 or unary.shape != candidates.shape:
+        raise ValueError("candidates / unary must be [lanes, positions, 16]")
+    lanes, positions, _ = candidates.shape
+    if hidden.shape != (lanes, positions, 256) or hidden.dtype != torch.float16:
+        raise ValueError("hidden must be fp16 [lanes, positions, 256]")
+    vocab = pred_codebook.shape[0] if vocabulary is None else vocabulary
+    for cb in (pred_codebook, succ_codebook):
+        if cb.dtype != torch.float16 or cb.dim() != 2 or cb.shape[1] != 256 or cb.shape[0] < vocab:
+            raise ValueError("codebooks must be fp16 [vocabulary, 256]")
+    dev = candidates.device
+    an = anchors.to(device=dev, dtype=torch.int64).contiguous()
+    cd = candidates.to(torch.int64).contiguous()
+    un = unary.to(torch.float32).contiguous()
+    hd, pc, sc = hidden.contiguous(), pred_codebook.contiguous(), succ_codebook.contiguous()
+    smp = None if sampling is None else to_device_bytes(np.ascontiguousarray(sampling, dtype=_abi.DRAFT_SAMPLING), dev)
+    out = torch.empty(lanes, positions, dtype=torch.int64, device=dev)
+    check(_lib().vi_selector_chain(lanes, positions, vocab, an.data_ptr(), cd.data_ptr(), un.data_ptr(), hd.data_ptr(),
+                                   pc.data_ptr(), sc.data_ptr(), _ptr(smp), out.data_ptr(), _stream()),
+          "vi_selector_chain")
+    return out
+
+
 def presence_reset(table: torch.Tensor) -> None:
     check(_lib().vi_presence_reset(table.data_ptr(), table.numel(), _stream()), "vi_presence_reset")
 
