@@ -163,6 +163,27 @@ vi_status vi_presence_truncate(int32_t* table, int vocabulary, int from, void* s
 vi_status vi_presence_record(int32_t* table, int vocabulary, int first,
                              const int64_t* tokens, size_t count, void* stream);
 
+/* ---- greedy-packet transport ------------------------------------------------
+ * Replaces the engine's pending-packet readback (Exl3GreedyPacketTransfer and
+ * submit_greedy_packet / finish_greedy_packet, src/exl3/text_model.cu:779-900,
+ * 12225-12355) and its cross-context batch (Exl3EngineGreedyPacketBatch,
+ * src/exl3/engine_greedy_packet_batch.h:17-60): a pool of `slots` pinned host
+ * buffers of `max_rows` packet rows, each with a completion event.  submit
+ * enqueues one device-to-host copy of `rows` contiguous device rows on `stream`
+ * (the packets of any number of lanes laid end to end travel as one copy) and
+ * returns the slot; query reports whether the copy completed; finish waits for
+ * it, copies the rows to `out` (host) and frees the slot.  Every slot in flight:
+ * VI_ERR_WORKSPACE.  A failed copy or wait returns VI_ERR_LAUNCH and retires
+ * the slot.  Host-side allocation happens in create only; destroy waits for
+ * copies still in flight.  Slots are guarded by a mutex (thread-safe). */
+typedef struct vi_packet_transport vi_packet_transport;
+vi_status vi_packet_transport_create(int slots, int max_rows, vi_packet_transport** out);
+vi_status vi_packet_transport_destroy(vi_packet_transport* transport);
+vi_status vi_packet_submit(vi_packet_transport* transport, const vi_greedy_row* device_rows, int rows,
+                           void* stream, int* slot);
+vi_status vi_packet_query(vi_packet_transport* transport, int slot, int* ready);
+vi_status vi_packet_finish(vi_packet_transport* transport, int slot, vi_greedy_row* out, int rows);
+
 /* ---- VeriCache row scores -----------------------------------------------------
  * Scoring of a verified block: per row r, the exact choice and the gap, in
  * logit units, by which the drafted token next[r] trails it (next < 0: gap 0).

@@ -1260,6 +1260,147 @@ inline void exl3_launch_greedy_packet(bool warp, int rows, void* stream, const s
                   "greedy packet");
 }
 
+// resource_inventory.h:18-23: a bounded pool had no free reservation.
+class Exl3ResourceReservationExhausted : public std::runtime_error {
+public:
+    Exl3ResourceReservationExhausted() : std::runtime_error("resource allocation reservation exhausted") {}
+};
+
+class Exl3GreedyPacketTransport;
+
+// A submitted packet whose rows are on their way to the host
+// (Exl3PendingGreedyPacket, text_model.h:159-173): the transport slot and the
+// identity (generation, position, serial, rows) of each packet it carries.
+// Move-only; dropping an unfinished one waits for its copy and frees the slot.
+class Exl3PendingGreedyPacket {
+public:
+    struct Member {
+        int rows = 0;
+        std::uint64_t generation = 0;
+        int position = 0;
+        std::uint64_t serial = 0;
+    };
+    Exl3PendingGreedyPacket() = default;
+    Exl3PendingGreedyPacket(Exl3PendingGreedyPacket&& o) noexcept { *this = std::move(o); }
+    Exl3PendingGreedyPacket& operator=(Exl3PendingGreedyPacket&& o) noexcept {
+        if (this != &o) {
+            drop();
+            transport_ = std::exchange(o.transport_, nullptr);
+            slot_ = std::exchange(o.slot_, -1);
+            rows_ = std::exchange(o.rows_, 0);
+            members_ = std::move(o.members_);
+        }
+        return *this;
+    }
+    Exl3PendingGreedyPacket(const Exl3PendingGreedyPacket&) = delete;
+    Exl3PendingGreedyPacket& operator=(const Exl3PendingGreedyPacket&) = delete;
+    ~Exl3PendingGreedyPacket() { drop(); }
+    [[nodiscard]] bool valid() const noexcept { return transport_ != nullptr; }
+    [[nodiscard]] std::span<const Member> members() const noexcept { return members_; }
+
+private:
+    friend class Exl3GreedyPacketTransport;
+    void drop() noexcept {
+        if (!transport_) return;
+        std::vector<vi_greedy_row> sink(static_cast<std::size_t>(rows_));
+        (void)vi_packet_finish(transport_, slot_, sink.data(), rows_);
+        transport_ = nullptr;
+    }
+    vi_packet_transport* transport_ = nullptr;
+    int slot_ = -1, rows_ = 0;
+    std::vector<Member> members_;
+};
+
+// The readback side of Exl3TextContext::submit_greedy_packet /
+// finish_greedy_packet (text_model.cu:12225-12355) and of the cross-context
+// batch (engine_greedy_packet_batch.h:17-60), over vi_packet_*: the packet
+// launch writes its rows to device memory, submit starts their copy, finish
+// waits and returns the validated packet.  A batch is several lanes' packets
+// laid end to end by one launch, copied once and split and validated per lane.
+class Exl3GreedyPacketTransport {
+public:
+    explicit Exl3GreedyPacketTransport(int slots = 2, int max_rows = int(kExl3GreedyPacketRows)) {
+        detail::check(vi_packet_transport_create(slots, max_rows, &t_), "greedy packet transport");
+    }
+    ~Exl3GreedyPacketTransport() {
+        if (t_) (void)vi_packet_transport_destroy(t_);
+    }
+    Exl3GreedyPacketTransport(const Exl3GreedyPacketTransport&) = delete;
+    Exl3GreedyPacketTransport& operator=(const Exl3GreedyPacketTransport&) = delete;
+
+    // One context's packet of `rows` rows (1..16) at `device_rows`.
+    [[nodiscard]] Exl3PendingGreedyPacket submit(const Exl3GreedyRow* device_rows, int rows, std::uint64_t generation,
+                                                 int position, std::uint64_t serial, void* stream) {
+        const Exl3PendingGreedyPacket::Member m{rows, generation, position, serial};
+        return submit_batch(device_rows, std::span<const Exl3PendingGreedyPacket::Member>(&m, 1), stream);
+    }
+    // Several lanes' packets, member i's rows following member i-1's.
+    [[nodiscard]] Exl3PendingGreedyPacket submit_batch(const Exl3GreedyRow* device_rows,
+                                                       std::span<const Exl3PendingGreedyPacket::Member> members,
+                                                       void* stream) {
+        int total = 0;
+        for (const auto& m : members) {
+            if (m.rows < 1 || m.rows > int(kExl3GreedyPacketRows) || m.serial == 0)
+                throw std::invalid_argument("greedy packet rows/serial");
+            total += m.rows;
+        }
+        if (members.empty()) throw std::invalid_argument("greedy packet batch is empty");
+        int slot = -1;
+        const vi_status st = vi_packet_submit(t_, reinterpret_cast<const vi_greedy_row*>(device_rows), total, stream,
+                                              &slot);
+        if (st == VI_ERR_WORKSPACE) throw Exl3ResourceReservationExhausted();
+        detail::check(st, "pending greedy packet download");
+        Exl3PendingGreedyPacket p;
+        p.transport_ = t_;
+        p.slot_ = slot;
+        p.rows_ = total;
+        p.members_.assign(members.begin(), members.end());
+        return p;
+    }
+    [[nodiscard]] bool ready(const Exl3PendingGreedyPacket& p) const {
+        if (p.transport_ != t_) throw std::logic_error("pending greedy packet belongs to another transport");
+        int r = 0;
+        detail::check(vi_packet_query(t_, p.slot_, &r), "pending greedy packet poll");
+        return r != 0;
+    }
+    // finish_greedy_packet: the packet must still be the one the caller waits
+    // for (its current generation, position and serial), else runtime_error.
+    Exl3GreedyPacket finish(Exl3PendingGreedyPacket&& p, std::uint64_t generation, int position,
+                            std::uint64_t serial, int vocabulary = int(kDefaultVocabulary)) {
+        if (p.members_.size() != 1) throw std::logic_error("finish takes a single packet; use finish_batch");
+        const auto m = p.members_[0];
+        auto packets = finish_batch(std::move(p), vocabulary);
+        if (m.generation != generation || m.position != position || m.serial != serial)
+            throw std::runtime_error("stale pending greedy packet");
+        return packets[0];
+    }
+    std::vector<Exl3GreedyPacket> finish_batch(Exl3PendingGreedyPacket&& p, int vocabulary = int(kDefaultVocabulary)) {
+        if (!p.valid() || p.transport_ != t_) throw std::logic_error("pending greedy packet is empty or foreign");
+        std::vector<vi_greedy_row> rows(static_cast<std::size_t>(p.rows_));
+        const vi_status st = vi_packet_finish(t_, p.slot_, rows.data(), p.rows_);
+        p.transport_ = nullptr;   // the slot is free (or retired) either way
+        if (st != VI_OK) throw std::runtime_error("pending greedy packet completion failed");
+        std::vector<Exl3GreedyPacket> out;
+        std::size_t at = 0;
+        for (const auto& m : p.members_) {
+            Exl3GreedyPacket g;
+            g.rows = std::uint32_t(m.rows);
+            g.generation = m.generation;
+            g.position = m.position;
+            g.serial = m.serial;
+            g.ready = true;
+            for (int r = 0; r < m.rows; ++r, ++at)
+                g.decisions[std::size_t(r)] = Exl3GreedyRow{rows[at].serial, rows[at].token, rows[at].nonfinite};
+            g.validate(std::uint32_t(m.rows), m.generation, m.position, m.serial, vocabulary);
+            out.push_back(g);
+        }
+        return out;
+    }
+
+private:
+    vi_packet_transport* t_ = nullptr;
+};
+
 // Caller-owned scratch of the sampled packet (sampled_select.cuh:200-216).
 struct Exl3SampledSliceScratch {
     void* base = nullptr;

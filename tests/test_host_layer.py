@@ -2,6 +2,8 @@
 
 * tests/cpp/test_host_contracts.cpp — the reference's own contract scenarios
   (tests/test_exl3_sampling_policy.cpp and its siblings) against this layer;
+* tests/cpp/test_transport_host.cpp — the greedy-packet transport classes over
+  a host stand-in of the vi_packet_* entry points;
 * oracle/_ref/ref_diff — random scripts run side by side through this layer and
   the reference's host headers compiled from /root/reference (skipped where the
   reference tree is absent and the binary was not built).
@@ -32,6 +34,14 @@ def test_host_contracts_program():
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "host contracts PASS" in res.stdout
+
+
+def test_transport_host_layer():
+    """Exl3GreedyPacketTransport over a host stand-in of the vi_packet_* entry points."""
+    exe = _compile(ROOT / "tests" / "cpp" / "test_transport_host.cpp", BUILD / "test_transport_host")
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "transport host layer PASS" in res.stdout
 
 
 def test_host_layer_matches_reference_headers():

@@ -12,7 +12,7 @@ from ._abi import (ABSENT_OCCURRENCE, BF16, F16, F32, FLAG_BAD_HISTORY, FLAG_EMP
 
 load()
 
-from .ops import (PenaltyState, draft_choice, greedy_packet, params_array, presence_record, presence_reset,  # noqa: E402,F401
+from .ops import (PacketTransport, PenaltyState, draft_choice, greedy_packet, params_array, presence_record, presence_reset,  # noqa: E402,F401
                   presence_truncate, probe_copy, probe_read, route_mask, row_scores, sample_rows, sample_rows_state,
                   sampled_packet, sampled_scores, selector_chain, stats_numpy,
                   to_device_bytes, topk_rows,

@@ -83,6 +83,11 @@ SIGNATURES = {
     "vi_penalty_state_update": ([_vp, _i, _i, _i, _vp, _vp, _i, _vp], _i),
     "vi_sample_rows_state": ([_vp, _i, _i, _i, _i64, _vp, _vp, _i, _i, _vp, _vp, _vp, _i64, _vp, _u32, _vp, _sz,
                               _vp], _i),
+    "vi_packet_transport_create": ([_i, _i, C.POINTER(C.c_void_p)], _i),
+    "vi_packet_transport_destroy": ([_vp], _i),
+    "vi_packet_submit": ([_vp, _vp, _i, _vp, C.POINTER(C.c_int)], _i),
+    "vi_packet_query": ([_vp, _i, C.POINTER(C.c_int)], _i),
+    "vi_packet_finish": ([_vp, _i, _vp, _i], _i),
     "vi_presence_reset": ([_vp, _i, _vp], _i),
     "vi_presence_truncate": ([_vp, _i, _i, _vp], _i),
     "vi_presence_record": ([_vp, _i, _i, _vp, _sz, _vp], _i),

@@ -216,6 +216,44 @@ def selector_chain(anchors: torch.Tensor, candidates: torch.Tensor, unary: torch
     return out
 
 
+class PacketTransport:
+    """Pinned readback slots for greedy-packet rows (vi_packet_*)."""
+
+    def __init__(self, slots: int = 2, max_rows: int = 16):
+        h = C.c_void_p()
+        check(_lib().vi_packet_transport_create(slots, max_rows, C.byref(h)), "vi_packet_transport_create")
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            check(_lib().vi_packet_transport_destroy(self.handle), "vi_packet_transport_destroy")
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def submit(self, device_rows: torch.Tensor, rows: int | None = None) -> int:
+        """Start the copy of `rows` GREEDY_ROW records (a uint8 device tensor); returns the slot."""
+        n = device_rows.numel() // GREEDY_ROW.itemsize if rows is None else rows
+        slot = C.c_int(-1)
+        check(_lib().vi_packet_submit(self.handle, device_rows.data_ptr(), n, _stream(), C.byref(slot)),
+              "vi_packet_submit")
+        return slot.value
+
+    def query(self, slot: int) -> bool:
+        r = C.c_int(0)
+        check(_lib().vi_packet_query(self.handle, slot, C.byref(r)), "vi_packet_query")
+        return bool(r.value)
+
+    def finish(self, slot: int, rows: int) -> np.ndarray:
+        out = np.zeros(rows, dtype=GREEDY_ROW)
+        check(_lib().vi_packet_finish(self.handle, slot, out.ctypes.data, rows), "vi_packet_finish")
+        return out
+
+
 def presence_reset(table: torch.Tensor) -> None:
     check(_lib().vi_presence_reset(table.data_ptr(), table.numel(), _stream()), "vi_presence_reset")
 
