@@ -215,3 +215,34 @@ def test_state_route_limits(dev, rng):
     tok, s = out.tokens.cpu().numpy(), vi.stats_numpy(out.stats)
     assert tok[0] == -1 and tok[1] == -1 and (s["flags"][:2] & FLAG_ERROR).all()
     assert (tok[2:] >= 0).all() and not (s["flags"][2:] & FLAG_ERROR).any()
+
+
+@pytest.mark.parametrize("vocab", [64, 1000, 65_537])
+def test_state_route_small_and_odd_vocabularies(orc, dev, rng, vocab):
+    """Half boundaries that do not fall on a bitmap word, the last word masked,
+    both routes, recording from the sampler: equal to the history route (whose
+    histories of up to 3 V tokens take its general path at V = 65,537)."""
+    import voidinfer_amd as vi
+    from voidinfer_amd import workloads as W
+    rows = 8
+    bits = W.encode(W.gaussian_zipf(rows, vocab, 1.0, int(rng.integers(1 << 30))), "bf16")
+    p = vi.params_array(rows, seed=rng.integers(1, 2**62, rows), position=rng.integers(0, 10**5, rows),
+                        temperature=0.9, top_k=np.array([0, 20, 0, 0, 64, 0, 0, 10]), top_p=0.95,
+                        repetition_penalty=1.2, presence_penalty=0.3, frequency_penalty=0.2)
+    hist = [rng.integers(0, vocab, int(rng.integers(1, 3 * vocab))).astype(np.int32) for _ in range(rows)]
+    hist[0] = np.full(50, vocab - 1, dtype=np.int32)          # only the last id, repeated
+    st = vi.PenaltyState(rows, vocab, 1 << 18, device=dev)   # >= 2 x the distinct tokens (up to V)
+    update(st, dev, hist)
+    assert (st.header()[:, 0] == 0).all()
+    logits = to_dev(bits, 0, dev)
+    for step in range(3):
+        toks, offs = csr(hist)
+        a = vi.sample_rows(logits, p, torch.from_numpy(toks).to(dev), torch.from_numpy(offs).to(dev),
+                           max_history=int(np.diff(offs).max()), want_probs=True)
+        b = vi.sample_rows_state(logits, p, st, record=True, want_probs=True)
+        torch.cuda.synchronize()
+        same_outputs(a, b, f"V={vocab} step {step}")
+        hist = [np.append(h, t).astype(np.int32) for h, t in zip(hist, b.tokens.cpu().numpy())]
+        p["position"] += 1
+    for r in range(rows):
+        check_lane(st, r, hist[r])
