@@ -130,12 +130,14 @@ constexpr int kOffDecEnd = kOffWM + 8 * (kCoarse + 4);
 constexpr int kOffBmap = 131072;
 constexpr int kOffPref = kOffBmap + 4 * (kBmapWords + 4);
 constexpr int kLdsDense = kOffPref + 2 * kBmapWords;
-constexpr int kOffP = 4 * kFT;            // D: penalized history bits by rank (u16), after fmask
+constexpr int kOffP = 24576;              // D: penalized history bits by rank (u16), filled during the
+                                          // decisions (past their tables), read by the owner
 constexpr int kOffML = kOffP + 2 * kHistMax;   // D: history tokens matching the drawn key
 constexpr int kMatchMax = 2048;
 static_assert(kOffML + 4 * kMatchMax <= 131072, "owner LDS");
+static_assert(4 * kFT <= kOffP, "owner candidate masks below the penalized bits");
 constexpr int kLdsGeneral = 131072 + 8 * kOvfMax;
-static_assert(kOffDecEnd <= 131072 && kOffDM % 8 == 0 && kOffPM % 8 == 0 && kOffWW % 8 == 0 && kOffWM % 8 == 0, "LDS map");
+static_assert(kOffDecEnd <= kOffP && kOffDM % 8 == 0 && kOffPM % 8 == 0 && kOffWW % 8 == 0 && kOffWM % 8 == 0, "LDS map");
 static_assert(kHistMax / 2 * 4 <= 131072, "dense counts");
 static_assert(kOffL3 + 4 * kList3 <= 131072 && kHistMax * 2 <= kOffB2, "one-pass history counting");
 
@@ -924,7 +926,19 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         DF[2 * (i & ~(kCoarse - 1)) + kCoarse + c] = Sh->end[c];
     }
     __syncthreads();
-    if (wave == 0) {
+    if (wave != 0) {
+        // meanwhile the other waves bring this half's penalized history bits by
+        // rank into LDS for the owner search (16-byte copies; the slice holds
+        // kHistMax entries, so rounding n_flag up stays inside it)
+        if constexpr (kDense) {
+            if (pen) {
+                const uint4* src = reinterpret_cast<const uint4*>(dpen);
+                uint4* dst = reinterpret_cast<uint4*>(lds + kOffP);
+                const int n16 = int((n_flag + 7u) >> 3);
+                for (int i = tid - kWave; i < n16; i += kFT - kWave) dst[i] = src[i];
+            }
+        }
+    } else {
         // merged coarse prefix: lane l owns q = 4l .. 4l + 3
         {
             uint32_t cq[4];
@@ -1127,14 +1141,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     if (tid < kFV + 2) sh.slot_tot[tid] = 0u;
     if (tid == 0) sh.n_match = 0u;
     __syncthreads();
-    // dense path: penalized history bits by rank into LDS (the merge region is free)
-    uint16_t* P = reinterpret_cast<uint16_t*>(lds + kOffP);
-    if constexpr (kDense) {
-        if (pen) {
-            for (uint32_t r = tid; r < n_flag; r += kFT) P[r] = dpen[r];
-            __syncthreads();
-        }
-    }
+    const uint16_t* P = reinterpret_cast<const uint16_t*>(lds + kOffP);   // dense path: filled above
     const int r_half = sh.r_half;
     const uint32_t r_key = uint32_t(sh.r_key);
 
