@@ -230,17 +230,41 @@ __device__ __forceinline__ uint32_t bits_of(uint64_t q0, uint64_t q1, int j) {
     return uint32_t(((j < 4 ? q0 : q1) >> ((j & 3) * 16)) & 0xffffu);
 }
 
-// Bit j set: element j of the vector is finite and has order key `key`.
+// The 16-bit patterns whose order key is `key`, for pattern compares in place
+// of computing keys: key16 is one-to-one on finite patterns except that -0
+// shares +0's key.  Both halves of each word hold the pattern (t2; alt2 also
+// admits -0 for the key of zero); nothing matches a non-finite key or 0x7fff
+// (the key only -0 would have before the fold): valid = false.
+struct KeyPattern {
+    uint32_t t2, alt2;
+    bool valid;
+};
 template <int DT>
-__device__ __forceinline__ uint32_t match_mask8(const uint4& v, uint32_t key) {
-    uint32_t m = 0;
+__device__ __forceinline__ KeyPattern key_pattern(uint32_t key) {
+    if (Elem<DT>::nonfinite_key(key) || key == 0x7fffu) return KeyPattern{0u, 0u, false};
+    const uint32_t t = unkey16(key);
+    return KeyPattern{t | (t << 16), t == 0u ? 0x80008000u : t | (t << 16), true};
+}
+template <int DT>
+__device__ __forceinline__ bool has_key(uint32_t b, const KeyPattern& k) {
+    return k.valid && (b == (k.t2 & 0xffffu) || b == (k.alt2 & 0xffffu));
+}
+
+// Bit j set: element j of the vector is finite and has order key `key`, two
+// elements per 32-bit word.
+template <int DT>
+__device__ __forceinline__ uint32_t match_mask8(const uint4& v, const KeyPattern& kp) {
+    const uint32_t t2 = kp.t2, alt = kp.alt2;
     const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    uint32_t m = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-        m |= (Elem<DT>::finite_bits(b) && key16(b) == key) ? (1u << j) : 0u;
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t x = w4[q] ^ t2, y = w4[q] ^ alt;
+        const uint32_t lo = ((x & 0xffffu) == 0u) | ((y & 0xffffu) == 0u);
+        const uint32_t hi = ((x >> 16) == 0u) | ((y >> 16) == 0u);
+        m |= (lo << (2 * q)) | (hi << (2 * q + 1));
     }
-    return m;
+    return kp.valid ? m : 0u;
 }
 
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
@@ -1150,8 +1174,9 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     if (half == r_half) {
         uint32_t* fmask = lds32;   // [kFT] history-token candidates per owning thread
         fmask[tid] = 0u;
-        const uint32_t c_head = (tid < head && !fl_head && Elem<DT>::finite_bits(hbits) && key16(hbits) == r_key);
-        const uint32_t c_tail = (tid < tail && !fl_tail && Elem<DT>::finite_bits(tbits) && key16(tbits) == r_key);
+        const KeyPattern rkp = key_pattern<DT>(r_key);
+        const uint32_t c_head = (tid < head && !fl_head && has_key<DT>(hbits, rkp));
+        const uint32_t c_tail = (tid < tail && !fl_tail && has_key<DT>(tbits, rkp));
         // per-slot counts summed over the wave with shuffles: one LDS atomic
         // per wave and slot instead of one per thread
         auto wave_add = [&](int s2, uint32_t c) {
@@ -1168,7 +1193,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
             for (int u = 0; u < kFV; ++u) {
                 const int i = i0 + u;
-                const uint32_t m = i * kFT + tid < nvec ? match_mask8<DT>(rv[u], r_key) & ~vflags(i) : 0u;
+                const uint32_t m = i * kFT + tid < nvec ? match_mask8<DT>(rv[u], rkp) & ~vflags(i) : 0u;
                 vm[i >> 2] |= m << (8 * (i & 3));
                 wave_add(1 + i, __builtin_popcount(m));
             }
@@ -1194,7 +1219,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                 const uint16_t* pref = reinterpret_cast<const uint16_t*>(lds + kOffPref);
                 for (uint32_t r = tid; r < n_flag; r += kFT) {
                     const uint32_t pb = P[r];
-                    if (!(Elem<DT>::finite_bits(pb) && key16(pb) == r_key)) continue;
+                    if (!has_key<DT>(pb, rkp)) continue;
                     int lo = 0, hi = kBmapWords;             // last word with pref <= r
                     while (lo < hi) {
                         const int mid = (lo + hi) >> 1;
@@ -1230,7 +1255,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
             walk_words([&](uint32_t rank, int off) {
                 const uint32_t pb = P[rank];
                 int o, j;
-                if (Elem<DT>::finite_bits(pb) && key16(pb) == r_key && place(off, &o, &j) == s) atomicOr(&fmask[o], 1u << j);
+                if (has_key<DT>(pb, rkp) && place(off, &o, &j) == s) atomicOr(&fmask[o], 1u << j);
             });
         }
         __syncthreads();
