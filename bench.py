@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    ap.add_argument("--workload", choices=("config5", "config3", "config4"), default="config5",
+                    help="config5 (the headline); config3 / config4 time the top-k and verification kernels")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel over 256 MiB x 10 (HBM-counter calibration) and exit")
     return ap.parse_args()
@@ -83,6 +85,140 @@ def calibrate_copy():
                                       "vi_probe_copy": {"bytes_written_per_launch": 1 << 28, "launches": 5}}}))
 
 
+def _timed(fn, stream, K: int, warmup: int):
+    """HIP events around every launch on `stream`: (mean ms per step, per-launch ms)."""
+    import numpy as np
+    import torch
+    for i in range(warmup):
+        st = fn(i)
+        assert st == 0, st
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    for i in range(K):
+        starts[i].record(stream)
+        fn(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return starts[0].elapsed_time(ends[-1]) / K, np.array([a.elapsed_time(b) for a, b in zip(starts, ends)])
+
+
+def secondary(args):
+    """Configuration 3 (DFlash2 draft top-8 + log-probs over 128 fp16 rows) or 4
+    (verification of 8 lanes x 16 drafted positions: sampled rejection with the
+    target softmax fused, and greedy prefix) on five rotating input sets; one JSON
+    line in the headline's schema.  Not the headline metric."""
+    import numpy as np
+    import torch
+
+    import voidinfer_amd as vi
+    from voidinfer_amd import workloads as W
+    dev = torch.device("cuda:0")
+    lib = vi.load()
+    assert lib.vi_init() == 0, "device is not gfx950"
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+    K, V = args.steps, VOCAB
+    t16 = lambda bits, dt: torch.from_numpy(bits.view(np.int16)).to(dev).view(dt)   # noqa: E731
+    extra = {}
+    if args.workload == "config3":
+        rows, k = 128, 8
+        bits = [W.config3(seed=300 + s, rows=rows) for s in range(SETS)]
+        logits = [t16(b, torch.float16) for b in bits]
+        ids = torch.empty(rows, k, dtype=torch.int64, device=dev)
+        vals = torch.empty(rows, k, dtype=torch.float32, device=dev)
+        lp = torch.empty(rows, k, dtype=torch.float32, device=dev)
+        nb = lib.vi_topk_workspace_bytes(rows, V, k)
+        ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+
+        def fn(i):
+            return lib.vi_topk_rows(logits[i % SETS].data_ptr(), vi.F16, rows, V, V, k, ids.data_ptr(),
+                                    vals.data_ptr(), lp.data_ptr(), None, ws.data_ptr(), nb, sptr)
+        bytes_per_launch = rows * V * 2 + rows * k * (8 + 4 + 4)
+        metric, kernel = "draft top-8 + log-probs rows/sec at 128x248,320 fp16", "topk_kernel (topk.hip)"
+        workload = "config3: 128 rows x 248,320 fp16 N(0,1.5) with 8 planted peaks +6..+10; exact top-8 ids + log-probs"
+        assert fn(0) == 0
+        torch.cuda.synchronize()
+        gpu = ids.cpu().numpy()
+    else:
+        lanes, drafts = 8, 16
+        rows = lanes * drafts
+        sets = [W.config4(seed=400 + s, lanes=lanes, drafts=drafts) for s in range(SETS)]
+        tgt = [t16(t, torch.bfloat16) for t, _, _, _ in sets]
+        dft = [t16(d, torch.float16) for _, d, _, _ in sets]
+        drafted = [torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev) for _, _, x, _ in sets]
+        params = [vi.to_device_bytes(p, dev) for _, _, _, p in sets]
+        acc = torch.empty(lanes, dtype=torch.int32, device=dev)
+        com = torch.empty(lanes, drafts + 1, dtype=torch.int32, device=dev)
+        cnt = torch.empty(lanes, dtype=torch.int32, device=dev)
+        flg = torch.empty(lanes, dtype=torch.int32, device=dev)
+        nb = lib.vi_verify_workspace_bytes(lanes, drafts, V)
+        ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+
+        def call(i, mode):
+            j = i % SETS
+            return lib.vi_verify_rows(mode, tgt[j].data_ptr(), vi.BF16, V, drafts,
+                                      dft[j].data_ptr() if mode == vi.VERIFY_SAMPLED else None,
+                                      vi.F16 if mode == vi.VERIFY_SAMPLED else 0, V if mode == vi.VERIFY_SAMPLED else 0,
+                                      lanes, drafts, V, drafted[j].data_ptr(),
+                                      params[j].data_ptr() if mode == vi.VERIFY_SAMPLED else None, None, 0,
+                                      acc.data_ptr(), com.data_ptr(), cnt.data_ptr(), flg.data_ptr(), ws.data_ptr(),
+                                      nb, sptr)
+
+        def fn(i):
+            return call(i, vi.VERIFY_SAMPLED)
+        g_ms, g_launch = _timed(lambda i: call(i, vi.VERIFY_GREEDY), stream, max(K // 2, 50), 10)
+        extra["greedy_mode"] = {"ms_per_step": g_ms, "kernel_ms": float(g_launch.mean()),
+                                "bytes_per_launch": rows * V * 2,
+                                "achieved_gbps": rows * V * 2 / (float(g_launch.mean()) / 1e3) / 1e9}
+        bytes_per_launch = rows * V * 2 * 2
+        metric, kernel = "verified drafted rows/sec (8 lanes x 16, sampled rejection)", "verify_* (verify.hip)"
+        workload = ("config4: 8 lanes x 16 drafted positions, target bf16 = draft fp16 + N(0,0.5), V=248,320, "
+                    "T .7 / top_p .8 / top_k 20; sampled rejection with the target softmax fused")
+        assert fn(0) == 0
+        torch.cuda.synchronize()
+        gpu = (acc.cpu().numpy().copy(), com.cpu().numpy().copy())
+    ms, launch = _timed(fn, stream, K, args.warmup)
+    kernel_ms = float(launch.mean())
+    achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
+    cpu = parity = None
+    if not args.no_cpu:
+        import oracle
+        threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 64)
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            if args.workload == "config3":
+                w_ids = oracle.topk_rows(bits[0], oracle.F16, 8)[0]
+            else:
+                t, d, x, p = sets[0]
+                w = oracle.verify_rows(vi.VERIFY_SAMPLED, t, oracle.BF16, d, oracle.F16, 8, 16, x, p, threads=threads)
+            reps += 1
+            if time.perf_counter() - t0 >= args.cpu_seconds or reps >= 1000:
+                break
+        cpu_s = time.perf_counter() - t0
+        if args.workload == "config3":
+            parity = {"rows": rows, "mismatched_rows": int((w_ids != gpu).any(axis=1).sum())}
+            cores = 1
+        else:
+            near = w[4] < 1e-6
+            parity = {"lanes": 8, "accepted_mismatches": int((w[0] != gpu[0]).sum()),
+                      "committed_mismatches": int(sum((w[1][l] != gpu[1][l]).any() for l in range(8)
+                                                      if not near[l].any()))}
+            cores = threads
+        cpu = {"value": rows * reps / cpu_s, "unit": "rows/s", "cores": cores, "kind": "port",
+               "sample": f"{reps} steps of input set 0 through oracle/liboracle.so ({cores} thread(s)), {cpu_s:.1f} s"}
+    print(json.dumps({
+        "metric": metric, "value": rows / (ms / 1e3), "unit": "rows/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16" if args.workload == "config3" else "bf16+fp16", "data": "synthetic",
+        "config": {"workload": workload, "rows": rows, "vocabulary": V, "input_sets": SETS, "kernel": kernel},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_GBPS, "traffic": None, "bytes_per_launch": bytes_per_launch,
+                     "kernel_ms": kernel_ms, "kernel_ms_p50": float(np.median(launch))},
+        **extra, "cpu_baseline": cpu, "parity": parity}))
+
+
 def traffic_from_profiles(route: str) -> float | None:
     """HBM bytes per launch of the full-vocabulary kernel on `route`, from the
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/ (None if absent)."""
@@ -105,6 +241,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.workload != "config5":
+        secondary(args)
         return
 
     import numpy as np

@@ -49,6 +49,45 @@ __device__ __forceinline__ void scan_slice(const void* row, int begin, int end, 
     }
 }
 
+// As scan_slice, with each full 16-byte vector handed over whole:
+// vfn(vector, id of its element 0, valid) for the vectors, fn(bits, id, valid)
+// for the elements past the last full vector (and for every element of a row
+// whose stride breaks 16-byte alignment).  Same trip-count guarantees.
+template <int DT, bool VEC, int NT, class FV, class F>
+__device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int end, FV&& vfn, F&& fn) {
+    constexpr int P = Elem<DT>::kPerVec;
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+        const int nvec = (end - begin) / P;
+        const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
+        constexpr int U = 4;
+        for (int vb = 0; vb < nvec; vb += U * NT) {
+            uint4 d[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = vb + u * NT + tid;
+                d[u] = v < nvec ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = vb + u * NT + tid;
+                vfn(d[u], begin + v * P, v < nvec);
+            }
+        }
+        for (int ib = begin + nvec * P; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    } else {
+        for (int ib = begin; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    }
+}
+
 // Slice boundaries: slice s of `slices` covers [s*len, min(V,(s+1)*len)), len a
 // multiple of 64 elements.
 __host__ __device__ inline int slice_len_for(int vocabulary, int slices) {

@@ -353,15 +353,75 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     uint32_t flags = 0, valid = 0;
     float lse_m = -kInfF, lse_s = 0.0f;
     const bool want_lse = MODE == kModeTopk && a.logprobs != nullptr;
-    scan_slice<DT, VEC, kTopkThreads>(row, begin, end, [&](uint32_t bits, int id, bool ok) {
+    constexpr float kL2E = 1.4426950408889634f;
+    // Whole vectors (top-k and verify modes): flags, counts and the running
+    // log-sum-exp per vector (one rescale by the vector's maximum, then one exp
+    // per element), and the list offered the vector's elements only when some
+    // lane's vector maximum reaches the list's K-th entry (no element of a vector
+    // below it can enter: it is exact).
+    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
+        constexpr int P = Elem<DT>::kPerVec;
+        float xs[P];
+        uint32_t candm = 0;
+        float vmax = -kInfF;
+        if constexpr (MODE == kModeTopk) {
+            uint32_t finm = 0;
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const uint32_t bits = vec_bits<DT>(dv, j);
+                xs[j] = Elem<DT>::decode(bits);
+                const bool finite = Elem<DT>::finite_bits(bits), nan = Elem<DT>::nan_bits(bits);
+                flags |= (ok & !finite) ? (nan ? (kSliceNan | kSliceNonfinite) : kSliceNonfinite) : 0u;
+                finm |= uint32_t(ok & finite) << j;
+                candm |= uint32_t(ok & !nan) << j;
+                vmax = (ok & !nan) ? fmaxf(vmax, xs[j]) : vmax;
+            }
+            if (want_lse && finm) {   // (per lane)
+                float m8 = -kInfF;
+#pragma unroll
+                for (int j = 0; j < P; ++j) m8 = ((finm >> j) & 1u) ? fmaxf(m8, xs[j]) : m8;
+                if (m8 > lse_m) {
+                    lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - m8) * kL2E);
+                    lse_m = m8;
+                }
+#pragma unroll
+                for (int j = 0; j < P; ++j)
+                    lse_s += ((finm >> j) & 1u) ? __builtin_amdgcn_exp2f((xs[j] - lse_m) * kL2E) : 0.0f;
+            }
+        } else {   // kModeVerify
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const uint32_t bits = vec_bits<DT>(dv, j);
+                const float x = Elem<DT>::decode(bits);
+                const bool finite = Elem<DT>::finite_bits(bits);
+                const float v = p.temperature > 0.0f ? x * inv_t : x;
+                const bool live = ok & finite & isfinite(v);
+                flags |= (ok & !live) ? kSliceNonfinite : 0u;
+                valid += live ? 1u : 0u;
+                xs[j] = v;
+                candm |= uint32_t(live) << j;
+                vmax = live ? fmaxf(vmax, v) : vmax;
+            }
+        }
+        if (ballot(candm != 0u && vmax >= L.kv) == 0) return;
+#pragma unroll
+        for (int j = 0; j < P; ++j) list_offer(L, K, (candm >> j) & 1u, xs[j], id0 + j);
+    };
+    auto elem_fn = [&](uint32_t bits, int id, bool ok) {
         const float x = Elem<DT>::decode(bits);
         const bool finite = Elem<DT>::finite_bits(bits);
         if constexpr (MODE == kModeTopk) {
-            if (ok && !finite) flags |= Elem<DT>::nan_bits(bits) ? (kSliceNan | kSliceNonfinite) : kSliceNonfinite;
-            const bool cand = ok && !Elem<DT>::nan_bits(bits);
-            if (want_lse && ok && finite) {
-                if (x > lse_m) { lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - x) * 1.4426950408889634f) + 1.0f; lse_m = x; }
-                else lse_s += __builtin_amdgcn_exp2f((x - lse_m) * 1.4426950408889634f);
+            // straight-line per element: flags, running log-sum-exp, then the list
+            const bool nan = Elem<DT>::nan_bits(bits);
+            flags |= (ok & !finite) ? (nan ? (kSliceNan | kSliceNonfinite) : kSliceNonfinite) : 0u;
+            const bool cand = ok & !nan;
+            if (want_lse) {   // (uniform)
+                const bool use = ok & finite;
+                const float m_new = use ? fmaxf(lse_m, x) : lse_m;
+                const float scale = m_new == lse_m ? 1.0f : __builtin_amdgcn_exp2f((lse_m - m_new) * 1.4426950408889634f);
+                const float term = use ? __builtin_amdgcn_exp2f((x - m_new) * 1.4426950408889634f) : 0.0f;
+                lse_s = lse_s * scale + term;
+                lse_m = m_new;
             }
             list_offer(L, K, cand, x, id);
         } else if constexpr (MODE == kModePacket) {
@@ -405,7 +465,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             valid += live ? 1u : 0u;
             list_offer(L, K, cand, v, id);
         }
-    });
+    };
+    if constexpr (MODE == kModeTopk || MODE == kModeVerify)
+        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, vec_fn, elem_fn);
+    else
+        scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
 
     // ---- merge the wave lists in LDS
     __shared__ float s_val[kTopkWaves][kMaxK];
@@ -620,8 +684,10 @@ Partials carve_partials(Carver& c, int rows, int slices) {
 }  // namespace
 
 TopkPlan topk_plan(int rows, int vocabulary) {
-    // >= 2048 workgroups (8 per CU) where the row count allows, slices >= 2048 logits.
-    int slices = rows >= 2048 ? 1 : (2048 + rows - 1) / rows;
+    // ~1024 workgroups (4 per CU: every one resident at once — the kernel fits 7
+    // per CU, and a ninth round of stragglers would double the time) where the
+    // row count allows, slices >= 2048 logits.
+    int slices = rows >= 1024 ? 1 : (1024 + rows - 1) / rows;
     slices = std::min(slices, std::max(1, vocabulary / 2048));
     slices = std::max(1, std::min(slices, 64));
     const int len = slice_len_for(vocabulary, slices);

@@ -38,7 +38,8 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xo
 
 // (value desc, id asc): exl3_sampled_better (sampled_select.cuh:55-57).
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-    return v > bv || (v == bv && i < bi);
+    // bitwise, not short-circuit: straight-line compares instead of exec-mask branches
+    return (v > bv) | ((v == bv) & (i < bi));
 }
 
 // --------------------------------------------------------------- element decode
