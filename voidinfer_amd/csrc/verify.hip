@@ -15,7 +15,8 @@
 // residual max(0, p - q) normalised, inverse CDF in token-id order with u_c
 // (last positive id on round-off).  u_a, u_c are Philox draws keyed by
 // (seed, lane, position + j, purpose 1 / 2).  The finalize kernel runs one
-// thread per lane over the <= 64-entry lists (fp64).
+// wave per lane over the <= 64-entry lists (fp64): entry-wise work on the
+// lanes, the order-dependent sums on lane 0.
 #include <math.h>
 
 #include "vi_device.h"
@@ -57,139 +58,186 @@ __global__ void verify_greedy_kernel(const vi_greedy_row* rows, int lanes, int d
     if (lane_flags) lane_flags[l] = flags;
 }
 
-// Filtered distribution of one sorted list: support size and weights.
+// Filtered distribution of one sorted list (in LDS): the lane's weights, the
+// support after the cap / min-p / top-p cuts and its mass.
 struct ListDist {
-    const float* z;
-    const int* id;
-    int support;
-    bool greedy;
     double w[kMaxK];
+    int id[kMaxK];
+    int support;
     double sn;
 };
 
+// One 64-lane workgroup per batch lane: lane k computes the weight of list
+// entry k; lane 0 then takes the cuts and sums sequentially, in the order of
+// the one-thread rule (the fp64 results are that rule's, bit for bit).
 __device__ void list_dist(const vi_row_params& p, const float* z, const int* id, uint32_t valid, ListDist& d) {
-    d.z = z; d.id = id; d.support = 0; d.sn = 0.0; d.greedy = !(p.temperature > 0.0f);
-    if (valid == 0) return;
-    if (d.greedy) { d.support = 1; d.w[0] = 1.0; d.sn = 1.0; return; }
-    const int cap = min(p.top_k, int(valid));
-    const double z0 = double(z[0]);
-    double s = 0.0;
-    for (int j = 0; j < cap; ++j) { d.w[j] = exp(double(z[j]) - z0); s += d.w[j]; }
-    const double minp = double(p.min_p), target = double(p.top_p) * s;
-    double cum = 0.0;
-    int n = 0;
-    for (int j = 0; j < cap; ++j) {
-        if (p.min_p > 0.0f && d.w[j] < minp * d.w[0]) break;
-        cum += d.w[j];
-        n = j + 1;
-        if (p.top_p < 1.0f && cum >= target) break;
+    const int k = threadIdx.x;
+    const bool greedy = !(p.temperature > 0.0f);
+    const int cap = valid == 0 ? 0 : (greedy ? 1 : min(p.top_k, int(valid)));
+    if (k < cap) {
+        d.id[k] = id[k];
+        d.w[k] = greedy ? 1.0 : exp(double(z[k]) - double(z[0]));
     }
-    if (n < 1) n = 1;
-    d.support = n;
-    for (int j = 0; j < n; ++j) d.sn += d.w[j];
+    __syncthreads();
+    if (k == 0) {
+        int n = 0;
+        double sn = 0.0;
+        if (cap > 0 && greedy) {
+            n = 1;
+            sn = 1.0;
+        } else if (cap > 0) {
+            double s = 0.0;
+            for (int j = 0; j < cap; ++j) s += d.w[j];
+            const double minp = double(p.min_p), target = double(p.top_p) * s;
+            double cum = 0.0;
+            for (int j = 0; j < cap; ++j) {
+                if (p.min_p > 0.0f && d.w[j] < minp * d.w[0]) break;
+                cum += d.w[j];
+                n = j + 1;
+                if (p.top_p < 1.0f && cum >= target) break;
+            }
+            if (n < 1) n = 1;
+            for (int j = 0; j < n; ++j) sn += d.w[j];
+        }
+        d.support = n;
+        d.sn = sn;
+    }
+    __syncthreads();
 }
 
-__device__ double list_prob(const ListDist& d, int token) {
-    for (int j = 0; j < d.support; ++j) if (d.id[j] == token) return d.w[j] / d.sn;
-    return 0.0;
+// Index of `token` in the support (first match), or -1: a ballot over the lanes.
+__device__ __forceinline__ int list_find(const ListDist& d, int64_t token) {
+    const int k = threadIdx.x;
+    const uint64_t m = ballot(k < d.support && int64_t(d.id[k]) == token);
+    return m ? __builtin_ctzll(m) : -1;
 }
 
-__global__ void verify_sampled_kernel(const float* tval, const int* tidx, const uint32_t* tvalid,
-                                      const uint32_t* tflags, const float* dval, const int* didx,
-                                      const uint32_t* dvalid, const uint32_t* dflags, int lanes, int drafts,
-                                      int target_rows, const int32_t* drafted, const vi_row_params* params,
-                                      const int64_t* terminal, int n_terminal, int vocabulary,
-                                      int32_t* accepted, int32_t* committed, int32_t* committed_count,
-                                      uint32_t* lane_flags) {
-    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+constexpr int kFinalizeThreads = kMaxK;   // one wave: lane k <-> list entry k
+
+__global__ __launch_bounds__(kFinalizeThreads) void verify_sampled_kernel(
+    const float* tval, const int* tidx, const uint32_t* tvalid, const uint32_t* tflags, const float* dval,
+    const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int lanes, int drafts, int target_rows,
+    const int32_t* drafted, const vi_row_params* params, const int64_t* terminal, int n_terminal, int vocabulary,
+    int32_t* accepted, int32_t* committed, int32_t* committed_count, uint32_t* lane_flags) {
+    __shared__ ListDist P, Q;
+    __shared__ double s_rv[kMaxK], s_pv[kMaxK];
+    __shared__ int s_rid[kMaxK];
+    __shared__ int s_go;   // lane 0's verdict for the position: 1 = next position, 0 = done
+    const int l = blockIdx.x, k = threadIdx.x;
     if (l >= lanes) return;
     const vi_row_params p = params[l];
     int32_t* out = committed + size_t(l) * (drafts + 1);
-    for (int j = 0; j <= drafts; ++j) out[j] = -1;
-    uint32_t flags = 0;
+    if (k == 0)
+        for (int j = 0; j <= drafts; ++j) out[j] = -1;
+    uint32_t flags = 0;   // (lane 0's)
     int c = 0, acc = 0;
     bool stopped = false, rejected = false;
-    ListDist P, Q;
-    for (int j = 0; j < drafts && !stopped; ++j) {
+    for (int j = 0; j < drafts; ++j) {
         const size_t tr = size_t(l) * target_rows + j, dr = size_t(l) * drafts + j;
-        flags |= tflags[tr] | dflags[dr];
         list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
         list_dist(p, dval + dr * kMaxK, didx + dr * kMaxK, dvalid[dr], Q);
-        if (tvalid[tr] == 0 || dvalid[dr] == 0) flags |= VI_FLAG_EMPTY;
         const int32_t d = drafted[dr];
-        const int pos = p.position + j;
-        const double ua = philox_uniform(p.seed, p.lane, pos, 1u), uc = philox_uniform(p.seed, p.lane, pos, 2u);
-        const double q = (d >= 0 && d < vocabulary) ? list_prob(Q, d) : 0.0;
-        double acc_p = 0.0;
-        if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
-        else acc_p = fmin(1.0, list_prob(P, d) / q);
-        if (q != 0.0 && ua < acc_p) {
-            out[c++] = d;
-            ++acc;
-            stopped = is_terminal(terminal, n_terminal, d);
-            continue;
+        const int iq = (d >= 0 && d < vocabulary) ? list_find(Q, d) : -1;
+        const int ip = list_find(P, d);
+        if (k == 0) {
+            flags |= tflags[tr] | dflags[dr];
+            if (tvalid[tr] == 0 || dvalid[dr] == 0) flags |= VI_FLAG_EMPTY;
+            const int pos = p.position + j;
+            const double ua = philox_uniform(p.seed, p.lane, pos, 1u);
+            const double q = iq >= 0 ? Q.w[iq] / Q.sn : 0.0;
+            double acc_p = 0.0;
+            if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
+            else acc_p = fmin(1.0, (ip >= 0 ? P.w[ip] / P.sn : 0.0) / q);
+            if (q != 0.0 && ua < acc_p) {
+                out[c++] = d;
+                ++acc;
+                stopped = is_terminal(terminal, n_terminal, d);
+                s_go = stopped ? 0 : 1;
+            } else {
+                rejected = true;
+                s_go = 0;
+            }
         }
-        // residual max(0, p - q) over p's support, in token-id order
-        int rid[kMaxK];
-        double rv[kMaxK];
-        int m = 0;
-        for (int k = 0; k < P.support; ++k) {
+        __syncthreads();
+        const int go = s_go;
+        const bool rej = __builtin_amdgcn_readfirstlane(int(rejected)) != 0;
+        __syncthreads();
+        if (go) continue;
+        if (!rej) break;
+        // residual max(0, p - q) over p's support, placed in token-id order by
+        // rank (ids within a list are distinct)
+        if (k < P.support) {
             const int t = P.id[k];
-            int at = m++;
-            while (at > 0 && rid[at - 1] > t) { rid[at] = rid[at - 1]; rv[at] = rv[at - 1]; --at; }
-            rid[at] = t;
-            rv[at] = P.w[k] / P.sn;
+            int rank = 0;
+            for (int i = 0; i < P.support; ++i) rank += P.id[i] < t ? 1 : 0;
+            double qt = 0.0;
+            for (int i = 0; i < Q.support; ++i)
+                if (Q.id[i] == t) { qt = Q.w[i] / Q.sn; break; }
+            const double pk = P.w[k] / P.sn;
+            s_rid[rank] = t;
+            s_pv[rank] = pk;
+            s_rv[rank] = fmax(0.0, pk - qt);
         }
-        double sum = 0.0;
-        for (int k = 0; k < m; ++k) { rv[k] = fmax(0.0, rv[k] - list_prob(Q, rid[k])); sum += rv[k]; }
-        int32_t corr = 0;
-        if (!(sum > 1e-9) || !isfinite(sum)) {
-            // No residual mass: correct from p itself (inverse CDF, id order).
-            flags |= VI_FLAG_NO_RESIDUAL;
-            double cum = 0.0;
-            int32_t last = 0;
-            bool found = false;
-            for (int k = 0; k < m; ++k) {
-                const double pv = list_prob(P, rid[k]);
-                if (pv > 0.0) last = rid[k];
-                cum += pv;
-                if (uc < cum) { corr = rid[k]; found = true; break; }
+        __syncthreads();
+        if (k == 0) {
+            const int m = P.support;
+            const double uc = philox_uniform(p.seed, p.lane, p.position + j, 2u);
+            double sum = 0.0;
+            for (int i = 0; i < m; ++i) sum += s_rv[i];
+            int32_t corr = 0;
+            if (!(sum > 1e-9) || !isfinite(sum)) {
+                // No residual mass: correct from p itself (inverse CDF, id order).
+                flags |= VI_FLAG_NO_RESIDUAL;
+                double cum = 0.0;
+                int32_t last = 0;
+                bool found = false;
+                for (int i = 0; i < m; ++i) {
+                    const double pv = s_pv[i];
+                    if (pv > 0.0) last = s_rid[i];
+                    cum += pv;
+                    if (uc < cum) { corr = s_rid[i]; found = true; break; }
+                }
+                if (!found) corr = last;
+            } else {
+                double cum = 0.0;
+                int32_t last = 0;
+                bool found = false;
+                for (int i = 0; i < m; ++i) {
+                    const double r = s_rv[i] / sum;
+                    if (r > 0.0) last = s_rid[i];
+                    cum += r;
+                    if (uc < cum) { corr = s_rid[i]; found = true; break; }
+                }
+                if (!found) corr = last;
             }
-            if (!found) corr = last;
-        } else {
-            double cum = 0.0;
-            int32_t last = 0;
-            bool found = false;
-            for (int k = 0; k < m; ++k) {
-                const double r = rv[k] / sum;
-                if (r > 0.0) last = rid[k];
-                cum += r;
-                if (uc < cum) { corr = rid[k]; found = true; break; }
-            }
-            if (!found) corr = last;
+            out[c++] = corr;
         }
-        out[c++] = corr;
-        rejected = true;
         break;
     }
-    if (!rejected && !stopped && acc == drafts && target_rows == drafts + 1) {
+    const bool bonus = __builtin_amdgcn_readfirstlane(
+                           int(!rejected && !stopped && acc == drafts && target_rows == drafts + 1)) != 0;
+    if (bonus) {
         const size_t tr = size_t(l) * target_rows + drafts;
-        flags |= tflags[tr];
         list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
-        if (tvalid[tr]) {
-            if (P.greedy) out[c++] = P.id[0];
-            else {
-                const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
-                double cum = 0.0;
-                int pick = P.support - 1;
-                for (int k = 0; k < P.support; ++k) { cum += P.w[k]; if (cum > t) { pick = k; break; } }
-                out[c++] = P.id[pick];
+        if (k == 0) {
+            flags |= tflags[tr];
+            if (tvalid[tr]) {
+                if (!(p.temperature > 0.0f)) out[c++] = P.id[0];
+                else {
+                    const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
+                    double cum = 0.0;
+                    int pick = P.support - 1;
+                    for (int i = 0; i < P.support; ++i) { cum += P.w[i]; if (cum > t) { pick = i; break; } }
+                    out[c++] = P.id[pick];
+                }
             }
         }
     }
-    accepted[l] = acc;
-    committed_count[l] = c;
-    if (lane_flags) lane_flags[l] = flags;
+    if (k == 0) {
+        accepted[l] = acc;
+        committed_count[l] = c;
+        if (lane_flags) lane_flags[l] = flags;
+    }
 }
 
 }  // namespace
@@ -257,7 +305,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     st = launch_verify_lists(a.draft, a.draft_dtype, drows, v.lrows, v.lslices, a.vocabulary, a.draft_stride,
                              a.params, a.drafts, dval, didx, dvalid, dflags, lws, lbytes, stream);
     if (st != VI_OK) return st;
-    hipLaunchKernelGGL(verify_sampled_kernel, dim3(blocks), dim3(threads), 0, stream, tval, tidx, tvalid, tflags,
+    hipLaunchKernelGGL(verify_sampled_kernel, dim3(a.lanes), dim3(kFinalizeThreads), 0, stream, tval, tidx, tvalid, tflags,
                        dval, didx, dvalid, dflags, a.lanes, a.drafts, a.target_rows, a.drafted, a.params,
                        a.terminal, a.n_terminal, a.vocabulary, a.accepted, a.committed, a.committed_count,
                        a.lane_flags);
