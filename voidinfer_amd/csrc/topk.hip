@@ -111,6 +111,23 @@ __device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci
     L.ki = readlane_i(L.i, K - 1);
 }
 
+// The k-th largest (1 <= k <= 64) of the wave's 64 values (none NaN): a
+// bitonic sort, descending, across the lanes.
+__device__ __forceinline__ float wave_kth_largest(float x, int k) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const float y = shfl_xor_f(x, stride);
+            const bool desc = (lane & size) == 0 || size == kWave;   // the last merge runs descending
+            const bool low = (lane & stride) == 0;
+            x = (low == desc) ? fmaxf(x, y) : fminf(x, y);
+        }
+    }
+    return readlane_f(x, k - 1);
+}
+
 // Offer one candidate per lane (wave-uniform call).
 __device__ __forceinline__ void list_offer(WaveList& L, int K, bool ok, float v, int id) {
     uint64_t m = ballot(ok && better(v, id, L.kv, L.ki));
@@ -359,6 +376,29 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     // per element), and the list offered the vector's elements only when some
     // lane's vector maximum reaches the list's K-th entry (no element of a vector
     // below it can enter: it is exact).
+    // Threshold from the first batch: the K-th largest of the lanes' maxima over
+    // their first four vectors.  At least K of the wave's elements reach it, so
+    // it never exceeds the row's K-th best: elements below it are never offered.
+    float tau = -kInfF;
+    auto first_fn = [&](const uint4 (&dv)[4], const bool (&okv)[4]) {
+        constexpr int P = Elem<DT>::kPerVec;
+        float lm = -kInfF;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const uint32_t bits = vec_bits<DT>(dv[u], j);
+                const float x = Elem<DT>::decode(bits);
+                if constexpr (MODE == kModeTopk) {
+                    lm = (okv[u] & !Elem<DT>::nan_bits(bits)) ? fmaxf(lm, x) : lm;
+                } else {
+                    const float v = p.temperature > 0.0f ? x * inv_t : x;
+                    lm = (okv[u] & Elem<DT>::finite_bits(bits) & isfinite(v)) ? fmaxf(lm, v) : lm;
+                }
+            }
+        }
+        tau = wave_kth_largest(lm, K);
+    };
     auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
         constexpr int P = Elem<DT>::kPerVec;
         float xs[P];
@@ -403,9 +443,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 vmax = live ? fmaxf(vmax, v) : vmax;
             }
         }
-        if (ballot(candm != 0u && vmax >= L.kv) == 0) return;
+        const float gate = fmaxf(L.kv, tau);
+        if (ballot(candm != 0u && vmax >= gate) == 0) return;
 #pragma unroll
-        for (int j = 0; j < P; ++j) list_offer(L, K, (candm >> j) & 1u, xs[j], id0 + j);
+        for (int j = 0; j < P; ++j) list_offer(L, K, ((candm >> j) & 1u) && xs[j] >= tau, xs[j], id0 + j);
     };
     auto elem_fn = [&](uint32_t bits, int id, bool ok) {
         const float x = Elem<DT>::decode(bits);
@@ -467,7 +508,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
     };
     if constexpr (MODE == kModeTopk || MODE == kModeVerify)
-        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, vec_fn, elem_fn);
+        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, first_fn, vec_fn, elem_fn);
     else
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
 
