@@ -52,11 +52,9 @@ __device__ __forceinline__ void scan_slice(const void* row, int begin, int end, 
 // As scan_slice, with each full 16-byte vector handed over whole:
 // vfn(vector, id of its element 0, valid) for the vectors, fn(bits, id, valid)
 // for the elements past the last full vector (and for every element of a row
-// whose stride breaks 16-byte alignment).  first(vectors[4], valid[4]) sees the
-// first batch of vectors once, before any of them is handed to vfn (wave-
-// uniform call).  Same trip-count guarantees.
-template <int DT, bool VEC, int NT, class FB, class FV, class F>
-__device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int end, FB&& first, FV&& vfn, F&& fn) {
+// whose stride breaks 16-byte alignment).  Same trip-count guarantees.
+template <int DT, bool VEC, int NT, class FV, class F>
+__device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int end, FV&& vfn, F&& fn) {
     constexpr int P = Elem<DT>::kPerVec;
     const int tid = threadIdx.x;
     if constexpr (VEC) {
@@ -69,12 +67,6 @@ __device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int e
             for (int u = 0; u < U; ++u) {
                 const int v = vb + u * NT + tid;
                 d[u] = v < nvec ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
-            }
-            if (vb == 0) {
-                bool okv[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) okv[u] = u * NT + tid < nvec;
-                first(d, okv);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
