@@ -14,9 +14,10 @@
 // u_a < min(1, p[d]/q[d]); at the first rejection draw the correction from the
 // residual max(0, p - q) normalised, inverse CDF in token-id order with u_c
 // (last positive id on round-off).  u_a, u_c are Philox draws keyed by
-// (seed, lane, position + j, purpose 1 / 2).  The finalize kernel runs one
-// wave per lane over the <= 64-entry lists (fp64): entry-wise work on the
-// lanes, the order-dependent sums on lane 0.
+// (seed, lane, position + j, purpose 1 / 2).  Every (lane, position) decision
+// is taken at once, one wave each over the <= 64-entry lists (fp64): entry-wise
+// work on the lanes, the order-dependent sums on lane 0; a per-lane pass then
+// walks the accept chain in order.
 #include <math.h>
 
 #include "vi_device.h"
@@ -114,130 +115,159 @@ __device__ __forceinline__ int list_find(const ListDist& d, int64_t token) {
 
 constexpr int kFinalizeThreads = kMaxK;   // one wave: lane k <-> list entry k
 
-__global__ __launch_bounds__(kFinalizeThreads) void verify_sampled_kernel(
+// The decision at one drafted position, which depends on that position's rows
+// and Philox draws only: accept (u_a < min(1, p(d)/q(d)), q(d) > 0) or the
+// correction token drawn from the residual; position `drafts` of a lane with a
+// bonus row holds the bonus draw.  Flags are the position's own.
+struct PosDecision {
+    int32_t token;    // correction / bonus token (-1: none)
+    uint32_t flags;
+    int32_t accept;
+    int32_t pad;
+};
+
+// One wave per (position, lane): every position of every lane at once; the
+// accept chain is resolved afterwards by verify_chain_kernel.
+__global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     const float* tval, const int* tidx, const uint32_t* tvalid, const uint32_t* tflags, const float* dval,
-    const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int lanes, int drafts, int target_rows,
-    const int32_t* drafted, const vi_row_params* params, const int64_t* terminal, int n_terminal, int vocabulary,
-    int32_t* accepted, int32_t* committed, int32_t* committed_count, uint32_t* lane_flags) {
+    const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int drafts, int target_rows,
+    const int32_t* drafted, const vi_row_params* params, int vocabulary, PosDecision* dec) {
     __shared__ ListDist P, Q;
     __shared__ double s_rv[kMaxK], s_pv[kMaxK];
     __shared__ int s_rid[kMaxK];
-    __shared__ int s_go;   // lane 0's verdict for the position: 1 = next position, 0 = done
-    const int l = blockIdx.x, k = threadIdx.x;
-    if (l >= lanes) return;
+    __shared__ int s_accept;
+    const int j = blockIdx.x, l = blockIdx.y, k = threadIdx.x;
     const vi_row_params p = params[l];
-    int32_t* out = committed + size_t(l) * (drafts + 1);
-    if (k == 0)
-        for (int j = 0; j <= drafts; ++j) out[j] = -1;
-    uint32_t flags = 0;   // (lane 0's)
-    int c = 0, acc = 0;
-    bool stopped = false, rejected = false;
-    for (int j = 0; j < drafts; ++j) {
-        const size_t tr = size_t(l) * target_rows + j, dr = size_t(l) * drafts + j;
-        list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
-        list_dist(p, dval + dr * kMaxK, didx + dr * kMaxK, dvalid[dr], Q);
-        const int32_t d = drafted[dr];
-        const int iq = (d >= 0 && d < vocabulary) ? list_find(Q, d) : -1;
-        const int ip = list_find(P, d);
-        if (k == 0) {
-            flags |= tflags[tr] | dflags[dr];
-            if (tvalid[tr] == 0 || dvalid[dr] == 0) flags |= VI_FLAG_EMPTY;
-            const int pos = p.position + j;
-            const double ua = philox_uniform(p.seed, p.lane, pos, 1u);
-            const double q = iq >= 0 ? Q.w[iq] / Q.sn : 0.0;
-            double acc_p = 0.0;
-            if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
-            else acc_p = fmin(1.0, (ip >= 0 ? P.w[ip] / P.sn : 0.0) / q);
-            if (q != 0.0 && ua < acc_p) {
-                out[c++] = d;
-                ++acc;
-                stopped = is_terminal(terminal, n_terminal, d);
-                s_go = stopped ? 0 : 1;
-            } else {
-                rejected = true;
-                s_go = 0;
-            }
-        }
-        __syncthreads();
-        const int go = s_go;
-        const bool rej = __builtin_amdgcn_readfirstlane(int(rejected)) != 0;
-        __syncthreads();
-        if (go) continue;
-        if (!rej) break;
-        // residual max(0, p - q) over p's support, placed in token-id order by
-        // rank (ids within a list are distinct)
-        if (k < P.support) {
-            const int t = P.id[k];
-            int rank = 0;
-            for (int i = 0; i < P.support; ++i) rank += P.id[i] < t ? 1 : 0;
-            double qt = 0.0;
-            for (int i = 0; i < Q.support; ++i)
-                if (Q.id[i] == t) { qt = Q.w[i] / Q.sn; break; }
-            const double pk = P.w[k] / P.sn;
-            s_rid[rank] = t;
-            s_pv[rank] = pk;
-            s_rv[rank] = fmax(0.0, pk - qt);
-        }
-        __syncthreads();
-        if (k == 0) {
-            const int m = P.support;
-            const double uc = philox_uniform(p.seed, p.lane, p.position + j, 2u);
-            double sum = 0.0;
-            for (int i = 0; i < m; ++i) sum += s_rv[i];
-            int32_t corr = 0;
-            if (!(sum > 1e-9) || !isfinite(sum)) {
-                // No residual mass: correct from p itself (inverse CDF, id order).
-                flags |= VI_FLAG_NO_RESIDUAL;
-                double cum = 0.0;
-                int32_t last = 0;
-                bool found = false;
-                for (int i = 0; i < m; ++i) {
-                    const double pv = s_pv[i];
-                    if (pv > 0.0) last = s_rid[i];
-                    cum += pv;
-                    if (uc < cum) { corr = s_rid[i]; found = true; break; }
-                }
-                if (!found) corr = last;
-            } else {
-                double cum = 0.0;
-                int32_t last = 0;
-                bool found = false;
-                for (int i = 0; i < m; ++i) {
-                    const double r = s_rv[i] / sum;
-                    if (r > 0.0) last = s_rid[i];
-                    cum += r;
-                    if (uc < cum) { corr = s_rid[i]; found = true; break; }
-                }
-                if (!found) corr = last;
-            }
-            out[c++] = corr;
-        }
-        break;
-    }
-    const bool bonus = __builtin_amdgcn_readfirstlane(
-                           int(!rejected && !stopped && acc == drafts && target_rows == drafts + 1)) != 0;
-    if (bonus) {
-        const size_t tr = size_t(l) * target_rows + drafts;
+    PosDecision* out = dec + size_t(l) * (drafts + 1) + j;
+    const size_t tr = size_t(l) * target_rows + j;
+    if (j == drafts) {   // the bonus row's draw (used when every draft is accepted)
+        if (target_rows != drafts + 1) return;
         list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
         if (k == 0) {
-            flags |= tflags[tr];
+            int32_t tok = -1;
             if (tvalid[tr]) {
-                if (!(p.temperature > 0.0f)) out[c++] = P.id[0];
+                if (!(p.temperature > 0.0f)) tok = P.id[0];
                 else {
                     const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
                     double cum = 0.0;
                     int pick = P.support - 1;
                     for (int i = 0; i < P.support; ++i) { cum += P.w[i]; if (cum > t) { pick = i; break; } }
-                    out[c++] = P.id[pick];
+                    tok = P.id[pick];
                 }
             }
+            *out = PosDecision{tok, tflags[tr], 0, 0};
         }
+        return;
     }
+    const size_t dr = size_t(l) * drafts + j;
+    list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
+    list_dist(p, dval + dr * kMaxK, didx + dr * kMaxK, dvalid[dr], Q);
+    const int32_t d = drafted[dr];
+    const int iq = (d >= 0 && d < vocabulary) ? list_find(Q, d) : -1;
+    const int ip = list_find(P, d);
+    uint32_t flags = 0;   // (lane 0's)
     if (k == 0) {
-        accepted[l] = acc;
-        committed_count[l] = c;
-        if (lane_flags) lane_flags[l] = flags;
+        flags = tflags[tr] | dflags[dr];
+        if (tvalid[tr] == 0 || dvalid[dr] == 0) flags |= VI_FLAG_EMPTY;
+        const double ua = philox_uniform(p.seed, p.lane, p.position + j, 1u);
+        const double q = iq >= 0 ? Q.w[iq] / Q.sn : 0.0;
+        double acc_p = 0.0;
+        if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
+        else acc_p = fmin(1.0, (ip >= 0 ? P.w[ip] / P.sn : 0.0) / q);
+        s_accept = (q != 0.0 && ua < acc_p) ? 1 : 0;
+        if (s_accept) *out = PosDecision{-1, flags, 1, 0};
     }
+    __syncthreads();
+    if (s_accept) return;
+    // residual max(0, p - q) over p's support, placed in token-id order by rank
+    // (ids within a list are distinct)
+    if (k < P.support) {
+        const int t = P.id[k];
+        int rank = 0;
+        for (int i = 0; i < P.support; ++i) rank += P.id[i] < t ? 1 : 0;
+        double qt = 0.0;
+        for (int i = 0; i < Q.support; ++i)
+            if (Q.id[i] == t) { qt = Q.w[i] / Q.sn; break; }
+        const double pk = P.w[k] / P.sn;
+        s_rid[rank] = t;
+        s_pv[rank] = pk;
+        s_rv[rank] = fmax(0.0, pk - qt);
+    }
+    __syncthreads();
+    if (k == 0) {
+        const int m = P.support;
+        const double uc = philox_uniform(p.seed, p.lane, p.position + j, 2u);
+        double sum = 0.0;
+        for (int i = 0; i < m; ++i) sum += s_rv[i];
+        int32_t corr = 0;
+        if (!(sum > 1e-9) || !isfinite(sum)) {
+            // No residual mass: correct from p itself (inverse CDF, id order).
+            flags |= VI_FLAG_NO_RESIDUAL;
+            double cum = 0.0;
+            int32_t last = 0;
+            bool found = false;
+            for (int i = 0; i < m; ++i) {
+                const double pv = s_pv[i];
+                if (pv > 0.0) last = s_rid[i];
+                cum += pv;
+                if (uc < cum) { corr = s_rid[i]; found = true; break; }
+            }
+            if (!found) corr = last;
+        } else {
+            double cum = 0.0;
+            int32_t last = 0;
+            bool found = false;
+            for (int i = 0; i < m; ++i) {
+                const double r = s_rv[i] / sum;
+                if (r > 0.0) last = s_rid[i];
+                cum += r;
+                if (uc < cum) { corr = s_rid[i]; found = true; break; }
+            }
+            if (!found) corr = last;
+        }
+        *out = PosDecision{corr, flags, 0, 0};
+    }
+}
+
+// The accept chain of each lane over its position decisions, in order: accepted
+// drafts are committed until the first rejection (its correction is committed
+// and ends the chain) or a terminal token; a lane that accepted every draft
+// commits the bonus draw.  Flags of the positions visited (and the bonus row).
+__global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int drafts, int target_rows,
+                                    const int32_t* drafted, const int64_t* terminal, int n_terminal,
+                                    int32_t* accepted, int32_t* committed, int32_t* committed_count,
+                                    uint32_t* lane_flags) {
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= lanes) return;
+    const PosDecision* D = dec + size_t(l) * (drafts + 1);
+    int32_t* out = committed + size_t(l) * (drafts + 1);
+    for (int j = 0; j <= drafts; ++j) out[j] = -1;
+    uint32_t flags = 0;
+    int c = 0, acc = 0;
+    bool stopped = false, rejected = false;
+    for (int j = 0; j < drafts; ++j) {
+        const PosDecision e = D[j];
+        flags |= e.flags;
+        if (e.accept) {
+            const int32_t d = drafted[size_t(l) * drafts + j];
+            out[c++] = d;
+            ++acc;
+            stopped = is_terminal(terminal, n_terminal, d);
+            if (stopped) break;
+            continue;
+        }
+        out[c++] = e.token;
+        rejected = true;
+        break;
+    }
+    if (!rejected && !stopped && acc == drafts && target_rows == drafts + 1) {
+        const PosDecision b = D[drafts];
+        flags |= b.flags;
+        if (b.token >= 0) out[c++] = b.token;
+    }
+    accepted[l] = acc;
+    committed_count[l] = c;
+    if (lane_flags) lane_flags[l] = flags;
 }
 
 }  // namespace
@@ -263,6 +293,7 @@ size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     b += 2 * align_up(size_t(v.trows + v.drows) * kMaxK * 4, 256) + 2 * align_up(size_t(v.trows + v.drows) * 4, 256);
     b += align_up(greedy_workspace(v.trows, vocabulary), 256);
     b += topk_partials_bytes_slices(v.lrows, v.lslices);
+    b += align_up(size_t(v.trows) * sizeof(PosDecision), 256);
     return b + 4096;
 }
 
@@ -281,6 +312,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     uint32_t* tflags = c.take<uint32_t>(size_t(v.trows));
     uint32_t* dvalid = c.take<uint32_t>(size_t(v.drows));
     uint32_t* dflags = c.take<uint32_t>(size_t(v.drows));
+    PosDecision* dec = c.take<PosDecision>(size_t(v.trows));
     const size_t gbytes = greedy_workspace(v.trows, a.vocabulary);
     unsigned char* gws = gbytes ? c.take<unsigned char>(gbytes) : nullptr;
     const size_t lbytes = topk_partials_bytes_slices(v.lrows, v.lslices);
@@ -305,10 +337,14 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     st = launch_verify_lists(a.draft, a.draft_dtype, drows, v.lrows, v.lslices, a.vocabulary, a.draft_stride,
                              a.params, a.drafts, dval, didx, dvalid, dflags, lws, lbytes, stream);
     if (st != VI_OK) return st;
-    hipLaunchKernelGGL(verify_sampled_kernel, dim3(a.lanes), dim3(kFinalizeThreads), 0, stream, tval, tidx, tvalid, tflags,
-                       dval, didx, dvalid, dflags, a.lanes, a.drafts, a.target_rows, a.drafted, a.params,
-                       a.terminal, a.n_terminal, a.vocabulary, a.accepted, a.committed, a.committed_count,
-                       a.lane_flags);
+    hipLaunchKernelGGL(verify_position_kernel, dim3(a.drafts + 1, a.lanes), dim3(kFinalizeThreads), 0, stream, tval,
+                       tidx, tvalid, tflags, dval, didx, dvalid, dflags, a.drafts, a.target_rows, a.drafted, a.params,
+                       a.vocabulary, dec);
+    st = launch_status();
+    if (st != VI_OK) return st;
+    hipLaunchKernelGGL(verify_chain_kernel, dim3(blocks), dim3(threads), 0, stream, dec, a.lanes, a.drafts,
+                       a.target_rows, a.drafted, a.terminal, a.n_terminal, a.accepted, a.committed,
+                       a.committed_count, a.lane_flags);
     return launch_status();
 }
 
