@@ -52,16 +52,32 @@ __device__ __forceinline__ void scan_slice(const void* row, int begin, int end, 
 // As scan_slice, with each full 16-byte vector handed over whole:
 // vfn(vector, id of its element 0, valid) for the vectors, fn(bits, id, valid)
 // for the elements past the last full vector (and for every element of a row
-// whose stride breaks 16-byte alignment).  Same trip-count guarantees.
-template <int DT, bool VEC, int NT, class FV, class F>
-__device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int end, FV&& vfn, F&& fn) {
+// whose stride breaks 16-byte alignment).  first(vectors[4], valid[4]) sees the
+// first batch once, after its loads and before vfn (the batch is peeled off the
+// loop); it is not called when the slice has no full vector.  Same trip-count
+// guarantees.
+template <int DT, bool VEC, int NT, class FB, class FV, class F>
+__device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int end, FB&& first, FV&& vfn, F&& fn) {
     constexpr int P = Elem<DT>::kPerVec;
     const int tid = threadIdx.x;
     if constexpr (VEC) {
         const int nvec = (end - begin) / P;
         const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
         constexpr int U = 4;
-        for (int vb = 0; vb < nvec; vb += U * NT) {
+        if (nvec > 0) {   // (uniform) the first batch
+            uint4 d[U];
+            bool okv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = u * NT + tid;
+                okv[u] = v < nvec;
+                d[u] = okv[u] ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+            }
+            first(d, okv);
+#pragma unroll
+            for (int u = 0; u < U; ++u) vfn(d[u], begin + (u * NT + tid) * P, okv[u]);
+        }
+        for (int vb = U * NT; vb < nvec; vb += U * NT) {
             uint4 d[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {

@@ -376,35 +376,29 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     // per element), and the list offered the vector's elements only when some
     // lane's vector maximum reaches the list's K-th entry (no element of a vector
     // below it can enter: it is exact).
-    // Threshold: the K-th largest of the lanes' maxima over the first vectors the
-    // wave scans (read once more here, from L2).  At least K of the wave's
-    // elements reach it, so it never exceeds the row's K-th best: elements below
-    // it are never offered.
+    // Threshold from the first batch: the K-th largest of the lanes' maxima over
+    // their first four vectors.  At least K of the wave's elements reach it, so
+    // it never exceeds the row's K-th best: elements below it are never offered.
     float tau = -kInfF;
-    if constexpr (VEC && (MODE == kModeTopk || MODE == kModeVerify)) {
+    auto first_fn = [&](const uint4 (&dv)[4], const bool (&okv)[4]) {
         constexpr int P = Elem<DT>::kPerVec;
-        const int nvec = (end - begin) / P;
-        const unsigned char* vbase = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
         float lm = -kInfF;
-#pragma unroll 1
+#pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int v = u * kTopkThreads + int(threadIdx.x);
-            if (v >= nvec) break;
-            const uint4 dv = load16(vbase + size_t(v) * 16);
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                const uint32_t bits = vec_bits<DT>(dv, j);
+                const uint32_t bits = vec_bits<DT>(dv[u], j);
                 const float x = Elem<DT>::decode(bits);
                 if constexpr (MODE == kModeTopk) {
-                    lm = !Elem<DT>::nan_bits(bits) ? fmaxf(lm, x) : lm;
+                    lm = (okv[u] & !Elem<DT>::nan_bits(bits)) ? fmaxf(lm, x) : lm;
                 } else {
                     const float v2 = p.temperature > 0.0f ? x * inv_t : x;
-                    lm = (Elem<DT>::finite_bits(bits) & isfinite(v2)) ? fmaxf(lm, v2) : lm;
+                    lm = (okv[u] & Elem<DT>::finite_bits(bits) & isfinite(v2)) ? fmaxf(lm, v2) : lm;
                 }
             }
         }
         tau = wave_kth_largest(lm, K);
-    }
+    };
     auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
         constexpr int P = Elem<DT>::kPerVec;
         float xs[P];
@@ -522,7 +516,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
     };
     if constexpr (MODE == kModeTopk || MODE == kModeVerify)
-        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, vec_fn, elem_fn);
+        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, first_fn, vec_fn, elem_fn);
     else
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
 
