@@ -111,6 +111,33 @@ __device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci
     L.ki = readlane_i(L.i, K - 1);
 }
 
+// Merge of two sorted lists (lane = rank, (value desc, id asc), unused ranks
+// (-inf, kInvalidId)): the better of each entry and the other list's entry of
+// rank 63 - lane forms a bitonic sequence holding the best 64 of both, which a
+// descending bitonic merge puts in order.  Ranks >= K are cleared afterwards,
+// so the list keeps its form.
+__device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi) {
+    const int lane = lane_id();
+    const int rsrc = (kWave - 1 - lane) << 2;
+    const float rv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(rsrc, __builtin_bit_cast(int, bv)));
+    const int ri = __builtin_amdgcn_ds_bpermute(rsrc, bi);
+    float v = L.v;
+    int i = L.i;
+    if (better(rv, ri, v, i)) { v = rv; i = ri; }
+#pragma unroll
+    for (int stride = kWave / 2; stride > 0; stride >>= 1) {
+        const float pv = shfl_xor_f(v, stride);
+        const int pi = shfl_xor_i(i, stride);
+        const bool low = (lane & stride) == 0;
+        const bool take = low ? better(pv, pi, v, i) : better(v, i, pv, pi);
+        if (take) { v = pv; i = pi; }
+    }
+    L.v = lane < K ? v : -kInfF;
+    L.i = lane < K ? i : kInvalidId;
+    L.kv = readlane_f(L.v, K - 1);
+    L.ki = readlane_i(L.i, K - 1);
+}
+
 // The k-th largest (1 <= k <= 64) of the wave's 64 values (none NaN): a
 // bitonic sort, descending, across the lanes.
 __device__ __forceinline__ float wave_kth_largest(float x, int k) {
@@ -546,7 +573,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     }
     __syncthreads();
     if (wave != 0) return;
-    for (int w = 1; w < kTopkWaves; ++w) list_offer(L, K, lane < K, s_val[w][lane], s_idx[w][lane]);
+    for (int w = 1; w < kTopkWaves; ++w)
+        list_merge(L, K, lane < K ? s_val[w][lane] : -kInfF, lane < K ? s_idx[w][lane] : kInvalidId);
     uint32_t f = 0, c = 0;
     float m = -kInfF;
     for (int w = 0; w < kTopkWaves; ++w) { f |= s_flags[w]; c += s_valid[w]; m = fmaxf(m, s_lm[w]); }
@@ -569,12 +597,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         __threadfence();
         L = WaveList{};
         f = 0; c = 0; m = -kInfF;
-        for (int base = 0; base < slices * K; base += kWave) {
-            const int e = base + lane;
-            const bool ok = e < slices * K;
-            const int sl = ok ? e / K : 0, j = ok ? e % K : 0;
-            const size_t src = (size_t(r) * slices + sl) * kMaxK + j;
-            list_offer(L, K, ok, ok ? a.pval[src] : -kInfF, ok ? a.pidx[src] : kInvalidId);
+        for (int sl = 0; sl < slices; ++sl) {   // every slice's sorted list, merged in
+            const size_t src = (size_t(r) * slices + sl) * kMaxK + lane;
+            list_merge(L, K, lane < K ? a.pval[src] : -kInfF, lane < K ? a.pidx[src] : kInvalidId);
         }
         for (int sl = 0; sl < slices; ++sl) {
             const SliceHeader h = a.phdr[size_t(r) * slices + sl];
