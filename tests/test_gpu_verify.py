@@ -101,3 +101,26 @@ def test_sampled_many_lanes_small_vocab(orc, dev, rng):
     g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
     exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-9}
     assert_same(g, w, exempt)
+
+
+def test_sampled_nonfinite_and_overflowing_targets(orc, dev, rng):
+    """Target rows holding +-Inf / NaN, and finite bf16 logits that overflow once
+    divided by the temperature (the exact per-element path of the slice scan),
+    beside clean rows (its all-finite fast path)."""
+    from voidinfer_amd import workloads as W
+    lanes, drafts, vocab = 16, 4, 5000
+    p0 = W.config4(lanes=lanes, drafts=drafts, vocab=vocab)[3]
+    p0["temperature"] = rng.choice([0.0, 0.25, 0.5, 1.0], lanes)
+    p0["top_k"] = rng.choice([1, 8, 20], lanes)
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, vocab=vocab, sample_fn=sampler_from_draft(orc, p0))
+    p[:] = p0
+    big = int(np.float32(3.0e38).view(np.uint32) >> 16)
+    for r in range(0, tb.shape[0], 3):
+        cols = rng.integers(0, vocab, 3)
+        tb[r, cols[0]] = big                                        # overflows at T < 1
+        tb[r, cols[1]] = [0x7F80, 0xFF80, 0x7FC0][r % 3]           # +Inf, -Inf, NaN
+        tb[r, cols[2]] = big | 0x8000                               # huge negative
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-9}
+    assert_same(g, w, exempt)
+    assert any(f != 0 for f in w[3])

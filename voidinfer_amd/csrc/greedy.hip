@@ -92,20 +92,20 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
             return;
         }
         GreedyPartial& p = partials[size_t(r) * slices + slice];
-        p.best = best; p.index = index; p.bad = b;
-        __threadfence();
+        put_agent(&p.best, best); put_agent(&p.index, index); put_agent(&p.bad, b);
+        handoff_stores_done();
         s_last = atomicAdd(&arrivals[r], 1u) == uint32_t(slices - 1);
     }
     if (slices == 1) return;
     __syncthreads();
     if (!s_last || wave != 0) return;
-    __threadfence();
+    handoff_acquire();
     best = -kInfF; index = vocabulary;
     uint32_t b = 0;
     for (int s = lane; s < slices; s += kWave) {
-        const GreedyPartial p = partials[size_t(r) * slices + s];
-        greedy_combine(best, index, p.best, p.index);
-        b |= p.bad;
+        const GreedyPartial& p = partials[size_t(r) * slices + s];
+        greedy_combine(best, index, get_agent(&p.best), get_agent(&p.index));
+        b |= get_agent(&p.bad);
     }
 #pragma unroll
     for (int o = 32; o; o >>= 1) greedy_combine(best, index, shfl_xor_f(best, o), shfl_xor_i(index, o));

@@ -138,6 +138,18 @@ __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi)
     L.ki = readlane_i(L.i, K - 1);
 }
 
+// Any non-finite element in a 16-byte vector, from the raw words: adding the
+// lowest exponent step to the magnitude carries into the sign position exactly
+// when the exponent field is all ones (no carry crosses into the next element).
+template <int DT>
+__device__ __forceinline__ bool any_nonfinite(const uint4& v) {
+    constexpr uint32_t M = DT == VI_F32 ? 0x7fffffffu : 0x7fff7fffu;
+    constexpr uint32_t A = DT == VI_F32 ? 0x00800000u : (DT == VI_F16 ? 0x04000400u : 0x00800080u);
+    constexpr uint32_t S = DT == VI_F32 ? 0x80000000u : 0x80008000u;
+    const uint32_t t = ((v.x & M) + A) | ((v.y & M) + A) | ((v.z & M) + A) | ((v.w & M) + A);
+    return (t & S) != 0u;
+}
+
 // The k-th largest (1 <= k <= 64) of the wave's 64 values (none NaN): a
 // bitonic sort, descending, across the lanes.
 __device__ __forceinline__ float wave_kth_largest(float x, int k) {
@@ -386,9 +398,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             if (lookups) table = a.hash + size_t(r) * size_t(a.hash_slots);
         }
         lookup_all = lookups && !penalties_lower_only(p);
-        if (a.probs) {
+        if (a.probs) {   // (the row's last arriver writes the support over these zeros:
+                         // they are written through, and drained before the arrival)
             float* pr = a.probs + size_t(r) * size_t(a.probs_stride);
-            for (int i = begin + threadIdx.x; i < end; i += kTopkThreads) pr[i] = 0.0f;
+            for (int i = begin + threadIdx.x; i < end; i += kTopkThreads) put_agent(&pr[i], 0.0f);
         }
     }
 
@@ -426,7 +439,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         tau = wave_kth_largest(lm, K);
     };
-    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
+    auto vec_exact = [&](const uint4& dv, int id0, bool ok) {
         constexpr int P = Elem<DT>::kPerVec;
         float xs[P];
         uint32_t candm = 0;
@@ -481,6 +494,49 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             float v = Elem<DT>::decode(bits);
             if constexpr (MODE == kModeVerify) v = p.temperature > 0.0f ? v * inv_t : v;
             list_offer(L, K, ((candm >> j) & 1u) && v >= tau, v, id0 + j);
+        }
+    };
+    // Fast path: when no lane's vector holds a non-finite element (nor, in verify
+    // mode, one whose scaled logit overflows), every element is a candidate, no
+    // flag is raised, and the maximum bounds the vector; otherwise the wave takes
+    // vec_exact.
+    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
+        constexpr int P = Elem<DT>::kPerVec;
+        float xs[P];
+        float xmax = -kInfF, xmin = kInfF;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            xs[j] = Elem<DT>::decode(vec_bits<DT>(dv, j));
+            xmax = fmaxf(xmax, xs[j]);
+            xmin = fminf(xmin, xs[j]);
+        }
+        bool clean = !any_nonfinite<DT>(dv);
+        const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
+        if (scaled) clean = clean && isfinite(xmax * inv_t) && isfinite(xmin * inv_t);
+        if (ballot(ok && !clean) != 0) {
+            vec_exact(dv, id0, ok);
+            return;
+        }
+        const float vmax = scaled ? xmax * inv_t : xmax;   // (x * inv_t is monotone: the scaled maximum)
+        if constexpr (MODE == kModeTopk) {
+            if (want_lse && ok) {
+                if (xmax > lse_m) {
+                    lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - xmax) * kL2E);
+                    lse_m = xmax;
+                }
+#pragma unroll
+                for (int j = 0; j < P; ++j) lse_s += __builtin_amdgcn_exp2f((xs[j] - lse_m) * kL2E);
+            }
+        } else {
+            valid += ok ? uint32_t(P) : 0u;
+        }
+        const float gate = fmaxf(L.kv, tau);
+        if (ballot(ok && vmax >= gate) == 0) return;
+#pragma unroll 1
+        for (int j = 0; j < P; ++j) {
+            float v = Elem<DT>::decode(vec_bits<DT>(dv, j));
+            if (scaled) v = v * inv_t;
+            list_offer(L, K, ok && v >= tau, v, id0 + j);
         }
     };
     auto elem_fn = [&](uint32_t bits, int id, bool ok) {
@@ -571,6 +627,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) { s_flags[wave] = f; s_valid[wave] = c; s_lm[wave] = m; s_ls[wave] = s; }
     }
+    if constexpr (MODE == kModeSample) handoff_stores_done();   // every wave's probability zeros
     __syncthreads();
     if (wave != 0) return;
     for (int w = 1; w < kTopkWaves; ++w)
@@ -584,31 +641,31 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     if (slices > 1) {
         // ---- publish the slice, last arriver merges
         const size_t at = (size_t(r) * slices + slice) * kMaxK;
-        if (lane < K) { a.pval[at + lane] = L.v; a.pidx[at + lane] = L.i; }
+        if (lane < K) { put_agent(&a.pval[at + lane], L.v); put_agent(&a.pidx[at + lane], L.i); }
         if (lane == 0) {
-            SliceHeader h;
-            h.flags = f; h.valid = c; h.lse_max = m; h.pad = 0.0f; h.lse_sum = s;
-            a.phdr[size_t(r) * slices + slice] = h;
+            SliceHeader& h = a.phdr[size_t(r) * slices + slice];
+            put_agent(&h.flags, f); put_agent(&h.valid, c); put_agent(&h.lse_max, m); put_agent(&h.lse_sum, s);
         }
-        __threadfence();
+        handoff_stores_done();
         uint32_t arrived = 0;
         if (lane == 0) arrived = atomicAdd(&a.arrivals[r], 1u);
         if (readlane_i(int(arrived), 0) != slices - 1) return;
-        __threadfence();
+        handoff_acquire();
         L = WaveList{};
         f = 0; c = 0; m = -kInfF;
         for (int sl = 0; sl < slices; ++sl) {   // every slice's sorted list, merged in
             const size_t src = (size_t(r) * slices + sl) * kMaxK + lane;
-            list_merge(L, K, lane < K ? a.pval[src] : -kInfF, lane < K ? a.pidx[src] : kInvalidId);
+            list_merge(L, K, lane < K ? get_agent(&a.pval[src]) : -kInfF, lane < K ? get_agent(&a.pidx[src]) : kInvalidId);
         }
         for (int sl = 0; sl < slices; ++sl) {
-            const SliceHeader h = a.phdr[size_t(r) * slices + sl];
-            f |= h.flags; c += h.valid; m = fmaxf(m, h.lse_max);
+            const SliceHeader& h = a.phdr[size_t(r) * slices + sl];
+            f |= get_agent(&h.flags); c += get_agent(&h.valid); m = fmaxf(m, get_agent(&h.lse_max));
         }
         s = 0.0;
         for (int sl = 0; sl < slices; ++sl) {
-            const SliceHeader h = a.phdr[size_t(r) * slices + sl];
-            if (h.lse_max != -kInfF) s += h.lse_sum * exp(double(h.lse_max) - double(m));
+            const SliceHeader& h = a.phdr[size_t(r) * slices + sl];
+            const float hm = get_agent(&h.lse_max);
+            if (hm != -kInfF) s += get_agent(&h.lse_sum) * exp(double(hm) - double(m));
         }
         if (lane == 0) a.arrivals[r] = 0u;
     }

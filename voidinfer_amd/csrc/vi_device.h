@@ -10,6 +10,8 @@
 
 #include "../../include/voidinfer_sampling.h"
 
+#include <type_traits>
+
 namespace vi {
 
 constexpr int kWave = 64;
@@ -40,6 +42,35 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xo
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     // bitwise, not short-circuit: straight-line compares instead of exec-mask branches
     return (v > bv) | ((v == bv) & (i < bi));
+}
+
+// ------------------------------------------- hand-off between workgroups
+// gfx950 has one L2 per XCD and the L2s are not coherent with one another, so an
+// agent-scope release / acquire fence writes back and invalidates the whole L2
+// of the XCD (buffer_wbl2 / buffer_inv), microseconds per workgroup.  Values one
+// workgroup hands to another within a launch therefore travel as agent-scope
+// atomic stores and loads (the compiler lowers those to accesses the L2 writes
+// through and never serves from a stale line): the writer stores with put_agent,
+// drains with handoff_stores_done (its stores acknowledged before the arrival
+// read-modify-write that follows), and the reader, once that RMW has told it
+// every writer arrived, reads with get_agent.
+template <class T> __device__ __forceinline__ void put_agent(T* p, T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    using U = std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>;
+    __hip_atomic_store(reinterpret_cast<U*>(p), __builtin_bit_cast(U, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ T get_agent(const T* p) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    using U = std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>;
+    return __builtin_bit_cast(T, __hip_atomic_load(reinterpret_cast<const U*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void handoff_stores_done() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // no store is moved below (compiler)
+    __builtin_amdgcn_s_waitcnt(0x0f70);                      // vmcnt(0): every store acknowledged
+}
+__device__ __forceinline__ void handoff_acquire() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // no load is moved above (compiler)
 }
 
 // --------------------------------------------------------------- element decode
