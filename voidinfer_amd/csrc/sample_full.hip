@@ -807,10 +807,10 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                     uint32_t key[4];
                     key[0] = kb + 2u * uint32_t(lane); key[1] = key[0] + 1u;
                     key[2] = key[0] + 128u; key[3] = key[0] + 129u;
-                    if (cnt[0]) my_list[r0] = (key[0] << 16) | cnt[0];
-                    if (cnt[1]) my_list[r0 + (cnt[0] != 0u)] = (key[1] << 16) | cnt[1];
-                    if (cnt[2]) my_list[r1] = (key[2] << 16) | cnt[2];
-                    if (cnt[3]) my_list[r1 + (cnt[2] != 0u)] = (key[3] << 16) | cnt[3];
+                    if (cnt[0]) put_agent(&my_list[r0], (key[0] << 16) | cnt[0]);
+                    if (cnt[1]) put_agent(&my_list[r0 + (cnt[0] != 0u)], (key[1] << 16) | cnt[1]);
+                    if (cnt[2]) put_agent(&my_list[r1], (key[2] << 16) | cnt[2]);
+                    if (cnt[3]) put_agent(&my_list[r1 + (cnt[2] != 0u)], (key[3] << 16) | cnt[3]);
                     at = at1 + uint32_t(__builtin_popcountll(bal[2]) + __builtin_popcountll(bal[3]));
                     // validity and the bin's reference key (largest valid key)
                     float z[4];
@@ -844,11 +844,11 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
         if (lane < kCoarse / kFW) {
             const int bin = lane * kFW + wave;
-            my_summary->first[bin] = v_first;
-            my_summary->end[bin] = v_end;
-            my_summary->ccnt[bin] = v_cnt;
-            my_summary->bref[bin] = v_ref;
-            my_summary->cmass[bin] = v_mass;
+            put_agent(&my_summary->first[bin], v_first);
+            put_agent(&my_summary->end[bin], v_end);
+            put_agent(&my_summary->ccnt[bin], v_cnt);
+            put_agent(&my_summary->bref[bin], v_ref);
+            put_agent(&my_summary->cmass[bin], v_mass);
         }
         const uint32_t wsum = wave_sum_u32(my_sum), wnf = wave_sum_u32(my_nf);
         const uint32_t wfin = wsum - wnf;
@@ -861,12 +861,12 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         }
     }
 
-    // ---- C. pair barrier (self-resetting; generation counter).  Every wave
-    // drains its own list / summary stores to L2 (s_waitcnt); one wave then
-    // writes the header and publishes with a single agent-scope release and,
-    // after the partner arrived, takes a single agent-scope acquire on behalf
-    // of the workgroup; the spin polls with relaxed loads so it does not
-    // invalidate caches each round.
+    // ---- C. pair barrier (self-resetting; generation counter).  The list and
+    // the summary were written through (put_agent); every wave drains its own
+    // stores (s_waitcnt), one thread writes the header, drains it and arrives;
+    // the partner's data is then read with agent-scope loads (get_agent), so
+    // neither L2 is written back or invalidated.  The spin polls with relaxed
+    // loads.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -874,12 +874,12 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
         if (sh.n_sum != uint32_t(n_el)) f |= kHdrOverflow;  // a key held >= 65,536 logits of this half
         uint32_t n_list = 0;
         for (int w = 0; w < kFW; ++w) n_list += sh.wcount[w];
-        my_summary->n_list = n_list;
-        my_summary->n_finite = sh.n_fin;
-        my_summary->flags = f;
-        my_summary->top_key = sh.top1 ? sh.top1 - 1u : 0xffffffffu;
+        put_agent(&my_summary->n_list, n_list);
+        put_agent(&my_summary->n_finite, uint32_t(sh.n_fin));
+        put_agent(&my_summary->flags, f);
+        put_agent(&my_summary->top_key, sh.top1 ? sh.top1 - 1u : 0xffffffffu);
         PairBarrier* bar = &a.barriers[row];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        handoff_stores_done();
         const uint32_t gen = __hip_atomic_load(&bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (arrived == 1u) {
@@ -892,13 +892,13 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
                 if (++it > kSpinLimit) { sh.flags |= kHdrError; break; }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        handoff_acquire();
     }
     __syncthreads();
     const HalfSummary* S0 = a.summaries + size_t(row) * 2;
     const HalfSummary* S1 = S0 + 1;
-    const uint32_t hflags = S0->flags | S1->flags | (sh.flags & kHdrError);
-    const uint32_t tk0 = S0->top_key, tk1 = S1->top_key;
+    const uint32_t hflags = get_agent(&S0->flags) | get_agent(&S1->flags) | (sh.flags & kHdrError);
+    const uint32_t tk0 = get_agent(&S0->top_key), tk1 = get_agent(&S1->top_key);
     uint32_t out_flags = 0;
     if (hflags & kHdrNonfinite) out_flags |= VI_FLAG_NONFINITE;
     if (hflags & kHdrBadHistory) out_flags |= VI_FLAG_BAD_HISTORY;
@@ -939,15 +939,15 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
     for (int i = tid; i < 2 * kCoarse; i += kFT) {   // masses rescaled to z0
         const HalfSummary* Sh = i < kCoarse ? S0 : S1;
         const int c = i & (kCoarse - 1);
-        const uint32_t cc = Sh->ccnt[c];
+        const uint32_t cc = get_agent(&Sh->ccnt[c]);
         DC[i] = cc;
-        DM[i] = cc ? Sh->cmass[c] * exp(double(key_z<DT>(Sh->bref[c], inv_t)) - z0) : 0.0;
+        DM[i] = cc ? get_agent(&Sh->cmass[c]) * exp(double(key_z<DT>(get_agent(&Sh->bref[c]), inv_t)) - z0) : 0.0;
     }
     for (int i = tid; i < 2 * kCoarse; i += kFT) {
         const HalfSummary* Sh = i < kCoarse ? S0 : S1;
         const int c = i & (kCoarse - 1);
-        DF[2 * (i & ~(kCoarse - 1)) + c] = Sh->first[c];
-        DF[2 * (i & ~(kCoarse - 1)) + kCoarse + c] = Sh->end[c];
+        DF[2 * (i & ~(kCoarse - 1)) + c] = get_agent(&Sh->first[c]);
+        DF[2 * (i & ~(kCoarse - 1)) + kCoarse + c] = get_agent(&Sh->end[c]);
     }
     __syncthreads();
     if (wave != 0) {
@@ -1022,7 +1022,7 @@ __global__ __launch_bounds__(kFT) void full_kernel(FullArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const uint32_t i = f0 + uint32_t(lane + k * kWave);
-                    ent[h * 4 + k] = i < f1 ? gl[i] : 0u;
+                    ent[h * 4 + k] = i < f1 ? get_agent(&gl[i]) : 0u;
                 }
             }
 #pragma unroll
