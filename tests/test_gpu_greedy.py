@@ -88,3 +88,18 @@ def test_repeat_and_unmutated(orc, dev, rng):
     b = vi.greedy_packet(t)
     assert np.array_equal(a, b)
     assert np.array_equal(t.view(torch.int16).cpu().numpy().view(np.uint16), bits)
+
+
+def test_ties_inside_vectors_and_signed_zeros(orc, dev, rng):
+    """Maxima repeated inside one 16-byte vector (the first must win), and rows
+    whose largest values are +0 / -0 mixed (the first zero wins, either sign)."""
+    rows, vocab = 24, 40_960
+    x = rng.standard_normal((rows, vocab)).astype(np.float16)
+    for r in range(rows):
+        v = int(rng.integers(0, vocab // 8)) * 8
+        x[r, v + int(rng.integers(1, 8)):v + 8] = 6.0           # tie inside one vector
+        x[r, int(rng.integers(0, vocab))] = 6.0 if r % 3 == 0 else x[r, 0]
+    z = -np.abs(x[:8])
+    z[:, rng.integers(0, vocab, 64)] = np.float16(0.0)
+    z[:, rng.integers(0, vocab, 64)] = np.float16(-0.0)
+    check(orc, dev, np.concatenate([x, z]).view(np.uint16), 1, vocab)

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     float best = -kInfF;
     int index = vocabulary;
     bool bad = false;
-    scan_slice<DT, VEC, kGreedyThreads>(row, begin, end, [&](uint32_t bits, int id, bool ok) {
+    auto elem = [&](uint32_t bits, int id, bool ok) {
         if (!ok) return;
         const float x = Elem<DT>::decode(bits);
         if constexpr (SCORE) {
@@ -73,7 +73,37 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
             if (!Elem<DT>::finite_bits(bits)) { bad = true; return; }
         }
         if (x > best || (x == best && id < index)) { best = x; index = id; }
-    });
+    };
+    // Whole vectors: a thread visits its elements in increasing id order, so
+    // within a vector free of non-finite values the first maximum is taken only
+    // if it beats the running best strictly; a vector holding one goes element
+    // by element.
+    scan_slice_vec<DT, VEC, kGreedyThreads>(
+        row, begin, end, [](const auto&, const auto&) {},
+        [&](const uint4& dv, int id0, bool ok) {
+            constexpr int P = Elem<DT>::kPerVec;
+            if (!ok) return;
+            if (any_nonfinite<DT>(dv)) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) elem(vec_bits<DT>(dv, j), id0 + j, true);
+                return;
+            }
+            float xs[P];
+            float vmax = -kInfF;
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                xs[j] = Elem<DT>::decode(vec_bits<DT>(dv, j));
+                vmax = fmaxf(vmax, xs[j]);
+            }
+            if (vmax > best) {
+                int jj = P - 1;
+#pragma unroll
+                for (int j = P - 2; j >= 0; --j) jj = xs[j] == vmax ? j : jj;
+                best = xs[jj];   // (the element's own value: +0 and -0 compare equal)
+                index = id0 + jj;
+            }
+        },
+        elem);
 #pragma unroll
     for (int o = 32; o; o >>= 1) greedy_combine(best, index, shfl_xor_f(best, o), shfl_xor_i(index, o));
     const bool wave_bad = ballot(bad) != 0;

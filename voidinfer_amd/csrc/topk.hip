@@ -138,18 +138,6 @@ __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi)
     L.ki = readlane_i(L.i, K - 1);
 }
 
-// Any non-finite element in a 16-byte vector, from the raw words: adding the
-// lowest exponent step to the magnitude carries into the sign position exactly
-// when the exponent field is all ones (no carry crosses into the next element).
-template <int DT>
-__device__ __forceinline__ bool any_nonfinite(const uint4& v) {
-    constexpr uint32_t M = DT == VI_F32 ? 0x7fffffffu : 0x7fff7fffu;
-    constexpr uint32_t A = DT == VI_F32 ? 0x00800000u : (DT == VI_F16 ? 0x04000400u : 0x00800080u);
-    constexpr uint32_t S = DT == VI_F32 ? 0x80000000u : 0x80008000u;
-    const uint32_t t = ((v.x & M) + A) | ((v.y & M) + A) | ((v.z & M) + A) | ((v.w & M) + A);
-    return (t & S) != 0u;
-}
-
 // The k-th largest (1 <= k <= 64) of the wave's 64 values (none NaN): a
 // bitonic sort, descending, across the lanes.
 __device__ __forceinline__ float wave_kth_largest(float x, int k) {
@@ -532,11 +520,36 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         const float gate = fmaxf(L.kv, tau);
         if (ballot(ok && vmax >= gate) == 0) return;
+        // the (lane, element) pairs reaching the gate, offered one at a time as
+        // wave-uniform values (the list only rises meanwhile: each is checked
+        // again against it; the final list does not depend on the order)
+        uint32_t cm = 0;
+#pragma unroll
+        for (int j = 0; j < P; ++j) cm |= uint32_t(ok && (scaled ? xs[j] * inv_t : xs[j]) >= gate) << j;
+        uint64_t lanes = ballot(cm != 0u);
+        if (__builtin_popcountll(lanes) > 8) {   // many (large k, early in the slice): element-wise
 #pragma unroll 1
-        for (int j = 0; j < P; ++j) {
-            float v = Elem<DT>::decode(vec_bits<DT>(dv, j));
-            if (scaled) v = v * inv_t;
-            list_offer(L, K, ok && v >= tau, v, id0 + j);
+            for (int j = 0; j < P; ++j) {
+                float v = Elem<DT>::decode(vec_bits<DT>(dv, j));
+                if (scaled) v = v * inv_t;
+                list_offer(L, K, ((cm >> j) & 1u) != 0u, v, id0 + j);
+            }
+            return;
+        }
+        while (lanes) {
+            const int src = __builtin_ctzll(lanes);
+            lanes &= lanes - 1;
+            uint32_t m = uint32_t(readlane_i(int(cm), src));
+            const uint4 w = make_uint4(uint32_t(readlane_i(int(dv.x), src)), uint32_t(readlane_i(int(dv.y), src)),
+                                       uint32_t(readlane_i(int(dv.z), src)), uint32_t(readlane_i(int(dv.w), src)));
+            const int base = readlane_i(id0, src);
+            while (m) {
+                const int j = __builtin_ctz(m);
+                m &= m - 1;
+                float v = Elem<DT>::decode(vec_bits<DT>(w, j));
+                if (scaled) v = v * inv_t;
+                if (better(v, base + j, L.kv, L.ki)) list_insert(L, K, v, base + j);
+            }
         }
     };
     auto elem_fn = [&](uint32_t bits, int id, bool ok) {

@@ -150,6 +150,18 @@ __device__ __forceinline__ uint32_t unkey16(uint32_t k) {
     return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
 }
 
+// Any non-finite element in a 16-byte vector, from the raw words: adding the
+// lowest exponent step to the magnitude carries into the sign position exactly
+// when the exponent field is all ones (no carry crosses into the next element).
+template <int DT>
+__device__ __forceinline__ bool any_nonfinite(const uint4& v) {
+    constexpr uint32_t M = DT == VI_F32 ? 0x7fffffffu : 0x7fff7fffu;
+    constexpr uint32_t A = DT == VI_F32 ? 0x00800000u : (DT == VI_F16 ? 0x04000400u : 0x00800080u);
+    constexpr uint32_t S = DT == VI_F32 ? 0x80000000u : 0x80008000u;
+    const uint32_t t = ((v.x & M) + A) | ((v.y & M) + A) | ((v.z & M) + A) | ((v.w & M) + A);
+    return (t & S) != 0u;
+}
+
 // ------------------------------------------------------------------ RNG
 // SplitMix64 finalizer (sampled_select.cuh:41-46).
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
