@@ -665,21 +665,41 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         if (readlane_i(int(arrived), 0) != slices - 1) return;
         handoff_acquire();
         L = WaveList{};
-        f = 0; c = 0; m = -kInfF;
-        for (int sl = 0; sl < slices; ++sl) {   // every slice's sorted list, merged in
-            const size_t src = (size_t(r) * slices + sl) * kMaxK + lane;
-            list_merge(L, K, lane < K ? get_agent(&a.pval[src]) : -kInfF, lane < K ? get_agent(&a.pidx[src]) : kInvalidId);
+        // every slice's sorted list, merged in; the loads of eight slices are in
+        // flight together (one round trip per eight lists, not one per list)
+        for (int sl0 = 0; sl0 < slices; sl0 += 8) {
+            float bv[8];
+            int bi[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool ld = sl0 + u < slices && lane < K;
+                const size_t src = (size_t(r) * slices + size_t(min(sl0 + u, slices - 1))) * kMaxK + lane;
+                bv[u] = ld ? get_agent(&a.pval[src]) : -kInfF;
+                bi[u] = ld ? get_agent(&a.pidx[src]) : kInvalidId;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (sl0 + u < slices) list_merge(L, K, bv[u], bi[u]);
         }
-        for (int sl = 0; sl < slices; ++sl) {
-            const SliceHeader& h = a.phdr[size_t(r) * slices + sl];
-            f |= get_agent(&h.flags); c += get_agent(&h.valid); m = fmaxf(m, get_agent(&h.lse_max));
+        // the headers: lane sl holds slice sl's (slices <= 64), then reductions
+        // across the lanes (the log-sum-exp partials summed in a fixed order)
+        uint32_t hf = 0, hc = 0;
+        float hm = -kInfF;
+        double hs = 0.0;
+        if (lane < slices) {
+            const SliceHeader& h = a.phdr[size_t(r) * slices + lane];
+            hf = get_agent(&h.flags); hc = get_agent(&h.valid); hm = get_agent(&h.lse_max); hs = get_agent(&h.lse_sum);
         }
-        s = 0.0;
-        for (int sl = 0; sl < slices; ++sl) {
-            const SliceHeader& h = a.phdr[size_t(r) * slices + sl];
-            const float hm = get_agent(&h.lse_max);
-            if (hm != -kInfF) s += get_agent(&h.lse_sum) * exp(double(hm) - double(m));
+        f = hf; c = hc; m = hm;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) {
+            f |= shfl_xor_u(f, o);
+            c += shfl_xor_u(c, o);
+            m = fmaxf(m, shfl_xor_f(m, o));
         }
+        s = (hm != -kInfF) ? hs * exp(double(hm) - double(m)) : 0.0;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) a.arrivals[r] = 0u;
     }
 
@@ -795,6 +815,7 @@ __global__ __launch_bounds__(256) void history_hash_kernel(
 
 template <int MODE>
 vi_status launch_mode(const TopkArgs& args, int dtype, bool vec, int rows, int slices, hipStream_t stream) {
+    if (slices < 1 || slices > 64) return VI_ERR_INVALID;   // the merge reads one slice header per lane
     const dim3 grid(slices, rows), block(kTopkThreads);
 #define VI_TOPK_LAUNCH(DT, V) hipLaunchKernelGGL((topk_kernel<DT, V, MODE>), grid, block, 0, stream, args)
     switch (dtype) {
