@@ -394,7 +394,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     }
 
     // ---- scan the slice
+    // Each wave's list K-th value, shared: an element below another wave's K-th
+    // entry has K better elements in the row and cannot be in its top k, so
+    // every wave gates on the largest of them (read without ordering: a stale
+    // value is smaller, so it only prunes less).
     WaveList L;
+    __shared__ float s_kth[kTopkWaves];
+    if (threadIdx.x < kTopkWaves) s_kth[threadIdx.x] = -kInfF;
+    __syncthreads();
+    auto shared_kth = [&]() {   // (top-k mode; verification keeps its per-wave gate)
+        float g = -kInfF;
+        if constexpr (MODE != kModeTopk) return g;
+#pragma unroll
+        for (int w = 0; w < kTopkWaves; ++w)
+            g = fmaxf(g, __hip_atomic_load(&s_kth[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        return g;
+    };
+    auto publish_kth = [&]() {
+        if (MODE == kModeTopk && lane_id() == 0) __hip_atomic_store(&s_kth[threadIdx.x / kWave], L.kv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
     uint32_t flags = 0, valid = 0;
     float lse_m = -kInfF, lse_s = 0.0f;
     const bool want_lse = MODE == kModeTopk && a.logprobs != nullptr;
@@ -471,7 +489,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 vmax = live ? fmaxf(vmax, v) : vmax;
             }
         }
-        const float gate = fmaxf(L.kv, tau);
+        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
         if (ballot(candm != 0u && vmax >= gate) == 0) return;
         // rare: offer the vector's elements, one list insertion site per vector
         // (the element is taken again from the vector: a rolled loop keeps the
@@ -481,8 +499,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             const uint32_t bits = vec_bits<DT>(dv, j);
             float v = Elem<DT>::decode(bits);
             if constexpr (MODE == kModeVerify) v = p.temperature > 0.0f ? v * inv_t : v;
-            list_offer(L, K, ((candm >> j) & 1u) && v >= tau, v, id0 + j);
+            list_offer(L, K, ((candm >> j) & 1u) && v >= gate, v, id0 + j);
         }
+        publish_kth();
     };
     // Fast path: when no lane's vector holds a non-finite element (nor, in verify
     // mode, one whose scaled logit overflows), every element is a candidate, no
@@ -518,7 +537,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         } else {
             valid += ok ? uint32_t(P) : 0u;
         }
-        const float gate = fmaxf(L.kv, tau);
+        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
         if (ballot(ok && vmax >= gate) == 0) return;
         // the (lane, element) pairs reaching the gate, offered one at a time as
         // wave-uniform values (the list only rises meanwhile: each is checked
@@ -534,6 +553,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 if (scaled) v = v * inv_t;
                 list_offer(L, K, ((cm >> j) & 1u) != 0u, v, id0 + j);
             }
+            publish_kth();
             return;
         }
         while (lanes) {
@@ -551,6 +571,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 if (better(v, base + j, L.kv, L.ki)) list_insert(L, K, v, base + j);
             }
         }
+        publish_kth();
     };
     auto elem_fn = [&](uint32_t bits, int id, bool ok) {
         const float x = Elem<DT>::decode(bits);
