@@ -347,7 +347,10 @@ vi_status vi_sample_rows_state(const void* logits, int dtype, int rows, int voca
  * `position` is the absolute position of drafted row 0); terminal: optional
  * device list of stop tokens.  Outputs: accepted[lanes], committed
  * [lanes][drafts + 1] (unused slots = -1), committed_count[lanes],
- * lane_flags[lanes] (optional).  Sampled mode requires 1 <= top_k <= 64. */
+ * lane_flags[lanes] (optional).  Sampled mode requires 1 <= top_k <= 64 on
+ * every lane with temperature > 0: any other such lane is refused on the
+ * device (accepted 0, committed_count 0, every committed slot -1,
+ * lane_flags VI_FLAG_ERROR) while the other lanes are decided as usual. */
 enum { VI_VERIFY_GREEDY = 0, VI_VERIFY_SAMPLED = 1 };
 size_t vi_verify_workspace_bytes(int lanes, int drafts, int vocabulary);
 vi_status vi_verify_rows(int mode, const void* target, int target_dtype,

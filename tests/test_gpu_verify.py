@@ -124,3 +124,25 @@ def test_sampled_nonfinite_and_overflowing_targets(orc, dev, rng):
     exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-9}
     assert_same(g, w, exempt)
     assert any(f != 0 for f in w[3])
+
+
+def test_sampled_refuses_top_k_outside_list_range(orc, dev):
+    """Lanes with temperature > 0 and top_k in {0, 65, 200} have no top-k list
+    (the lists hold 64 entries): they are refused with VI_FLAG_ERROR, accept and
+    commit nothing, and leave the other config-4 lanes bit-exact with the oracle."""
+    from voidinfer_amd import workloads as W
+    from voidinfer_amd._abi import FLAG_ERROR
+    lanes, drafts = 8, 16
+    p0 = W.config4(lanes=lanes, drafts=drafts)[3]
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, sample_fn=sampler_from_draft(orc, p0))
+    refused = {1: 0, 4: 65, 6: 200}
+    for l, k in refused.items():
+        p["top_k"][l] = k
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    ga, gc, gn, gf = g
+    for l in refused:
+        assert gf[l] == FLAG_ERROR and ga[l] == 0 and gn[l] == 0 and np.all(gc[l] == -1), (l, ga[l], gn[l], gf[l])
+    keep = [l for l in range(lanes) if l not in refused]
+    exempt = {l for l in keep if np.min(w[4][l]) < 1e-9} | set(refused)
+    assert_same(g, w, exempt)
+    assert len(exempt) <= len(refused) + 1

@@ -366,7 +366,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         slack = a.cfg.presence_penalty < 0.0f ? -a.cfg.presence_penalty : 0.0f;
     } else if constexpr (MODE == kModeVerify) {
         p = a.params[r / a.params_div];
-        if (p.temperature > 0.0f) { K = p.top_k; inv_t = 1.0f / p.temperature; }
+        // a sampled lane whose top_k lies outside [1, 64] has no list here: the
+        // row is scanned with K = 1 and reported refused (VI_FLAG_ERROR)
+        if (p.temperature > 0.0f) { K = verify_list_k(p); inv_t = 1.0f / p.temperature; }
     } else {
         p = a.params[r];
         if (!topk_route(p)) {
@@ -769,7 +771,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
     } else if constexpr (MODE == kModeVerify) {
         if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
-        if (lane == 0) { a.lvalid[r] = c; a.lflags[r] = (f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u; }
+        if (lane == 0) {
+            const bool refused = verify_list_refused(p);
+            a.lvalid[r] = refused ? 0u : c;
+            a.lflags[r] = ((f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u) | (refused ? VI_FLAG_ERROR : 0u);
+        }
     } else {
         if (lane == 0) {
             uint32_t flags_out = 0;

@@ -74,7 +74,9 @@ struct ListDist {
 __device__ void list_dist(const vi_row_params& p, const float* z, const int* id, uint32_t valid, ListDist& d) {
     const int k = threadIdx.x;
     const bool greedy = !(p.temperature > 0.0f);
-    const int cap = valid == 0 ? 0 : (greedy ? 1 : min(p.top_k, int(valid)));
+    // (callers refuse lanes with top_k outside [1, kMaxK]; the clamp keeps every
+    // index inside the 64-entry lists regardless)
+    const int cap = valid == 0 ? 0 : (greedy ? 1 : min(min(max(p.top_k, 0), kMaxK), int(valid)));
     if (k < cap) {
         d.id[k] = id[k];
         d.w[k] = greedy ? 1.0 : exp(double(z[k]) - double(z[0]));
@@ -140,6 +142,10 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     const vi_row_params p = params[l];
     PosDecision* out = dec + size_t(l) * (drafts + 1) + j;
     const size_t tr = size_t(l) * target_rows + j;
+    if (verify_list_refused(p)) {   // no list of this lane's top_k: refused, nothing decided
+        if (k == 0 && (j < drafts || target_rows == drafts + 1)) *out = PosDecision{-1, VI_FLAG_ERROR, 0, 0};
+        return;
+    }
     if (j == drafts) {   // the bonus row's draw (used when every draft is accepted)
         if (target_rows != drafts + 1) return;
         list_dist(p, tval + tr * kMaxK, tidx + tr * kMaxK, tvalid[tr], P);
@@ -234,14 +240,20 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
 // and ends the chain) or a terminal token; a lane that accepted every draft
 // commits the bonus draw.  Flags of the positions visited (and the bonus row).
 __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int drafts, int target_rows,
-                                    const int32_t* drafted, const int64_t* terminal, int n_terminal,
-                                    int32_t* accepted, int32_t* committed, int32_t* committed_count,
-                                    uint32_t* lane_flags) {
+                                    const int32_t* drafted, const vi_row_params* params, const int64_t* terminal,
+                                    int n_terminal, int32_t* accepted, int32_t* committed,
+                                    int32_t* committed_count, uint32_t* lane_flags) {
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
     if (l >= lanes) return;
     const PosDecision* D = dec + size_t(l) * (drafts + 1);
     int32_t* out = committed + size_t(l) * (drafts + 1);
     for (int j = 0; j <= drafts; ++j) out[j] = -1;
+    if (verify_list_refused(params[l])) {   // refused lane: nothing accepted, nothing committed
+        accepted[l] = 0;
+        committed_count[l] = 0;
+        if (lane_flags) lane_flags[l] = VI_FLAG_ERROR;
+        return;
+    }
     uint32_t flags = 0;
     int c = 0, acc = 0;
     bool stopped = false, rejected = false;
@@ -343,7 +355,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     st = launch_status();
     if (st != VI_OK) return st;
     hipLaunchKernelGGL(verify_chain_kernel, dim3(blocks), dim3(threads), 0, stream, dec, a.lanes, a.drafts,
-                       a.target_rows, a.drafted, a.terminal, a.n_terminal, a.accepted, a.committed,
+                       a.target_rows, a.drafted, a.params, a.terminal, a.n_terminal, a.accepted, a.committed,
                        a.committed_count, a.lane_flags);
     return launch_status();
 }

@@ -237,6 +237,15 @@ __device__ __forceinline__ uint32_t hash_count(const uint2* table, int shift, in
     return 0u;
 }
 // Rows served by the top-k kernel family: argmax rows and 1 <= top_k <= 64.
+// Sampled verification from top-k lists needs 1 <= top_k <= 64 on a lane with
+// temperature > 0; any other sampled lane is refused (VI_FLAG_ERROR).
+__device__ __forceinline__ bool verify_list_refused(const vi_row_params& p) {
+    return p.temperature > 0.0f && (p.top_k < 1 || p.top_k > 64);
+}
+// The list length the verification scan keeps for such a lane (1 when refused).
+__device__ __forceinline__ int verify_list_k(const vi_row_params& p) {
+    return verify_list_refused(p) ? 1 : p.top_k;
+}
 __device__ __forceinline__ bool topk_route(const vi_row_params& p) {
     return !(p.temperature > 0.0f) || (p.top_k >= 1 && p.top_k <= 64);
 }
