@@ -126,6 +126,19 @@ vi_status vi_greedy_rows(const void* logits, int dtype, int rows, int vocabulary
                          int64_t row_stride, uint64_t serial, vi_greedy_row* out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of vi_greedy_rows, with no counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  Same results as vi_greedy_rows; the
+ * slice partials and arrival counters live in a 64 KiB device array of the
+ * library (one per GPU, held until the process ends), which holds the
+ * workspace of every shape (VI_ERR_WORKSPACE otherwise).  No call allocates
+ * memory.  Every call on one GPU shares that array and leaves its contents
+ * behind: calls that overlap on one GPU (other streams, other threads) race,
+ * so order them on one stream.  `stream` must belong to the current device. */
+vi_status vi_greedy_rows_noalloc(const void* logits, int dtype, int rows, int vocabulary,
+                                 int64_t row_stride, uint64_t serial, vi_greedy_row* out,
+                                 void* stream);
+
 /* ---- exact top-k ------------------------------------------------------------
  * Replaces dflash2_topk16_for_test / launch_dflash_topk16_segmented
  * (src/exl3/dflash2_draft.cu:2366-2420; dflash2_draft.h:198-202).

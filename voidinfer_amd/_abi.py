@@ -65,6 +65,7 @@ SIGNATURES = {
     "vi_abi_version": ([], _u32),
     "vi_greedy_workspace_bytes": ([_i, _i], _sz),
     "vi_greedy_rows": ([_vp, _i, _i, _i, _i64, _u64, _vp, _vp, _sz, _vp], _i),
+    "vi_greedy_rows_noalloc": ([_vp, _i, _i, _i, _i64, _u64, _vp, _vp], _i),
     "vi_topk_workspace_bytes": ([_i, _i, _i], _sz),
     "vi_topk_rows": ([_vp, _i, _i, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i),
     "vi_sampled_packet_workspace_bytes": ([_i, _i], _sz),

@@ -25,7 +25,9 @@ vi_status vi_init(void) {
     if (hipGetDevice(&dev) != hipSuccess) return VI_ERR_DEVICE;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return VI_ERR_DEVICE;
-    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? VI_OK : VI_ERR_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return VI_ERR_DEVICE;
+    // per-device address of the allocation-free greedy's scratch array
+    return greedy_scratch_setup(nullptr);
 }
 
 const char* vi_status_string(vi_status status) {
@@ -53,6 +55,14 @@ vi_status vi_greedy_rows(const void* logits, int dtype, int rows, int vocabulary
         return VI_ERR_INVALID;
     return launch_greedy(logits, dtype, rows, vocabulary, row_stride, serial, out, workspace, workspace_bytes,
                          as_stream(stream));
+}
+
+vi_status vi_greedy_rows_noalloc(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
+                                 uint64_t serial, vi_greedy_row* out, void* stream) {
+    if (rows == 0) return VI_OK;
+    if (rows < 0 || vocabulary <= 0 || row_stride < vocabulary || !dtype_ok(dtype) || !logits || !out)
+        return VI_ERR_INVALID;
+    return launch_greedy_noalloc(logits, dtype, rows, vocabulary, row_stride, serial, out, as_stream(stream));
 }
 
 size_t vi_topk_workspace_bytes(int rows, int vocabulary, int k) {

@@ -17,6 +17,8 @@
 // are the values that compare greater than -Inf (NaN and -Inf never win, +Inf
 // can), nothing is flagged, and the row's writer also emits the gap
 // max - logit(next[r]) for a next in [0, V) other than the argmax (else 0).
+#include <mutex>
+
 #include "row_scan.h"
 #include "vi_internal.h"
 
@@ -200,6 +202,60 @@ vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary,
                         hipStream_t stream) {
     return launch_greedy_kind<false>(logits, dtype, rows, vocabulary, stride, serial, out, nullptr, nullptr, nullptr,
                                      ws, ws_bytes, stream);
+}
+
+// ---- allocation-free greedy (vi_greedy_rows_noalloc) ---------------------------
+// The slice partials and arrival counters live in a file-scope device array
+// instead of a caller workspace.  Every GPU the library runs on holds its own
+// copy until the process ends; host code never passes `scratch` itself to a
+// kernel (its host-side name is not a device address) but the per-device address
+// that hipGetSymbolAddress returned, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[kGreedyScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* words, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) words[i] = 0u;
+}
+
+}  // namespace
+
+vi_status greedy_scratch_setup(void** ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return VI_ERR_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return VI_ERR_DEVICE;
+        g_scratch_ptr[dev] = p;
+    }
+    if (ptr) *ptr = g_scratch_ptr[dev];
+    return VI_OK;
+}
+
+vi_status launch_greedy_noalloc(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                                uint64_t serial, vi_greedy_row* out, hipStream_t stream) {
+    const size_t need = greedy_workspace(rows, vocabulary);
+    if (need > kGreedyScratchBytes) return VI_ERR_WORKSPACE;
+    void* ws = nullptr;
+    const vi_status st = greedy_scratch_setup(&ws);
+    if (st != VI_OK) return st;
+    if (need > 0) {
+        // The arrival counters must start at zero; their offset depends on the
+        // shape, and an earlier call of another shape left partials there.
+        const GreedyPlan p = greedy_plan(rows, vocabulary);
+        uint32_t* arrivals = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(ws) +
+                                                         align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256));
+        hipLaunchKernelGGL(zero_words_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, arrivals, rows);
+        if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
+    }
+    return launch_greedy_kind<false>(logits, dtype, rows, vocabulary, stride, serial, out, nullptr, nullptr, nullptr,
+                                     ws, kGreedyScratchBytes, stream);
 }
 
 vi_status launch_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,

@@ -36,6 +36,13 @@ size_t greedy_workspace(int rows, int vocabulary);
 vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                         uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
                         hipStream_t stream);
+// Allocation-free greedy: the workspace is a 64 KiB device array of the library
+// (every shape's greedy workspace fits it), its per-device address looked up by
+// greedy_scratch_setup (vi_init, or the first call on a device).
+constexpr size_t kGreedyScratchBytes = 65536;
+vi_status greedy_scratch_setup(void** ptr);
+vi_status launch_greedy_noalloc(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
+                                uint64_t serial, vi_greedy_row* out, hipStream_t stream);
 // VeriCache exact row scores (argmax + gap of next[r]); workspace as greedy.
 vi_status launch_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                             const int64_t* next, int64_t* greedy, float* gap, void* ws, size_t ws_bytes,
