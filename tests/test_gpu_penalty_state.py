@@ -199,22 +199,35 @@ def test_state_route_config5_subset(orc, dev):
     same_outputs(a, b, "config5")
 
 
-def test_state_route_limits(dev, rng):
-    """A full-route row fails when its half holds more than 32,768 distinct
-    recorded tokens or a count above 65,535; a top-k row has no such limit."""
+def test_state_route_without_distinct_token_limits(orc, dev, rng):
+    """Lanes holding 40,000 distinct recorded tokens in the low vocabulary, or one
+    token recorded 70,000 times (a count past the LDS repeat hash's 16 bits, so
+    the slice counts in its dense table instead): every route samples them, the
+    state route equals the history route bit for bit, and both match the oracle."""
     import voidinfer_amd as vi
     vocab = 248_320
     st = vi.PenaltyState(4, vocab, 1 << 18, device=dev)
-    many = np.arange(40_000)                                 # all in the first half
-    heavy = np.full(70_000, 1234)
-    update(st, dev, [many, heavy, many, heavy])
+    hist = [np.arange(40_000), np.full(70_000, 1234), np.arange(40_000), np.full(70_000, 1234)]
+    update(st, dev, hist)
     bits = np.stack([np.asarray(rng.standard_normal(vocab), np.float32).view(np.uint32) >> 16] * 4).astype(np.uint16)
-    p = vi.params_array(4, seed=[1, 2, 3, 4], temperature=1.0, top_k=np.array([0, 0, 20, 20]),
+    bits[1, 1234] = 0x4200                                    # 32.0: the heavy token would win unpenalized
+    p = vi.params_array(4, seed=[1, 2, 3, 4], position=[7, 8, 9, 10], temperature=1.0,
+                        top_k=np.array([0, 0, 20, 20]), top_p=0.9, repetition_penalty=1.1,
                         frequency_penalty=0.001, presence_penalty=0.1)
-    out = vi.sample_rows_state(to_dev(bits, 0, dev), p, st)
-    tok, s = out.tokens.cpu().numpy(), vi.stats_numpy(out.stats)
-    assert tok[0] == -1 and tok[1] == -1 and (s["flags"][:2] & FLAG_ERROR).all()
-    assert (tok[2:] >= 0).all() and not (s["flags"][2:] & FLAG_ERROR).any()
+    logits = to_dev(bits, 0, dev)
+    toks, offs = csr(hist)
+    a = vi.sample_rows(logits, p, torch.from_numpy(toks).to(dev), torch.from_numpy(offs).to(dev),
+                       max_history=70_000, want_probs=True)
+    b = vi.sample_rows_state(logits, p, st, want_probs=True)
+    torch.cuda.synchronize()
+    same_outputs(a, b, "limits")
+    w_tok, w_u, w_probs, w_stats, margins = orc.sample_rows(bits, 0, p, toks, offs, want_probs=True)
+    s = vi.stats_numpy(b.stats)
+    assert not (s["flags"] & FLAG_ERROR).any()
+    for r in range(4):
+        if not exempt_draw(margins[r]):
+            assert b.tokens[r].item() == w_tok[r] and s["support"][r] == w_stats["support"][r], r
+            np.testing.assert_allclose(s["support_mass"][r], w_stats["support_mass"][r], rtol=1e-9)
 
 
 @pytest.mark.parametrize("vocab", [64, 1000, 65_537])

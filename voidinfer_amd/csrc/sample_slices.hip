@@ -1,0 +1,1646 @@
+// sample_slices.hip — full-vocabulary rows of the batched sampler (temperature
+// > 0 and top_k = 0 or > 64): penalties, temperature, top-k / min-p / top-p over
+// the whole vocabulary and the Philox inverse-CDF draw.  The row is read from
+// HBM once; one slice of it is read again (from cache) to name the token.
+//
+// Key fact: bf16 / fp16 logits, and penalized logits stored back in the same
+// dtype, take one of 65,536 bit patterns, and z = x' * (1/T) is a strictly
+// monotone function of the pattern's order key (for T <= 65,536: distinct
+// patterns give distinct fp32 products; +0 and -0 share z = 0).  The multiset
+// of z over a row is therefore exactly a count histogram over patterns, and
+// every truncation (top-k count, min-p ratio, top-p mass) and the draw reduce to
+// prefix sums over the occupied patterns in z order; the float work (one fp64
+// exp) is per occupied pattern, not per token.
+//
+// Shape.  A row is cut into slices of 32,768 tokens.  Persistent workgroups of
+// 1024 threads (one per CU; the slices of a row on one XCD when there are at
+// least 8 rows) take slices in turn.  A workgroup holds its slice in registers
+// (4 x 16 bytes per thread) and has already requested the next slice's logits
+// when it starts on the current one, so the HBM stream overlaps the LDS work.
+// Per slice:
+//   1. penalties: a bitmap of the slice's history tokens and an LDS hash of the
+//      repeated ones' counts, from the lane's penalty state or its history;
+//   2. a u16 count histogram indexed by raw pattern (word = pattern & 0x7fff,
+//      half = sign bit), every logit counted as it arrives; the increment that
+//      finds a word at zero marks it in an occupancy bitmap;
+//   3. history tokens, gathered again from cache, are penalized and moved from
+//      their raw pattern's count to the penalized pattern's;
+//   4. the occupied patterns become a key-sorted (key << 16 | count) list, and
+//      each coarse bin of 256 keys (bin = (key + 128) >> 8) gets its valid
+//      count, its largest valid key and the mass sum of count * exp(z(key) -
+//      z(largest key)), published to HBM with write-through stores.
+// The last slice of a row to arrive merges; no workgroup waits for another.
+// The merge sums the coarse tables, locates the bins holding the top-k, min-p
+// and top-p cuts and the draw, resolves each inside its bin from the slices'
+// list entries of that bin (exact key and rank), and reads the slice that holds
+// the drawn rank again to name the token (id order among equal keys).
+//
+// Roofline: HBM; V x 2 bytes of logits per row, plus the penalty state's
+// bitmap (V / 8 bytes) and repeat list, or the history.
+#include <math.h>
+
+#include "penalty_state.h"
+#include "vi_device.h"
+#include "vi_internal.h"
+
+namespace vi {
+namespace {
+
+constexpr int kT = 512;                   // threads per workgroup (one per CU: the LDS is the limit)
+constexpr int kW = kT / kWave;            // waves per workgroup
+constexpr int kSL = 32768;                // tokens per slice
+constexpr int kNV = kSL / 8 / kT;         // 16-byte vectors per thread and slice
+constexpr int kBins = 257;                // coarse bins, bin(key) = (key + 128) >> 8
+constexpr int kBP = 264;                  // padded
+constexpr int kHash = 2048;               // LDS repeat-count hash slots
+constexpr uint32_t kHashFill = kHash * 3 / 4;
+constexpr int kStage = 4096;              // history offsets staged per penalty round (u16)
+constexpr int kChunk = 2048;              // list entries staged per compaction round (u32)
+constexpr int kMaxSlices = 16;
+constexpr int kPL = 2;                    // repeat-list entries prefetched per thread
+constexpr int kPHist = 4;                 // history tokens prefetched per thread
+constexpr uint32_t kTakeAll = 0xffffffffu;
+constexpr double kMassScale = 0x1p38;     // fixed-point unit of the slices' bin masses
+constexpr float kMaxTemperature = 65536.0f;
+
+// LDS map (bytes).  H: histogram, u16 counts in pairs (word p & 0x7fff: low half
+// the pattern with sign 0, high half with sign 1); the merge reuses it.  O:
+// occupancy of H's words.  B: history bitmap of the slice.  X: repeat hash,
+// then the compaction's bin tables.  F: staged history offsets / list entries.
+constexpr int kOffH = 0;
+constexpr int kOffO = kOffH + 4 * kSL;
+constexpr int kOffB = kOffO + 4 * kT;
+constexpr int kOffX = kOffB + 4 * (kSL / 32);
+constexpr int kOffF = kOffX + 4 * kHash;
+constexpr int kLds = kOffF + 2 * kStage;
+constexpr int kWPT = kSL / 32 / kT;       // bitmap / occupancy words per thread
+constexpr int kSeg = kNV + 2;             // id-order segments: head, vectors, tail
+static_assert(kWPT * kT * 32 == kSL, "whole bitmap words per thread");
+static_assert(kChunk * 4 == kStage * 2, "staging region");
+static_assert(4 * 4 * kBP + 8 * kBP <= 4 * kHash && kBP % 2 == 0, "compaction bin tables fit the hash region");
+
+// Merge map inside H (bytes): per-slice bin (first | entries << 16), bin
+// counts and masses summed over slices, four gather slots (entries per slice
+// and per-key counts).
+constexpr int kOffMFE = 0;
+constexpr int kOffMC = kOffMFE + 4 * kMaxSlices * kBP;
+constexpr int kOffMR = kOffMC + 4 * kBP;
+constexpr int kGatherSlots = 5;   // cap, min-p, top-p, support end, draw
+constexpr int kGatherBytes = 4 * kMaxSlices * 256 + 4 * 256 + 4 * kMaxSlices;
+constexpr int kOffGather = kOffMR + 8 * kBP;
+static_assert(kOffGather + kGatherSlots * kGatherBytes <= 4 * kSL, "merge map");
+static_assert(8 * kMaxSlices * kBP <= kGatherSlots * kGatherBytes, "slice masses fit the gather slots");
+
+struct RowBound {          // what the probs kernel needs to rebuild the support
+    double z0, s_n;
+    float inv_t;
+    uint32_t end_key, end_take, valid;
+};
+
+struct SliceArgs {
+    const void* logits;
+    int rows, vocabulary, slices, grid, xcd_aware;
+    int64_t stride;
+    const vi_row_params* params;
+    const int32_t* histories;
+    const int64_t* offsets;
+    unsigned char* pstate;     // per-lane penalty states instead of histories (or null)
+    PenaltyLayout pl;
+    int record;
+    int32_t* tokens;
+    double* uniforms;
+    float* probs;
+    int64_t probs_stride;
+    vi_sample_stats* stats;
+    // workspace
+    uint32_t* arrivals;        // [rows]
+    uint32_t* heads;           // [rows][slices][4]: n_list, n_valid, flags, top_key
+    uint32_t* bfe;             // [rows][slices][kBP]: first | entries << 16
+    uint32_t* bcnt;            // [rows][slices][kBP]: valid logits
+    uint32_t* bref;            // [rows][slices][kBP]: largest valid key
+    double* bmass;             // [rows][slices][kBP], in units of 2^-38
+    uint32_t* lists;           // [rows][slices][kSL]; a slice's dense repeat counts before its list
+    RowBound* bounds;          // [rows]
+    uint32_t* bases;           // [rows][kMaxSlices]: end-key logits in the slices before
+};
+
+struct Shared {
+    uint32_t scan[kW + 1];
+    uint32_t segs[kW][kSeg];
+    // slice
+    uint32_t flags, n_hash, overflow;
+    uint32_t kmin, kmax, top_key, n_valid, n_neg, n_list, last;
+    // merge
+    uint32_t row_flags, row_valid, row_top;
+    int32_t slot_bin[kGatherSlots];
+    int32_t cap_bin, minp_bin, topp_bin, draw_bin, end_bin;
+    int32_t cap_slot, minp_slot, topp_slot, draw_slot, end_slot;
+    uint32_t cap_key, cap_take, minp_key, topp_key, topp_take, end_key, end_take, end_all;
+    uint32_t n_support, draw_key, draw_rank, owner_slice, owner_rank, ok;
+    int32_t token;
+    double s_all, cap_mass, topp_target, s_n, u, draw_target;
+};
+
+__device__ __forceinline__ int bin_of(uint32_t key) { return int((key + 128u) >> 8); }
+__device__ __forceinline__ uint32_t bin_first_key(int b) { return uint32_t(b) * 256u - 128u; }
+
+template <int DT>
+__device__ __forceinline__ float key_z(uint32_t key, float inv_t) {
+    return Elem<DT>::decode(unkey16(key)) * inv_t;
+}
+
+// Smallest i in [lo, hi) with pred(i) (pred monotone false -> true), or hi.
+// Wave-uniform call; 64 probes per round.
+template <class P>
+__device__ __forceinline__ int wave_search(int lo, int hi, P pred) {
+    const int lane = lane_id();
+    while (hi > lo) {
+        const int n = hi - lo;
+        if (n <= kWave) {
+            const uint64_t m = ballot(lane < n && pred(lo + lane));
+            return m ? lo + __builtin_ctzll(m) : hi;
+        }
+        const int step = (n + kWave - 1) / kWave;
+        const int p = lo + lane * step;
+        const uint64_t valid = ballot(p < hi);
+        const uint64_t m = ballot(p < hi && pred(p));
+        if (!m) {
+            const int last = 63 - __builtin_clzll(valid);
+            lo = lo + last * step + 1;
+            continue;
+        }
+        const int f = __builtin_ctzll(m);
+        if (f == 0) return lo;
+        const int nlo = lo + (f - 1) * step + 1;
+        hi = lo + f * step;
+        lo = nlo;
+        if (lo == hi) return lo;
+    }
+    return lo;
+}
+
+// value of lane `src` (per-lane source) for a 64-bit double
+__device__ __forceinline__ double bperm_f64(double v, int src) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(src << 2, int(uint32_t(b))));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(src << 2, int(uint32_t(b >> 32))));
+    return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+}
+
+// Adds each lane's value into dst[bin], where the lanes' bins are
+// non-decreasing across the wave (bin < 0: nothing); one LDS atomic per run of
+// equal bins.
+__device__ __forceinline__ void wave_run_add(int bin, double v, double* dst) {
+    const int lane = lane_id();
+    const double incl = wave_incl_scan_f64(v);
+    const int prev = __builtin_amdgcn_ds_bpermute(max(lane - 1, 0) << 2, bin);
+    const int next = __builtin_amdgcn_ds_bpermute(min(lane + 1, kWave - 1) << 2, bin);
+    const uint64_t heads = ballot(lane == 0 || prev != bin);
+    const int start = 63 - __builtin_clzll(heads & ((2ull << lane) - 1ull));
+    const double before = bperm_f64(incl, max(start - 1, 0));
+    const double run = start == 0 ? incl : incl - before;
+    if (bin >= 0 && (lane == kWave - 1 || next != bin)) atomicAdd(&dst[bin], run);
+}
+
+// A workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load of the calling wave (its release fence covers
+// global memory), so a barrier issued while the next slice's logits are in
+// flight would wait for them; the slice pass synchronizes through LDS alone
+// and orders its global stores explicitly.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// block_exclusive_scan_u32 with LDS-only barriers.
+__device__ __forceinline__ uint32_t block_scan_lds(uint32_t v, uint32_t* tmp, uint32_t* total) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    const uint32_t x = wave_incl_scan_u32(v);
+    if (lane == kWave - 1) tmp[wave] = x;
+    lds_barrier();
+    if (wave == 0) {
+        const uint32_t t = lane < kW ? tmp[lane] : 0u;
+        const uint32_t it = wave_incl_scan_u32(t);
+        if (lane < kW) tmp[lane] = it - t;
+        if (lane == kW - 1) tmp[kW] = it;
+    }
+    lds_barrier();
+    const uint32_t r = tmp[wave] + x - v;
+    *total = tmp[kW];
+    lds_barrier();
+    return r;
+}
+
+// Slice geometry inside the row.
+struct Geo {
+    int s0, n, head, nvec, tail;
+    const uint16_t* base16;        // element s0 of the row
+    const unsigned char* vbase;    // first 16-byte aligned element
+};
+__device__ __forceinline__ Geo geo_of(const SliceArgs& a, int row, int s) {
+    Geo g;
+    g.s0 = s * kSL;
+    g.n = min(kSL, a.vocabulary - g.s0);
+    const int64_t e0 = int64_t(row) * a.stride + g.s0;
+    g.head = min(g.n, int((8 - (e0 & 7)) & 7));
+    g.nvec = (g.n - g.head) / 8;
+    g.tail = g.n - g.head - 8 * g.nvec;
+    g.base16 = static_cast<const uint16_t*>(a.logits) + e0;
+    g.vbase = reinterpret_cast<const unsigned char*>(g.base16 + g.head);
+    return g;
+}
+
+struct SliceRegs {
+    uint4 v[kNV];
+    uint32_t hb, tb;
+};
+__device__ __forceinline__ void load_slice(const Geo& g, SliceRegs& r) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kNV; ++i) {
+        const int v = i * kT + tid;
+        r.v[i] = v < g.nvec ? load16_cached(g.vbase + size_t(v) * 16) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    r.hb = tid < g.head ? uint32_t(g.base16[tid]) : 0u;
+    r.tb = tid < g.tail ? uint32_t(g.base16[g.head + 8 * g.nvec + tid]) : 0u;
+}
+
+// Item k of workgroup w: (row, slice), or false past the end.
+__device__ __forceinline__ bool item_of(const SliceArgs& a, int w, int k, int* row, int* s) {
+    if (a.xcd_aware) {
+        const int x = w & 7, j = w >> 3;
+        const int nx = (a.grid - x + 7) >> 3;      // workgroups on XCD x
+        const int rx = (a.rows - x + 7) >> 3;      // rows on XCD x
+        const int q = j + k * nx;
+        if (q >= rx * a.slices) return false;
+        *row = x + 8 * (q / a.slices);
+        *s = q % a.slices;
+        return true;
+    }
+    const int q = w + k * a.grid;
+    if (q >= a.rows * a.slices) return false;
+    *row = q / a.slices;
+    *s = q % a.slices;
+    return true;
+}
+
+__device__ __forceinline__ bool full_route_row(const vi_row_params& p) { return !topk_route(p); }
+
+// ----------------------------------------------------------------- penalties
+// Prefetched penalty inputs of one slice: its bitmap word (state route), the
+// lane's header fields and the first repeat-list entries / history tokens.
+struct PenPrefetch {
+    uint32_t bword[kWPT], hflags, nrep;
+    uint2 le[kPL];
+    int32_t ht[kPHist];
+};
+
+struct PenCtx {
+    bool pen, state;
+    const unsigned char* lstate;
+    const int32_t* hist;
+    int64_t hn;
+};
+__device__ __forceinline__ PenCtx pen_ctx(const SliceArgs& a, int row, const vi_row_params& p) {
+    PenCtx c{};
+    c.state = a.pstate != nullptr;
+    if (c.state) {
+        c.lstate = a.pstate + size_t(row) * a.pl.lane_bytes;
+        c.pen = penalties_active(p);
+    } else {
+        const int64_t b = a.offsets ? a.offsets[row] : 0;
+        c.hn = (a.offsets && a.histories) ? a.offsets[row + 1] - b : 0;
+        c.hist = a.histories ? a.histories + b : nullptr;
+        c.pen = penalties_active(p) && c.hn > 0;
+    }
+    return c;
+}
+
+// First loads of a slice's penalty inputs (header, bitmap word, list / history
+// head); issued a slice ahead.
+__device__ __forceinline__ void pen_prefetch_head(const SliceArgs& a, const PenCtx& c, const Geo& g, PenPrefetch& f) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) f.bword[q] = 0u;
+    f.hflags = 0u; f.nrep = 0u;
+    if (!c.pen) return;
+    if (c.state) {
+        const PenaltyHeader* h = reinterpret_cast<const PenaltyHeader*>(c.lstate);
+        f.hflags = __builtin_amdgcn_readfirstlane(h->flags);
+        f.nrep = __builtin_amdgcn_readfirstlane(h->nrep);
+        const uint32_t* b1 = reinterpret_cast<const uint32_t*>(c.lstate + a.pl.off_b1);
+        const int nw = (g.n + 31) >> 5;
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q)
+            if (q * kT + tid < nw) f.bword[q] = b1[(g.s0 >> 5) + q * kT + tid];
+    } else {
+#pragma unroll
+        for (int j = 0; j < kPHist; ++j) {
+            const int64_t i = int64_t(j) * kT + tid;
+            f.ht[j] = i < c.hn ? c.hist[i] : -1;
+        }
+    }
+}
+// The repeat-list head (state route), once the header has arrived.
+__device__ __forceinline__ void pen_prefetch_list(const SliceArgs& a, const PenCtx& c, PenPrefetch& f) {
+    if (!c.pen || !c.state) return;
+    const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
+    const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
+#pragma unroll
+    for (int j = 0; j < kPL; ++j) {
+        const uint32_t i = uint32_t(j) * kT + threadIdx.x;
+        f.le[j] = i < nrep ? list[i] : make_uint2(0u, 0u);
+    }
+}
+
+__device__ __forceinline__ uint32_t hash_slot(uint32_t off) { return (off * 0x9E3779B1u) >> 21; }
+
+// Builds the slice's history bitmap in B and the repeat counts in X (or, when X
+// overflows, full counts in the slice's dense table).  Sets sh.flags bits
+// (BAD_HISTORY, ERROR) and sh.overflow.  All threads.
+template <int DT>
+__device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, const Geo& g, const PenPrefetch& f,
+                          unsigned char* lds, Shared& sh, uint32_t* dense) {
+    const int tid = threadIdx.x;
+    uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
+    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
+    const int nw = (g.n + 31) >> 5;
+    for (int i = tid; i < kHash; i += kT) X[i] = 0u;
+    if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
+    if (c.state) {
+        const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) {
+            const int wd = q * kT + tid;
+            B[wd] = wd < nw ? (f.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
+        }
+        if (tid == 0 && f.hflags) atomicOr(&sh.flags, f.hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
+    } else {
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) B[q * kT + tid] = 0u;
+    }
+    lds_barrier();
+    auto hash_put = [&](uint32_t off, uint32_t extra, bool add) {
+        if (extra > 0xffffu) { sh.overflow = 1u; return; }
+        uint32_t h = hash_slot(off);
+        const uint32_t key = (off + 1u) << 16;
+        for (int probe = 0; probe < 64; ++probe) {
+            uint32_t e = X[h];
+            if (e == 0u) {
+                e = atomicCAS(&X[h], 0u, key | extra);
+                if (e == 0u) {
+                    if (atomicAdd(&sh.n_hash, 1u) >= kHashFill) sh.overflow = 1u;
+                    return;
+                }
+            }
+            if ((e & 0xffff0000u) == key) {
+                if (add) {
+                    const uint32_t old = atomicAdd(&X[h], 1u);
+                    if ((old & 0xffffu) == 0xffffu) sh.overflow = 1u;
+                } else {
+                    sh.overflow = 1u;   // a token twice in the repeat list: not a state's list
+                }
+                return;
+            }
+            h = (h + 1u) & uint32_t(kHash - 1);
+        }
+        sh.overflow = 1u;
+    };
+    const int s1 = g.s0 + g.n;
+    if (c.state) {
+        const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
+        const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
+        auto put = [&](uint2 e) {
+            const int t = int(e.x);
+            if (e.y < 2u || t < g.s0 || t >= s1) return;
+            hash_put(uint32_t(t - g.s0), e.y - 1u, false);
+        };
+#pragma unroll
+        for (int j = 0; j < kPL; ++j)
+            if (uint32_t(j) * kT + tid < nrep) put(f.le[j]);
+        for (uint32_t i = uint32_t(kPL) * kT + tid; i < nrep; i += kT) put(list[i]);
+    } else {
+        auto rec = [&](int32_t t) {
+            if (t < 0 || t >= a.vocabulary) { atomicOr(&sh.flags, uint32_t(VI_FLAG_BAD_HISTORY)); return; }
+            if (t < g.s0 || t >= s1) return;
+            const uint32_t off = uint32_t(t - g.s0), bit = 1u << (off & 31);
+            const uint32_t old = atomicOr(&B[off >> 5], bit);
+            if (old & bit) hash_put(off, 1u, true);
+        };
+#pragma unroll
+        for (int j = 0; j < kPHist; ++j)
+            if (int64_t(j) * kT + tid < c.hn) rec(f.ht[j]);
+        for (int64_t i = int64_t(kPHist) * kT + tid; i < c.hn; i += kT) rec(c.hist[i]);
+    }
+    lds_barrier();
+    if (sh.overflow) {   // (uniform) full counts of the slice's tokens in its dense table
+        for (int i = tid; i < g.n; i += kT) put_agent(&dense[i], 0u);
+        handoff_stores_done();
+        __syncthreads();
+        if (c.state) {
+            const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
+            const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
+            for (uint32_t i = tid; i < nrep; i += kT) {
+                const uint2 e = list[i];
+                const int t = int(e.x);
+                if (e.y >= 2u && t >= g.s0 && t < s1) put_agent(&dense[t - g.s0], e.y);
+            }
+        } else {
+            for (int64_t i = tid; i < c.hn; i += kT) {
+                const int32_t t = c.hist[i];
+                if (t >= g.s0 && t < s1) atomicAdd(&dense[t - g.s0], 1u);
+            }
+        }
+        handoff_stores_done();
+        __syncthreads();
+    }
+}
+
+// Occurrences of slice token `off` (its bitmap bit is set).
+__device__ __forceinline__ uint32_t pen_count(const unsigned char* lds, const Shared& sh, const uint32_t* dense,
+                                              uint32_t off) {
+    if (sh.overflow) {
+        const uint32_t c = get_agent(&dense[off]);
+        return c ? c : 1u;
+    }
+    const uint32_t* X = reinterpret_cast<const uint32_t*>(lds + kOffX);
+    uint32_t h = hash_slot(off);
+    const uint32_t key = (off + 1u) << 16;
+    for (int probe = 0; probe < kHash; ++probe) {
+        const uint32_t e = X[h];
+        if (e == 0u) return 1u;
+        if ((e & 0xffff0000u) == key) return 1u + (e & 0xffffu);
+        h = (h + 1u) & uint32_t(kHash - 1);
+    }
+    return 1u;
+}
+
+// Penalized bits of slice element `off` with raw bits `b` (b when not a history
+// token or not finite).  `unrecord`: the slice offset of a token recorded into
+// the state after the counts were to be taken (one occurrence is discounted), or
+// ~0u.
+template <int DT>
+__device__ __forceinline__ uint32_t pen_bits(const unsigned char* lds, const Shared& sh, const uint32_t* dense,
+                                             const vi_row_params& p, uint32_t off, uint32_t b,
+                                             uint32_t unrecord = ~0u) {
+    const uint32_t* B = reinterpret_cast<const uint32_t*>(lds + kOffB);
+    if (!((B[off >> 5] >> (off & 31)) & 1u) || !Elem<DT>::finite_bits(b)) return b;
+    uint32_t c = pen_count(lds, sh, dense, off);
+    if (off == unrecord && --c == 0u) return b;
+    return penalize_bits<DT>(b, c, p) & 0xffffu;
+}
+
+// Element j (0..7, possibly lane-varying) of a 16-byte vector of 16-bit values.
+__device__ __forceinline__ uint32_t vec_elem(const uint4& v, int j) {
+    const int q = j >> 1;
+    const uint32_t w = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+    return (j & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Order key of slice element `off` after penalties, 0 when not finite (no
+// finite pattern has key 0).
+template <int DT>
+__device__ __forceinline__ uint32_t elem_key(const unsigned char* lds, const Shared& sh, const uint32_t* dense,
+                                             const vi_row_params& p, bool pen, uint32_t off, uint32_t b,
+                                             uint32_t unrecord = ~0u) {
+    const uint32_t pb = pen ? pen_bits<DT>(lds, sh, dense, p, off, b, unrecord) : b;
+    return Elem<DT>::finite_bits(pb) ? key16(pb) : 0u;
+}
+
+// ------------------------------------------------------------ id-order ranks
+// Positions of a per-element predicate over a slice held in registers, in id
+// order: segment 0 the head elements (one per thread), segments 1..kNV the
+// vectors i * kT + tid, segment kNV + 1 the tail elements.  cnt[x]: this
+// thread's matches in segment x; excl[x] receives the matches before them in
+// id order.  Returns the total.
+__device__ __forceinline__ uint32_t id_order_prefix(const uint32_t cnt[kSeg], uint32_t excl[kSeg], Shared& sh) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    uint32_t incl[kSeg];
+#pragma unroll
+    for (int g = 0; g < kSeg; ++g) {
+        incl[g] = wave_incl_scan_u32(cnt[g]);
+        if (lane == kWave - 1) sh.segs[wave][g] = incl[g];
+    }
+    __syncthreads();
+    uint32_t total = 0u;
+#pragma unroll
+    for (int g = 0; g < kSeg; ++g) {
+        uint32_t waves_before = 0u, seg_total = 0u;
+        for (int w = 0; w < kW; ++w) {
+            const uint32_t t = sh.segs[w][g];
+            seg_total += t;
+            if (w < wave) waves_before += t;
+        }
+        excl[g] = total + waves_before + incl[g] - cnt[g];
+        total += seg_total;
+    }
+    __syncthreads();
+    return total;
+}
+
+// ------------------------------------------------------------------ merge
+constexpr int kSlotsAll = kGatherSlots;
+constexpr int kOffPC = kOffGather + kSlotsAll * kGatherBytes;   // [kMaxSlices] per-slice counts
+static_assert(kOffPC + 4 * 2 * kMaxSlices <= 4 * kSL, "merge map");
+
+struct Slot {
+    uint32_t* E;    // [kMaxSlices][256] list entries of the bin, per slice
+    uint32_t* FK;   // [256] logits per key of the bin (all slices)
+    uint32_t* NE;   // [kMaxSlices] entries per slice
+};
+__device__ __forceinline__ Slot slot_at(unsigned char* lds, int i) {
+    unsigned char* b = lds + kOffGather + i * kGatherBytes;
+    Slot s;
+    s.E = reinterpret_cast<uint32_t*>(b);
+    s.FK = s.E + kMaxSlices * 256;
+    s.NE = s.FK + 256;
+    return s;
+}
+
+// All threads: the list entries of bin b of every slice of `row`.
+__device__ __forceinline__ void gather_bin(const SliceArgs& a, int row, int b, const Slot& sl, const uint32_t* MFE) {
+    const int tid = threadIdx.x, S = a.slices;
+    if (tid < 256) sl.FK[tid] = 0u;
+    __syncthreads();
+    const uint32_t k0 = bin_first_key(b);
+    for (int idx = tid; idx < S * 256; idx += kT) {
+        const int s = idx >> 8, j = idx & 255;
+        const uint32_t fe = MFE[s * kBP + b], ne = fe >> 16, f0 = fe & 0xffffu;
+        if (j == 0) sl.NE[s] = ne;
+        if (uint32_t(j) < ne) {
+            const uint32_t e = get_agent(&a.lists[(size_t(row) * S + s) * kSL + f0 + j]);
+            sl.E[s * 256 + j] = e;
+            const uint32_t kj = (e >> 16) - k0;   // (< 256 for every entry of bin b)
+            if (kj < 256u) atomicAdd(&sl.FK[kj], e & 0xffffu);
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l))) |
+                       (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l))) << 32);
+    return __builtin_bit_cast(double, r);
+}
+
+// Wave 0 helpers over the coarse bins, in descending order: lane l holds bins
+// 256 - 5l - i (i = 0..4).
+struct CoarseHit {
+    int bin;
+    double mass_before;
+    uint32_t cnt_before;
+};
+// First non-empty bin b >= lo (descending) at which the cumulative count
+// (mode 0: >= target) or mass (mode 1: >= target, mode 2: > target) is reached;
+// bin -1 when none is.
+__device__ __forceinline__ CoarseHit coarse_find(const double* MR, const uint32_t* MC, int lo, int mode, double target) {
+    const int lane = lane_id();
+    double vm[5], tm = 0.0;
+    uint32_t vc[5], tc = 0u;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int b = 256 - 5 * lane - i;
+        const bool ok = b >= lo && b >= 0;
+        vm[i] = ok ? MR[b] : 0.0;
+        vc[i] = ok ? MC[b] : 0u;
+        tm += vm[i];
+        tc += vc[i];
+    }
+    double cm = wave_incl_scan_f64(tm) - tm;
+    uint32_t cc = wave_incl_scan_u32(tc) - tc;
+    int fi = -1;
+    double fm = 0.0;
+    uint32_t fc = 0u;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const double nm = cm + vm[i];
+        const uint32_t nc = cc + vc[i];
+        const bool hit = mode == 0 ? double(nc) >= target : (mode == 1 ? nm >= target : nm > target);
+        if (fi < 0 && hit && vc[i] > 0u) { fi = i; fm = cm; fc = cc; }
+        cm = nm;
+        cc = nc;
+    }
+    const uint64_t m = ballot(fi >= 0);
+    if (!m) return CoarseHit{-1, 0.0, 0u};
+    const int L = __builtin_ctzll(m);
+    return CoarseHit{256 - 5 * L - readlane_i(fi, L), readlane_d(fm, L), uint32_t(readlane_i(int(fc), L))};
+}
+// Mass and count of the bins above bin b.
+__device__ __forceinline__ void coarse_above(const double* MR, const uint32_t* MC, int b, double* m, uint32_t* c) {
+    const int lane = lane_id();
+    double tm = 0.0;
+    uint32_t tc = 0u;
+    for (int x = b + 1 + lane; x < kBins; x += kWave) { tm += MR[x]; tc += MC[x]; }
+    *m = wave_sum_f64(tm);
+    *c = wave_sum_u32(tc);
+}
+
+struct FineHit {
+    bool found;
+    uint32_t key, rank;
+    double mass_before;     // mass of the bin's keys above `key`
+    uint32_t cnt_before;
+    double total_mass;      // of the (limited) bin
+    uint32_t total_cnt;
+    uint32_t last_key, last_cnt;   // the lowest key with logits (limited)
+};
+// Wave 0.  The keys of bin b in descending order (lane l: 255 - 4l - i), with
+// counts limited to the position (lim_key, lim_take): keys below lim_key count
+// none, lim_key at most lim_take.  Finds the first element (key, rank) at which
+// the cumulative count (mode 0: >= target) or mass (mode 1: >= target, mode 2:
+// > target) is reached; mode 3 only totals.  Masses are exp(z - zmax) per logit.
+template <int DT>
+__device__ __forceinline__ FineHit fine_find(const uint32_t* FK, int b, int mode, double target, uint32_t lim_key, uint32_t lim_take,
+                             double zmax, float inv_t) {
+    const int lane = lane_id();
+    const int k0 = b * 256 - 128;
+    uint32_t c[4];
+    double w[4], tm = 0.0;
+    uint32_t tc = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = 255 - 4 * lane - i, key = k0 + j;
+        uint32_t cc = (key >= 0 && key <= 0xffff) ? FK[j] : 0u;
+        if (uint32_t(key) < lim_key) cc = 0u;
+        else if (uint32_t(key) == lim_key) cc = min(cc, lim_take);
+        c[i] = cc;
+        w[i] = cc ? exp(double(key_z<DT>(uint32_t(key), inv_t)) - zmax) : 0.0;
+        tm += double(cc) * w[i];
+        tc += cc;
+    }
+    const double im = wave_incl_scan_f64(tm);
+    const uint32_t ic = wave_incl_scan_u32(tc);
+    double cm = im - tm;
+    uint32_t cc = ic - tc;
+    int fi = -1, li = -1;
+    uint32_t fr = 0u;
+    double fm = 0.0;
+    uint32_t fc = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const double nm = cm + double(c[i]) * w[i];
+        const uint32_t nc = cc + c[i];
+        if (c[i]) li = i;
+        if (fi < 0 && c[i] && mode != 3) {
+            bool hit;
+            if (mode == 0) hit = double(nc) >= target;
+            else if (mode == 1) hit = nm >= target;
+            else hit = nm > target;
+            if (hit) {
+                uint32_t r;
+                if (mode == 0) {
+                    r = uint32_t(max(0.0, target - double(cc) - 1.0));
+                } else {
+                    const double x = (target - cm) / w[i];
+                    double rr = mode == 1 ? ceil(x) - 1.0 : floor(x);
+                    rr = fmin(fmax(rr, 0.0), double(c[i] - 1u));
+                    r = uint32_t(rr);
+                    for (int it = 0; it < 4; ++it) {   // settle the rounding of the estimate
+                        if (r > 0u && (mode == 1 ? cm + double(r) * w[i] >= target : cm + double(r) * w[i] > target)) --r;
+                        else if (r + 1u < c[i] && (mode == 1 ? cm + double(r + 1u) * w[i] < target
+                                                              : cm + double(r + 1u) * w[i] <= target)) ++r;
+                        else break;
+                    }
+                }
+                fi = i; fr = min(r, c[i] - 1u); fm = cm; fc = cc;
+            }
+        }
+        cm = nm;
+        cc = nc;
+    }
+    FineHit h{};
+    h.total_mass = readlane_d(im, kWave - 1);
+    h.total_cnt = uint32_t(readlane_i(int(ic), kWave - 1));
+    const uint64_t lm = ballot(li >= 0);
+    if (lm) {
+        const int L = 63 - __builtin_clzll(lm);
+        const int i = readlane_i(li, L);
+        h.last_key = uint32_t(k0 + 255 - 4 * L - i);
+        h.last_cnt = uint32_t(readlane_i(int(c[0]), L));
+        // (c[] indexed by a lane-uniform i: pick it per lane first)
+        uint32_t mine = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) if (q == li) mine = c[q];
+        h.last_cnt = uint32_t(readlane_i(int(mine), L));
+    }
+    const uint64_t m = ballot(fi >= 0);
+    if (m) {
+        const int L = __builtin_ctzll(m);
+        const int i = readlane_i(fi, L);
+        h.found = true;
+        h.key = uint32_t(k0 + 255 - 4 * L - i);
+        h.rank = uint32_t(readlane_i(int(fr), L));
+        h.mass_before = readlane_d(fm, L);
+        h.cnt_before = uint32_t(readlane_i(int(fc), L));
+    }
+    return h;
+}
+
+__device__ __forceinline__ void write_row(const SliceArgs& a, int row, int32_t token, double u, uint32_t flags,
+                                          uint32_t support, uint32_t finite, double s_n) {
+    a.tokens[row] = token;
+    if (a.uniforms) a.uniforms[row] = u;
+    if (a.stats) {
+        vi_sample_stats st{};
+        st.flags = flags;
+        st.support = support;
+        st.finite = finite;
+        st.support_mass = s_n;
+        st.uniform = u;
+        a.stats[row] = st;
+    }
+}
+
+// The row's decisions and its token, by the last slice to arrive.
+// (a call: once per row, and its registers stay out of the slice loop's budget)
+template <int DT>
+__device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row_params& p, float inv_t, unsigned char* lds,
+                          Shared& sh) {
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave, S = a.slices, V = a.vocabulary;
+    uint32_t* MFE = reinterpret_cast<uint32_t*>(lds + kOffMFE);
+    uint32_t* MC = reinterpret_cast<uint32_t*>(lds + kOffMC);
+    double* MR = reinterpret_cast<double*>(lds + kOffMR);
+    uint32_t* PC = reinterpret_cast<uint32_t*>(lds + kOffPC);   // [kMaxSlices] drawn key, [kMaxSlices] end key
+    const size_t rs = size_t(row) * S;
+
+    // ---- 0. slice heads and bin tables, one round trip
+    uint32_t h4[4] = {0u, 0u, 0u, 0u};
+    if (tid < S) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h4[q] = get_agent(&a.heads[(rs + tid) * 4 + q]);
+    }
+    constexpr int kPer = (kMaxSlices * kBP + kT - 1) / kT;
+    uint32_t lfe[kPer], lcnt[kPer], lref[kPer];
+    double lmass[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int idx = u * kT + tid;
+        const bool ok = idx < S * kBP;
+        lfe[u] = ok ? get_agent(&a.bfe[rs * kBP + idx]) : 0u;
+        lcnt[u] = ok ? get_agent(&a.bcnt[rs * kBP + idx]) : 0u;
+        lref[u] = ok ? get_agent(&a.bref[rs * kBP + idx]) : 0u;
+        lmass[u] = ok ? get_agent(&a.bmass[rs * kBP + idx]) : 0.0;
+    }
+    double* MRS = reinterpret_cast<double*>(lds + kOffGather);   // [S][kBP] rescaled slice masses (then gathers)
+    if (tid < kBP) MC[tid] = 0u;
+    if (tid < kGatherSlots) sh.slot_bin[tid] = -1;
+    if (tid == 0) { sh.row_flags = 0u; sh.row_valid = 0u; sh.row_top = 0u; sh.token = -1; sh.ok = 1u; }
+    __syncthreads();
+    if (tid < S) { atomicAdd(&sh.row_valid, h4[1]); atomicOr(&sh.row_flags, h4[2]); atomicMax(&sh.row_top, h4[3]); }
+    __syncthreads();
+    const uint32_t top = sh.row_top, N = sh.row_valid;
+    const double zmax = double(key_z<DT>(top, inv_t));
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int idx = u * kT + tid;
+        if (idx < S * kBP) {
+            MFE[idx] = lfe[u];
+            MRS[idx] = lcnt[u] ? lmass[u] * (1.0 / kMassScale) * exp(double(key_z<DT>(lref[u], inv_t)) - zmax) : 0.0;
+            if (lcnt[u]) atomicAdd(&MC[idx % kBP], lcnt[u]);
+        }
+    }
+    __syncthreads();
+    if (tid < kBP) {   // each bin summed over the slices in slice order (deterministic)
+        double m = 0.0;
+        for (int q = 0; q < S; ++q) m += MRS[q * kBP + tid];
+        MR[tid] = m;
+    }
+    __syncthreads();
+    const uint32_t out_flags = sh.row_flags & (VI_FLAG_NONFINITE | VI_FLAG_BAD_HISTORY);
+    const bool fail = (sh.row_flags & VI_FLAG_ERROR) != 0u || !(p.temperature <= kMaxTemperature);
+    if (fail || N == 0u) {
+        if (tid == 0) {
+            write_row(a, row, fail ? -1 : V, 0.0, out_flags | (fail ? VI_FLAG_ERROR : VI_FLAG_EMPTY), 0u, 0u, 0.0);
+            if (a.probs) a.bounds[row] = RowBound{0.0, 0.0, 0.0f, 0u, 0u, 0u};
+        }
+        __syncthreads();
+        return;
+    }
+    // All threads: slot holding bin b (gathered into `slot` if absent).
+    auto gather_into = [&](int b, int slot) -> int {
+        for (int i = 0; i < kSlotsAll; ++i)
+            if (sh.slot_bin[i] == b) return i;
+        gather_bin(a, row, b, slot_at(lds, slot), MFE);
+        if (tid == 0) sh.slot_bin[slot] = b;
+        __syncthreads();
+        return slot;
+    };
+
+    // ---- 1. totals; bins of the top-k cap and of the min-p cut
+    if (wave == 0) {
+        double tm = 0.0;
+        for (int b = lane; b < kBP; b += kWave) tm += MR[b];
+        const double s_all = wave_sum_f64(tm);
+        int cap_bin = -1;
+        if (p.top_k > 0 && uint32_t(p.top_k) < N) cap_bin = coarse_find(MR, MC, 0, 0, double(p.top_k)).bin;
+        int minp_bin = -1;
+        uint32_t kf = 0u;
+        if (p.min_p > 0.0f) {
+            const double mp = double(p.min_p);
+            kf = uint32_t(wave_search(int(sh.kmin), int(top) + 1, [&](int key) {
+                return exp(double(key_z<DT>(uint32_t(key), inv_t)) - zmax) >= mp;
+            }));
+            minp_bin = kf <= top ? bin_of(kf) : -1;
+        }
+        if (lane == 0) { sh.s_all = s_all; sh.cap_bin = cap_bin; sh.minp_bin = minp_bin; sh.minp_key = kf; }
+    }
+    __syncthreads();
+    const int cap_slot = sh.cap_bin >= 0 ? gather_into(sh.cap_bin, 0) : -1;
+    if (sh.minp_bin >= 0) (void)gather_into(sh.minp_bin, 1);
+
+    // ---- 2. the cap's position and mass; the bin of the top-p cut
+    if (wave == 0) {
+        uint32_t ck = 0u, ct = kTakeAll;
+        double cap_mass = sh.s_all;
+        if (cap_slot >= 0) {
+            double am;
+            uint32_t ac;
+            coarse_above(MR, MC, sh.cap_bin, &am, &ac);
+            const FineHit f = fine_find<DT>(slot_at(lds, cap_slot).FK, sh.cap_bin, 0, double(p.top_k) - double(ac),
+                                            0u, kTakeAll, zmax, inv_t);
+            ck = f.found ? f.key : f.last_key;
+            ct = f.found ? f.rank + 1u : max(f.last_cnt, 1u);
+            const double mb = f.found ? f.mass_before : f.total_mass - double(f.last_cnt) *
+                                                                       exp(double(key_z<DT>(ck, inv_t)) - zmax);
+            cap_mass = am + mb + double(ct) * exp(double(key_z<DT>(ck, inv_t)) - zmax);
+        }
+        int topp_bin = -1;
+        double target = 0.0;
+        if (p.top_p < 1.0f) {
+            target = double(p.top_p) * cap_mass;
+            const CoarseHit h = coarse_find(MR, MC, cap_slot >= 0 ? sh.cap_bin + 1 : 0, 1, target);
+            topp_bin = h.bin >= 0 ? h.bin : (cap_slot >= 0 ? sh.cap_bin : -1);
+        }
+        if (lane == 0) {
+            sh.cap_key = ck; sh.cap_take = ct; sh.cap_mass = cap_mass;
+            sh.topp_bin = topp_bin; sh.topp_target = target;
+        }
+    }
+    __syncthreads();
+    const int topp_slot = sh.topp_bin >= 0 ? gather_into(sh.topp_bin, 2) : -1;
+
+    // ---- 3. the top-p position; the support's end: the earliest of the cap,
+    // the min-p cut and the top-p cut, at least one logit
+    if (wave == 0) {
+        bool has_topp = false;
+        uint32_t tk = 0u, tt = kTakeAll;
+        if (topp_slot >= 0) {
+            double am;
+            uint32_t ac;
+            coarse_above(MR, MC, sh.topp_bin, &am, &ac);
+            const bool in_cap = cap_slot >= 0 && sh.topp_bin == sh.cap_bin;
+            const FineHit f = fine_find<DT>(slot_at(lds, topp_slot).FK, sh.topp_bin, 1, sh.topp_target - am,
+                                            in_cap ? sh.cap_key : 0u, in_cap ? sh.cap_take : kTakeAll, zmax, inv_t);
+            if (f.found) { tk = f.key; tt = f.rank + 1u; has_topp = true; }
+        }
+        bool all = true;
+        uint32_t ek = 0u, et = kTakeAll;
+        auto consider = [&](uint32_t k, uint32_t t) {
+            if (all || k > ek || (k == ek && t < et)) { ek = k; et = t; all = false; }
+        };
+        if (cap_slot >= 0) consider(sh.cap_key, sh.cap_take);
+        if (p.min_p > 0.0f) consider(sh.minp_key, kTakeAll);
+        if (has_topp) consider(tk, tt);
+        if (!all && ek > top) { ek = top; et = 1u; }   // no logit passes (min_p > 1): the best one
+        if (lane == 0) { sh.end_all = all ? 1u : 0u; sh.end_key = ek; sh.end_take = et; sh.end_bin = all ? -1 : bin_of(ek); }
+    }
+    __syncthreads();
+    const int end_slot = sh.end_all ? -1 : gather_into(sh.end_bin, 3);
+
+    // ---- 4. support mass, the draw's target and bin
+    if (wave == 0) {
+        double sn;
+        uint32_t n;
+        if (sh.end_all) {
+            sn = sh.s_all;
+            n = N;
+        } else {
+            double am;
+            uint32_t ac;
+            coarse_above(MR, MC, sh.end_bin, &am, &ac);
+            const FineHit f = fine_find<DT>(slot_at(lds, end_slot).FK, sh.end_bin, 3, 0.0, sh.end_key, sh.end_take,
+                                            zmax, inv_t);
+            sn = am + f.total_mass;
+            n = ac + f.total_cnt;
+        }
+        const double u = philox_uniform(p.seed, p.lane, p.position, 0u);
+        const double t = u * sn;
+        const CoarseHit h = coarse_find(MR, MC, sh.end_all ? 0 : sh.end_bin + 1, 2, t);
+        int db = h.bin;
+        if (db < 0 && !sh.end_all) db = sh.end_bin;
+        if (db < 0) {   // (rounding past the last logit) the lowest bin holding one
+            int lo = kBins;
+            for (int b = lane; b < kBins; b += kWave) if (MC[b]) lo = min(lo, b);
+#pragma unroll
+            for (int o = 32; o; o >>= 1) lo = min(lo, __shfl_xor(lo, o, kWave));
+            db = lo;
+        }
+        if (lane == 0) { sh.s_n = sn; sh.n_support = n; sh.u = u; sh.draw_target = t; sh.draw_bin = db; }
+    }
+    __syncthreads();
+    const int draw_slot = gather_into(sh.draw_bin, 4);
+
+    // ---- 5. the drawn (key, rank), then the slice holding it
+    if (wave == 0) {
+        double am;
+        uint32_t ac;
+        coarse_above(MR, MC, sh.draw_bin, &am, &ac);
+        const bool in_end = !sh.end_all && sh.draw_bin == sh.end_bin;
+        const FineHit f = fine_find<DT>(slot_at(lds, draw_slot).FK, sh.draw_bin, 2, sh.draw_target - am,
+                                        in_end ? sh.end_key : 0u, in_end ? sh.end_take : kTakeAll, zmax, inv_t);
+        if (lane == 0) {
+            if (f.found) { sh.draw_key = f.key; sh.draw_rank = f.rank; }
+            else if (f.last_cnt) { sh.draw_key = f.last_key; sh.draw_rank = f.last_cnt - 1u; }
+            else sh.ok = 0u;
+        }
+    }
+    if (tid < 2 * kMaxSlices) PC[tid] = 0u;
+    __syncthreads();
+    {
+        const Slot ds = slot_at(lds, draw_slot);
+        const uint32_t dk = sh.draw_key;
+        for (int idx = tid; idx < S * 256; idx += kT) {
+            const int s = idx >> 8, j = idx & 255;
+            if (uint32_t(j) < ds.NE[s]) {
+                const uint32_t e = ds.E[s * 256 + j];
+                if ((e >> 16) == dk) PC[s] = e & 0xffffu;
+            }
+        }
+        if (a.probs && end_slot >= 0) {
+            const Slot es = slot_at(lds, end_slot);
+            const uint32_t ek = sh.end_key;
+            for (int idx = tid; idx < S * 256; idx += kT) {
+                const int s = idx >> 8, j = idx & 255;
+                if (uint32_t(j) < es.NE[s]) {
+                    const uint32_t e = es.E[s * 256 + j];
+                    if ((e >> 16) == ek) PC[kMaxSlices + s] = e & 0xffffu;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t c = lane < S ? PC[lane] : 0u;
+        const uint32_t incl = wave_incl_scan_u32(c);
+        const uint32_t want = sh.draw_rank;
+        const uint64_t m = ballot(lane < S && incl > want);
+        if (m) {
+            const int L = __builtin_ctzll(m);
+            if (lane == L) { sh.owner_slice = uint32_t(L); sh.owner_rank = want - (incl - c); }
+        } else if (lane == 0) {
+            sh.ok = 0u;
+        }
+        if (a.probs) {   // end-key logits in the slices before each slice (id order)
+            const uint32_t ce = lane < S ? PC[kMaxSlices + lane] : 0u;
+            const uint32_t ie = wave_incl_scan_u32(ce);
+            if (lane < kMaxSlices) a.bases[size_t(row) * kMaxSlices + lane] = ie - ce;
+        }
+    }
+    __syncthreads();
+
+    // ---- 6. the owner slice read again: the owner_rank-th logit of the drawn
+    // key in id order (penalties applied as in the slice pass)
+    if (sh.ok) {
+        const int os = int(sh.owner_slice);
+        const Geo g = geo_of(a, row, os);
+        SliceRegs r;
+        load_slice(g, r);
+        const PenCtx pc = pen_ctx(a, row, p);
+        uint32_t* dense = a.lists + (rs + os) * kSL;
+        if (pc.pen) {
+            PenPrefetch f{};
+            pen_prefetch_head(a, pc, g, f);
+            pen_prefetch_list(a, pc, f);
+            pen_build<DT>(a, pc, g, f, lds, sh, dense);
+        }
+        const uint32_t dk = sh.draw_key;
+        uint32_t mask[kSeg], cnt[kSeg], excl[kSeg];
+        mask[0] = (tid < g.head && elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(tid), r.hb) == dk) ? 1u : 0u;
+#pragma unroll
+        for (int i = 0; i < kNV; ++i) {
+            const int v = i * kT + tid;
+            uint32_t mm = 0u;
+            if (v < g.nvec) {
+#pragma unroll 1
+                for (int j = 0; j < 8; ++j)
+                    if (elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(g.head + 8 * v + j), vec_elem(r.v[i], j)) == dk)
+                        mm |= 1u << j;
+            }
+            mask[1 + i] = mm;
+        }
+        mask[kSeg - 1] = (tid < g.tail && elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(g.head + 8 * g.nvec + tid),
+                                                         r.tb) == dk) ? 1u : 0u;
+#pragma unroll
+        for (int x = 0; x < kSeg; ++x) cnt[x] = __builtin_popcount(mask[x]);
+        (void)id_order_prefix(cnt, excl, sh);
+        const uint32_t want = sh.owner_rank;
+#pragma unroll
+        for (int x = 0; x < kSeg; ++x) {
+            if (want >= excl[x] && want < excl[x] + cnt[x]) {
+                uint32_t mm = mask[x];
+                for (uint32_t q = want - excl[x]; q > 0u; --q) mm &= mm - 1u;
+                const int j = __builtin_ctz(mm);
+                int off;
+                if (x == 0) off = tid;
+                else if (x == kSeg - 1) off = g.head + 8 * g.nvec + tid;
+                else off = g.head + 8 * ((x - 1) * kT + tid) + j;
+                sh.token = g.s0 + off;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const int32_t tok = sh.token;
+        if (tok < 0) {   // the tables disagree with the slice: cannot happen for consistent inputs
+            write_row(a, row, -1, sh.u, out_flags | VI_FLAG_ERROR, 0u, 0u, 0.0);
+        } else {
+            write_row(a, row, tok, sh.u, out_flags, sh.n_support, N, sh.s_n);
+            if (a.record && tok < V) {   // every slice of this row has finished reading the state
+                const LaneState ls = lane_state(a.pstate + size_t(row) * a.pl.lane_bytes, a.pl);
+                state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
+            }
+        }
+        if (a.probs)
+            a.bounds[row] = RowBound{zmax, sh.s_n, inv_t, sh.end_all ? 0u : sh.end_key,
+                                     sh.end_all ? kTakeAll : sh.end_take, tok >= 0 ? 1u : 0u};
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ kernel
+template <int DT>
+__global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+    __shared__ Shared sh;
+    uint32_t* H = reinterpret_cast<uint32_t*>(lds + kOffH);
+    uint32_t* O = reinterpret_cast<uint32_t*>(lds + kOffO);
+    uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave, w = blockIdx.x;
+    const int S = a.slices;
+
+    int row = 0, s = 0;
+    if (!item_of(a, w, 0, &row, &s)) return;
+    // the histogram and occupancy start empty (every slice leaves them so)
+    for (int i = tid; i < kSL; i += kT) H[i] = 0u;
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) O[q * kT + tid] = 0u;
+    Geo g = geo_of(a, row, s);
+    vi_row_params p = a.params[row];
+    SliceRegs cur{};
+    PenPrefetch pf{};
+    PenCtx pc{};
+    if (full_route_row(p)) {
+        load_slice(g, cur);
+        pc = pen_ctx(a, row, p);
+        pen_prefetch_head(a, pc, g, pf);
+        pen_prefetch_list(a, pc, pf);
+    }
+
+    // One slice per iteration.  `cur` / `pf` hold its logits and penalty inputs,
+    // requested during the previous iteration: the next slice's logits are loaded
+    // into `cur` as soon as this slice's histogram has consumed it, and land
+    // while the penalties, the compaction and the publication run.
+    // The previous slice's arrival: after its publication stores are
+    // acknowledged (every thread's), one atomic on the row's counter; the last
+    // slice of the row to arrive merges it.
+    bool pend = false;
+    int prow = 0;
+    vi_row_params pp{};
+    auto arrive = [&]() {
+        handoff_stores_done();
+        lds_barrier();
+        if (tid == 0) {
+            const uint32_t old = atomicAdd(&a.arrivals[prow], 1u);
+            sh.last = old == uint32_t(S - 1) ? 1u : 0u;
+            if (sh.last) put_agent(&a.arrivals[prow], 0u);
+        }
+        lds_barrier();
+        if (sh.last) {
+            handoff_acquire();
+            merge_row<DT>(a, prow, pp, 1.0f / pp.temperature, lds, sh);
+            // (the merge used the histogram's space: empty it again)
+            constexpr int kZ = kSL / kT / 4;
+#pragma unroll
+            for (int q = 0; q < kZ; ++q) reinterpret_cast<uint4*>(H)[tid * kZ + q] = make_uint4(0u, 0u, 0u, 0u);
+            lds_barrier();
+        }
+        pend = false;
+    };
+    for (int k = 0;; ++k) {
+        // this slice's loads have landed (waited for here, before anything else is
+        // requested: later waits then never include the next slice's loads), and
+        // with them the previous slice's publication stores
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        if (pend) arrive();
+        int nrow = 0, ns = 0;
+        const bool has_next = item_of(a, w, k + 1, &nrow, &ns);
+        const vi_row_params np = has_next ? a.params[nrow] : vi_row_params{};
+        const bool next_full = has_next && full_route_row(np);
+        const bool full = full_route_row(p);
+        const float inv_t = 1.0f / p.temperature;
+        uint32_t* dense = a.lists + (size_t(row) * S + s) * kSL;
+        constexpr int kG = kStage / kT;   // history tokens gathered per thread and round
+        uint32_t graw[kG], goff[kG];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) { graw[u] = 0u; goff[u] = 0xffffffffu; }
+        uint32_t bw[kWPT], rank0 = 0u, nf = 0u;
+        uint16_t* F = reinterpret_cast<uint16_t*>(lds + kOffF);
+
+        if (full) {
+            if (tid == 0) { sh.flags = 0u; sh.top_key = 0u; sh.n_valid = 0u; sh.n_neg = 0u; }
+            // valid keys: finite pattern and finite z
+            if (wave == 0) {
+                constexpr int kPosMax = DT == VI_BF16 ? 0xff7f : 0xfbff;   // largest finite key
+                constexpr int kNegMin = DT == VI_BF16 ? 0x0080 : 0x0400;   // smallest finite key
+                const bool t_ok = p.temperature <= kMaxTemperature && isfinite(inv_t);
+                const int kbad = wave_search(0x8000, kPosMax + 1,
+                                             [&](int key) { return !isfinite(key_z<DT>(uint32_t(key), inv_t)); });
+                const int kgood = wave_search(kNegMin, 0x8000,
+                                              [&](int key) { return isfinite(key_z<DT>(uint32_t(key), inv_t)); });
+                if (lane == 0) {
+                    sh.kmax = t_ok ? uint32_t(kbad - 1) : 0u;
+                    sh.kmin = t_ok ? uint32_t(kgood) : 1u;
+                }
+            }
+            // ---- 1. penalties; the first round of history tokens staged and
+            // their raw logits requested (before the next slice's loads)
+            if (pc.pen) {
+                pen_build<DT>(a, pc, g, pf, lds, sh, dense);
+                // this thread's bitmap words tid * kWPT .. + kWPT - 1: ranks of their tokens
+                uint32_t pc_ = 0u;
+#pragma unroll
+                for (int q = 0; q < kWPT; ++q) { bw[q] = B[tid * kWPT + q]; pc_ += __builtin_popcount(bw[q]); }
+                rank0 = block_scan_lds(pc_, sh.scan, &nf);
+                uint32_t r = rank0;
+#pragma unroll
+                for (int q = 0; q < kWPT; ++q) {
+                    uint32_t bits = bw[q];
+                    while (bits && r < uint32_t(kStage)) {
+                        const int j = __builtin_ctz(bits);
+                        bits &= bits - 1u;
+                        F[r++] = uint16_t((tid * kWPT + q) * 32 + j);
+                    }
+                }
+                lds_barrier();
+                const uint32_t m = min(uint32_t(kStage), nf);
+#pragma unroll
+                for (int u = 0; u < kG; ++u) {
+                    const uint32_t e = uint32_t(u) * kT + tid;
+                    goff[u] = e < m ? uint32_t(F[e]) : 0xffffffffu;
+                    graw[u] = e < m ? uint32_t(g.base16[goff[u]]) : 0u;
+                }
+            }
+        }
+        Geo ng{};
+        PenCtx npc{};
+        if (next_full) {
+            ng = geo_of(a, nrow, ns);
+            npc = pen_ctx(a, nrow, np);
+        }
+
+        if (full) {
+            // ---- 2. raw-pattern histogram of the slice
+            auto hist_add = [&](uint32_t b) {
+                const uint32_t idx = b & 0x7fffu, inc = (b & 0x8000u) ? 0x10000u : 1u;
+                const uint32_t old = atomicAdd(&H[idx], inc);
+                if (old == 0u) atomicOr(&O[idx >> 5], 1u << (idx & 31));
+            };
+            // the eight counts of a vector are added before any result is looked at
+            // (a wave's LDS operations complete in order: one wait per vector)
+            auto hist_add8 = [&](const uint4& v, bool ok) {
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                uint32_t idx[8], old[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // (unconditional: a masked lane adds 0; a conditional atomic would be
+                    // a branch with its own wait)
+                    const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                    idx[j] = b & 0x7fffu;
+                    old[j] = atomicAdd(&H[idx[j]], ok ? ((b & 0x8000u) ? 0x10000u : 1u) : 0u);
+                }
+                uint32_t first = 0u;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) first |= (old[j] == 0u ? 1u : 0u) << j;
+                first = ok ? first : 0u;
+                if (first) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if ((first >> j) & 1u) atomicOr(&O[idx[j] >> 5], 1u << (idx[j] & 31));
+                }
+            };
+#pragma unroll
+            for (int i = 0; i < kNV; ++i) hist_add8(cur.v[i], i * kT + tid < g.nvec);
+            if (tid < g.head) hist_add(cur.hb);
+            if (tid < g.tail) hist_add(cur.tb);
+            // ---- the next slice: its penalty inputs, then its logits (into the
+            // registers this slice's logits occupied)
+            if (next_full) {
+                pen_prefetch_head(a, npc, ng, pf);
+                load_slice(ng, cur);
+            }
+
+            // ---- 3. history tokens move from their raw pattern to the penalized one
+            if (pc.pen) {
+                auto move = [&](uint32_t off, uint32_t b) {
+                    if (!Elem<DT>::finite_bits(b)) return;
+                    const uint32_t pb = penalize_bits<DT>(b, pen_count(lds, sh, dense, off), p) & 0xffffu;
+                    if (pb == b) return;
+                    atomicSub(&H[b & 0x7fffu], (b & 0x8000u) ? 0x10000u : 1u);
+                    hist_add(pb);
+                };
+#pragma unroll
+                for (int u = 0; u < kG; ++u)
+                    if (goff[u] != 0xffffffffu) move(goff[u], graw[u]);
+                lds_barrier();
+                for (uint32_t c0 = kStage; c0 < nf; c0 += kStage) {   // (long histories) further rounds
+                    uint32_t r = rank0;
+#pragma unroll
+                    for (int q = 0; q < kWPT; ++q) {
+                        uint32_t bits = bw[q];
+                        while (bits) {
+                            const int j = __builtin_ctz(bits);
+                            bits &= bits - 1u;
+                            if (r >= c0 && r < c0 + kStage) F[r - c0] = uint16_t((tid * kWPT + q) * 32 + j);
+                            ++r;
+                        }
+                    }
+                    lds_barrier();
+                    const uint32_t m = min(uint32_t(kStage), nf - c0);
+                    uint32_t rr[kG], oo[kG];
+#pragma unroll
+                    for (int u = 0; u < kG; ++u) {
+                        const uint32_t e = uint32_t(u) * kT + tid;
+                        oo[u] = e < m ? uint32_t(F[e]) : 0xffffffffu;
+                        rr[u] = e < m ? uint32_t(g.base16[oo[u]]) : 0u;
+                    }
+#pragma unroll
+                    for (int u = 0; u < kG; ++u)
+                        if (oo[u] != 0xffffffffu) move(oo[u], rr[u]);
+                    lds_barrier();
+                }
+            }
+            lds_barrier();
+
+            // ---- 4. compaction: key-sorted list and coarse bin tables
+            uint32_t* bent = reinterpret_cast<uint32_t*>(lds + kOffX);     // entries per bin
+            uint32_t* bcnt = bent + kBP;                                   // valid logits per bin
+            uint32_t* bref = bcnt + kBP;                                   // largest valid key per bin
+            uint32_t* bfirst = bref + kBP;                                 // first list index per bin
+            double* bmass = reinterpret_cast<double*>(bfirst + kBP);       // mass per bin (8-byte aligned)
+            if (tid < kBP) { bent[tid] = 0u; bcnt[tid] = 0u; bref[tid] = 0u; bmass[tid] = 0.0; }
+            lds_barrier();
+            const uint32_t kmin = sh.kmin, kmax = sh.kmax;
+            // (a) occupied histogram words in ascending order, staged kStage at a time
+            // in C (u16); each thread then takes kPer consecutive staged words, so the
+            // list positions follow from one block scan and the work is balanced
+            uint16_t* C = reinterpret_cast<uint16_t*>(lds + kOffF);
+            uint32_t occ[kWPT], npc = 0u;
+#pragma unroll
+            for (int q = 0; q < kWPT; ++q) { occ[q] = O[tid * kWPT + q]; npc += __builtin_popcount(occ[q]); }
+            uint32_t M;
+            const uint32_t obase = block_scan_lds(npc, sh.scan, &M);
+            auto stage_words = [&](uint32_t c0) {
+                if (obase >= c0 + kStage || obase + npc <= c0) return;
+                uint32_t r = obase;
+#pragma unroll
+                for (int q = 0; q < kWPT; ++q) {
+                    uint32_t bits = occ[q];
+                    while (bits) {
+                        const int j = __builtin_ctz(bits);
+                        bits &= bits - 1u;
+                        if (r >= c0 && r < c0 + kStage) C[r - c0] = uint16_t((tid * kWPT + q) * 32 + j);
+                        ++r;
+                    }
+                }
+            };
+            constexpr int kPer = kStage / kT;   // staged words per thread
+            uint32_t wd[kPer], wv[kPer];        // a thread's staged words and their two counts
+            auto load_staged = [&](uint32_t m) {
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const uint32_t e = uint32_t(tid * kPer + u);
+                    wd[u] = e < m ? uint32_t(C[e]) : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const uint32_t e = uint32_t(tid * kPer + u);
+                    uint32_t v = e < m ? H[wd[u]] : 0u;
+                    if (wd[u] == 0u && e < m) v = (v & 0xffffu) + (v >> 16);   // -0 joins +0 (both z = 0)
+                    wv[u] = v;
+                }
+            };
+            // the positive pattern d has key 0x8000 | d; the negative one 0x7fff - d
+            auto pos_ok = [&](uint32_t d, uint32_t v) { return (v & 0xffffu) && (0x8000u | d) >= kmin && (0x8000u | d) <= kmax; };
+            auto neg_ok = [&](uint32_t d, uint32_t v) { return (v >> 16) && (0x7fffu - d) >= kmin && (0x7fffu - d) <= kmax; };
+            // (b) per bin: entries, valid logits, largest valid key; runs of one bin
+            // are flushed with one atomic each
+            uint32_t nn_all = 0u, nv_all = 0u, top = 0u;
+            bool invalid = false;
+            for (uint32_t c0 = 0u; c0 < M; c0 += kStage) {
+                stage_words(c0);
+                lds_barrier();
+                load_staged(min(uint32_t(kStage), M - c0));
+                int pb = -1, nb = -1;
+                uint32_t pe = 0u, pc = 0u, pk = 0u, ne = 0u, nc = 0u, nk = 0u;
+                auto flush = [&](int b, uint32_t& e, uint32_t& c, uint32_t& k) {
+                    if (b >= 0 && e) { atomicAdd(&bent[b], e); atomicAdd(&bcnt[b], c); atomicMax(&bref[b], k); }
+                    e = 0u; c = 0u; k = 0u;
+                };
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const uint32_t d = wd[u], v = wv[u];
+                    if (v & 0xffffu) {
+                        if (pos_ok(d, v)) {
+                            const uint32_t key = 0x8000u | d;
+                            const int b = bin_of(key);
+                            if (b != pb) { flush(pb, pe, pc, pk); pb = b; }
+                            ++pe; pc += v & 0xffffu; pk = max(pk, key);
+                            nv_all += v & 0xffffu; top = max(top, key);
+                        } else {
+                            invalid = true;
+                        }
+                    }
+                    if (v >> 16) {
+                        if (neg_ok(d, v)) {
+                            const uint32_t key = 0x7fffu - d;
+                            const int b = bin_of(key);
+                            if (b != nb) { flush(nb, ne, nc, nk); nb = b; }
+                            ++ne; nc += v >> 16; nk = max(nk, key);
+                            ++nn_all; nv_all += v >> 16; top = max(top, key);
+                        } else {
+                            invalid = true;
+                        }
+                    }
+                }
+                flush(pb, pe, pc, pk);
+                flush(nb, ne, nc, nk);
+                lds_barrier();
+            }
+            if (ballot(invalid) && lane == 0) atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE));
+            {
+                uint32_t t2 = top;
+#pragma unroll
+                for (int o = 32; o; o >>= 1) t2 = max(t2, uint32_t(__shfl_xor(int(t2), o, kWave)));
+                const uint32_t nv = wave_sum_u32(nv_all), nn = wave_sum_u32(nn_all);
+                if (lane == 0) { atomicMax(&sh.top_key, t2); atomicAdd(&sh.n_valid, nv); atomicAdd(&sh.n_neg, nn); }
+            }
+            lds_barrier();
+            if (wave == 0) {   // first list index of each bin (bins ascending = keys ascending)
+                uint32_t e[5], t = 0u;
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    const int b = lane * 5 + i;
+                    e[i] = b < kBP ? bent[b] : 0u;
+                    t += e[i];
+                }
+                uint32_t x = wave_incl_scan_u32(t) - t;
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    const int b = lane * 5 + i;
+                    if (b < kBP) bfirst[b] = x;
+                    x += e[i];
+                }
+                if (lane == kWave - 1) sh.n_list = x;
+            }
+            lds_barrier();
+            const uint32_t NL = sh.n_list;
+            // (c) the list in key order: the NN negative-pattern entries first (their
+            // keys fall as d rises, so they fill the list from position NN - 1 down),
+            // then the positive ones (d ascending); and the bins' fixed-point masses
+            uint32_t* list = a.lists + (size_t(row) * S + s) * kSL;
+            uint32_t pos_before = 0u, neg_before = 0u;
+            const uint32_t NN = sh.n_neg;
+            for (uint32_t c0 = 0u; c0 < M; c0 += kStage) {
+                stage_words(c0);
+                lds_barrier();
+                load_staged(min(uint32_t(kStage), M - c0));
+                uint32_t np = 0u, nn = 0u;
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    np += pos_ok(wd[u], wv[u]) ? 1u : 0u;
+                    nn += neg_ok(wd[u], wv[u]) ? 1u : 0u;
+                }
+                uint32_t tot2;
+                const uint32_t pre2 = block_scan_lds(np | (nn << 16), sh.scan, &tot2);
+                uint32_t ip = NN + pos_before + (pre2 & 0xffffu);
+                uint32_t in_ = NN - 1u - (neg_before + (pre2 >> 16));
+                int pb = -1, nb = -1;
+                double pm = 0.0, nm = 0.0;
+                auto mass_of = [&](uint32_t key, uint32_t cnt, int b) {
+                    const double z = double(key_z<DT>(key, inv_t)), zr = double(key_z<DT>(bref[b], inv_t));
+                    // in units of 2^-38: integer-valued, and a bin's sum stays below 2^53
+                    // (<= 32,768 logits of weight <= 1), so the additions are exact and
+                    // their order cannot change the result
+                    return rint(double(cnt) * exp(z - zr) * kMassScale);
+                };
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const uint32_t d = wd[u], v = wv[u];
+                    if (pos_ok(d, v)) {
+                        const uint32_t key = 0x8000u | d, cnt = v & 0xffffu;
+                        const int b = bin_of(key);
+                        if (b != pb) { if (pb >= 0) atomicAdd(&bmass[pb], pm); pb = b; pm = 0.0; }
+                        pm += mass_of(key, cnt, b);
+                        put_agent(&list[ip++], (key << 16) | cnt);
+                    }
+                    if (neg_ok(d, v)) {
+                        const uint32_t key = 0x7fffu - d, cnt = v >> 16;
+                        const int b = bin_of(key);
+                        if (b != nb) { if (nb >= 0) atomicAdd(&bmass[nb], nm); nb = b; nm = 0.0; }
+                        nm += mass_of(key, cnt, b);
+                        put_agent(&list[in_--], (key << 16) | cnt);
+                    }
+                }
+                if (pb >= 0) atomicAdd(&bmass[pb], pm);
+                if (nb >= 0) atomicAdd(&bmass[nb], nm);
+                pos_before += tot2 & 0xffffu;
+                neg_before += tot2 >> 16;
+                lds_barrier();
+            }
+            // ---- publish the slice (write-through), then arrive
+            const size_t sb = (size_t(row) * S + s) * kBP;
+            if (tid < kBP) {
+                put_agent(&a.bfe[sb + tid], bfirst[tid] | (bent[tid] << 16));
+                put_agent(&a.bcnt[sb + tid], bcnt[tid]);
+                put_agent(&a.bref[sb + tid], bref[tid]);
+                put_agent(&a.bmass[sb + tid], bmass[tid]);
+            }
+            if (tid == 0) {
+                uint32_t* hd = a.heads + (size_t(row) * S + s) * 4;
+                put_agent(&hd[0], NL);
+                put_agent(&hd[1], sh.n_valid);
+                put_agent(&hd[2], sh.flags);
+                put_agent(&hd[3], sh.top_key);
+            }
+            // the histogram and occupancy back to empty for the next slice
+            constexpr int kZ = kSL / kT / 4;   // 16-byte stores per thread
+#pragma unroll
+            for (int q = 0; q < kZ; ++q) reinterpret_cast<uint4*>(H)[tid * kZ + q] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int q = 0; q < kWPT; ++q) O[tid * kWPT + q] = 0u;
+            // (the arrival waits for these stores: it is made at the top of the next
+            // iteration, whose wait for the next slice's logits covers them)
+            pend = true;
+            prow = row;
+            pp = p;
+        } else if (next_full) {
+            pen_prefetch_head(a, npc, ng, pf);
+            load_slice(ng, cur);
+        }
+        if (!has_next) break;
+        if (next_full) pen_prefetch_list(a, npc, pf);   // (the next slice's header has arrived)
+        row = nrow; s = ns; g = ng; p = np; pc = npc;
+    }
+    if (pend) arrive();
+}
+
+// Filtered distribution of the full-route rows (test / diagnostics path): per
+// slice, the penalized logits' keys decide support membership (keys above the
+// support's end key; of the end key, the first end_take in id order over the
+// row), and the support gets exp(z - z0) / S_n.
+template <int DT>
+__global__ __launch_bounds__(kT) void slice_probs_kernel(SliceArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+    __shared__ Shared sh;
+    const int tid = threadIdx.x, w = blockIdx.x, S = a.slices;
+    int row = 0, s = 0;
+    for (int k = 0; item_of(a, w, k, &row, &s); ++k) {
+        const vi_row_params p = a.params[row];
+        if (!full_route_row(p)) continue;
+        const RowBound bd = a.bounds[row];
+        const Geo g = geo_of(a, row, s);
+        float* pr = a.probs + size_t(row) * size_t(a.probs_stride) + g.s0;
+        if (!bd.valid) {
+            for (int i = tid; i < g.n; i += kT) pr[i] = 0.0f;
+            continue;
+        }
+        SliceRegs r;
+        load_slice(g, r);
+        const PenCtx pc = pen_ctx(a, row, p);
+        uint32_t* dense = a.lists + (size_t(row) * S + s) * kSL;
+        if (pc.pen) {
+            if (tid == 0) sh.flags = 0u;
+            PenPrefetch f{};
+            pen_prefetch_head(a, pc, g, f);
+            pen_prefetch_list(a, pc, f);
+            pen_build<DT>(a, pc, g, f, lds, sh, dense);
+        }
+        // pass 1: logits of the support's end key, in id order
+        uint32_t mask[kSeg], cnt[kSeg], excl[kSeg];
+        const uint32_t ek = bd.end_key;
+        // with record = 1 the sampler has already recorded the row's token into the
+        // lane's state: the distribution is the one before that occurrence
+        uint32_t unrec = ~0u;
+        if (a.record && pc.pen) {
+            const int32_t t = a.tokens[row];
+            if (t >= g.s0 && t < g.s0 + g.n) unrec = uint32_t(t - g.s0);
+        }
+        auto keyof = [&](uint32_t off, uint32_t b) { return elem_key<DT>(lds, sh, dense, p, pc.pen, off, b, unrec); };
+        mask[0] = (tid < g.head && keyof(uint32_t(tid), r.hb) == ek) ? 1u : 0u;
+        mask[kSeg - 1] = (tid < g.tail && keyof(uint32_t(g.head + 8 * g.nvec + tid), r.tb) == ek) ? 1u : 0u;
+#pragma unroll
+        for (int i = 0; i < kNV; ++i) {
+            const int v = i * kT + tid;
+            uint32_t mm = 0u;
+            if (v < g.nvec) {
+#pragma unroll 1
+                for (int j = 0; j < 8; ++j)
+                    if (keyof(uint32_t(g.head + 8 * v + j), vec_elem(r.v[i], j)) == ek) mm |= 1u << j;
+            }
+            mask[1 + i] = mm;
+        }
+#pragma unroll
+        for (int x = 0; x < kSeg; ++x) cnt[x] = __builtin_popcount(mask[x]);
+        (void)id_order_prefix(cnt, excl, sh);
+        const uint32_t base = bd.end_take == kTakeAll ? 0u : a.bases[size_t(row) * kMaxSlices + s];
+        auto prob = [&](uint32_t key, uint32_t rank) -> float {
+            if (!key || key < ek) return 0.0f;
+            if (key == ek && bd.end_take != kTakeAll && base + rank >= bd.end_take) return 0.0f;
+            const float z = key_z<DT>(key, bd.inv_t);
+            return isfinite(z) ? float(exp(double(z) - bd.z0) / bd.s_n) : 0.0f;
+        };
+        // pass 2: probabilities
+        if (tid < g.head) pr[tid] = prob(keyof(uint32_t(tid), r.hb), excl[0]);
+        if (tid < g.tail)
+            pr[g.head + 8 * g.nvec + tid] = prob(keyof(uint32_t(g.head + 8 * g.nvec + tid), r.tb), excl[kSeg - 1]);
+#pragma unroll
+        for (int i = 0; i < kNV; ++i) {
+            const int v = i * kT + tid;
+            if (v >= g.nvec) continue;
+            uint32_t rk = excl[1 + i];
+            float* out = pr + g.head + 8 * v;
+#pragma unroll 1
+            for (int j = 0; j < 8; ++j) {
+                out[j] = prob(keyof(uint32_t(g.head + 8 * v + j), vec_elem(r.v[i], j)), rk);
+                rk += (mask[1 + i] >> j) & 1u;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+inline int slices_of(int vocabulary) { return (vocabulary + kSL - 1) / kSL; }
+
+}  // namespace
+
+bool full_supported(int dtype, int vocabulary, int64_t stride) {
+    return (dtype == VI_BF16 || dtype == VI_F16) && vocabulary > 0 && vocabulary <= kMaxSlices * kSL &&
+           stride >= vocabulary;
+}
+
+size_t full_workspace(int rows, int vocabulary) {
+    if (rows <= 0 || vocabulary <= 0) return 0;
+    const size_t rs = size_t(rows) * size_t(slices_of(vocabulary));
+    return align_up(size_t(rows) * 4, 256) + align_up(rs * 16, 256) + 3 * align_up(rs * kBP * 4, 256) +
+           align_up(rs * kBP * 8, 256) + align_up(rs * kSL * 4, 256) + align_up(size_t(rows) * sizeof(RowBound), 256) +
+           align_up(size_t(rows) * kMaxSlices * 4, 256) + 256;
+}
+
+vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream) {
+    if (reinterpret_cast<uintptr_t>(s.logits) % 16) return VI_ERR_UNSUPPORTED;
+    if (!full_supported(s.dtype, s.vocabulary, s.stride)) return VI_ERR_UNSUPPORTED;
+    SliceArgs a{};
+    a.slices = slices_of(s.vocabulary);
+    const size_t rs = size_t(s.rows) * size_t(a.slices);
+    Carver c(ws, ws_bytes);
+    a.arrivals = c.take<uint32_t>(size_t(s.rows));
+    a.heads = c.take<uint32_t>(rs * 4);
+    a.bfe = c.take<uint32_t>(rs * kBP);
+    a.bcnt = c.take<uint32_t>(rs * kBP);
+    a.bref = c.take<uint32_t>(rs * kBP);
+    a.bmass = c.take<double>(rs * kBP);
+    a.lists = c.take<uint32_t>(rs * kSL);
+    a.bounds = c.take<RowBound>(size_t(s.rows));
+    a.bases = c.take<uint32_t>(size_t(s.rows) * kMaxSlices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary; a.stride = s.stride;
+    a.params = s.params; a.histories = s.histories; a.offsets = s.offsets;
+    if (s.pstate) { a.pstate = s.pstate; a.pl = s.playout; a.record = s.record; }
+    a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
+    a.stats = s.stats;
+    const int items = s.rows * a.slices;
+    a.grid = std::min(device_cus(), items);
+    a.xcd_aware = (s.rows >= 8 && a.grid % 8 == 0) ? 1 : 0;
+    if (s.dtype == VI_BF16) hipLaunchKernelGGL(slice_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);
+    else hipLaunchKernelGGL(slice_kernel<VI_F16>, dim3(a.grid), dim3(kT), 0, stream, a);
+    vi_status st = launch_status();
+    if (st != VI_OK || !s.probs) return st;
+    if (s.dtype == VI_BF16) hipLaunchKernelGGL(slice_probs_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);
+    else hipLaunchKernelGGL(slice_probs_kernel<VI_F16>, dim3(a.grid), dim3(kT), 0, stream, a);
+    return launch_status();
+}
+
+}  // namespace vi

@@ -153,7 +153,7 @@ size_t sample_workspace(int rows, int vocabulary, int64_t max_history);
 vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // ---- full-vocabulary pair kernel --------------------------------------------
-size_t full_workspace(int rows);
+size_t full_workspace(int rows, int vocabulary);
 vi_status launch_full(const SampleArgs& a, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 bool full_supported(int dtype, int vocabulary, int64_t stride);
 
