@@ -227,7 +227,7 @@ def test_state_route_without_distinct_token_limits(orc, dev, rng):
     for r in range(4):
         if not exempt_draw(margins[r]):
             assert b.tokens[r].item() == w_tok[r] and s["support"][r] == w_stats["support"][r], r
-            np.testing.assert_allclose(s["support_mass"][r], w_stats["support_mass"][r], rtol=1e-9)
+            np.testing.assert_allclose(s["support_mass"][r], w_stats["support_mass"][r], rtol=1e-6)
 
 
 @pytest.mark.parametrize("vocab", [64, 1000, 65_537])

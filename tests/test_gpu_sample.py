@@ -16,6 +16,7 @@ from helpers import exempt_draw, to_dev
 pytestmark = pytest.mark.gpu
 
 RTOL_PROBS = 1e-5
+RTOL_MASS = 1e-6
 
 
 def run_both(orc, dev, bits, dtype, params, hist=None, offs=None, want_probs=True):
@@ -47,7 +48,9 @@ def compare(g, w, params, label=""):
         assert g["stats"]["finite"][r] == w["stats"]["finite"][r], (label, r)
         if params["temperature"][r] > 0 and not (w["stats"]["flags"][r] & 2):
             assert g["u"][r] == w["u"][r], (label, r)
-            np.testing.assert_allclose(g["stats"]["support_mass"][r], w["stats"]["support_mass"][r], rtol=1e-9)
+            # (the full route's coarse bin masses use single-precision weights:
+            # within the north-star's 1e-6 relative mass tolerance)
+            np.testing.assert_allclose(g["stats"]["support_mass"][r], w["stats"]["support_mass"][r], rtol=RTOL_MASS)
         if g["probs"] is not None:
             gp, wp = g["probs"][r], w["probs"][r]
             assert np.array_equal(gp > 0, wp > 0), (label, r, np.flatnonzero((gp > 0) != (wp > 0))[:10])

@@ -21,19 +21,18 @@
 //   1. penalties: a bitmap of the slice's history tokens and an LDS hash of the
 //      repeated ones' counts, from the lane's penalty state or its history;
 //   2. a u16 count histogram indexed by raw pattern (word = pattern & 0x7fff,
-//      half = sign bit), every logit counted as it arrives; the increment that
-//      finds a word at zero marks it in an occupancy bitmap;
+//      half = sign bit), every logit counted as it arrives;
 //   3. history tokens, gathered again from cache, are penalized and moved from
 //      their raw pattern's count to the penalized pattern's;
-//   4. the occupied patterns become a key-sorted (key << 16 | count) list, and
-//      each coarse bin of 256 keys (bin = (key + 128) >> 8) gets its valid
-//      count, its largest valid key and the mass sum of count * exp(z(key) -
-//      z(largest key)), published to HBM with write-through stores.
-// The last slice of a row to arrive merges; no workgroup waits for another.
-// The merge sums the coarse tables, locates the bins holding the top-k, min-p
-// and top-p cuts and the draw, resolves each inside its bin from the slices'
-// list entries of that bin (exact key and rank), and reads the slice that holds
-// the drawn rank again to name the token (id order among equal keys).
+//   4. one pass over the histogram: each coarse bin of 128 keys (bin = key >>
+//      7) gets its (key << 16 | count) entries in key order, its valid count,
+//      its largest valid key and the mass sum of count * exp(z(key) -
+//      z(largest key)); entries and bin records go to HBM.
+// A second launch merges, one workgroup per row: it sums the coarse tables,
+// locates the bins holding the top-k, min-p and top-p cuts and the draw,
+// resolves each inside its bin from the slices' list entries of that bin
+// (exact key and rank), and reads the slice that holds the drawn rank again to
+// name the token (id order among equal keys).
 //
 // Roofline: HBM; V x 2 bytes of logits per row, plus the penalty state's
 // bitmap (V / 8 bytes) and repeat list, or the history.
@@ -46,50 +45,48 @@
 namespace vi {
 namespace {
 
-constexpr int kT = 512;                   // threads per workgroup (one per CU: the LDS is the limit)
+constexpr int kT = 1024;                  // threads per workgroup (one per CU: the LDS is the limit)
 constexpr int kW = kT / kWave;            // waves per workgroup
 constexpr int kSL = 32768;                // tokens per slice
 constexpr int kNV = kSL / 8 / kT;         // 16-byte vectors per thread and slice
-constexpr int kBins = 257;                // coarse bins, bin(key) = (key + 128) >> 8
-constexpr int kBP = 264;                  // padded
+constexpr int kBins = 512;                // coarse bins of 128 keys, bin(key) = key >> 7
+constexpr int kBinKeys = 128;
+constexpr int kHeadWords = 32;            // slice head: n_list, n_valid, flags, top_key, bin mask [16]
 constexpr int kHash = 2048;               // LDS repeat-count hash slots
 constexpr uint32_t kHashFill = kHash * 3 / 4;
 constexpr int kStage = 4096;              // history offsets staged per penalty round (u16)
-constexpr int kChunk = 2048;              // list entries staged per compaction round (u32)
 constexpr int kMaxSlices = 16;
 constexpr int kPL = 2;                    // repeat-list entries prefetched per thread
 constexpr int kPHist = 4;                 // history tokens prefetched per thread
 constexpr uint32_t kTakeAll = 0xffffffffu;
-constexpr double kMassScale = 0x1p38;     // fixed-point unit of the slices' bin masses
 constexpr float kMaxTemperature = 65536.0f;
 
 // LDS map (bytes).  H: histogram, u16 counts in pairs (word p & 0x7fff: low half
-// the pattern with sign 0, high half with sign 1); the merge reuses it.  O:
-// occupancy of H's words.  B: history bitmap of the slice.  X: repeat hash,
-// then the compaction's bin tables.  F: staged history offsets / list entries.
+// the pattern with sign 0, high half with sign 1), then the staged list; the
+// merge reuses it.  B: history bitmap of the slice.  X: repeat hash, then the
+// compaction's bin tables.  F: staged history offsets.
 constexpr int kOffH = 0;
-constexpr int kOffO = kOffH + 4 * kSL;
-constexpr int kOffB = kOffO + 4 * kT;
+constexpr int kOffB = kOffH + 4 * kSL;
 constexpr int kOffX = kOffB + 4 * (kSL / 32);
 constexpr int kOffF = kOffX + 4 * kHash;
 constexpr int kLds = kOffF + 2 * kStage;
-constexpr int kWPT = kSL / 32 / kT;       // bitmap / occupancy words per thread
+constexpr int kWPT = kSL / 32 / kT;       // history bitmap words per thread
+constexpr int kQ = kSL / 2 / kT;          // 2-word histogram groups per thread (compaction)
 constexpr int kSeg = kNV + 2;             // id-order segments: head, vectors, tail
 static_assert(kWPT * kT * 32 == kSL, "whole bitmap words per thread");
-static_assert(kChunk * 4 == kStage * 2, "staging region");
-static_assert(4 * 4 * kBP + 8 * kBP <= 4 * kHash && kBP % 2 == 0, "compaction bin tables fit the hash region");
+static_assert(kQ * kW == 256 && kQ * 2 * kT == kSL, "compaction blocks of 128 patterns");
 
-// Merge map inside H (bytes): per-slice bin (first | entries << 16), bin
-// counts and masses summed over slices, four gather slots (entries per slice
-// and per-key counts).
+// Merge map inside H (bytes): per-slice bin (first | entries << 16), the
+// slices' bin masks, bin counts and masses summed over slices, five gather
+// slots (entries per slice and per-key counts).
 constexpr int kOffMFE = 0;
-constexpr int kOffMC = kOffMFE + 4 * kMaxSlices * kBP;
-constexpr int kOffMR = kOffMC + 4 * kBP;
+constexpr int kOffMM = kOffMFE + 4 * kMaxSlices * kBins;
+constexpr int kOffMC = kOffMM + 4 * kMaxSlices * (kBins / 32);
+constexpr int kOffMR = kOffMC + 4 * kBins;
 constexpr int kGatherSlots = 5;   // cap, min-p, top-p, support end, draw
-constexpr int kGatherBytes = 4 * kMaxSlices * 256 + 4 * 256 + 4 * kMaxSlices;
-constexpr int kOffGather = kOffMR + 8 * kBP;
+constexpr int kGatherBytes = 4 * kMaxSlices * kBinKeys + 4 * kBinKeys + 4 * kMaxSlices;
+constexpr int kOffGather = kOffMR + 8 * kBins;
 static_assert(kOffGather + kGatherSlots * kGatherBytes <= 4 * kSL, "merge map");
-static_assert(8 * kMaxSlices * kBP <= kGatherSlots * kGatherBytes, "slice masses fit the gather slots");
 
 struct RowBound {          // what the probs kernel needs to rebuild the support
     double z0, s_n;
@@ -113,12 +110,9 @@ struct SliceArgs {
     int64_t probs_stride;
     vi_sample_stats* stats;
     // workspace
-    uint32_t* arrivals;        // [rows]
-    uint32_t* heads;           // [rows][slices][4]: n_list, n_valid, flags, top_key
-    uint32_t* bfe;             // [rows][slices][kBP]: first | entries << 16
-    uint32_t* bcnt;            // [rows][slices][kBP]: valid logits
-    uint32_t* bref;            // [rows][slices][kBP]: largest valid key
-    double* bmass;             // [rows][slices][kBP], in units of 2^-38
+    uint32_t* heads;           // [rows][slices][kHeadWords]: n_list, n_valid, flags, top_key, occupied-bin mask
+    uint4* brec;               // [rows][slices][kBins], occupied bins only: first | entries << 16,
+                               // valid logits | largest valid key << 16, mass relative to that key (double)
     uint32_t* lists;           // [rows][slices][kSL]; a slice's dense repeat counts before its list
     RowBound* bounds;          // [rows]
     uint32_t* bases;           // [rows][kMaxSlices]: end-key logits in the slices before
@@ -129,20 +123,31 @@ struct Shared {
     uint32_t segs[kW][kSeg];
     // slice
     uint32_t flags, n_hash, overflow;
-    uint32_t kmin, kmax, top_key, n_valid, n_neg, n_list, last;
+    uint32_t kmin, kmax, top_key, n_valid, n_list;
+    uint32_t krange[kW];          // valid key range (kmin | kmax << 16) of items k .. k + kW - 1
+    uint32_t bmask[kBins / 32];
     // merge
     uint32_t row_flags, row_valid, row_top;
     int32_t slot_bin[kGatherSlots];
     int32_t cap_bin, minp_bin, topp_bin, draw_bin, end_bin;
     int32_t cap_slot, minp_slot, topp_slot, draw_slot, end_slot;
     uint32_t cap_key, cap_take, minp_key, topp_key, topp_take, end_key, end_take, end_all;
-    uint32_t n_support, draw_key, draw_rank, owner_slice, owner_rank, ok;
+    uint32_t n_support, draw_key, draw_rank, owner_slice, owner_rank, ok, hmask, tmask;
     int32_t token;
     double s_all, cap_mass, topp_target, s_n, u, draw_target;
 };
 
-__device__ __forceinline__ int bin_of(uint32_t key) { return int((key + 128u) >> 8); }
-__device__ __forceinline__ uint32_t bin_first_key(int b) { return uint32_t(b) * 256u - 128u; }
+// threadIdx.x behind an empty asm: arithmetic on it stays where it is written
+// (the persistent loop's address computations would otherwise be hoisted out
+// of the loop and held, or spilled, across it)
+__device__ __forceinline__ int opaque_tid() {
+    int t = int(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+__device__ __forceinline__ int bin_of(uint32_t key) { return int(key >> 7); }
+__device__ __forceinline__ uint32_t bin_first_key(int b) { return uint32_t(b) * uint32_t(kBinKeys); }
 
 template <int DT>
 __device__ __forceinline__ float key_z(uint32_t key, float inv_t) {
@@ -255,7 +260,7 @@ struct SliceRegs {
     uint32_t hb, tb;
 };
 __device__ __forceinline__ void load_slice(const Geo& g, SliceRegs& r) {
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
 #pragma unroll
     for (int i = 0; i < kNV; ++i) {
         const int v = i * kT + tid;
@@ -319,7 +324,7 @@ __device__ __forceinline__ PenCtx pen_ctx(const SliceArgs& a, int row, const vi_
 // First loads of a slice's penalty inputs (header, bitmap word, list / history
 // head); issued a slice ahead.
 __device__ __forceinline__ void pen_prefetch_head(const SliceArgs& a, const PenCtx& c, const Geo& g, PenPrefetch& f) {
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
 #pragma unroll
     for (int q = 0; q < kWPT; ++q) f.bword[q] = 0u;
     f.hflags = 0u; f.nrep = 0u;
@@ -348,7 +353,7 @@ __device__ __forceinline__ void pen_prefetch_list(const SliceArgs& a, const PenC
     const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
 #pragma unroll
     for (int j = 0; j < kPL; ++j) {
-        const uint32_t i = uint32_t(j) * kT + threadIdx.x;
+        const uint32_t i = uint32_t(j) * kT + uint32_t(opaque_tid());
         f.le[j] = i < nrep ? list[i] : make_uint2(0u, 0u);
     }
 }
@@ -361,7 +366,7 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t off) { return (off * 0x9E
 template <int DT>
 __device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, const Geo& g, const PenPrefetch& f,
                           unsigned char* lds, Shared& sh, uint32_t* dense) {
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
     uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
     uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
     const int nw = (g.n + 31) >> 5;
@@ -430,7 +435,19 @@ __device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, c
 #pragma unroll
         for (int j = 0; j < kPHist; ++j)
             if (int64_t(j) * kT + tid < c.hn) rec(f.ht[j]);
-        for (int64_t i = int64_t(kPHist) * kT + tid; i < c.hn; i += kT) rec(c.hist[i]);
+        // the rest in rounds of kHB tokens per thread, all requested before any is used
+        constexpr int kHB = 8;
+        for (int64_t i0 = int64_t(kPHist) * kT; i0 < c.hn; i0 += int64_t(kHB) * kT) {
+            int32_t t8[kHB];
+#pragma unroll
+            for (int u = 0; u < kHB; ++u) {
+                const int64_t i = i0 + int64_t(u) * kT + tid;
+                t8[u] = i < c.hn ? c.hist[i] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < kHB; ++u)
+                if (i0 + int64_t(u) * kT + tid < c.hn) rec(t8[u]);
+        }
     }
     lds_barrier();
     if (sh.overflow) {   // (uniform) full counts of the slice's tokens in its dense table
@@ -544,34 +561,34 @@ constexpr int kOffPC = kOffGather + kSlotsAll * kGatherBytes;   // [kMaxSlices] 
 static_assert(kOffPC + 4 * 2 * kMaxSlices <= 4 * kSL, "merge map");
 
 struct Slot {
-    uint32_t* E;    // [kMaxSlices][256] list entries of the bin, per slice
-    uint32_t* FK;   // [256] logits per key of the bin (all slices)
+    uint32_t* E;    // [kMaxSlices][kBinKeys] list entries of the bin, per slice
+    uint32_t* FK;   // [kBinKeys] logits per key of the bin (all slices)
     uint32_t* NE;   // [kMaxSlices] entries per slice
 };
 __device__ __forceinline__ Slot slot_at(unsigned char* lds, int i) {
     unsigned char* b = lds + kOffGather + i * kGatherBytes;
     Slot s;
     s.E = reinterpret_cast<uint32_t*>(b);
-    s.FK = s.E + kMaxSlices * 256;
-    s.NE = s.FK + 256;
+    s.FK = s.E + kMaxSlices * kBinKeys;
+    s.NE = s.FK + kBinKeys;
     return s;
 }
 
 // All threads: the list entries of bin b of every slice of `row`.
 __device__ __forceinline__ void gather_bin(const SliceArgs& a, int row, int b, const Slot& sl, const uint32_t* MFE) {
     const int tid = threadIdx.x, S = a.slices;
-    if (tid < 256) sl.FK[tid] = 0u;
+    if (tid < kBinKeys) sl.FK[tid] = 0u;
     __syncthreads();
     const uint32_t k0 = bin_first_key(b);
-    for (int idx = tid; idx < S * 256; idx += kT) {
-        const int s = idx >> 8, j = idx & 255;
-        const uint32_t fe = MFE[s * kBP + b], ne = fe >> 16, f0 = fe & 0xffffu;
+    for (int idx = tid; idx < S * kBinKeys; idx += kT) {
+        const int s = idx / kBinKeys, j = idx % kBinKeys;
+        const uint32_t fe = MFE[s * kBins + b], ne = fe >> 16, f0 = fe & 0xffffu;
         if (j == 0) sl.NE[s] = ne;
         if (uint32_t(j) < ne) {
-            const uint32_t e = get_agent(&a.lists[(size_t(row) * S + s) * kSL + f0 + j]);
-            sl.E[s * 256 + j] = e;
-            const uint32_t kj = (e >> 16) - k0;   // (< 256 for every entry of bin b)
-            if (kj < 256u) atomicAdd(&sl.FK[kj], e & 0xffffu);
+            const uint32_t e = a.lists[(size_t(row) * S + s) * kSL + f0 + j];
+            sl.E[s * kBinKeys + j] = e;
+            const uint32_t kj = (e >> 16) - k0;   // (< kBinKeys for every entry of bin b)
+            if (kj < uint32_t(kBinKeys)) atomicAdd(&sl.FK[kj], e & 0xffffu);
         }
     }
     __syncthreads();
@@ -585,7 +602,8 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
 }
 
 // Wave 0 helpers over the coarse bins, in descending order: lane l holds bins
-// 256 - 5l - i (i = 0..4).
+// kBins - 1 - kCPL l - i (i < kCPL).
+constexpr int kCPL = kBins / kWave;
 struct CoarseHit {
     int bin;
     double mass_before;
@@ -596,12 +614,12 @@ struct CoarseHit {
 // bin -1 when none is.
 __device__ __forceinline__ CoarseHit coarse_find(const double* MR, const uint32_t* MC, int lo, int mode, double target) {
     const int lane = lane_id();
-    double vm[5], tm = 0.0;
-    uint32_t vc[5], tc = 0u;
+    double vm[kCPL], tm = 0.0;
+    uint32_t vc[kCPL], tc = 0u;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const int b = 256 - 5 * lane - i;
-        const bool ok = b >= lo && b >= 0;
+    for (int i = 0; i < kCPL; ++i) {
+        const int b = kBins - 1 - kCPL * lane - i;
+        const bool ok = b >= lo;
         vm[i] = ok ? MR[b] : 0.0;
         vc[i] = ok ? MC[b] : 0u;
         tm += vm[i];
@@ -613,7 +631,7 @@ __device__ __forceinline__ CoarseHit coarse_find(const double* MR, const uint32_
     double fm = 0.0;
     uint32_t fc = 0u;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < kCPL; ++i) {
         const double nm = cm + vm[i];
         const uint32_t nc = cc + vc[i];
         const bool hit = mode == 0 ? double(nc) >= target : (mode == 1 ? nm >= target : nm > target);
@@ -624,7 +642,7 @@ __device__ __forceinline__ CoarseHit coarse_find(const double* MR, const uint32_
     const uint64_t m = ballot(fi >= 0);
     if (!m) return CoarseHit{-1, 0.0, 0u};
     const int L = __builtin_ctzll(m);
-    return CoarseHit{256 - 5 * L - readlane_i(fi, L), readlane_d(fm, L), uint32_t(readlane_i(int(fc), L))};
+    return CoarseHit{kBins - 1 - kCPL * L - readlane_i(fi, L), readlane_d(fm, L), uint32_t(readlane_i(int(fc), L))};
 }
 // Mass and count of the bins above bin b.
 __device__ __forceinline__ void coarse_above(const double* MR, const uint32_t* MC, int b, double* m, uint32_t* c) {
@@ -636,6 +654,7 @@ __device__ __forceinline__ void coarse_above(const double* MR, const uint32_t* M
     *c = wave_sum_u32(tc);
 }
 
+constexpr int kKPL = kBinKeys / kWave;   // keys per lane in fine_find
 struct FineHit {
     bool found;
     uint32_t key, rank;
@@ -645,7 +664,7 @@ struct FineHit {
     uint32_t total_cnt;
     uint32_t last_key, last_cnt;   // the lowest key with logits (limited)
 };
-// Wave 0.  The keys of bin b in descending order (lane l: 255 - 4l - i), with
+// Wave 0.  The keys of bin b in descending order (lane l: kBinKeys - 1 - kKPL l - i), with
 // counts limited to the position (lim_key, lim_take): keys below lim_key count
 // none, lim_key at most lim_take.  Finds the first element (key, rank) at which
 // the cumulative count (mode 0: >= target) or mass (mode 1: >= target, mode 2:
@@ -654,14 +673,14 @@ template <int DT>
 __device__ __forceinline__ FineHit fine_find(const uint32_t* FK, int b, int mode, double target, uint32_t lim_key, uint32_t lim_take,
                              double zmax, float inv_t) {
     const int lane = lane_id();
-    const int k0 = b * 256 - 128;
-    uint32_t c[4];
-    double w[4], tm = 0.0;
+    const int k0 = int(bin_first_key(b));
+    uint32_t c[kKPL];
+    double w[kKPL], tm = 0.0;
     uint32_t tc = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = 255 - 4 * lane - i, key = k0 + j;
-        uint32_t cc = (key >= 0 && key <= 0xffff) ? FK[j] : 0u;
+    for (int i = 0; i < kKPL; ++i) {
+        const int j = kBinKeys - 1 - kKPL * lane - i, key = k0 + j;
+        uint32_t cc = FK[j];
         if (uint32_t(key) < lim_key) cc = 0u;
         else if (uint32_t(key) == lim_key) cc = min(cc, lim_take);
         c[i] = cc;
@@ -678,7 +697,7 @@ __device__ __forceinline__ FineHit fine_find(const uint32_t* FK, int b, int mode
     double fm = 0.0;
     uint32_t fc = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kKPL; ++i) {
         const double nm = cm + double(c[i]) * w[i];
         const uint32_t nc = cc + c[i];
         if (c[i]) li = i;
@@ -716,12 +735,11 @@ __device__ __forceinline__ FineHit fine_find(const uint32_t* FK, int b, int mode
     if (lm) {
         const int L = 63 - __builtin_clzll(lm);
         const int i = readlane_i(li, L);
-        h.last_key = uint32_t(k0 + 255 - 4 * L - i);
-        h.last_cnt = uint32_t(readlane_i(int(c[0]), L));
+        h.last_key = uint32_t(k0 + kBinKeys - 1 - kKPL * L - i);
         // (c[] indexed by a lane-uniform i: pick it per lane first)
         uint32_t mine = 0u;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) if (q == li) mine = c[q];
+        for (int q = 0; q < kKPL; ++q) if (q == li) mine = c[q];
         h.last_cnt = uint32_t(readlane_i(int(mine), L));
     }
     const uint64_t m = ballot(fi >= 0);
@@ -729,7 +747,7 @@ __device__ __forceinline__ FineHit fine_find(const uint32_t* FK, int b, int mode
         const int L = __builtin_ctzll(m);
         const int i = readlane_i(fi, L);
         h.found = true;
-        h.key = uint32_t(k0 + 255 - 4 * L - i);
+        h.key = uint32_t(k0 + kBinKeys - 1 - kKPL * L - i);
         h.rank = uint32_t(readlane_i(int(fr), L));
         h.mass_before = readlane_d(fm, L);
         h.cnt_before = uint32_t(readlane_i(int(fc), L));
@@ -752,10 +770,9 @@ __device__ __forceinline__ void write_row(const SliceArgs& a, int row, int32_t t
     }
 }
 
-// The row's decisions and its token, by the last slice to arrive.
-// (a call: once per row, and its registers stay out of the slice loop's budget)
+// The row's decisions and its token (sh.kmin set).
 template <int DT>
-__device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row_params& p, float inv_t, unsigned char* lds,
+__device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_row_params& p, float inv_t, unsigned char* lds,
                           Shared& sh) {
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave, S = a.slices, V = a.vocabulary;
     uint32_t* MFE = reinterpret_cast<uint32_t*>(lds + kOffMFE);
@@ -764,48 +781,55 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
     uint32_t* PC = reinterpret_cast<uint32_t*>(lds + kOffPC);   // [kMaxSlices] drawn key, [kMaxSlices] end key
     const size_t rs = size_t(row) * S;
 
-    // ---- 0. slice heads and bin tables, one round trip
-    uint32_t h4[4] = {0u, 0u, 0u, 0u};
+    // ---- 0. slice heads (totals and occupied-bin masks), then the occupied bins'
+    // records; each bin summed over the slices in slice order (deterministic)
+    uint32_t* MM = reinterpret_cast<uint32_t*>(lds + kOffMM);   // [S][kBins / 32] occupied-bin masks
+    constexpr int kMW = kBins / 32;
+    if (tid < S * kMW) MM[tid] = a.heads[(rs + tid / kMW) * kHeadWords + 4 + tid % kMW];
+    uint32_t h3[3] = {0u, 0u, 0u};
     if (tid < S) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) h4[q] = get_agent(&a.heads[(rs + tid) * 4 + q]);
+        for (int q = 0; q < 3; ++q) h3[q] = a.heads[(rs + tid) * kHeadWords + 1 + q];
     }
-    constexpr int kPer = (kMaxSlices * kBP + kT - 1) / kT;
-    uint32_t lfe[kPer], lcnt[kPer], lref[kPer];
-    double lmass[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int idx = u * kT + tid;
-        const bool ok = idx < S * kBP;
-        lfe[u] = ok ? get_agent(&a.bfe[rs * kBP + idx]) : 0u;
-        lcnt[u] = ok ? get_agent(&a.bcnt[rs * kBP + idx]) : 0u;
-        lref[u] = ok ? get_agent(&a.bref[rs * kBP + idx]) : 0u;
-        lmass[u] = ok ? get_agent(&a.bmass[rs * kBP + idx]) : 0.0;
-    }
-    double* MRS = reinterpret_cast<double*>(lds + kOffGather);   // [S][kBP] rescaled slice masses (then gathers)
-    if (tid < kBP) MC[tid] = 0u;
     if (tid < kGatherSlots) sh.slot_bin[tid] = -1;
     if (tid == 0) { sh.row_flags = 0u; sh.row_valid = 0u; sh.row_top = 0u; sh.token = -1; sh.ok = 1u; }
     __syncthreads();
-    if (tid < S) { atomicAdd(&sh.row_valid, h4[1]); atomicOr(&sh.row_flags, h4[2]); atomicMax(&sh.row_top, h4[3]); }
+    if (tid < S) { atomicAdd(&sh.row_valid, h3[0]); atomicOr(&sh.row_flags, h3[1]); atomicMax(&sh.row_top, h3[2]); }
     __syncthreads();
     const uint32_t top = sh.row_top, N = sh.row_valid;
     const double zmax = double(key_z<DT>(top, inv_t));
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int idx = u * kT + tid;
-        if (idx < S * kBP) {
-            MFE[idx] = lfe[u];
-            MRS[idx] = lcnt[u] ? lmass[u] * (1.0 / kMassScale) * exp(double(key_z<DT>(lref[u], inv_t)) - zmax) : 0.0;
-            if (lcnt[u]) atomicAdd(&MC[idx % kBP], lcnt[u]);
+    // the occupied (slice, bin) pairs in slice-major order, one record load each;
+    // the rescaled masses are summed as 2^-44 fixed point (u64 atomics: exact
+    // in any order, so the sums do not depend on the order of arrival)
+    uint32_t* OCC = reinterpret_cast<uint32_t*>(lds + kOffGather);   // (slice << 16 | bin) pairs (then gathers)
+    uint64_t* MRI = reinterpret_cast<uint64_t*>(MR);
+    for (int i = tid; i < S * kBins; i += kT) MFE[i] = 0u;
+    if (tid < kBins) { MC[tid] = 0u; MRI[tid] = 0ull; }
+    uint32_t mw = tid < S * kMW ? MM[tid] : 0u, npairs = 0u;
+    const uint32_t pbase = block_scan_lds(uint32_t(__builtin_popcount(mw)), sh.scan, &npairs);
+    {
+        uint32_t o = pbase;
+        const uint32_t s_ = uint32_t(tid / kMW), b0 = uint32_t(tid % kMW) * 32u;
+        while (mw) {
+            const int j = __builtin_ctz(mw);
+            mw &= mw - 1u;
+            OCC[o++] = (s_ << 16) | (b0 + uint32_t(j));
         }
     }
     __syncthreads();
-    if (tid < kBP) {   // each bin summed over the slices in slice order (deterministic)
-        double m = 0.0;
-        for (int q = 0; q < S; ++q) m += MRS[q * kBP + tid];
-        MR[tid] = m;
+    constexpr double kRowScale = 0x1p44;   // row masses <= V <= 2^19: sums stay below 2^63
+    for (uint32_t i = tid; i < npairs; i += kT) {
+        const uint32_t sb = OCC[i], q = sb >> 16, b = sb & 0xffffu;
+        const uint4 r = a.brec[(rs + q) * kBins + b];
+        MFE[q * kBins + b] = r.x;
+        const uint32_t cnt = r.y & 0xffffu;
+        atomicAdd(&MC[b], cnt);
+        const double ms = __builtin_bit_cast(double, (uint64_t(r.w) << 32) | r.z);
+        const double m = ms * exp(double(key_z<DT>(r.y >> 16, inv_t)) - zmax);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&MRI[b]), (unsigned long long)(rint(m * kRowScale)));
     }
+    __syncthreads();
+    if (tid < kBins) MR[tid] = double(MRI[tid]) * (1.0 / kRowScale);
     __syncthreads();
     const uint32_t out_flags = sh.row_flags & (VI_FLAG_NONFINITE | VI_FLAG_BAD_HISTORY);
     const bool fail = (sh.row_flags & VI_FLAG_ERROR) != 0u || !(p.temperature <= kMaxTemperature);
@@ -830,7 +854,7 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
     // ---- 1. totals; bins of the top-k cap and of the min-p cut
     if (wave == 0) {
         double tm = 0.0;
-        for (int b = lane; b < kBP; b += kWave) tm += MR[b];
+        for (int b = lane; b < kBins; b += kWave) tm += MR[b];
         const double s_all = wave_sum_f64(tm);
         int cap_bin = -1;
         if (p.top_k > 0 && uint32_t(p.top_k) < N) cap_bin = coarse_find(MR, MC, 0, 0, double(p.top_k)).bin;
@@ -960,20 +984,20 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
     {
         const Slot ds = slot_at(lds, draw_slot);
         const uint32_t dk = sh.draw_key;
-        for (int idx = tid; idx < S * 256; idx += kT) {
-            const int s = idx >> 8, j = idx & 255;
+        for (int idx = tid; idx < S * kBinKeys; idx += kT) {
+            const int s = idx / kBinKeys, j = idx % kBinKeys;
             if (uint32_t(j) < ds.NE[s]) {
-                const uint32_t e = ds.E[s * 256 + j];
+                const uint32_t e = ds.E[s * kBinKeys + j];
                 if ((e >> 16) == dk) PC[s] = e & 0xffffu;
             }
         }
         if (a.probs && end_slot >= 0) {
             const Slot es = slot_at(lds, end_slot);
             const uint32_t ek = sh.end_key;
-            for (int idx = tid; idx < S * 256; idx += kT) {
-                const int s = idx >> 8, j = idx & 255;
+            for (int idx = tid; idx < S * kBinKeys; idx += kT) {
+                const int s = idx / kBinKeys, j = idx % kBinKeys;
                 if (uint32_t(j) < es.NE[s]) {
-                    const uint32_t e = es.E[s * 256 + j];
+                    const uint32_t e = es.E[s * kBinKeys + j];
                     if ((e >> 16) == ek) PC[kMaxSlices + s] = e & 0xffffu;
                 }
             }
@@ -1000,12 +1024,20 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
     __syncthreads();
 
     // ---- 6. the owner slice read again: the owner_rank-th logit of the drawn
-    // key in id order (penalties applied as in the slice pass)
+    // key in id order (penalties applied as in the slice pass).  Thread t takes
+    // body vectors kNV t .. kNV t + kNV - 1, so thread order is id order: the head
+    // logits (offsets < head, threads < head), the body, the tail.
     if (sh.ok) {
         const int os = int(sh.owner_slice);
         const Geo g = geo_of(a, row, os);
-        SliceRegs r;
-        load_slice(g, r);
+        uint4 v[kNV];
+#pragma unroll
+        for (int i = 0; i < kNV; ++i) {
+            const int vi = kNV * tid + i;
+            v[i] = vi < g.nvec ? load16_cached(g.vbase + size_t(vi) * 16) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        const uint32_t hb = tid < g.head ? uint32_t(g.base16[tid]) : 0u;
+        const uint32_t tb = tid < g.tail ? uint32_t(g.base16[g.head + 8 * g.nvec + tid]) : 0u;
         const PenCtx pc = pen_ctx(a, row, p);
         uint32_t* dense = a.lists + (rs + os) * kSL;
         if (pc.pen) {
@@ -1015,38 +1047,61 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
             pen_build<DT>(a, pc, g, f, lds, sh, dense);
         }
         const uint32_t dk = sh.draw_key;
-        uint32_t mask[kSeg], cnt[kSeg], excl[kSeg];
-        mask[0] = (tid < g.head && elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(tid), r.hb) == dk) ? 1u : 0u;
+        // raw patterns of the drawn key (+0 and -0 for key 0x8000): logits that
+        // penalties leave alone match on their raw pattern
+        const uint32_t P1 = unkey16(dk), P2 = dk == 0x8000u ? 0x8000u : P1;
+        const uint32_t* Bm = reinterpret_cast<const uint32_t*>(lds + kOffB);
+        auto key_at = [&](uint32_t off, uint32_t b) { return elem_key<DT>(lds, sh, dense, p, pc.pen, off, b); };
+        uint32_t bits = 0u;
 #pragma unroll
         for (int i = 0; i < kNV; ++i) {
-            const int v = i * kT + tid;
-            uint32_t mm = 0u;
-            if (v < g.nvec) {
-#pragma unroll 1
-                for (int j = 0; j < 8; ++j)
-                    if (elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(g.head + 8 * v + j), vec_elem(r.v[i], j)) == dk)
-                        mm |= 1u << j;
+            const int vi = kNV * tid + i;
+            if (vi >= g.nvec) continue;
+            const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            uint32_t m8 = 0u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                m8 |= (b == P1 || b == P2) ? 1u << j : 0u;
             }
-            mask[1 + i] = mm;
+            if (pc.pen) {   // history tokens among the eight: their penalized keys
+                const uint32_t off = uint32_t(g.head + 8 * vi), wd = off >> 5, sft = off & 31u;
+                const uint64_t two = uint64_t(Bm[wd]) | (sft > 24u && wd + 1u < uint32_t(kSL / 32) ? uint64_t(Bm[wd + 1u]) << 32 : 0ull);
+                uint32_t hist8 = uint32_t(two >> sft) & 0xffu;
+                while (hist8) {
+                    const int j = __builtin_ctz(hist8);
+                    hist8 &= hist8 - 1u;
+                    const bool hit = key_at(off + uint32_t(j), vec_elem(v[i], j)) == dk;
+                    m8 = hit ? (m8 | (1u << j)) : (m8 & ~(1u << j));
+                }
+            }
+            bits |= m8 << (8 * i);
         }
-        mask[kSeg - 1] = (tid < g.tail && elem_key<DT>(lds, sh, dense, p, pc.pen, uint32_t(g.head + 8 * g.nvec + tid),
-                                                         r.tb) == dk) ? 1u : 0u;
-#pragma unroll
-        for (int x = 0; x < kSeg; ++x) cnt[x] = __builtin_popcount(mask[x]);
-        (void)id_order_prefix(cnt, excl, sh);
+        const bool hm = tid < g.head && key_at(uint32_t(tid), hb) == dk;
+        const bool tm = tid < g.tail && key_at(uint32_t(g.head + 8 * g.nvec + tid), tb) == dk;
+        if (wave == 0) {   // (head and tail logits belong to threads < 8)
+            const uint64_t hmask = ballot(hm), tmask = ballot(tm);
+            if (lane == 0) { sh.hmask = uint32_t(hmask); sh.tmask = uint32_t(tmask); }
+        }
+        const uint32_t nb = uint32_t(__builtin_popcount(bits));
+        uint32_t nbody = 0u;
+        const uint32_t bexcl = block_scan_lds(nb, sh.scan, &nbody);
+        auto nth_bit = [](uint32_t m, uint32_t n) {   // index of the n-th set bit (n < popcount)
+            for (; n > 0u; --n) m &= m - 1u;
+            return __builtin_ctz(m);
+        };
+        const uint32_t hmask = sh.hmask, tmask = sh.tmask, nh = uint32_t(__builtin_popcount(hmask));
         const uint32_t want = sh.owner_rank;
-#pragma unroll
-        for (int x = 0; x < kSeg; ++x) {
-            if (want >= excl[x] && want < excl[x] + cnt[x]) {
-                uint32_t mm = mask[x];
-                for (uint32_t q = want - excl[x]; q > 0u; --q) mm &= mm - 1u;
-                const int j = __builtin_ctz(mm);
-                int off;
-                if (x == 0) off = tid;
-                else if (x == kSeg - 1) off = g.head + 8 * g.nvec + tid;
-                else off = g.head + 8 * ((x - 1) * kT + tid) + j;
-                sh.token = g.s0 + off;
+        if (want < nh) {
+            if (tid == nth_bit(hmask, want)) sh.token = g.s0 + tid;
+        } else if (want - nh < nbody) {
+            const uint32_t r = want - nh;
+            if (r >= bexcl && r < bexcl + nb) {
+                const int j = nth_bit(bits, r - bexcl);
+                sh.token = g.s0 + g.head + 8 * (kNV * tid + j / 8) + j % 8;
             }
+        } else if (want - nh - nbody < uint32_t(__builtin_popcount(tmask))) {
+            if (tid == nth_bit(tmask, want - nh - nbody)) sh.token = g.s0 + g.head + 8 * g.nvec + tid;
         }
         __syncthreads();
     }
@@ -1056,7 +1111,7 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
             write_row(a, row, -1, sh.u, out_flags | VI_FLAG_ERROR, 0u, 0u, 0.0);
         } else {
             write_row(a, row, tok, sh.u, out_flags, sh.n_support, N, sh.s_n);
-            if (a.record && tok < V) {   // every slice of this row has finished reading the state
+            if (a.record && tok < V) {   // (the slice pass, an earlier launch, has read the state)
                 const LaneState ls = lane_state(a.pstate + size_t(row) * a.pl.lane_bytes, a.pl);
                 state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
             }
@@ -1068,77 +1123,89 @@ __device__ __noinline__ void merge_row(const SliceArgs& a, int row, const vi_row
     __syncthreads();
 }
 
-// ------------------------------------------------------------------ kernel
+// ------------------------------------------------------------------ kernels
+// Smallest and largest valid keys (finite pattern, finite z) at a temperature,
+// kmin | kmax << 16 (1 | 0 << 16: none); one wave.
+template <int DT>
+__device__ __forceinline__ uint32_t valid_key_range(float temperature) {
+    constexpr int kPosMax = DT == VI_BF16 ? 0xff7f : 0xfbff;   // largest finite key
+    constexpr int kNegMin = DT == VI_BF16 ? 0x0080 : 0x0400;   // smallest finite key
+    const float inv_t = 1.0f / temperature;
+    if (!(temperature <= kMaxTemperature) || !isfinite(inv_t)) return 1u;
+    const int kbad = wave_search(0x8000, kPosMax + 1, [&](int key) { return !isfinite(key_z<DT>(uint32_t(key), inv_t)); });
+    const int kgood = wave_search(kNegMin, 0x8000, [&](int key) { return isfinite(key_z<DT>(uint32_t(key), inv_t)); });
+    return uint32_t(kgood) | (uint32_t(kbad - 1) << 16);
+}
+
 template <int DT>
 __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
     __shared__ Shared sh;
     uint32_t* H = reinterpret_cast<uint32_t*>(lds + kOffH);
-    uint32_t* O = reinterpret_cast<uint32_t*>(lds + kOffO);
+    uint4* H4 = reinterpret_cast<uint4*>(lds + kOffH);
+    uint2* H2 = reinterpret_cast<uint2*>(lds + kOffH);
     uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
-    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave, w = blockIdx.x;
+    const int w = blockIdx.x;
     const int S = a.slices;
 
     int row = 0, s = 0;
     if (!item_of(a, w, 0, &row, &s)) return;
-    // the histogram and occupancy start empty (every slice leaves them so)
-    for (int i = tid; i < kSL; i += kT) H[i] = 0u;
+    // the histogram and the slice head's counters start empty (every slice leaves
+    // them so)
 #pragma unroll
-    for (int q = 0; q < kWPT; ++q) O[q * kT + tid] = 0u;
-    Geo g = geo_of(a, row, s);
-    vi_row_params p = a.params[row];
+    for (int q = 0; q < kSL / 4 / kT; ++q) H4[q * kT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x < kBins / 32) sh.bmask[threadIdx.x] = 0u;
+    if (threadIdx.x == 0) { sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u; }
     SliceRegs cur{};
     PenPrefetch pf{};
-    PenCtx pc{};
-    if (full_route_row(p)) {
-        load_slice(g, cur);
-        pc = pen_ctx(a, row, p);
-        pen_prefetch_head(a, pc, g, pf);
-        pen_prefetch_list(a, pc, pf);
+    {
+        const vi_row_params p0 = a.params[row];
+        if (full_route_row(p0)) {
+            const Geo g0 = geo_of(a, row, s);
+            const PenCtx pc0 = pen_ctx(a, row, p0);
+            load_slice(g0, cur);
+            pen_prefetch_head(a, pc0, g0, pf);
+            pen_prefetch_list(a, pc0, pf);
+        }
     }
+    lds_barrier();
 
     // One slice per iteration.  `cur` / `pf` hold its logits and penalty inputs,
     // requested during the previous iteration: the next slice's logits are loaded
     // into `cur` as soon as this slice's histogram has consumed it, and land
-    // while the penalties, the compaction and the publication run.
-    // The previous slice's arrival: after its publication stores are
-    // acknowledged (every thread's), one atomic on the row's counter; the last
-    // slice of the row to arrive merges it.
-    bool pend = false;
-    int prow = 0;
-    vi_row_params pp{};
-    auto arrive = [&]() {
-        handoff_stores_done();
-        lds_barrier();
-        if (tid == 0) {
-            const uint32_t old = atomicAdd(&a.arrivals[prow], 1u);
-            sh.last = old == uint32_t(S - 1) ? 1u : 0u;
-            if (sh.last) put_agent(&a.arrivals[prow], 0u);
-        }
-        lds_barrier();
-        if (sh.last) {
-            handoff_acquire();
-            merge_row<DT>(a, prow, pp, 1.0f / pp.temperature, lds, sh);
-            // (the merge used the histogram's space: empty it again)
-            constexpr int kZ = kSL / kT / 4;
-#pragma unroll
-            for (int q = 0; q < kZ; ++q) reinterpret_cast<uint4*>(H)[tid * kZ + q] = make_uint4(0u, 0u, 0u, 0u);
-            lds_barrier();
-        }
-        pend = false;
-    };
+    // while the penalties, the compaction and the publication run.  Barriers
+    // order LDS only, so nothing but the loop's first wait waits for them.
+    // (Only the item indices are carried between iterations: parameters and
+    // geometry are reloaded from the constant cache where they are used.)
     for (int k = 0;; ++k) {
-        // this slice's loads have landed (waited for here, before anything else is
-        // requested: later waits then never include the next slice's loads), and
-        // with them the previous slice's publication stores
+        // this slice's loads have landed (and the previous slice's stores)
         __builtin_amdgcn_s_waitcnt(0x0f70);
-        if (pend) arrive();
+        const int tid = opaque_tid();
+        if (k % kW == 0) {   // the valid key ranges of this item and the next kW - 1, a wave each
+            int r2 = 0, s2 = 0;
+            if (item_of(a, w, k + tid / kWave, &r2, &s2)) {
+                const uint32_t km = valid_key_range<DT>(a.params[r2].temperature);
+                if ((tid & (kWave - 1)) == 0) sh.krange[tid / kWave] = km;
+            }
+        }
+        const int lane = tid & (kWave - 1), wave = tid / kWave;
         int nrow = 0, ns = 0;
         const bool has_next = item_of(a, w, k + 1, &nrow, &ns);
-        const vi_row_params np = has_next ? a.params[nrow] : vi_row_params{};
-        const bool next_full = has_next && full_route_row(np);
+        const vi_row_params p = a.params[row];
+        const Geo g = geo_of(a, row, s);
+        const PenCtx pc = pen_ctx(a, row, p);
         const bool full = full_route_row(p);
         const float inv_t = 1.0f / p.temperature;
+        // the next slice's penalty inputs, then its logits (into the registers this
+        // slice's logits occupied)
+        auto prefetch_next = [&]() {
+            if (!has_next) return;
+            const vi_row_params np = a.params[nrow];
+            if (!full_route_row(np)) return;
+            const Geo ng = geo_of(a, nrow, ns);
+            pen_prefetch_head(a, pen_ctx(a, nrow, np), ng, pf);
+            load_slice(ng, cur);
+        };
         uint32_t* dense = a.lists + (size_t(row) * S + s) * kSL;
         constexpr int kG = kStage / kT;   // history tokens gathered per thread and round
         uint32_t graw[kG], goff[kG];
@@ -1148,21 +1215,7 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
         uint16_t* F = reinterpret_cast<uint16_t*>(lds + kOffF);
 
         if (full) {
-            if (tid == 0) { sh.flags = 0u; sh.top_key = 0u; sh.n_valid = 0u; sh.n_neg = 0u; }
-            // valid keys: finite pattern and finite z
-            if (wave == 0) {
-                constexpr int kPosMax = DT == VI_BF16 ? 0xff7f : 0xfbff;   // largest finite key
-                constexpr int kNegMin = DT == VI_BF16 ? 0x0080 : 0x0400;   // smallest finite key
-                const bool t_ok = p.temperature <= kMaxTemperature && isfinite(inv_t);
-                const int kbad = wave_search(0x8000, kPosMax + 1,
-                                             [&](int key) { return !isfinite(key_z<DT>(uint32_t(key), inv_t)); });
-                const int kgood = wave_search(kNegMin, 0x8000,
-                                              [&](int key) { return isfinite(key_z<DT>(uint32_t(key), inv_t)); });
-                if (lane == 0) {
-                    sh.kmax = t_ok ? uint32_t(kbad - 1) : 0u;
-                    sh.kmin = t_ok ? uint32_t(kgood) : 1u;
-                }
-            }
+            if (tid == 0) sh.flags = 0u;
             // ---- 1. penalties; the first round of history tokens staged and
             // their raw logits requested (before the next slice's loads)
             if (pc.pen) {
@@ -1192,53 +1245,23 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                 }
             }
         }
-        Geo ng{};
-        PenCtx npc{};
-        if (next_full) {
-            ng = geo_of(a, nrow, ns);
-            npc = pen_ctx(a, nrow, np);
-        }
-
         if (full) {
-            // ---- 2. raw-pattern histogram of the slice
-            auto hist_add = [&](uint32_t b) {
-                const uint32_t idx = b & 0x7fffu, inc = (b & 0x8000u) ? 0x10000u : 1u;
-                const uint32_t old = atomicAdd(&H[idx], inc);
-                if (old == 0u) atomicOr(&O[idx >> 5], 1u << (idx & 31));
-            };
-            // the eight counts of a vector are added before any result is looked at
-            // (a wave's LDS operations complete in order: one wait per vector)
-            auto hist_add8 = [&](const uint4& v, bool ok) {
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-                uint32_t idx[8], old[8];
+            // ---- 2. raw-pattern histogram of the slice (no returned values: the
+            // adds stream through the LDS).  Vectors past the slice's end are skipped
+            // by a branch that is uniform in all waves but one (masked adds of 0
+            // would all hit one word and serialize).
+            auto hist_add = [&](uint32_t b) { atomicAdd(&H[b & 0x7fffu], (b & 0x8000u) ? 0x10000u : 1u); };
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    // (unconditional: a masked lane adds 0; a conditional atomic would be
-                    // a branch with its own wait)
-                    const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                    idx[j] = b & 0x7fffu;
-                    old[j] = atomicAdd(&H[idx[j]], ok ? ((b & 0x8000u) ? 0x10000u : 1u) : 0u);
+            for (int i = 0; i < kNV; ++i) {
+                if (i * kT + tid < g.nvec) {
+                    const uint32_t w4[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
                 }
-                uint32_t first = 0u;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) first |= (old[j] == 0u ? 1u : 0u) << j;
-                first = ok ? first : 0u;
-                if (first) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if ((first >> j) & 1u) atomicOr(&O[idx[j] >> 5], 1u << (idx[j] & 31));
-                }
-            };
-#pragma unroll
-            for (int i = 0; i < kNV; ++i) hist_add8(cur.v[i], i * kT + tid < g.nvec);
+            }
             if (tid < g.head) hist_add(cur.hb);
             if (tid < g.tail) hist_add(cur.tb);
-            // ---- the next slice: its penalty inputs, then its logits (into the
-            // registers this slice's logits occupied)
-            if (next_full) {
-                pen_prefetch_head(a, npc, ng, pf);
-                load_slice(ng, cur);
-            }
+            prefetch_next();
 
             // ---- 3. history tokens move from their raw pattern to the penalized one
             if (pc.pen) {
@@ -1282,217 +1305,171 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             }
             lds_barrier();
 
-            // ---- 4. compaction: key-sorted list and coarse bin tables
-            uint32_t* bent = reinterpret_cast<uint32_t*>(lds + kOffX);     // entries per bin
-            uint32_t* bcnt = bent + kBP;                                   // valid logits per bin
-            uint32_t* bref = bcnt + kBP;                                   // largest valid key per bin
-            uint32_t* bfirst = bref + kBP;                                 // first list index per bin
-            double* bmass = reinterpret_cast<double*>(bfirst + kBP);       // mass per bin (8-byte aligned)
-            if (tid < kBP) { bent[tid] = 0u; bcnt[tid] = 0u; bref[tid] = 0u; bmass[tid] = 0.0; }
-            lds_barrier();
-            const uint32_t kmin = sh.kmin, kmax = sh.kmax;
-            // (a) occupied histogram words in ascending order, staged kStage at a time
-            // in C (u16); each thread then takes kPer consecutive staged words, so the
-            // list positions follow from one block scan and the work is balanced
-            uint16_t* C = reinterpret_cast<uint16_t*>(lds + kOffF);
-            uint32_t occ[kWPT], npc = 0u;
-#pragma unroll
-            for (int q = 0; q < kWPT; ++q) { occ[q] = O[tid * kWPT + q]; npc += __builtin_popcount(occ[q]); }
-            uint32_t M;
-            const uint32_t obase = block_scan_lds(npc, sh.scan, &M);
-            auto stage_words = [&](uint32_t c0) {
-                if (obase >= c0 + kStage || obase + npc <= c0) return;
-                uint32_t r = obase;
-#pragma unroll
-                for (int q = 0; q < kWPT; ++q) {
-                    uint32_t bits = occ[q];
-                    while (bits) {
-                        const int j = __builtin_ctz(bits);
-                        bits &= bits - 1u;
-                        if (r >= c0 && r < c0 + kStage) C[r - c0] = uint16_t((tid * kWPT + q) * 32 + j);
-                        ++r;
-                    }
-                }
+            // ---- 4. compaction, one pass over the histogram.  Thread t takes the
+            // words of patterns d = 2 (q kT + t) + j (q < kQ, j < 2): a wave's 128
+            // patterns of round q are the block m = q kW + wave, which fills exactly
+            // one coarse bin of each sign (bins of 128 keys, bin = key >> 7):
+            // positive keys 0x8000 | d in bin 256 + m, negative keys 0x7fff - d in
+            // bin 255 - m.  A block's entries take one region of the slice's list,
+            // [positive][negative], each bin's entries in ascending key order.  Bin
+            // masses are sums of count * exp(z - z(bin's largest key)), one wave's
+            // reduction in a fixed order; the weights only locate bins (the merge
+            // resolves inside a bin in double precision): single precision,
+            // |error| <= 1e-7 of the bin's largest weight.
+            const uint32_t km = sh.krange[k % kW], kmin = km & 0xffffu, kmax = km >> 16;
+            // the two words of round q, -0 merged into +0 (both z = 0)
+            auto words = [&](int q) {
+                uint2 v = H2[q * kT + tid];
+                if (q == 0 && tid == 0) v.x = (v.x & 0xffffu) + (v.x >> 16);
+                return v;
             };
-            constexpr int kPer = kStage / kT;   // staged words per thread
-            uint32_t wd[kPer], wv[kPer];        // a thread's staged words and their two counts
-            auto load_staged = [&](uint32_t m) {
-#pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    const uint32_t e = uint32_t(tid * kPer + u);
-                    wd[u] = e < m ? uint32_t(C[e]) : 0u;
-                }
-#pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    const uint32_t e = uint32_t(tid * kPer + u);
-                    uint32_t v = e < m ? H[wd[u]] : 0u;
-                    if (wd[u] == 0u && e < m) v = (v & 0xffffu) + (v >> 16);   // -0 joins +0 (both z = 0)
-                    wv[u] = v;
-                }
+            // weight of `cnt` logits of `key` in a bin whose largest logit is xr
+            auto weight = [&](uint32_t key, float xr, uint32_t cnt) {
+                // (x - x_ref) / T: the difference of two logits is exact when within a
+                // factor 2 (Sterbenz) and within half an ulp otherwise; (finite inv_t:
+                // the product is finite or -inf, never NaN)
+                const float x = Elem<DT>::decode(unkey16(key));
+                return float(cnt) * __builtin_amdgcn_exp2f(((x - xr) * inv_t) * 1.44269504088896340736f);
             };
-            // the positive pattern d has key 0x8000 | d; the negative one 0x7fff - d
-            auto pos_ok = [&](uint32_t d, uint32_t v) { return (v & 0xffffu) && (0x8000u | d) >= kmin && (0x8000u | d) <= kmax; };
-            auto neg_ok = [&](uint32_t d, uint32_t v) { return (v >> 16) && (0x7fffu - d) >= kmin && (0x7fffu - d) <= kmax; };
-            // (b) per bin: entries, valid logits, largest valid key; runs of one bin
-            // are flushed with one atomic each
-            uint32_t nn_all = 0u, nv_all = 0u, top = 0u;
+            uint32_t* list = a.lists + (size_t(row) * S + s) * kSL;
+            uint4* rec = a.brec + (size_t(row) * S + s) * kBins;
             bool invalid = false;
-            for (uint32_t c0 = 0u; c0 < M; c0 += kStage) {
-                stage_words(c0);
-                lds_barrier();
-                load_staged(min(uint32_t(kStage), M - c0));
-                int pb = -1, nb = -1;
-                uint32_t pe = 0u, pc = 0u, pk = 0u, ne = 0u, nc = 0u, nk = 0u;
-                auto flush = [&](int b, uint32_t& e, uint32_t& c, uint32_t& k) {
-                    if (b >= 0 && e) { atomicAdd(&bent[b], e); atomicAdd(&bcnt[b], c); atomicMax(&bref[b], k); }
-                    e = 0u; c = 0u; k = 0u;
-                };
+            // the wave's non-empty rounds (wave-uniform bits), from reads issued back to
+            // back; then one iteration per non-empty round
+            uint32_t rounds = 0u;
 #pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    const uint32_t d = wd[u], v = wv[u];
-                    if (v & 0xffffu) {
-                        if (pos_ok(d, v)) {
-                            const uint32_t key = 0x8000u | d;
-                            const int b = bin_of(key);
-                            if (b != pb) { flush(pb, pe, pc, pk); pb = b; }
-                            ++pe; pc += v & 0xffffu; pk = max(pk, key);
-                            nv_all += v & 0xffffu; top = max(top, key);
-                        } else {
-                            invalid = true;
-                        }
+            for (int q = 0; q < kQ; ++q) {
+                const uint2 v = H2[q * kT + tid];
+                rounds |= ballot((v.x | v.y) != 0u) ? 1u << q : 0u;
+            }
+            rounds = uint32_t(__builtin_amdgcn_readfirstlane(int(rounds)));
+#pragma unroll 1
+            while (rounds) {
+                const int q = __builtin_ctz(rounds);
+                rounds &= rounds - 1u;
+                const uint2 v = words(q);
+                if ((v.x | v.y) != 0u) H2[q * kT + tid] = make_uint2(0u, 0u);   // empty again for the next slice
+                const int m = q * kW + wave;
+                const uint32_t d0 = uint32_t(2 * (q * kT + tid));
+                // valid entries: bit j of pm / nm for the positive / negative pattern of
+                // d0 + j; a block whose keys all lie in [kmin, kmax] (wave-uniform test)
+                // needs no per-word key test
+                const uint32_t w2[2] = {v.x, v.y};
+                uint32_t pm = 0u, nm = 0u;
+                const uint32_t dl = uint32_t(m) * 128u + 127u;   // the block's largest d
+                if ((0x8000u | dl) <= kmax && 0x7fffu - dl >= kmin) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        pm |= (w2[j] & 0xffffu) ? 1u << j : 0u;
+                        nm |= (w2[j] >> 16) ? 1u << j : 0u;
                     }
-                    if (v >> 16) {
-                        if (neg_ok(d, v)) {
-                            const uint32_t key = 0x7fffu - d;
-                            const int b = bin_of(key);
-                            if (b != nb) { flush(nb, ne, nc, nk); nb = b; }
-                            ++ne; nc += v >> 16; nk = max(nk, key);
-                            ++nn_all; nv_all += v >> 16; top = max(top, key);
-                        } else {
-                            invalid = true;
-                        }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t d = d0 + uint32_t(j), cp = w2[j] & 0xffffu, cn = w2[j] >> 16;
+                        const uint32_t kp = 0x8000u | d, kn = 0x7fffu - d;
+                        const bool vp = kp >= kmin && kp <= kmax, vn = kn >= kmin && kn <= kmax;
+                        pm |= (cp && vp) ? 1u << j : 0u;
+                        nm |= (cn && vn) ? 1u << j : 0u;
+                        invalid |= (cp && !vp) || (cn && !vn);
                     }
                 }
-                flush(pb, pe, pc, pk);
-                flush(nb, ne, nc, nk);
-                lds_barrier();
+                const uint32_t ne = uint32_t(__builtin_popcount(pm)) | (uint32_t(__builtin_popcount(nm)) << 16);
+                const uint32_t ie = wave_incl_scan_u32(ne);
+                const uint32_t e63 = uint32_t(readlane_i(int(ie), kWave - 1));
+                if (e63 == 0u) continue;   // (wave-uniform) nothing valid in the block
+                const uint32_t NP = e63 & 0xffffu, NB = e63 >> 16;
+                uint32_t base = 0u;
+                if (lane == 0) base = atomicAdd(&sh.n_list, NP + NB);
+                // valid logits per sign (packed halves add without carry: a slice has at
+                // most 32,768 logits) and the bins' largest valid keys
+                const uint32_t vc = ((pm & 1u) ? (v.x & 0xffffu) : 0u) + ((pm & 2u) ? (v.y & 0xffffu) : 0u) +
+                                    ((nm & 1u) ? (v.x & 0xffff0000u) : 0u) + ((nm & 2u) ? (v.y & 0xffff0000u) : 0u);
+                const uint32_t c63 = wave_sum_u32(vc);
+                const uint32_t pk = pm ? 0x8000u | (d0 + ((pm & 2u) ? 1u : 0u)) : 0u;   // largest: the last j
+                const uint32_t nk = nm ? 0x7fffu - (d0 + ((nm & 1u) ? 0u : 1u)) : 0u;   // largest: the first j
+                const uint64_t bp = ballot(pk != 0u), bn = ballot(nk != 0u);
+                const uint32_t pkm = bp ? uint32_t(readlane_i(int(pk), 63 - __builtin_clzll(bp))) : 0u;
+                const uint32_t nkm = bn ? uint32_t(readlane_i(int(nk), __builtin_ctzll(bn))) : 0u;
+                base = uint32_t(__builtin_amdgcn_readfirstlane(int(base)));
+                // entries in key order, and masses
+                const uint32_t ex = ie - ne;
+                uint32_t ip = base + (ex & 0xffffu);
+                uint32_t in_ = base + NP + NB - 1u - (ex >> 16);
+                const float xp = Elem<DT>::decode(unkey16(max(pkm, 1u)));
+                const float xn = Elem<DT>::decode(unkey16(max(nkm, 1u)));
+                float mp = 0.0f, mn = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint32_t d = d0 + uint32_t(j);
+                    if ((pm >> j) & 1u) {
+                        const uint32_t kp = 0x8000u | d, cp = w2[j] & 0xffffu;
+                        list[ip++] = (kp << 16) | cp;
+                        mp += weight(kp, xp, cp);
+                    }
+                    if ((nm >> j) & 1u) {
+                        const uint32_t kn = 0x7fffu - d, cn = w2[j] >> 16;
+                        list[in_--] = (kn << 16) | cn;
+                        mn += weight(kn, xn, cn);
+                    }
+                }
+                const float sp = wave_sum_f32(mp), sn = wave_sum_f32(mn);
+                if (lane == 0) {
+                    auto put = [&](int b, uint32_t first, uint32_t n, uint32_t cnt, uint32_t ref, float ms) {
+                        const uint64_t mb = __builtin_bit_cast(uint64_t, double(ms));
+                        rec[b] = make_uint4(first | (n << 16), cnt | (ref << 16), uint32_t(mb), uint32_t(mb >> 32));
+                    };
+                    const int bp_ = 256 + m, bn_ = 255 - m;
+                    if (NP) { put(bp_, base, NP, c63 & 0xffffu, pkm, sp); atomicOr(&sh.bmask[bp_ >> 5], 1u << (bp_ & 31)); }
+                    if (NB) { put(bn_, base + NP, NB, c63 >> 16, nkm, sn); atomicOr(&sh.bmask[bn_ >> 5], 1u << (bn_ & 31)); }
+                    atomicAdd(&sh.n_valid, (c63 & 0xffffu) + (c63 >> 16));
+                    atomicMax(&sh.top_key, max(pkm, nkm));
+                }
             }
             if (ballot(invalid) && lane == 0) atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE));
-            {
-                uint32_t t2 = top;
-#pragma unroll
-                for (int o = 32; o; o >>= 1) t2 = max(t2, uint32_t(__shfl_xor(int(t2), o, kWave)));
-                const uint32_t nv = wave_sum_u32(nv_all), nn = wave_sum_u32(nn_all);
-                if (lane == 0) { atomicMax(&sh.top_key, t2); atomicAdd(&sh.n_valid, nv); atomicAdd(&sh.n_neg, nn); }
-            }
             lds_barrier();
-            if (wave == 0) {   // first list index of each bin (bins ascending = keys ascending)
-                uint32_t e[5], t = 0u;
-#pragma unroll
-                for (int i = 0; i < 5; ++i) {
-                    const int b = lane * 5 + i;
-                    e[i] = b < kBP ? bent[b] : 0u;
-                    t += e[i];
-                }
-                uint32_t x = wave_incl_scan_u32(t) - t;
-#pragma unroll
-                for (int i = 0; i < 5; ++i) {
-                    const int b = lane * 5 + i;
-                    if (b < kBP) bfirst[b] = x;
-                    x += e[i];
-                }
-                if (lane == kWave - 1) sh.n_list = x;
-            }
-            lds_barrier();
-            const uint32_t NL = sh.n_list;
-            // (c) the list in key order: the NN negative-pattern entries first (their
-            // keys fall as d rises, so they fill the list from position NN - 1 down),
-            // then the positive ones (d ascending); and the bins' fixed-point masses
-            uint32_t* list = a.lists + (size_t(row) * S + s) * kSL;
-            uint32_t pos_before = 0u, neg_before = 0u;
-            const uint32_t NN = sh.n_neg;
-            for (uint32_t c0 = 0u; c0 < M; c0 += kStage) {
-                stage_words(c0);
-                lds_barrier();
-                load_staged(min(uint32_t(kStage), M - c0));
-                uint32_t np = 0u, nn = 0u;
-#pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    np += pos_ok(wd[u], wv[u]) ? 1u : 0u;
-                    nn += neg_ok(wd[u], wv[u]) ? 1u : 0u;
-                }
-                uint32_t tot2;
-                const uint32_t pre2 = block_scan_lds(np | (nn << 16), sh.scan, &tot2);
-                uint32_t ip = NN + pos_before + (pre2 & 0xffffu);
-                uint32_t in_ = NN - 1u - (neg_before + (pre2 >> 16));
-                int pb = -1, nb = -1;
-                double pm = 0.0, nm = 0.0;
-                auto mass_of = [&](uint32_t key, uint32_t cnt, int b) {
-                    const double z = double(key_z<DT>(key, inv_t)), zr = double(key_z<DT>(bref[b], inv_t));
-                    // in units of 2^-38: integer-valued, and a bin's sum stays below 2^53
-                    // (<= 32,768 logits of weight <= 1), so the additions are exact and
-                    // their order cannot change the result
-                    return rint(double(cnt) * exp(z - zr) * kMassScale);
-                };
-#pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    const uint32_t d = wd[u], v = wv[u];
-                    if (pos_ok(d, v)) {
-                        const uint32_t key = 0x8000u | d, cnt = v & 0xffffu;
-                        const int b = bin_of(key);
-                        if (b != pb) { if (pb >= 0) atomicAdd(&bmass[pb], pm); pb = b; pm = 0.0; }
-                        pm += mass_of(key, cnt, b);
-                        put_agent(&list[ip++], (key << 16) | cnt);
-                    }
-                    if (neg_ok(d, v)) {
-                        const uint32_t key = 0x7fffu - d, cnt = v >> 16;
-                        const int b = bin_of(key);
-                        if (b != nb) { if (nb >= 0) atomicAdd(&bmass[nb], nm); nb = b; nm = 0.0; }
-                        nm += mass_of(key, cnt, b);
-                        put_agent(&list[in_--], (key << 16) | cnt);
-                    }
-                }
-                if (pb >= 0) atomicAdd(&bmass[pb], pm);
-                if (nb >= 0) atomicAdd(&bmass[nb], nm);
-                pos_before += tot2 & 0xffffu;
-                neg_before += tot2 >> 16;
-                lds_barrier();
-            }
-            // ---- publish the slice (write-through), then arrive
-            const size_t sb = (size_t(row) * S + s) * kBP;
-            if (tid < kBP) {
-                put_agent(&a.bfe[sb + tid], bfirst[tid] | (bent[tid] << 16));
-                put_agent(&a.bcnt[sb + tid], bcnt[tid]);
-                put_agent(&a.bref[sb + tid], bref[tid]);
-                put_agent(&a.bmass[sb + tid], bmass[tid]);
-            }
+            // ---- publish the slice's head (the merge is a later launch: plain
+            // stores); each word is emptied by the thread that read it
+            uint32_t* hd = a.heads + (size_t(row) * S + s) * kHeadWords;
             if (tid == 0) {
-                uint32_t* hd = a.heads + (size_t(row) * S + s) * 4;
-                put_agent(&hd[0], NL);
-                put_agent(&hd[1], sh.n_valid);
-                put_agent(&hd[2], sh.flags);
-                put_agent(&hd[3], sh.top_key);
+                hd[0] = sh.n_list;
+                hd[1] = sh.n_valid;
+                hd[2] = sh.flags;
+                hd[3] = sh.top_key;
+                sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u;
             }
-            // the histogram and occupancy back to empty for the next slice
-            constexpr int kZ = kSL / kT / 4;   // 16-byte stores per thread
-#pragma unroll
-            for (int q = 0; q < kZ; ++q) reinterpret_cast<uint4*>(H)[tid * kZ + q] = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-            for (int q = 0; q < kWPT; ++q) O[tid * kWPT + q] = 0u;
-            // (the arrival waits for these stores: it is made at the top of the next
-            // iteration, whose wait for the next slice's logits covers them)
-            pend = true;
-            prow = row;
-            pp = p;
-        } else if (next_full) {
-            pen_prefetch_head(a, npc, ng, pf);
-            load_slice(ng, cur);
+            if (tid < kBins / 32) {
+                hd[4 + tid] = sh.bmask[tid];
+                sh.bmask[tid] = 0u;
+            }
+            lds_barrier();
+        } else {
+            prefetch_next();
         }
         if (!has_next) break;
-        if (next_full) pen_prefetch_list(a, npc, pf);   // (the next slice's header has arrived)
-        row = nrow; s = ns; g = ng; p = np; pc = npc;
+        {   // (the next slice's header has arrived)
+            const vi_row_params np = a.params[nrow];
+            if (full_route_row(np)) pen_prefetch_list(a, pen_ctx(a, nrow, np), pf);
+        }
+        row = nrow; s = ns;
     }
-    if (pend) arrive();
+}
+
+// One workgroup per full-route row: the decisions and the token.
+template <int DT>
+__global__ __launch_bounds__(kT) void merge_kernel(SliceArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+    __shared__ Shared sh;
+    const int row = blockIdx.x;
+    const vi_row_params p = a.params[row];
+    if (!full_route_row(p)) return;
+    const float inv_t = 1.0f / p.temperature;
+    if (threadIdx.x / kWave == 0) {
+        const uint32_t km = valid_key_range<DT>(p.temperature);
+        if (lane_id() == 0) { sh.kmin = km & 0xffffu; sh.kmax = km >> 16; }
+    }
+    __syncthreads();
+    merge_row<DT>(a, row, p, inv_t, lds, sh);
 }
 
 // Filtered distribution of the full-route rows (test / diagnostics path): per
@@ -1604,8 +1581,8 @@ bool full_supported(int dtype, int vocabulary, int64_t stride) {
 size_t full_workspace(int rows, int vocabulary) {
     if (rows <= 0 || vocabulary <= 0) return 0;
     const size_t rs = size_t(rows) * size_t(slices_of(vocabulary));
-    return align_up(size_t(rows) * 4, 256) + align_up(rs * 16, 256) + 3 * align_up(rs * kBP * 4, 256) +
-           align_up(rs * kBP * 8, 256) + align_up(rs * kSL * 4, 256) + align_up(size_t(rows) * sizeof(RowBound), 256) +
+    return align_up(rs * kHeadWords * 4, 256) + align_up(rs * kBins * 16, 256) + align_up(rs * kSL * 4, 256) +
+           align_up(size_t(rows) * sizeof(RowBound), 256) +
            align_up(size_t(rows) * kMaxSlices * 4, 256) + 256;
 }
 
@@ -1616,12 +1593,8 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.slices = slices_of(s.vocabulary);
     const size_t rs = size_t(s.rows) * size_t(a.slices);
     Carver c(ws, ws_bytes);
-    a.arrivals = c.take<uint32_t>(size_t(s.rows));
-    a.heads = c.take<uint32_t>(rs * 4);
-    a.bfe = c.take<uint32_t>(rs * kBP);
-    a.bcnt = c.take<uint32_t>(rs * kBP);
-    a.bref = c.take<uint32_t>(rs * kBP);
-    a.bmass = c.take<double>(rs * kBP);
+    a.heads = c.take<uint32_t>(rs * kHeadWords);
+    a.brec = c.take<uint4>(rs * kBins);
     a.lists = c.take<uint32_t>(rs * kSL);
     a.bounds = c.take<RowBound>(size_t(s.rows));
     a.bases = c.take<uint32_t>(size_t(s.rows) * kMaxSlices);
@@ -1634,8 +1607,13 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     const int items = s.rows * a.slices;
     a.grid = std::min(device_cus(), items);
     a.xcd_aware = (s.rows >= 8 && a.grid % 8 == 0) ? 1 : 0;
-    if (s.dtype == VI_BF16) hipLaunchKernelGGL(slice_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);
-    else hipLaunchKernelGGL(slice_kernel<VI_F16>, dim3(a.grid), dim3(kT), 0, stream, a);
+    if (s.dtype == VI_BF16) {
+        hipLaunchKernelGGL(slice_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);
+        hipLaunchKernelGGL(merge_kernel<VI_BF16>, dim3(s.rows), dim3(kT), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(slice_kernel<VI_F16>, dim3(a.grid), dim3(kT), 0, stream, a);
+        hipLaunchKernelGGL(merge_kernel<VI_F16>, dim3(s.rows), dim3(kT), 0, stream, a);
+    }
     vi_status st = launch_status();
     if (st != VI_OK || !s.probs) return st;
     if (s.dtype == VI_BF16) hipLaunchKernelGGL(slice_probs_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);

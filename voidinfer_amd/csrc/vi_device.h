@@ -283,6 +283,17 @@ __device__ __forceinline__ double wave_incl_scan_f64(double x) {
     x += dpp_f64<0x143, 0xc, false>(x);
     return x;
 }
+// Sum over the wave in a fixed order (the scan's), returned in every lane.
+__device__ __forceinline__ float wave_sum_f32(float x) {
+    auto step = [](float v, auto dpp) { return v + __builtin_bit_cast(float, dpp(__builtin_bit_cast(uint32_t, v))); };
+    x = step(x, [](uint32_t u) { return dpp_u32<0x111, 0xf, true>(u); });
+    x = step(x, [](uint32_t u) { return dpp_u32<0x112, 0xf, true>(u); });
+    x = step(x, [](uint32_t u) { return dpp_u32<0x114, 0xf, true>(u); });
+    x = step(x, [](uint32_t u) { return dpp_u32<0x118, 0xf, true>(u); });
+    x = step(x, [](uint32_t u) { return dpp_u32<0x142, 0xa, false>(u); });
+    x = step(x, [](uint32_t u) { return dpp_u32<0x143, 0xc, false>(u); });
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), kWave - 1));
+}
 // Sum over the wave, returned in every lane.
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
     return uint32_t(__builtin_amdgcn_readlane(int(wave_incl_scan_u32(x)), kWave - 1));
