@@ -47,8 +47,11 @@ namespace {
 
 constexpr int kT = 1024;                  // threads per workgroup (one per CU: the LDS is the limit)
 constexpr int kW = kT / kWave;            // waves per workgroup
-constexpr int kSL = 32768;                // tokens per slice
-constexpr int kNV = kSL / 8 / kT;         // 16-byte vectors per thread and slice
+constexpr int kSL = 32768;                // tokens per slice (counts fit 16 bits, whole bitmap words)
+constexpr int kHW = 32768;                // histogram words (pattern & 0x7fff)
+constexpr int kNV = (kSL + 8 * kT - 1) / (8 * kT);   // 16-byte vectors per thread and slice
+constexpr int kWPT = (kSL / 32 + kT - 1) / kT;   // history bitmap words per thread (consecutive words)
+constexpr int kBW = kWPT * kT;            // history bitmap words (a slice uses kSL / 32)
 constexpr int kBins = 512;                // coarse bins of 128 keys, bin(key) = key >> 7
 constexpr int kBinKeys = 128;
 constexpr int kHeadWords = 32;            // slice head: n_list, n_valid, flags, top_key, bin mask [16]
@@ -62,19 +65,19 @@ constexpr uint32_t kTakeAll = 0xffffffffu;
 constexpr float kMaxTemperature = 65536.0f;
 
 // LDS map (bytes).  H: histogram, u16 counts in pairs (word p & 0x7fff: low half
-// the pattern with sign 0, high half with sign 1), then the staged list; the
-// merge reuses it.  B: history bitmap of the slice.  X: repeat hash, then the
-// compaction's bin tables.  F: staged history offsets.
+// the pattern with sign 0, high half with sign 1); the merge reuses it.  B:
+// history bitmap of the slice.  X: repeat hash (counts of the tokens seen more
+// than once).  F: staged history offsets.  R: bitmap of the repeated tokens.
 constexpr int kOffH = 0;
-constexpr int kOffB = kOffH + 4 * kSL;
-constexpr int kOffX = kOffB + 4 * (kSL / 32);
+constexpr int kOffB = kOffH + 4 * kHW;
+constexpr int kOffX = kOffB + 4 * kBW;
 constexpr int kOffF = kOffX + 4 * kHash;
-constexpr int kLds = kOffF + 2 * kStage;
-constexpr int kWPT = kSL / 32 / kT;       // history bitmap words per thread
-constexpr int kQ = kSL / 2 / kT;          // 2-word histogram groups per thread (compaction)
+constexpr int kOffR = kOffF + 2 * kStage;     // R: the slice's tokens seen more than once (bitmap)
+constexpr int kLds = kOffR + 4 * kBW;
+constexpr int kQ = kHW / 2 / kT;          // 2-word histogram groups per thread (compaction)
 constexpr int kSeg = kNV + 2;             // id-order segments: head, vectors, tail
-static_assert(kWPT * kT * 32 == kSL, "whole bitmap words per thread");
-static_assert(kQ * kW == 256 && kQ * 2 * kT == kSL, "compaction blocks of 128 patterns");
+static_assert(kWPT * kT == kBW && kSL % 32 == 0 && kSL < 65536 && kNV * 8 * kT >= kSL, "slice geometry");
+static_assert(kQ * kW == 256 && kQ * 2 * kT == kHW, "compaction blocks of 128 patterns");
 
 // Merge map inside H (bytes): per-slice bin (first | entries << 16), the
 // slices' bin masks, bin counts and masses summed over slices, five gather
@@ -86,7 +89,7 @@ constexpr int kOffMR = kOffMC + 4 * kBins;
 constexpr int kGatherSlots = 5;   // cap, min-p, top-p, support end, draw
 constexpr int kGatherBytes = 4 * kMaxSlices * kBinKeys + 4 * kBinKeys + 4 * kMaxSlices;
 constexpr int kOffGather = kOffMR + 8 * kBins;
-static_assert(kOffGather + kGatherSlots * kGatherBytes <= 4 * kSL, "merge map");
+static_assert(kOffGather + kGatherSlots * kGatherBytes <= 4 * kHW, "merge map");
 
 struct RowBound {          // what the probs kernel needs to rebuild the support
     double z0, s_n;
@@ -114,6 +117,8 @@ struct SliceArgs {
     uint4* brec;               // [rows][slices][kBins], occupied bins only: first | entries << 16,
                                // valid logits | largest valid key << 16, mass relative to that key (double)
     uint32_t* lists;           // [rows][slices][kSL]; a slice's dense repeat counts before its list
+    uint16_t* ptab;            // [rows][slices][kSL]: penalized patterns of the history tokens, in id order
+    uint32_t* hbits;           // [rows][slices][kBW]: history bitmaps (history route; the state holds its own)
     RowBound* bounds;          // [rows]
     uint32_t* bases;           // [rows][kMaxSlices]: end-key logits in the slices before
 };
@@ -321,8 +326,9 @@ __device__ __forceinline__ PenCtx pen_ctx(const SliceArgs& a, int row, const vi_
     return c;
 }
 
-// First loads of a slice's penalty inputs (header, bitmap word, list / history
-// head); issued a slice ahead.
+// A slice's penalty inputs (header, bitmap word and the repeat list's first
+// kPL kT slots, read whatever the list's length: one round trip; or the
+// history's head); issued a slice ahead.
 __device__ __forceinline__ void pen_prefetch_head(const SliceArgs& a, const PenCtx& c, const Geo& g, PenPrefetch& f) {
     const int tid = opaque_tid();
 #pragma unroll
@@ -331,13 +337,19 @@ __device__ __forceinline__ void pen_prefetch_head(const SliceArgs& a, const PenC
     if (!c.pen) return;
     if (c.state) {
         const PenaltyHeader* h = reinterpret_cast<const PenaltyHeader*>(c.lstate);
-        f.hflags = __builtin_amdgcn_readfirstlane(h->flags);
-        f.nrep = __builtin_amdgcn_readfirstlane(h->nrep);
+        f.hflags = h->flags;
+        f.nrep = h->nrep;
         const uint32_t* b1 = reinterpret_cast<const uint32_t*>(c.lstate + a.pl.off_b1);
         const int nw = (g.n + 31) >> 5;
 #pragma unroll
         for (int q = 0; q < kWPT; ++q)
-            if (q * kT + tid < nw) f.bword[q] = b1[(g.s0 >> 5) + q * kT + tid];
+            if (tid * kWPT + q < nw) f.bword[q] = b1[(g.s0 >> 5) + tid * kWPT + q];
+        const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
+#pragma unroll
+        for (int j = 0; j < kPL; ++j) {
+            const uint32_t i = uint32_t(j) * kT + uint32_t(tid);
+            f.le[j] = i < uint32_t(a.pl.slots) ? list[i] : make_uint2(0u, 0u);
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < kPHist; ++j) {
@@ -346,46 +358,43 @@ __device__ __forceinline__ void pen_prefetch_head(const SliceArgs& a, const PenC
         }
     }
 }
-// The repeat-list head (state route), once the header has arrived.
-__device__ __forceinline__ void pen_prefetch_list(const SliceArgs& a, const PenCtx& c, PenPrefetch& f) {
-    if (!c.pen || !c.state) return;
-    const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
-    const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
-#pragma unroll
-    for (int j = 0; j < kPL; ++j) {
-        const uint32_t i = uint32_t(j) * kT + uint32_t(opaque_tid());
-        f.le[j] = i < nrep ? list[i] : make_uint2(0u, 0u);
-    }
-}
 
 __device__ __forceinline__ uint32_t hash_slot(uint32_t off) { return (off * 0x9E3779B1u) >> 21; }
 
-// Builds the slice's history bitmap in B and the repeat counts in X (or, when X
-// overflows, full counts in the slice's dense table).  Sets sh.flags bits
-// (BAD_HISTORY, ERROR) and sh.overflow.  All threads.
-template <int DT>
-__device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, const Geo& g, const PenPrefetch& f,
-                          unsigned char* lds, Shared& sh, uint32_t* dense) {
+// Full counts of the slice's tokens in its dense table (when the repeat hash
+// overflows).  All threads; uniform.
+__device__ __forceinline__ void pen_dense_fill(const SliceArgs& a, const PenCtx& c, const Geo& g, const PenPrefetch& f,
+                                               uint32_t* dense) {
     const int tid = opaque_tid();
-    uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
-    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
-    const int nw = (g.n + 31) >> 5;
-    for (int i = tid; i < kHash; i += kT) X[i] = 0u;
-    if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
+    const int s1 = g.s0 + g.n;
+    for (int i = tid; i < g.n; i += kT) put_agent(&dense[i], 0u);
+    handoff_stores_done();
+    __syncthreads();
     if (c.state) {
-        const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
-#pragma unroll
-        for (int q = 0; q < kWPT; ++q) {
-            const int wd = q * kT + tid;
-            B[wd] = wd < nw ? (f.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
+        const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
+        const uint32_t nrep = min(uint32_t(__builtin_amdgcn_readfirstlane(int(f.nrep))), uint32_t(a.pl.slots));
+        for (uint32_t i = tid; i < nrep; i += kT) {
+            const uint2 e = list[i];
+            const int t = int(e.x);
+            if (e.y >= 2u && t >= g.s0 && t < s1) put_agent(&dense[t - g.s0], e.y);
         }
-        if (tid == 0 && f.hflags) atomicOr(&sh.flags, f.hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
     } else {
-#pragma unroll
-        for (int q = 0; q < kWPT; ++q) B[q * kT + tid] = 0u;
+        for (int64_t i = tid; i < c.hn; i += kT) {
+            const int32_t t = c.hist[i];
+            if (t >= g.s0 && t < s1) atomicAdd(&dense[t - g.s0], 1u);
+        }
     }
-    lds_barrier();
-    auto hash_put = [&](uint32_t off, uint32_t extra, bool add) {
+    handoff_stores_done();
+    __syncthreads();
+}
+
+// Records slice token `off` as seen 1 + extra times (add: one more occurrence of
+// a token already recorded) in the repeat hash X and bitmap R; sets
+// sh.overflow when the hash cannot hold it.
+__device__ __forceinline__ void repeat_put(unsigned char* lds, Shared& sh, uint32_t off, uint32_t extra, bool add) {
+    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
+    uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
+        atomicOr(&R[off >> 5], 1u << (off & 31));
         if (extra > 0xffffu) { sh.overflow = 1u; return; }
         uint32_t h = hash_slot(off);
         const uint32_t key = (off + 1u) << 16;
@@ -410,11 +419,42 @@ __device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, c
             h = (h + 1u) & uint32_t(kHash - 1);
         }
         sh.overflow = 1u;
-    };
+    }
+
+// Builds the slice's history bitmap in B and the repeat counts in X (or, when X
+// overflows, full counts in the slice's dense table).  Sets sh.flags bits
+// (BAD_HISTORY, ERROR) and sh.overflow.  All threads.
+template <int DT>
+__device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, const Geo& g, const PenPrefetch& f,
+                          unsigned char* lds, Shared& sh, uint32_t* dense) {
+    const int tid = opaque_tid();
+    uint32_t* B = reinterpret_cast<uint32_t*>(lds + kOffB);
+    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
+    uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
+    const int nw = (g.n + 31) >> 5;
+    for (int i = tid; i < kHash; i += kT) X[i] = 0u;
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) R[q * kT + tid] = 0u;
+    if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
+    if (c.state) {
+        const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) {
+            const int wd = tid * kWPT + q;
+            B[wd] = wd < nw ? (f.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
+        }
+        const uint32_t hflags = uint32_t(__builtin_amdgcn_readfirstlane(int(f.hflags)));
+        if (tid == 0 && hflags) atomicOr(&sh.flags, hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
+    } else {
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) B[q * kT + tid] = 0u;
+    }
+    lds_barrier();
+    auto hash_put = [&](uint32_t off, uint32_t extra, bool add) { repeat_put(lds, sh, off, extra, add); };
     const int s1 = g.s0 + g.n;
     if (c.state) {
         const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
-        const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
+        const uint32_t nrep = min(uint32_t(__builtin_amdgcn_readfirstlane(int(f.nrep))), uint32_t(a.pl.slots));
         auto put = [&](uint2 e) {
             const int t = int(e.x);
             if (e.y < 2u || t < g.s0 || t >= s1) return;
@@ -450,27 +490,7 @@ __device__ __forceinline__ void pen_build(const SliceArgs& a, const PenCtx& c, c
         }
     }
     lds_barrier();
-    if (sh.overflow) {   // (uniform) full counts of the slice's tokens in its dense table
-        for (int i = tid; i < g.n; i += kT) put_agent(&dense[i], 0u);
-        handoff_stores_done();
-        __syncthreads();
-        if (c.state) {
-            const uint2* list = reinterpret_cast<const uint2*>(c.lstate + a.pl.off_list);
-            const uint32_t nrep = min(f.nrep, uint32_t(a.pl.slots));
-            for (uint32_t i = tid; i < nrep; i += kT) {
-                const uint2 e = list[i];
-                const int t = int(e.x);
-                if (e.y >= 2u && t >= g.s0 && t < s1) put_agent(&dense[t - g.s0], e.y);
-            }
-        } else {
-            for (int64_t i = tid; i < c.hn; i += kT) {
-                const int32_t t = c.hist[i];
-                if (t >= g.s0 && t < s1) atomicAdd(&dense[t - g.s0], 1u);
-            }
-        }
-        handoff_stores_done();
-        __syncthreads();
-    }
+    if (sh.overflow) pen_dense_fill(a, c, g, f, dense);   // (uniform)
 }
 
 // Occurrences of slice token `off` (its bitmap bit is set).
@@ -480,6 +500,8 @@ __device__ __forceinline__ uint32_t pen_count(const unsigned char* lds, const Sh
         const uint32_t c = get_agent(&dense[off]);
         return c ? c : 1u;
     }
+    const uint32_t* R = reinterpret_cast<const uint32_t*>(lds + kOffR);
+    if (!((R[off >> 5] >> (off & 31)) & 1u)) return 1u;   // seen once
     const uint32_t* X = reinterpret_cast<const uint32_t*>(lds + kOffX);
     uint32_t h = hash_slot(off);
     const uint32_t key = (off + 1u) << 16;
@@ -558,7 +580,7 @@ __device__ __forceinline__ uint32_t id_order_prefix(const uint32_t cnt[kSeg], ui
 // ------------------------------------------------------------------ merge
 constexpr int kSlotsAll = kGatherSlots;
 constexpr int kOffPC = kOffGather + kSlotsAll * kGatherBytes;   // [kMaxSlices] per-slice counts
-static_assert(kOffPC + 4 * 2 * kMaxSlices <= 4 * kSL, "merge map");
+static_assert(kOffPC + 4 * 2 * kMaxSlices <= 4 * kHW, "merge map");
 
 struct Slot {
     uint32_t* E;    // [kMaxSlices][kBinKeys] list entries of the bin, per slice
@@ -1024,9 +1046,12 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
     __syncthreads();
 
     // ---- 6. the owner slice read again: the owner_rank-th logit of the drawn
-    // key in id order (penalties applied as in the slice pass).  Thread t takes
-    // body vectors kNV t .. kNV t + kNV - 1, so thread order is id order: the head
-    // logits (offsets < head, threads < head), the body, the tail.
+    // key in id order.  Thread t takes body vectors kNV t .. kNV t + kNV - 1, so
+    // thread order is id order: the head logits (offsets < head, threads <
+    // head), the body, the tail.  History tokens take their penalized patterns
+    // from the slice pass's table (rank = their order among the slice's history
+    // tokens); the history bitmap comes from the lane's state, or as the slice
+    // pass published it.
     if (sh.ok) {
         const int os = int(sh.owner_slice);
         const Geo g = geo_of(a, row, os);
@@ -1039,49 +1064,66 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
         const uint32_t hb = tid < g.head ? uint32_t(g.base16[tid]) : 0u;
         const uint32_t tb = tid < g.tail ? uint32_t(g.base16[g.head + 8 * g.nvec + tid]) : 0u;
         const PenCtx pc = pen_ctx(a, row, p);
-        uint32_t* dense = a.lists + (rs + os) * kSL;
+        // history flags: bit e of hmask for body element e of this thread; head / tail
+        static_assert(kNV * 8 == 32, "a thread's body elements fill one 32-bit mask");
+        const int nbv = max(0, min(kNV, g.nvec - kNV * tid));   // this thread's body vectors
+        const uint32_t bodym = nbv >= kNV ? ~0u : (1u << (8 * nbv)) - 1u;
+        uint32_t hmask = 0u;
+        bool hh = false, th = false;
         if (pc.pen) {
-            PenPrefetch f{};
-            pen_prefetch_head(a, pc, g, f);
-            pen_prefetch_list(a, pc, f);
-            pen_build<DT>(a, pc, g, f, lds, sh, dense);
+            const uint32_t* bm = pc.state ? reinterpret_cast<const uint32_t*>(pc.lstate + a.pl.off_b1) + (g.s0 >> 5)
+                                          : a.hbits + (rs + os) * kBW;
+            const int nw = (g.n + 31) >> 5;
+            const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
+            auto word = [&](int wd) { return wd < nw ? (bm[wd] & (wd == nw - 1 ? lastm : ~0u)) : 0u; };
+            const uint32_t off0 = uint32_t(g.head + 8 * kNV * tid), wd0 = off0 >> 5, sft = off0 & 31u;
+            const uint64_t two = uint64_t(word(int(wd0))) | (uint64_t(word(int(wd0) + 1)) << 32);
+            hmask = nbv > 0 ? uint32_t(two >> sft) & bodym : 0u;
+            if (tid < g.head) hh = (word(0) >> tid) & 1u;
+            const uint32_t to = uint32_t(g.head + 8 * g.nvec + tid);
+            if (tid < g.tail) th = (word(int(to >> 5)) >> (to & 31u)) & 1u;
         }
+        // ranks of the history tokens: the head's (wave 0), the body's in thread
+        // order, the tail's
+        uint32_t hrank = 0u, trank = 0u, nhist = 0u, hexcl = 0u, h0 = 0u;
+        if (pc.pen) {   // (uniform)
+            if (wave == 0) {
+                const uint64_t hb_ = ballot(hh), tb_ = ballot(th);
+                const uint64_t below = (1ull << lane) - 1ull;
+                hrank = uint32_t(__builtin_popcountll(hb_ & below));
+                trank = uint32_t(__builtin_popcountll(tb_ & below));
+                if (lane == 0) sh.n_hash = uint32_t(__builtin_popcountll(hb_));   // (history tokens among the head)
+            }
+            hexcl = block_scan_lds(uint32_t(__builtin_popcount(hmask)), sh.scan, &nhist);
+            h0 = sh.n_hash;
+        }
+        const uint16_t* tab = a.ptab + (rs + os) * kSL;
         const uint32_t dk = sh.draw_key;
-        // raw patterns of the drawn key (+0 and -0 for key 0x8000): logits that
-        // penalties leave alone match on their raw pattern
+        // raw patterns of the drawn key (+0 and -0 for key 0x8000)
         const uint32_t P1 = unkey16(dk), P2 = dk == 0x8000u ? 0x8000u : P1;
-        const uint32_t* Bm = reinterpret_cast<const uint32_t*>(lds + kOffB);
-        auto key_at = [&](uint32_t off, uint32_t b) { return elem_key<DT>(lds, sh, dense, p, pc.pen, off, b); };
+        auto match = [&](uint32_t b) { return b == P1 || b == P2; };
+        auto match_pen = [&](uint32_t pb) { return Elem<DT>::finite_bits(pb) && key16(pb) == dk; };
         uint32_t bits = 0u;
+        uint32_t r = h0 + hexcl;
 #pragma unroll
         for (int i = 0; i < kNV; ++i) {
-            const int vi = kNV * tid + i;
-            if (vi >= g.nvec) continue;
             const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-            uint32_t m8 = 0u;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+                const int e = 8 * i + j;
                 const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                m8 |= (b == P1 || b == P2) ? 1u << j : 0u;
+                const bool hist = (hmask >> e) & 1u;
+                const bool m = hist ? match_pen(uint32_t(tab[r])) : match(b);
+                r += hist ? 1u : 0u;
+                bits |= m ? 1u << e : 0u;
             }
-            if (pc.pen) {   // history tokens among the eight: their penalized keys
-                const uint32_t off = uint32_t(g.head + 8 * vi), wd = off >> 5, sft = off & 31u;
-                const uint64_t two = uint64_t(Bm[wd]) | (sft > 24u && wd + 1u < uint32_t(kSL / 32) ? uint64_t(Bm[wd + 1u]) << 32 : 0ull);
-                uint32_t hist8 = uint32_t(two >> sft) & 0xffu;
-                while (hist8) {
-                    const int j = __builtin_ctz(hist8);
-                    hist8 &= hist8 - 1u;
-                    const bool hit = key_at(off + uint32_t(j), vec_elem(v[i], j)) == dk;
-                    m8 = hit ? (m8 | (1u << j)) : (m8 & ~(1u << j));
-                }
-            }
-            bits |= m8 << (8 * i);
         }
-        const bool hm = tid < g.head && key_at(uint32_t(tid), hb) == dk;
-        const bool tm = tid < g.tail && key_at(uint32_t(g.head + 8 * g.nvec + tid), tb) == dk;
+        bits &= bodym;
+        const bool hm = tid < g.head && (hh ? match_pen(uint32_t(tab[hrank])) : match(hb));
+        const bool tm = tid < g.tail && (th ? match_pen(uint32_t(tab[h0 + nhist + trank])) : match(tb));
         if (wave == 0) {   // (head and tail logits belong to threads < 8)
-            const uint64_t hmask = ballot(hm), tmask = ballot(tm);
-            if (lane == 0) { sh.hmask = uint32_t(hmask); sh.tmask = uint32_t(tmask); }
+            const uint64_t hmk = ballot(hm), tmk = ballot(tm);
+            if (lane == 0) { sh.hmask = uint32_t(hmk); sh.tmask = uint32_t(tmk); }
         }
         const uint32_t nb = uint32_t(__builtin_popcount(bits));
         uint32_t nbody = 0u;
@@ -1090,18 +1132,18 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
             for (; n > 0u; --n) m &= m - 1u;
             return __builtin_ctz(m);
         };
-        const uint32_t hmask = sh.hmask, tmask = sh.tmask, nh = uint32_t(__builtin_popcount(hmask));
+        const uint32_t hmk = sh.hmask, tmk = sh.tmask, nh = uint32_t(__builtin_popcount(hmk));
         const uint32_t want = sh.owner_rank;
         if (want < nh) {
-            if (tid == nth_bit(hmask, want)) sh.token = g.s0 + tid;
+            if (tid == nth_bit(hmk, want)) sh.token = g.s0 + tid;
         } else if (want - nh < nbody) {
-            const uint32_t r = want - nh;
-            if (r >= bexcl && r < bexcl + nb) {
-                const int j = nth_bit(bits, r - bexcl);
+            const uint32_t rr = want - nh;
+            if (rr >= bexcl && rr < bexcl + nb) {
+                const int j = nth_bit(bits, rr - bexcl);
                 sh.token = g.s0 + g.head + 8 * (kNV * tid + j / 8) + j % 8;
             }
-        } else if (want - nh - nbody < uint32_t(__builtin_popcount(tmask))) {
-            if (tid == nth_bit(tmask, want - nh - nbody)) sh.token = g.s0 + g.head + 8 * g.nvec + tid;
+        } else if (want - nh - nbody < uint32_t(__builtin_popcount(tmk))) {
+            if (tid == nth_bit(tmk, want - nh - nbody)) sh.token = g.s0 + g.head + 8 * g.nvec + tid;
         }
         __syncthreads();
     }
@@ -1153,7 +1195,7 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
     // the histogram and the slice head's counters start empty (every slice leaves
     // them so)
 #pragma unroll
-    for (int q = 0; q < kSL / 4 / kT; ++q) H4[q * kT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    for (int q = 0; q < kHW / 4 / kT; ++q) H4[q * kT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
     if (threadIdx.x < kBins / 32) sh.bmask[threadIdx.x] = 0u;
     if (threadIdx.x == 0) { sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u; }
     SliceRegs cur{};
@@ -1165,7 +1207,6 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             const PenCtx pc0 = pen_ctx(a, row, p0);
             load_slice(g0, cur);
             pen_prefetch_head(a, pc0, g0, pf);
-            pen_prefetch_list(a, pc0, pf);
         }
     }
     lds_barrier();
@@ -1216,15 +1257,62 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
 
         if (full) {
             if (tid == 0) sh.flags = 0u;
-            // ---- 1. penalties; the first round of history tokens staged and
-            // their raw logits requested (before the next slice's loads)
+            // ---- 1. penalties: the slice's history bitmap B, the repeat hash X / bitmap
+            // R, and the first round of history tokens staged in id order with their
+            // raw logits requested (before the next slice's loads)
             if (pc.pen) {
-                pen_build<DT>(a, pc, g, pf, lds, sh, dense);
-                // this thread's bitmap words tid * kWPT .. + kWPT - 1: ranks of their tokens
-                uint32_t pc_ = 0u;
+                if (pc.state) {
+                    // the state's bitmap word is this thread's B word: two barriers
+                    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
+                    uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
+                    for (int i = tid; i < kHash; i += kT) X[i] = 0u;
+                    if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
+                    const int nw = (g.n + 31) >> 5;
+                    const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
+                    uint32_t pc_ = 0u;
 #pragma unroll
-                for (int q = 0; q < kWPT; ++q) { bw[q] = B[tid * kWPT + q]; pc_ += __builtin_popcount(bw[q]); }
-                rank0 = block_scan_lds(pc_, sh.scan, &nf);
+                    for (int q = 0; q < kWPT; ++q) {
+                        const int wd = tid * kWPT + q;
+                        bw[q] = wd < nw ? (pf.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
+                        B[wd] = bw[q];
+                        R[wd] = 0u;
+                        pc_ += uint32_t(__builtin_popcount(bw[q]));
+                    }
+                    const uint32_t hflags = uint32_t(__builtin_amdgcn_readfirstlane(int(pf.hflags)));
+                    if (tid == 0 && hflags) atomicOr(&sh.flags, hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
+                    const uint32_t incl = wave_incl_scan_u32(pc_);
+                    if (lane == kWave - 1) sh.scan[wave] = incl;
+                    lds_barrier();
+                    const uint32_t st = lane < kW ? sh.scan[lane] : 0u;
+                    const uint32_t si = wave_incl_scan_u32(st);
+                    nf = uint32_t(readlane_i(int(si), kW - 1));
+                    rank0 = (wave > 0 ? uint32_t(readlane_i(int(si), wave - 1)) : 0u) + incl - pc_;
+                    // repeat counts of the slice's tokens from the state's repeat list
+                    const uint2* list = reinterpret_cast<const uint2*>(pc.lstate + a.pl.off_list);
+                    const uint32_t nrep = min(uint32_t(__builtin_amdgcn_readfirstlane(int(pf.nrep))), uint32_t(a.pl.slots));
+                    const int s1 = g.s0 + g.n;
+                    auto put = [&](uint2 e) {
+                        const int t = int(e.x);
+                        if (e.y < 2u || t < g.s0 || t >= s1) return;
+                        repeat_put(lds, sh, uint32_t(t - g.s0), e.y - 1u, false);
+                    };
+#pragma unroll
+                    for (int j = 0; j < kPL; ++j)
+                        if (uint32_t(j) * kT + tid < nrep) put(pf.le[j]);
+                    for (uint32_t i = uint32_t(kPL) * kT + tid; i < nrep; i += kT) put(list[i]);
+                } else {
+                    pen_build<DT>(a, pc, g, pf, lds, sh, dense);
+                    uint32_t pc_ = 0u;
+                    uint32_t* hb = a.hbits + (size_t(row) * S + s) * kBW;   // (for the merge's owner scan)
+#pragma unroll
+                    for (int q = 0; q < kWPT; ++q) {
+                        bw[q] = B[tid * kWPT + q];
+                        hb[tid * kWPT + q] = bw[q];
+                        pc_ += __builtin_popcount(bw[q]);
+                    }
+                    rank0 = block_scan_lds(pc_, sh.scan, &nf);
+                }
+                // this thread's history tokens, staged at their ranks
                 uint32_t r = rank0;
 #pragma unroll
                 for (int q = 0; q < kWPT; ++q) {
@@ -1236,6 +1324,7 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                     }
                 }
                 lds_barrier();
+                if (pc.state && sh.overflow) pen_dense_fill(a, pc, g, pf, dense);   // (uniform)
                 const uint32_t m = min(uint32_t(kStage), nf);
 #pragma unroll
                 for (int u = 0; u < kG; ++u) {
@@ -1251,32 +1340,66 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             // by a branch that is uniform in all waves but one (masked adds of 0
             // would all hit one word and serialize).
             auto hist_add = [&](uint32_t b) { atomicAdd(&H[b & 0x7fffu], (b & 0x8000u) ? 0x10000u : 1u); };
-#pragma unroll
-            for (int i = 0; i < kNV; ++i) {
-                if (i * kT + tid < g.nvec) {
-                    const uint32_t w4[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
-                }
-            }
-            if (tid < g.head) hist_add(cur.hb);
-            if (tid < g.tail) hist_add(cur.tb);
-            prefetch_next();
-
-            // ---- 3. history tokens move from their raw pattern to the penalized one
-            if (pc.pen) {
-                auto move = [&](uint32_t off, uint32_t b) {
-                    if (!Elem<DT>::finite_bits(b)) return;
-                    const uint32_t pb = penalize_bits<DT>(b, pen_count(lds, sh, dense, off), p) & 0xffffu;
-                    if (pb == b) return;
-                    atomicSub(&H[b & 0x7fffu], (b & 0x8000u) ? 0x10000u : 1u);
-                    hist_add(pb);
+            if (pc.pen) {   // history tokens are left out here: the moves add their penalized patterns
+                auto hist8 = [&](uint32_t off) {   // B bits off .. off + 7
+                    const uint32_t wd = off >> 5, sft = off & 31u;
+                    const uint64_t two = uint64_t(B[wd]) | (sft > 24u && wd + 1u < uint32_t(kBW) ? uint64_t(B[wd + 1u]) << 32 : 0ull);
+                    return uint32_t(two >> sft) & 0xffu;
                 };
 #pragma unroll
-                for (int u = 0; u < kG; ++u)
-                    if (goff[u] != 0xffffffffu) move(goff[u], graw[u]);
-                lds_barrier();
+                for (int i = 0; i < kNV; ++i) {
+                    const int vi = i * kT + tid;
+                    if (vi < g.nvec) {
+                        const uint32_t h8 = hist8(uint32_t(g.head + 8 * vi));
+                        const uint32_t w4[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (!((h8 >> j) & 1u)) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+                    }
+                }
+                if (tid < g.head && !((B[tid >> 5] >> (tid & 31)) & 1u)) hist_add(cur.hb);
+                const uint32_t to = uint32_t(g.head + 8 * g.nvec + tid);
+                if (tid < g.tail && !((B[to >> 5] >> (to & 31)) & 1u)) hist_add(cur.tb);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kNV; ++i) {
+                    if (i * kT + tid < g.nvec) {
+                        const uint32_t w4[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+                    }
+                }
+                if (tid < g.head) hist_add(cur.hb);
+                if (tid < g.tail) hist_add(cur.tb);
+            }
+            prefetch_next();
+
+            // ---- 3. the history tokens' penalized patterns (non-finite logits keep
+            // their own)
+            if (pc.pen) {
+                // (all the patterns first, then the adds: the count lookups do not
+                // wait behind earlier atomics)
+                // (the patterns also go to the slice's table, by rank: the merge's
+                // owner scan reads them instead of penalizing again)
+                uint16_t* tab = a.ptab + (size_t(row) * S + s) * kSL;
+                auto moves = [&](const uint32_t* off, const uint32_t* b, uint32_t c0) {
+                    uint32_t pb[kG];
+#pragma unroll
+                    for (int u = 0; u < kG; ++u)
+                        pb[u] = (off[u] != 0xffffffffu && Elem<DT>::finite_bits(b[u]))
+                                    ? penalize_bits<DT>(b[u], pen_count(lds, sh, dense, off[u]), p) & 0xffffu
+                                    : b[u];
+#pragma unroll
+                    for (int u = 0; u < kG; ++u) {
+                        if (off[u] != 0xffffffffu) {
+                            hist_add(pb[u]);
+                            tab[c0 + uint32_t(u) * kT + tid] = uint16_t(pb[u]);
+                        }
+                    }
+                };
+                moves(goff, graw, 0u);
                 for (uint32_t c0 = kStage; c0 < nf; c0 += kStage) {   // (long histories) further rounds
+                    lds_barrier();   // (every thread has read the staged offsets)
                     uint32_t r = rank0;
 #pragma unroll
                     for (int q = 0; q < kWPT; ++q) {
@@ -1297,10 +1420,7 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                         oo[u] = e < m ? uint32_t(F[e]) : 0xffffffffu;
                         rr[u] = e < m ? uint32_t(g.base16[oo[u]]) : 0u;
                     }
-#pragma unroll
-                    for (int u = 0; u < kG; ++u)
-                        if (oo[u] != 0xffffffffu) move(oo[u], rr[u]);
-                    lds_barrier();
+                    moves(oo, rr, c0);
                 }
             }
             lds_barrier();
@@ -1447,10 +1567,6 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             prefetch_next();
         }
         if (!has_next) break;
-        {   // (the next slice's header has arrived)
-            const vi_row_params np = a.params[nrow];
-            if (full_route_row(np)) pen_prefetch_list(a, pen_ctx(a, nrow, np), pf);
-        }
         row = nrow; s = ns;
     }
 }
@@ -1500,7 +1616,6 @@ __global__ __launch_bounds__(kT) void slice_probs_kernel(SliceArgs a) {
             if (tid == 0) sh.flags = 0u;
             PenPrefetch f{};
             pen_prefetch_head(a, pc, g, f);
-            pen_prefetch_list(a, pc, f);
             pen_build<DT>(a, pc, g, f, lds, sh, dense);
         }
         // pass 1: logits of the support's end key, in id order
@@ -1582,6 +1697,7 @@ size_t full_workspace(int rows, int vocabulary) {
     if (rows <= 0 || vocabulary <= 0) return 0;
     const size_t rs = size_t(rows) * size_t(slices_of(vocabulary));
     return align_up(rs * kHeadWords * 4, 256) + align_up(rs * kBins * 16, 256) + align_up(rs * kSL * 4, 256) +
+           align_up(rs * kSL * 2, 256) + align_up(rs * kBW * 4, 256) +
            align_up(size_t(rows) * sizeof(RowBound), 256) +
            align_up(size_t(rows) * kMaxSlices * 4, 256) + 256;
 }
@@ -1596,6 +1712,8 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.heads = c.take<uint32_t>(rs * kHeadWords);
     a.brec = c.take<uint4>(rs * kBins);
     a.lists = c.take<uint32_t>(rs * kSL);
+    a.ptab = c.take<uint16_t>(rs * kSL);
+    a.hbits = c.take<uint32_t>(rs * kBW);
     a.bounds = c.take<RowBound>(size_t(s.rows));
     a.bases = c.take<uint32_t>(size_t(s.rows) * kMaxSlices);
     if (!c.ok) return VI_ERR_WORKSPACE;
