@@ -54,7 +54,7 @@ constexpr int kWPT = (kSL / 32 + kT - 1) / kT;   // history bitmap words per thr
 constexpr int kBW = kWPT * kT;            // history bitmap words (a slice uses kSL / 32)
 constexpr int kBins = 512;                // coarse bins of 128 keys, bin(key) = key >> 7
 constexpr int kBinKeys = 128;
-constexpr int kHeadWords = 32;            // slice head: n_list, n_valid, flags, top_key, bin mask [16]
+constexpr int kHeadWords = 32;            // slice head: n_list, n_valid, flags, top_key, bin mask [16], history tokens
 constexpr int kHash = 2048;               // LDS repeat-count hash slots
 constexpr uint32_t kHashFill = kHash * 3 / 4;
 constexpr int kStage = 4096;              // history offsets staged per penalty round (u16)
@@ -138,6 +138,7 @@ struct Shared {
     int32_t cap_slot, minp_slot, topp_slot, draw_slot, end_slot;
     uint32_t cap_key, cap_take, minp_key, topp_key, topp_take, end_key, end_take, end_all;
     uint32_t n_support, draw_key, draw_rank, owner_slice, owner_rank, ok, hmask, tmask;
+    uint32_t slice_hist[kMaxSlices];   // history tokens per slice
     int32_t token;
     double s_all, cap_mass, topp_target, s_n, u, draw_target;
 };
@@ -580,7 +581,9 @@ __device__ __forceinline__ uint32_t id_order_prefix(const uint32_t cnt[kSeg], ui
 // ------------------------------------------------------------------ merge
 constexpr int kSlotsAll = kGatherSlots;
 constexpr int kOffPC = kOffGather + kSlotsAll * kGatherBytes;   // [kMaxSlices] per-slice counts
-static_assert(kOffPC + 4 * 2 * kMaxSlices <= 4 * kHW, "merge map");
+constexpr int kOffTab = (kOffPC + 4 * 2 * kMaxSlices + 15) / 16 * 16;   // the owner slice's penalized patterns
+constexpr int kTabCap = (4 * kHW - kOffTab) / 2 / 8 * 8;              // (u16 entries staged; more are read from HBM)
+static_assert(kTabCap >= 8192, "merge map");
 
 struct Slot {
     uint32_t* E;    // [kMaxSlices][kBinKeys] list entries of the bin, per slice
@@ -812,6 +815,7 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
     if (tid < S) {
 #pragma unroll
         for (int q = 0; q < 3; ++q) h3[q] = a.heads[(rs + tid) * kHeadWords + 1 + q];
+        sh.slice_hist[tid] = a.heads[(rs + tid) * kHeadWords + 4 + kBins / 32];
     }
     if (tid < kGatherSlots) sh.slot_bin[tid] = -1;
     if (tid == 0) { sh.row_flags = 0u; sh.row_valid = 0u; sh.row_top = 0u; sh.token = -1; sh.ok = 1u; }
@@ -1064,6 +1068,14 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
         const uint32_t hb = tid < g.head ? uint32_t(g.base16[tid]) : 0u;
         const uint32_t tb = tid < g.tail ? uint32_t(g.base16[g.head + 8 * g.nvec + tid]) : 0u;
         const PenCtx pc = pen_ctx(a, row, p);
+        // the slice pass's table of penalized patterns, staged in LDS (loads issued
+        // with the logits')
+        const uint16_t* tab = a.ptab + (rs + os) * kSL;
+        uint16_t* T = reinterpret_cast<uint16_t*>(lds + kOffTab);
+        const uint32_t ntab = pc.pen ? min(sh.slice_hist[os], uint32_t(kTabCap)) : 0u;
+        for (uint32_t i = tid; i < (ntab + 7u) / 8u; i += kT)
+            reinterpret_cast<uint4*>(T)[i] = reinterpret_cast<const uint4*>(tab)[i];
+        auto tab_at = [&](uint32_t rank) { return rank < ntab ? uint32_t(T[rank]) : uint32_t(tab[rank]); };
         // history flags: bit e of hmask for body element e of this thread; head / tail
         static_assert(kNV * 8 == 32, "a thread's body elements fill one 32-bit mask");
         const int nbv = max(0, min(kNV, g.nvec - kNV * tid));   // this thread's body vectors
@@ -1097,30 +1109,46 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
             hexcl = block_scan_lds(uint32_t(__builtin_popcount(hmask)), sh.scan, &nhist);
             h0 = sh.n_hash;
         }
-        const uint16_t* tab = a.ptab + (rs + os) * kSL;
         const uint32_t dk = sh.draw_key;
-        // raw patterns of the drawn key (+0 and -0 for key 0x8000)
+        // patterns of the drawn key (+0 and -0 for key 0x8000): a logit matches when
+        // its (penalized) pattern is one of them (the key map is one to one but
+        // for the zeros, and the drawn key is finite)
         const uint32_t P1 = unkey16(dk), P2 = dk == 0x8000u ? 0x8000u : P1;
         auto match = [&](uint32_t b) { return b == P1 || b == P2; };
-        auto match_pen = [&](uint32_t pb) { return Elem<DT>::finite_bits(pb) && key16(pb) == dk; };
         uint32_t bits = 0u;
         uint32_t r = h0 + hexcl;
+        if (!pc.pen || sh.slice_hist[os] <= uint32_t(kTabCap)) {   // (uniform) the table is staged whole
 #pragma unroll
-        for (int i = 0; i < kNV; ++i) {
-            const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            for (int i = 0; i < kNV; ++i) {
+                const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int e = 8 * i + j;
-                const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                const bool hist = (hmask >> e) & 1u;
-                const bool m = hist ? match_pen(uint32_t(tab[r])) : match(b);
-                r += hist ? 1u : 0u;
-                bits |= m ? 1u << e : 0u;
+                for (int j = 0; j < 8; ++j) {
+                    const int e = 8 * i + j;
+                    const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                    const bool hist = (hmask >> e) & 1u;
+                    const uint32_t pb = hist ? uint32_t(T[min(r, uint32_t(kTabCap - 1))]) : b;
+                    r += hist ? 1u : 0u;
+                    bits |= match(pb) ? 1u << e : 0u;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kNV; ++i) {
+                const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int e = 8 * i + j;
+                    const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                    const bool hist = (hmask >> e) & 1u;
+                    const uint32_t pb = hist ? tab_at(r) : b;
+                    r += hist ? 1u : 0u;
+                    bits |= match(pb) ? 1u << e : 0u;
+                }
             }
         }
         bits &= bodym;
-        const bool hm = tid < g.head && (hh ? match_pen(uint32_t(tab[hrank])) : match(hb));
-        const bool tm = tid < g.tail && (th ? match_pen(uint32_t(tab[h0 + nhist + trank])) : match(tb));
+        const bool hm = tid < g.head && match(hh ? tab_at(hrank) : hb);
+        const bool tm = tid < g.tail && match(th ? tab_at(h0 + nhist + trank) : tb);
         if (wave == 0) {   // (head and tail logits belong to threads < 8)
             const uint64_t hmk = ballot(hm), tmk = ballot(tm);
             if (lane == 0) { sh.hmask = uint32_t(hmk); sh.tmask = uint32_t(tmk); }
@@ -1346,15 +1374,19 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                     const uint64_t two = uint64_t(B[wd]) | (sft > 24u && wd + 1u < uint32_t(kBW) ? uint64_t(B[wd + 1u]) << 32 : 0ull);
                     return uint32_t(two >> sft) & 0xffu;
                 };
+                const unsigned char* B8 = reinterpret_cast<const unsigned char*>(B);
 #pragma unroll
                 for (int i = 0; i < kNV; ++i) {
                     const int vi = i * kT + tid;
                     if (vi < g.nvec) {
-                        const uint32_t h8 = hist8(uint32_t(g.head + 8 * vi));
+                        // (a history token adds 0 to its raw pattern's word: no per-element branch)
+                        const uint32_t h8 = g.head == 0 ? uint32_t(B8[vi]) : hist8(uint32_t(g.head + 8 * vi));
                         const uint32_t w4[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
 #pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            if (!((h8 >> j) & 1u)) hist_add((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t b = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                            atomicAdd(&H[b & 0x7fffu], ((h8 >> j) & 1u) ? 0u : ((b & 0x8000u) ? 0x10000u : 1u));
+                        }
                     }
                 }
                 if (tid < g.head && !((B[tid >> 5] >> (tid & 31)) & 1u)) hist_add(cur.hb);
@@ -1556,6 +1588,7 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                 hd[1] = sh.n_valid;
                 hd[2] = sh.flags;
                 hd[3] = sh.top_key;
+                hd[4 + kBins / 32] = nf;
                 sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u;
             }
             if (tid < kBins / 32) {
