@@ -7,8 +7,8 @@ penalties over 32,768-token int32 histories, an independent Philox stream per ro
 Five distinct input sets (~402 MB of logits) rotate across steps so the 256 MB
 Infinity Cache cannot serve repeats.
 
-One step is one decode step of all 128 lanes, a single kernel launch (every row
-takes the full-vocabulary route):
+One step is one decode step of all 128 lanes, one call (every row takes the
+full-vocabulary route: the slice kernel, then the merge kernel):
 
 * ``--route state`` (default): ``vi_sample_rows_state`` with record = 1.  Each
   lane's penalties come from its device penalty state (presence bitmap, count
@@ -19,9 +19,9 @@ takes the full-vocabulary route):
 
 With the state route, the history route is also timed (``--compare-steps``) and
 reported beside it.  Prints ONE JSON line: rows/s (whole job), achieved HBM GB/s
-of the kernel against MI355X's 8 TB/s peak (per-launch HIP events on the launch
-stream), the oracle's CPU rate on the same inputs, and a GPU-vs-oracle parity
-count for one step.
+of the call (both kernels) against MI355X's 8 TB/s peak (per-call HIP events on
+the launch stream), the oracle's CPU rate on the same inputs, and a GPU-vs-oracle
+parity count for one step.
 """
 from __future__ import annotations
 
@@ -220,9 +220,10 @@ def secondary(args):
 
 
 def traffic_from_profiles(route: str) -> float | None:
-    """HBM bytes per launch of the full-vocabulary kernel on `route`, from the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/ (None if absent)."""
-    f = ROOT / "profiles" / f"full_kernel_config5_{route}_traffic.md"
+    """HBM bytes per call of the full-vocabulary route (slice and merge kernels) on
+    `route`, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/
+    (None if absent)."""
+    f = ROOT / "profiles" / f"full_route_config5_{route}_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -413,7 +414,7 @@ def main():
                                "rep/presence/frequency penalties over 32,768-token histories, Philox per row",
                    "rows": rows, "vocabulary": VOCAB, "history": HISTORY, "input_sets": SETS,
                    "route": args.route, "penalty_state": state_info,
-                   "kernel": "full_kernel<bf16> (voidinfer_amd/csrc/sample_full.hip)"},
+                   "kernel": "slice_kernel<bf16> + merge_kernel<bf16> (voidinfer_amd/csrc/sample_slices.hip)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBPS, "traffic": traffic_from_profiles(args.route),
                      "bytes_per_launch": bytes_per_launch, "kernel_ms": kernel_ms,
