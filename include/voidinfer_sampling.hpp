@@ -30,6 +30,7 @@
 #include <cstdlib>
 #include <limits>
 #include <memory>
+#include <numeric>
 #include <optional>
 #include <span>
 #include <stdexcept>
@@ -388,6 +389,8 @@ inline constexpr std::uint64_t exl3_splitmix64(std::uint64_t x) noexcept {
 
 class Exl3RequestSamplingState {
 public:
+    // One speculative round's lease on the request's draws (begin() to commit()
+    // or rollback()).  Callers keep it and hand it back; they do not edit it.
     struct Transaction {
         const Exl3RequestSamplingState* owner = nullptr;
         std::uint64_t nonce = 0, acquisition = 0, base_counter = 0, tentative_counter = 0;
@@ -400,139 +403,148 @@ public:
                              std::uint64_t input_fingerprint, std::uint64_t seed,
                              Exl3SamplingReproducibility reproducibility =
                                  Exl3SamplingReproducibility::seeded_request_replay_across_reload)
-        : epoch_(engine_epoch), generation_(request_generation), fingerprint_(input_fingerprint), seed_(seed),
-          reproducibility_(reproducibility) {
-        if (epoch_ == 0 || generation_ == 0 || fingerprint_ == 0)
-            throw std::invalid_argument("request sampling identity has a zero field");
+        : id_{engine_epoch, request_generation, input_fingerprint, seed}, reproducibility_(reproducibility) {
+        if (id_.epoch == 0 || id_.generation == 0 || id_.fingerprint == 0)
+            throw std::invalid_argument("request identity needs a non-zero epoch, generation and input fingerprint");
     }
 
-    // Binds the state to one physical acquisition and root; refused while a
-    // transaction is open or after cancellation.
     void bind_acquisition(std::uint64_t acquisition, std::shared_ptr<const void> root_revision,
                           std::size_t accepted_prefix) {
-        if (cancelled() || acquisition == 0 || !root_revision || open_nonce_ != 0)
-            throw std::invalid_argument("sampling acquisition cannot be bound");
-        acquisition_ = acquisition;
-        root_ = std::move(root_revision);
-        prefix_ = accepted_prefix;
+        const bool refused = cancelled() || acquisition == 0 || !owned(root_revision) || lease_ != 0;
+        if (refused) throw std::invalid_argument("request state cannot take this acquisition now");
+        bound_.acquisition = acquisition;
+        bound_.root = std::move(root_revision);
+        progress_.prefix = accepted_prefix;
     }
 
     [[nodiscard]] Transaction begin(std::size_t accepted_prefix) {
-        if (cancelled() || acquisition_ == 0 || !root_ || open_nonce_ != 0 || nonce_source_ == 0 ||
-            accepted_prefix != prefix_)
-            throw std::logic_error("no sampling transaction can begin");
-        open_nonce_ = nonce_source_++;
+        const bool bound = bound_.acquisition != 0 && bound_.root != nullptr;
+        if (cancelled() || !bound || lease_ != 0 || next_lease_ == 0 || accepted_prefix != progress_.prefix)
+            throw std::logic_error("request state cannot open a round now");
+        lease_ = next_lease_++;
         Transaction t;
         t.owner = this;
-        t.nonce = open_nonce_;
-        t.acquisition = acquisition_;
-        t.base_counter = t.tentative_counter = counter_;
+        t.nonce = lease_;
+        t.acquisition = bound_.acquisition;
+        t.base_counter = progress_.draws;
+        t.tentative_counter = progress_.draws;
         t.accepted_prefix = accepted_prefix;
-        t.root_revision = root_;
+        t.root_revision = bound_.root;
         return t;
     }
 
     [[nodiscard]] std::uint64_t draw(Transaction& t) const {
-        require_current(t, false);
+        expect_live(t, false);
         if (t.tentative_counter == std::numeric_limits<std::uint64_t>::max())
-            throw std::overflow_error("sampling counter exhausted");
-        const std::uint64_t i = t.tentative_counter++;
-        return exl3_splitmix64(seed_ ^ fingerprint_ ^ generation_ ^ i);
+            throw std::overflow_error("request draw index exhausted");
+        return exl3_splitmix64(id_.seed ^ id_.fingerprint ^ id_.generation ^ t.tentative_counter++);
     }
 
     void claim_publication(Transaction& t) {
-        require_current(t, false);
-        if (t.publication_claimed) throw std::logic_error("sampling publication claimed twice");
+        expect_live(t, false);
+        if (t.publication_claimed) throw std::logic_error("round publication is already claimed");
         t.publication_claimed = true;
     }
 
-    // Commits the first `draws_to_commit` tentative draws and the new prefix;
-    // needs a claimed publication (which cancellation no longer revokes).
     void commit(Transaction& t, std::uint64_t draws_to_commit, std::size_t accepted_prefix,
                 std::shared_ptr<const void> new_root_revision) {
-        require_current(t, true);
-        const std::uint64_t drawn = t.tentative_counter - t.base_counter;
-        if (!t.publication_claimed || draws_to_commit > drawn || accepted_prefix < t.accepted_prefix ||
-            !new_root_revision || draws_to_commit > std::numeric_limits<std::uint64_t>::max() - counter_)
-            throw std::invalid_argument("sampling commit extent");
-        counter_ += draws_to_commit;
-        prefix_ = accepted_prefix;
-        root_ = std::move(new_root_revision);
-        close(t);
+        expect_live(t, true);
+        const std::uint64_t tentative = t.tentative_counter - t.base_counter;
+        const bool extent_ok = t.publication_claimed && draws_to_commit <= tentative &&
+                               accepted_prefix >= t.accepted_prefix && owned(new_root_revision) &&
+                               draws_to_commit <= std::numeric_limits<std::uint64_t>::max() - progress_.draws;
+        if (!extent_ok) throw std::invalid_argument("round commit outside what the round drew or claimed");
+        progress_.draws += draws_to_commit;
+        progress_.prefix = accepted_prefix;
+        bound_.root = std::move(new_root_revision);
+        end_round(t);
     }
 
     void rollback(Transaction& t) {
-        require_current(t, t.publication_claimed);
-        close(t);
+        expect_live(t, t.publication_claimed);
+        end_round(t);
     }
 
-    // Tokens the engine forced (control tokens) advance the prefix without
-    // consuming randomness, once they are resident.
     void advance_forced_control(std::size_t tokens, std::shared_ptr<const void> new_root_revision,
                                 bool resident_committed) {
-        if (!resident_committed || tokens == 0 || acquisition_ == 0 || open_nonce_ != 0 || !new_root_revision ||
-            tokens > std::numeric_limits<std::size_t>::max() - prefix_)
-            throw std::invalid_argument("forced control advance refused");
-        prefix_ += tokens;
-        root_ = std::move(new_root_revision);
+        const bool ok = resident_committed && tokens != 0 && bound_.acquisition != 0 && lease_ == 0 &&
+                        owned(new_root_revision) && tokens <= std::numeric_limits<std::size_t>::max() - progress_.prefix;
+        if (!ok) throw std::invalid_argument("forced control tokens cannot advance the request now");
+        progress_.prefix += tokens;
+        bound_.root = std::move(new_root_revision);
     }
 
     void cancel() noexcept { cancelled_.store(true, std::memory_order_release); }
 
-    [[nodiscard]] std::uint64_t engine_epoch() const noexcept { return epoch_; }
-    [[nodiscard]] std::uint64_t request_generation() const noexcept { return generation_; }
-    [[nodiscard]] std::uint64_t committed_draws() const noexcept { return counter_; }
-    [[nodiscard]] std::size_t committed_prefix() const noexcept { return prefix_; }
+    [[nodiscard]] std::uint64_t engine_epoch() const noexcept { return id_.epoch; }
+    [[nodiscard]] std::uint64_t request_generation() const noexcept { return id_.generation; }
+    [[nodiscard]] std::uint64_t committed_draws() const noexcept { return progress_.draws; }
+    [[nodiscard]] std::size_t committed_prefix() const noexcept { return progress_.prefix; }
     [[nodiscard]] Exl3SamplingReproducibility reproducibility() const noexcept { return reproducibility_; }
     [[nodiscard]] bool cancelled() const noexcept { return cancelled_.load(std::memory_order_acquire); }
 
 private:
-    void require_current(const Transaction& t, bool claimed_survives_cancel) const {
-        const bool cancel_blocks = cancelled() && !(claimed_survives_cancel && t.publication_claimed);
-        const bool same_root = t.root_revision.get() == root_.get() && !t.root_revision.owner_before(root_) &&
-                               !root_.owner_before(t.root_revision);
-        if (cancel_blocks || t.owner != this || open_nonce_ == 0 || t.nonce != open_nonce_ ||
-            t.acquisition != acquisition_ || !same_root)
-            throw std::logic_error("sampling transaction is stale or foreign");
+    // Why a round handed back is not the live one (none: it is).
+    enum class RoundFault : std::uint8_t { none, cancelled, not_ours, no_open_round, other_round, rebound, other_root };
+
+    [[nodiscard]] RoundFault fault(const Transaction& t, bool claimed_outlives_cancel) const noexcept {
+        if (cancelled() && !(claimed_outlives_cancel && t.publication_claimed)) return RoundFault::cancelled;
+        if (t.owner != this) return RoundFault::not_ours;
+        if (lease_ == 0) return RoundFault::no_open_round;
+        if (t.nonce != lease_) return RoundFault::other_round;
+        if (t.acquisition != bound_.acquisition) return RoundFault::rebound;
+        const auto& r = t.root_revision;
+        const bool same_root = r.get() == bound_.root.get() && !r.owner_before(bound_.root) && !bound_.root.owner_before(r);
+        return same_root ? RoundFault::none : RoundFault::other_root;
     }
-    void close(Transaction& t) noexcept {
-        open_nonce_ = 0;
+    void expect_live(const Transaction& t, bool claimed_outlives_cancel) const {
+        static constexpr const char* kWhy[] = {"", "request cancelled", "round of another request state",
+                                               "no round is open", "round already closed or superseded",
+                                               "request rebound to another acquisition", "root revision changed"};
+        const RoundFault f = fault(t, claimed_outlives_cancel);
+        if (f != RoundFault::none) throw std::logic_error(std::string("sampling round refused: ") + kWhy[int(f)]);
+    }
+    // (a root revision without an owner cannot be kept alive by the state)
+    static bool owned(const std::shared_ptr<const void>& r) noexcept { return r != nullptr && r.use_count() > 0; }
+    void end_round(Transaction& t) noexcept {
+        lease_ = 0;
         t.owner = nullptr;
         t.nonce = 0;
         t.publication_claimed = false;
         t.root_revision.reset();
     }
 
-    std::uint64_t epoch_ = 0, generation_ = 0, fingerprint_ = 0, seed_ = 0;
+    struct Identity { std::uint64_t epoch, generation, fingerprint, seed; } id_;
     Exl3SamplingReproducibility reproducibility_;
-    std::uint64_t acquisition_ = 0, counter_ = 0, nonce_source_ = 1, open_nonce_ = 0;
-    std::size_t prefix_ = 0;
-    std::shared_ptr<const void> root_;
+    struct Binding { std::uint64_t acquisition = 0; std::shared_ptr<const void> root; } bound_;
+    struct Progress { std::uint64_t draws = 0; std::size_t prefix = 0; } progress_;
+    std::uint64_t lease_ = 0;        // the open round's id (0: none)
+    std::uint64_t next_lease_ = 1;   // (0 once every id is used)
     std::atomic<bool> cancelled_{false};
 };
 
 // =====================================================================
-// Draw window of one speculative round — src/exl3/sampling_window_transaction.h:17-128.
-// Each decided token owns two draws (proposal, acceptance); the first
-// rejection adds a correction draw and seals the window; a commit counts the
-// draws of the published tokens only.
+// One speculative round's window of draws — src/exl3/sampling_window_transaction.h:17-128.
+// Every decided token spent a proposal draw and an acceptance draw; a rejected
+// one also spent a correction draw and closes the round to further tokens.  A
+// commit of n published tokens commits the draws of those n tokens only.
 // =====================================================================
 
 class Exl3SamplingWindowTransaction {
 public:
     Exl3SamplingWindowTransaction(Exl3RequestSamplingState& state, std::size_t accepted_prefix,
                                   std::size_t maximum_tokens)
-        : state_(&state), prefix_(accepted_prefix), capacity_(maximum_tokens) {
+        : state_(&state), first_(accepted_prefix), capacity_(maximum_tokens) {
         if (maximum_tokens == 0 || maximum_tokens > std::numeric_limits<std::size_t>::max() - accepted_prefix)
-            throw std::invalid_argument("sampling window needs an output capacity");
-        draws_per_token_.reserve(maximum_tokens);
-        txn_ = state.begin(accepted_prefix);
-        active_ = true;
+            throw std::invalid_argument("a sampling window needs room for at least one token");
+        spent_.reserve(maximum_tokens);
+        round_ = state.begin(accepted_prefix);
+        stage_ = Stage::idle;
     }
 
     ~Exl3SamplingWindowTransaction() {
-        if (active_ && state_ && !state_->cancelled()) {
-            try { state_->rollback(txn_); } catch (...) {}
+        if (stage_ != Stage::closed && !state_->cancelled()) {
+            try { state_->rollback(round_); } catch (...) {}
         }
     }
 
@@ -540,90 +552,93 @@ public:
     Exl3SamplingWindowTransaction& operator=(const Exl3SamplingWindowTransaction&) = delete;
 
     [[nodiscard]] std::uint64_t draw_proposal() {
-        require_open();
-        if (proposal_drawn_ || acceptance_drawn_ || draws_per_token_.size() >= capacity_)
-            throw std::logic_error("proposal draw out of order");
-        proposal_drawn_ = true;
-        return state_->draw(txn_);
+        expect_open_to_tokens();
+        if (stage_ != Stage::idle || spent_.size() >= capacity_)
+            throw std::logic_error("a proposal draw needs a decided previous token and room in the window");
+        stage_ = Stage::proposed;   // (kept when the state refuses the draw)
+        return state_->draw(round_);
     }
 
     [[nodiscard]] std::uint64_t draw_acceptance() {
-        require_open();
-        if (!proposal_drawn_ || acceptance_drawn_) throw std::logic_error("acceptance draw out of order");
-        acceptance_drawn_ = true;
-        return state_->draw(txn_);
+        expect_open_to_tokens();
+        if (stage_ != Stage::proposed) throw std::logic_error("an acceptance draw follows a proposal draw");
+        stage_ = Stage::acceptance_drawn;
+        return state_->draw(round_);
     }
 
     void accept_proposal() {
-        require_decision_pending();
-        draws_per_token_.push_back(2);
-        proposal_drawn_ = acceptance_drawn_ = false;
+        expect_decision();
+        spent_.push_back(2);
+        stage_ = Stage::idle;
     }
 
     [[nodiscard]] std::uint64_t reject_and_draw_correction() {
-        require_decision_pending();
-        const std::uint64_t correction = state_->draw(txn_);
-        draws_per_token_.push_back(3);
-        proposal_drawn_ = acceptance_drawn_ = false;
+        expect_decision();
+        const std::uint64_t correction = state_->draw(round_);
+        spent_.push_back(3);
+        stage_ = Stage::idle;
         sealed_ = true;
         return correction;
     }
 
     void seal_stop_boundary() {
-        require_open();
-        if (proposal_drawn_ || acceptance_drawn_) throw std::logic_error("stop inside an undecided token");
+        expect_open_to_tokens();
+        if (stage_ != Stage::idle) throw std::logic_error("a stop cannot split an undecided token");
         sealed_ = true;
     }
 
     void claim_publication() {
-        require_active();
-        if (proposal_drawn_ || acceptance_drawn_) throw std::logic_error("publication with an undecided token");
-        state_->claim_publication(txn_);
+        expect_round();
+        if (stage_ != Stage::idle) throw std::logic_error("publication with an undecided token");
+        state_->claim_publication(round_);
         claimed_ = true;
     }
 
     void commit(std::size_t published_tokens, std::shared_ptr<const void> new_root_revision) {
-        require_active();
-        if (!claimed_ || proposal_drawn_ || acceptance_drawn_ || published_tokens > draws_per_token_.size())
-            throw std::invalid_argument("sampling publication extent");
-        std::uint64_t draws = 0;
-        for (std::size_t i = 0; i < published_tokens; ++i) draws += draws_per_token_[i];
-        state_->commit(txn_, draws, prefix_ + published_tokens, std::move(new_root_revision));
-        active_ = false;
+        expect_round();
+        if (!claimed_ || stage_ != Stage::idle || published_tokens > spent_.size())
+            throw std::invalid_argument("commit needs a claimed publication of decided tokens");
+        const std::uint64_t draws = std::accumulate(spent_.begin(), spent_.begin() + std::ptrdiff_t(published_tokens),
+                                                    std::uint64_t(0));
+        state_->commit(round_, draws, first_ + published_tokens, std::move(new_root_revision));
+        stage_ = Stage::closed;
     }
 
     void rollback() {
-        require_active();
-        proposal_drawn_ = acceptance_drawn_ = false;
-        state_->rollback(txn_);
-        active_ = false;
+        expect_round();
+        stage_ = Stage::idle;
+        state_->rollback(round_);
+        stage_ = Stage::closed;
     }
 
-    [[nodiscard]] std::size_t decided_tokens() const noexcept { return draws_per_token_.size(); }
+    [[nodiscard]] std::size_t decided_tokens() const noexcept { return spent_.size(); }
     [[nodiscard]] bool sealed() const noexcept { return sealed_; }
 
 private:
-    void require_active() const {
-        if (!active_ || !state_) throw std::logic_error("sampling window is closed");
+    // Where the current token stands; closed once committed or rolled back.
+    enum class Stage : std::uint8_t { idle, proposed, acceptance_drawn, closed };
+
+    void expect_round() const {
+        if (stage_ == Stage::closed) throw std::logic_error("the sampling window is closed");
     }
-    void require_open() const {
-        require_active();
-        if (sealed_) throw std::logic_error("sampling window is sealed");
+    void expect_open_to_tokens() const {
+        expect_round();
+        if (sealed_) throw std::logic_error("the sampling window takes no more tokens");
     }
-    void require_decision_pending() const {
-        require_open();
-        if (!acceptance_drawn_) throw std::logic_error("acceptance draw missing");
+    void expect_decision() const {
+        expect_open_to_tokens();
+        if (stage_ != Stage::acceptance_drawn) throw std::logic_error("a decision needs the acceptance draw");
     }
 
-    Exl3RequestSamplingState* state_ = nullptr;
-    std::size_t prefix_ = 0, capacity_ = 0;
-    std::vector<std::uint8_t> draws_per_token_;
-    Exl3RequestSamplingState::Transaction txn_;
-    bool active_ = false, proposal_drawn_ = false, acceptance_drawn_ = false;
+    Exl3RequestSamplingState* state_;
+    std::size_t first_, capacity_;
+    std::vector<std::uint8_t> spent_;   // draws spent by each decided token (2, or 3 with a correction)
+    Exl3RequestSamplingState::Transaction round_;
+    Stage stage_ = Stage::closed;
     bool sealed_ = false, claimed_ = false;
 };
 
-// Stop / control-token accounting — src/exl3/sampling_control_stop_semantics.h:13-42.
+// Forced control tokens and terminal tokens — src/exl3/sampling_control_stop_semantics.h:13-42.
 struct Exl3SamplingPublicationCount {
     std::size_t resident_tokens = 0, visible_tokens = 0;
     bool terminal = false, terminal_visible = false;
@@ -631,26 +646,24 @@ struct Exl3SamplingPublicationCount {
 
 class Exl3SamplingControlStopSemantics {
 public:
+    // Control tokens the engine forced advance the prefix once resident; they
+    // spend no draw.
     static void commit_forced_control_after_resident(Exl3RequestSamplingState& state, std::size_t tokens,
                                                      std::shared_ptr<const void> new_root_revision) {
         state.advance_forced_control(tokens, std::move(new_root_revision), true);
     }
     static void claim_model_publication(Exl3SamplingWindowTransaction& window) { window.claim_publication(); }
-    // A terminal token that is resident but not published stays out of the
-    // visible count; its draws are still committed.
+    // All resident tokens' draws are committed; a terminal token the caller does
+    // not publish is left out of the visible count only.
     static Exl3SamplingPublicationCount commit_model_after_resident(Exl3SamplingWindowTransaction& window,
                                                                     std::size_t resident_tokens, bool terminal,
                                                                     bool publish_terminal,
                                                                     std::shared_ptr<const void> new_root_revision) {
         if (resident_tokens == 0 || (publish_terminal && !terminal))
-            throw std::invalid_argument("terminal publication extent");
+            throw std::invalid_argument("publishing a terminal token needs one among the resident tokens");
         window.commit(resident_tokens, std::move(new_root_revision));
-        Exl3SamplingPublicationCount c;
-        c.resident_tokens = resident_tokens;
-        c.visible_tokens = resident_tokens - ((terminal && !publish_terminal) ? 1u : 0u);
-        c.terminal = terminal;
-        c.terminal_visible = terminal && publish_terminal;
-        return c;
+        const bool hidden_terminal = terminal && !publish_terminal;
+        return {resident_tokens, resident_tokens - (hidden_terminal ? 1u : 0u), terminal, terminal && publish_terminal};
     }
     static void abandon_before_correction(Exl3SamplingWindowTransaction& window) { window.rollback(); }
 };
@@ -717,22 +730,26 @@ inline int exl3_promote_sibling(Exl3OuterDecision& decision, std::span<const std
 
 // =====================================================================
 // Verification tree of a DFlash2 round — src/exl3/verification_tree.h:27-112.
-// A chain prefix of the drafts plus sibling leaves (the draft's next-best
-// candidates at each depth), chosen to maximise the expected committed tokens
-// per verifier round time (1 + E[accepted]) / (1 + row_cost * rows).  Node
-// acceptance comes from the draft's top-16 unary softmax: a chain token's hit
-// rate by its probability decile, a sibling's by its unary rank (1..3 among
-// the non-chain candidates) and decile, from the reference's measured tables.
+// The tree is a prefix of the draft chain plus leaves: at each depth, the
+// draft's best candidates other than the chain token, each standing in for the
+// chain token at that position.  Of all (chain length, leaves) shapes within
+// the row budget, the builder keeps the first with the highest
+// (1 + expected accepted tokens) / (1 + row_cost x rows).  Expected acceptance
+// comes from the draft's top-16 scores through a softmax: the chain token's by
+// the tenth its probability falls in, a leaf's by its rank among the other
+// candidates (three ranks) and its probability's tenth, read from tables
+// measured on the engine's rounds.
 // =====================================================================
 
 struct Exl3VerificationTree {
-    int chain_drafts = 0;                   // chain rows 1..chain_drafts
+    int chain_drafts = 0;                   // drafts 1..chain_drafts are verified as a chain
     std::vector<std::int64_t> sibling_tokens;
-    std::vector<int> sibling_offsets;       // logical offset (depth) of each leaf
+    std::vector<int> sibling_offsets;       // the chain position each leaf stands in for (1-based)
 };
 
-// Row cost relative to the fixed verifier round, and the empirical hit-rate
-// tables (verification_tree.h:33-40; the values are the reference's data).
+// Row cost as a fraction of a verifier round, and the measured hit rates by
+// probability tenth (verification_tree.h:31-40): chain tokens, then leaves of
+// rank 1, 2, 3.
 inline constexpr float kExl3TreeRowCost = 0.0141f;
 inline constexpr std::array<float, 10> kExl3TreeChainHit{
     0.32f, 0.38f, 0.35f, 0.44f, 0.42f, 0.49f, 0.57f, 0.67f, 0.78f, 0.97f};
@@ -742,92 +759,111 @@ inline constexpr std::array<std::array<float, 10>, 3> kExl3TreeSiblingHit{{
     {0.03f, 0.10f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f, 0.15f},
 }};
 
-// drafts: chain proposals at depths 1..D; candidate_ids / candidate_unary:
-// [D][16] in unary order (the draft's top-16); budget: verifier rows besides
-// the anchor.  The float arithmetic, the scan order over (rows, chain) and the
-// partial selection of the leaf pool follow the reference step for step: the
-// chosen tree, ties included, is part of the contract.  Candidate arrays
-// shorter than D x 16 are refused (std::invalid_argument).
+namespace tree_detail {
+inline constexpr int kCandidates = 16, kLeafRanks = 3;
+
+struct LeafOption {
+    float expected;        // expected accepted tokens it adds (hit rate x chance its position is reached)
+    int position;          // 1-based chain position it stands in for
+    std::int64_t token;    // -1: no such candidate
+};
+
+// What one depth of the draft offers: the chain token's hit rate and the best
+// three other candidates as leaves.
+struct DepthOffer {
+    float chain_hit = 0.0f;
+    std::array<LeafOption, kLeafRanks> leaves{};
+};
+
+inline int probability_tenth(float p) { return std::clamp(static_cast<int>(p * 10.0f), 0, 9); }
+
+inline DepthOffer offer_at(const std::int64_t* ids, const float* scores, std::int64_t chain_token, int depth) {
+    // softmax of the candidate scores, accumulated in candidate order
+    const float peak = *std::max_element(scores, scores + kCandidates);
+    std::array<float, kCandidates> weight{};
+    float total = 0.0f;
+    for (int c = 0; c < kCandidates; ++c) {
+        weight[std::size_t(c)] = std::exp(scores[c] - peak);
+        total += weight[std::size_t(c)];
+    }
+    DepthOffer offer;
+    float chain_p = 0.0f;   // (of the chain token's last occurrence in the list)
+    for (int c = 0; c < kCandidates; ++c)
+        if (ids[c] == chain_token) chain_p = weight[std::size_t(c)] / total;
+    offer.chain_hit = kExl3TreeChainHit[std::size_t(probability_tenth(chain_p))];
+    // candidates by descending score, equal scores in list order
+    std::array<int, kCandidates> by_score{};
+    std::iota(by_score.begin(), by_score.end(), 0);
+    std::stable_sort(by_score.begin(), by_score.end(), [&](int x, int y) { return scores[x] > scores[y]; });
+    int rank = 0;
+    for (const int c : by_score) {
+        if (rank == kLeafRanks) break;
+        if (ids[c] == chain_token) continue;
+        const float hit = kExl3TreeSiblingHit[std::size_t(rank)][std::size_t(probability_tenth(weight[std::size_t(c)] / total))];
+        offer.leaves[std::size_t(rank++)] = {hit, depth + 1, ids[c]};
+    }
+    for (; rank < kLeafRanks; ++rank) offer.leaves[std::size_t(rank)] = {0.0f, depth + 1, -1};
+    return offer;
+}
+}  // namespace tree_detail
+
+// drafts: the chain proposals at positions 1..D; candidate_ids /
+// candidate_unary: [D][16], the draft's top-16 per position in unary order;
+// budget: verifier rows besides the anchor.  Ties are settled as the reference
+// settles them: equal scores keep list order; among leaves of equal value,
+// the order std::partial_sort leaves a pool built in the same order in; the
+// first strictly best shape wins.  Candidate arrays shorter than D x 16 are
+// refused (std::invalid_argument).
 inline Exl3VerificationTree exl3_build_verification_tree(std::span<const std::int64_t> drafts,
                                                          std::span<const std::int64_t> candidate_ids,
                                                          std::span<const float> candidate_unary, int budget,
                                                          int max_siblings, float row_cost = kExl3TreeRowCost) {
-    constexpr int kTop = 16, kRanks = 3;
-    const int depth = std::min(static_cast<int>(drafts.size()), budget);
-    if (depth > 0 && (candidate_ids.size() < std::size_t(depth) * kTop ||
-                      candidate_unary.size() < std::size_t(depth) * kTop))
-        throw std::invalid_argument("verification tree candidate extent");
-    struct Leaf {
-        float value;
-        int offset;
-        std::int64_t token;
-    };
-    const auto decile = [](float pr) { return std::clamp(static_cast<int>(pr * 10.0f), 0, 9); };
-    // per depth: the chain token's hit rate and up to three sibling leaves
-    std::vector<float> hit(std::size_t(std::max(depth, 0)));
-    std::vector<std::array<Leaf, kRanks>> leaf(std::size_t(std::max(depth, 0)));
-    for (int d = 0; d < depth; ++d) {
-        const std::int64_t* id = candidate_ids.data() + std::size_t(d) * kTop;
-        const float* un = candidate_unary.data() + std::size_t(d) * kTop;
-        const std::int64_t chain_token = drafts[std::size_t(d)];
-        const float top = *std::max_element(un, un + kTop);
-        std::array<float, kTop> w{};
-        float total = 0.0f;
-        for (int c = 0; c < kTop; ++c) total += w[std::size_t(c)] = std::exp(un[c] - top);
-        float chain_pr = 0.0f;   // (the last candidate carrying the chain token)
-        for (int c = 0; c < kTop; ++c)
-            if (id[c] == chain_token) chain_pr = w[std::size_t(c)] / total;
-        hit[std::size_t(d)] = kExl3TreeChainHit[std::size_t(decile(chain_pr))];
-        std::array<int, kTop> rank_order{};
-        for (int c = 0; c < kTop; ++c) rank_order[std::size_t(c)] = c;
-        std::stable_sort(rank_order.begin(), rank_order.end(), [&](int x, int y) { return un[x] > un[y]; });
-        int r = 0;
-        for (int i = 0; i < kTop && r < kRanks; ++i) {
-            const int c = rank_order[std::size_t(i)];
-            if (id[c] == chain_token) continue;
-            leaf[std::size_t(d)][std::size_t(r)] = {
-                kExl3TreeSiblingHit[std::size_t(r)][std::size_t(decile(w[std::size_t(c)] / total))], d + 1, id[c]};
-            ++r;
+    using namespace tree_detail;
+    const int depth = std::max(0, std::min(static_cast<int>(drafts.size()), budget));
+    if (candidate_ids.size() < std::size_t(depth) * kCandidates || candidate_unary.size() < std::size_t(depth) * kCandidates)
+        throw std::invalid_argument("verification tree needs 16 candidates per draft position");
+    std::vector<DepthOffer> offers;
+    offers.reserve(std::size_t(depth));
+    for (int d = 0; d < depth; ++d)
+        offers.push_back(offer_at(candidate_ids.data() + std::size_t(d) * kCandidates,
+                                  candidate_unary.data() + std::size_t(d) * kCandidates, drafts[std::size_t(d)], d));
+    // For a chain of length L: its expected accepted length (the chance each of
+    // its positions is reached and hit, summed) and the leaves it can carry
+    // (each leaf's hit rate times the chance its position is reached).
+    std::vector<float> chain_gain(std::size_t(depth) + 1, 0.0f);
+    std::vector<std::vector<LeafOption>> carried(std::size_t(depth) + 1);
+    for (int len = 1; len <= depth; ++len) {
+        float reach = 1.0f, gain = 0.0f;
+        for (int d = 0; d < len; ++d) {
+            for (const LeafOption& l : offers[std::size_t(d)].leaves)
+                if (l.token >= 0) carried[std::size_t(len)].push_back({reach * l.expected, l.position, l.token});
+            reach *= offers[std::size_t(d)].chain_hit;
+            gain += reach;
         }
-        for (; r < kRanks; ++r) leaf[std::size_t(d)][std::size_t(r)] = {0.0f, d + 1, -1};
-    }
-    // per chain length: its expected accepted chain length and its leaf pool
-    // (each leaf weighted by the chain's survival down to its parent)
-    std::vector<float> chain_value(std::size_t(std::max(depth, 0)) + 1, 0.0f);
-    std::vector<std::vector<Leaf>> pool(std::size_t(std::max(depth, 0)) + 1);
-    for (int chain = 1; chain <= depth; ++chain) {
-        float survive = 1.0f, value = 0.0f;
-        auto& pl = pool[std::size_t(chain)];
-        for (int d = 0; d < chain; ++d) {
-            for (const Leaf& l : leaf[std::size_t(d)])
-                if (l.token >= 0) pl.push_back({survive * l.value, l.offset, l.token});
-            survive *= hit[std::size_t(d)];
-            value += survive;
-        }
-        chain_value[std::size_t(chain)] = value;
+        chain_gain[std::size_t(len)] = gain;
     }
     Exl3VerificationTree best;
     float best_rate = -1.0f;
-    std::vector<Leaf> scratch;
-    for (int nodes = 1; nodes <= budget; ++nodes) {
-        for (int chain = std::max(1, nodes - std::max(0, max_siblings)); chain <= std::min(depth, nodes); ++chain) {
-            const int count = nodes - chain;
-            if (count > static_cast<int>(pool[std::size_t(chain)].size())) continue;
-            scratch = pool[std::size_t(chain)];
-            std::partial_sort(scratch.begin(), scratch.begin() + count, scratch.end(),
-                              [](const Leaf& x, const Leaf& y) { return x.value > y.value; });
-            float value = chain_value[std::size_t(chain)];
-            for (int i = 0; i < count; ++i) value += scratch[std::size_t(i)].value;
-            const float rate = (1.0f + value) / (1.0f + row_cost * static_cast<float>(nodes));
-            if (rate > best_rate) {
-                best_rate = rate;
-                best.chain_drafts = chain;
-                best.sibling_tokens.clear();
-                best.sibling_offsets.clear();
-                for (int i = 0; i < count; ++i) {
-                    best.sibling_tokens.push_back(scratch[std::size_t(i)].token);
-                    best.sibling_offsets.push_back(scratch[std::size_t(i)].offset);
-                }
+    std::vector<LeafOption> pick;
+    for (int rows = 1; rows <= budget; ++rows) {
+        const int shortest = std::max(1, rows - std::max(0, max_siblings)), longest = std::min(depth, rows);
+        for (int len = shortest; len <= longest; ++len) {
+            const int leaves = rows - len;
+            if (leaves > static_cast<int>(carried[std::size_t(len)].size())) continue;
+            pick = carried[std::size_t(len)];
+            std::partial_sort(pick.begin(), pick.begin() + leaves, pick.end(),
+                              [](const LeafOption& x, const LeafOption& y) { return x.expected > y.expected; });
+            float gain = chain_gain[std::size_t(len)];
+            for (int i = 0; i < leaves; ++i) gain += pick[std::size_t(i)].expected;
+            const float rate = (1.0f + gain) / (1.0f + row_cost * static_cast<float>(rows));
+            if (!(rate > best_rate)) continue;
+            best_rate = rate;
+            best.chain_drafts = len;
+            best.sibling_tokens.resize(std::size_t(leaves));
+            best.sibling_offsets.resize(std::size_t(leaves));
+            for (int i = 0; i < leaves; ++i) {
+                best.sibling_tokens[std::size_t(i)] = pick[std::size_t(i)].token;
+                best.sibling_offsets[std::size_t(i)] = pick[std::size_t(i)].position;
             }
         }
     }
@@ -835,7 +871,10 @@ inline Exl3VerificationTree exl3_build_verification_tree(std::span<const std::in
 }
 
 // FP64 rejection sampling of one speculative position —
-// src/exl3/sampled_acceptance_reference.h:15-89.
+// src/exl3/sampled_acceptance_reference.h:15-89.  The proposed token was drawn
+// from the draft's q; it is kept when the acceptance uniform is below
+// min(1, p / q), otherwise the correction uniform draws from the normalised
+// residual max(0, p - q) by inverse CDF in token-id order.
 struct Exl3SampledAcceptanceOutcome {
     bool accepted = false;
     bool correction_draw_used = false;
@@ -845,66 +884,67 @@ struct Exl3SampledAcceptanceOutcome {
 };
 
 class Exl3IndependentAcceptanceReference {
-    static constexpr double kNormTolerance = 1e-9;
-
-    static void require_distribution(std::span<const double> v) {
-        if (v.empty()) throw std::invalid_argument("sampled distribution is empty");
-        double sum = 0.0;
-        for (const double x : v) {
-            if (!(std::isfinite(x) && x >= 0.0 && x <= 1.0))
-                throw std::invalid_argument("sampled distribution entry outside [0, 1]");
-            sum += x;
-        }
-        if (!std::isfinite(sum) || std::abs(sum - 1.0) > kNormTolerance)
-            throw std::invalid_argument("sampled distribution does not sum to one");
-    }
-    static void require_uniform(double u) {
-        if (!(std::isfinite(u) && u >= 0.0 && u < 1.0)) throw std::invalid_argument("uniform draw outside [0, 1)");
-    }
-
 public:
-    // accept iff u_a < min(1, p/q); otherwise the correction is the inverse CDF
-    // of the normalised residual max(0, p - q) at u_c, in token-id order.
     static Exl3SampledAcceptanceOutcome evaluate(std::span<const double> target_p, std::span<const double> draft_q,
                                                  std::uint32_t proposed_token, double acceptance_draw,
                                                  double correction_draw) {
-        require_distribution(target_p);
-        require_distribution(draft_q);
-        require_uniform(acceptance_draw);
-        require_uniform(correction_draw);
+        // input checks, in this order: p, q, the two uniforms, the extents, q of the proposal
+        for (const std::span<const double> dist : {target_p, draft_q})
+            if (const char* why = distribution_fault(dist)) throw std::invalid_argument(why);
+        for (const double u : {acceptance_draw, correction_draw})
+            if (!(std::isfinite(u) && u >= 0.0 && u < 1.0)) throw std::invalid_argument("uniform draw outside [0, 1)");
         if (target_p.size() != draft_q.size() || proposed_token >= target_p.size())
-            throw std::invalid_argument("acceptance distribution extent");
-        const double q = draft_q[proposed_token];
-        if (q == 0.0) throw std::invalid_argument("proposed token has zero draft probability");
+            throw std::invalid_argument("p, q and the proposed token disagree on the vocabulary");
+        if (draft_q[proposed_token] == 0.0)
+            throw std::invalid_argument("the proposed token has zero draft probability");
+
         Exl3SampledAcceptanceOutcome out;
-        out.acceptance_probability = std::min(1.0, target_p[proposed_token] / q);
-        if (acceptance_draw < out.acceptance_probability) {
-            out.accepted = true;
+        out.acceptance_probability = std::min(1.0, target_p[proposed_token] / draft_q[proposed_token]);
+        out.accepted = acceptance_draw < out.acceptance_probability;
+        if (out.accepted) {
             out.token = proposed_token;
             return out;
         }
-        out.residual.resize(target_p.size());
-        double mass = 0.0;
-        for (std::size_t i = 0; i < target_p.size(); ++i) {
-            out.residual[i] = std::max(0.0, target_p[i] - draft_q[i]);
-            mass += out.residual[i];
-        }
-        if (!std::isfinite(mass) || mass <= kNormTolerance)
-            throw std::logic_error("rejection left no residual mass");
-        for (double& r : out.residual) r /= mass;
+        out.residual = normalised_residual(target_p, draft_q);
         out.correction_draw_used = true;
-        double cum = 0.0;
-        std::uint32_t last_positive = 0;
-        for (std::uint32_t t = 0; t < out.residual.size(); ++t) {
-            if (out.residual[t] > 0.0) last_positive = t;
-            cum += out.residual[t];
-            if (correction_draw < cum) {
-                out.token = t;
-                return out;
-            }
-        }
-        out.token = last_positive;  // round-off: the last token the residual supports
+        out.token = inverse_cdf(out.residual, correction_draw);
         return out;
+    }
+
+private:
+    static constexpr double kSumTolerance = 1e-9;
+
+    // nullptr when `v` is a distribution: entries in [0, 1] summing to 1 within
+    // kSumTolerance
+    static const char* distribution_fault(std::span<const double> v) {
+        if (v.empty()) return "empty distribution";
+        double sum = 0.0;
+        for (const double x : v) {
+            if (!std::isfinite(x) || x < 0.0 || x > 1.0) return "distribution entry outside [0, 1]";
+            sum += x;
+        }
+        return std::isfinite(sum) && std::abs(sum - 1.0) <= kSumTolerance ? nullptr : "distribution does not sum to one";
+    }
+    // max(0, p - q), summed in id order, then divided by that sum
+    static std::vector<double> normalised_residual(std::span<const double> p, std::span<const double> q) {
+        std::vector<double> r(p.size());
+        double mass = 0.0;
+        for (std::size_t i = 0; i < p.size(); ++i) mass += (r[i] = std::max(0.0, p[i] - q[i]));
+        if (!std::isfinite(mass) || mass <= kSumTolerance) throw std::logic_error("a rejection left no residual mass");
+        for (double& x : r) x /= mass;
+        return r;
+    }
+    // first id whose running sum exceeds u; past the end (rounding), the last id
+    // with residual mass
+    static std::uint32_t inverse_cdf(const std::vector<double>& r, double u) {
+        double running = 0.0;
+        std::uint32_t last_supported = 0;
+        for (std::uint32_t t = 0; t < r.size(); ++t) {
+            if (r[t] > 0.0) last_supported = t;
+            running += r[t];
+            if (u < running) return t;
+        }
+        return last_supported;
     }
 };
 
@@ -1182,36 +1222,13 @@ struct Exl3SampledAdmissionDecision {
 
 class Exl3SampledAuthorityBoundary {
 public:
-    // The gates in order; the first that fails names the disposition.
+    // Admission gates (sampled_authority_boundary.h:58-98), in the contract's
+    // order: the first gate a request fails names its disposition; one that
+    // passes them all is source-ready.
     static Exl3SampledAdmissionDecision decide(const Exl3SampledAdmissionRequest& r) noexcept {
-        using D = Exl3SampledAdmissionDisposition;
-        if (!r.policy.requires_sampled_distribution()) return {D::greedy};
-        if (!r.draft_availability.supports(Exl3SampledAcceptanceMethod::independent_rejection_with_residual))
-            return {D::draft_distribution_unavailable};
-        if (r.exposure != Exl3SampledApiExposure::unqualified_source_api) return {D::public_sampled_disabled};
-        if (!r.request_state || r.request_state->cancelled() ||
-            r.request_state->request_generation() != r.request_generation ||
-            r.request_state->committed_prefix() != static_cast<std::size_t>(r.first_position))
-            return {D::request_state_unavailable};
-        if (!r.draft_q) return {D::draft_distribution_invalid};
-        if (!r.target_p) return {D::target_distribution_unavailable};
-        try {
-            r.draft_q->require(Exl3SampledAcceptanceMethod::independent_rejection_with_residual, r.rows,
-                               r.vocabulary, r.request_generation, r.root_revision, r.first_position);
-        } catch (...) {
-            return {D::draft_distribution_invalid};
-        }
-        try {
-            Exl3SelectionAuthorityRequirement::sampled(r.rows, r.request_generation, r.first_position,
-                                                       r.target_serial, r.vocabulary)
-                .validate(*r.target_p);
-        } catch (...) {
-            return {D::target_distribution_invalid};
-        }
-        if (!r.workspace || !r.workspace_plan ||
-            !r.workspace->matches(*r.workspace_plan, r.request_generation, r.root_revision, r.acquisition))
-            return {D::workspace_unavailable};
-        return {D::unqualified_source_ready};
+        for (const Gate& g : kGates)
+            if (!g.passes(r)) return {g.refusal};
+        return {Exl3SampledAdmissionDisposition::unqualified_source_ready};
     }
 
     static std::string_view message(Exl3SampledAdmissionDisposition value) noexcept {
@@ -1229,6 +1246,55 @@ public:
         }
         return "invalid sampled admission disposition";
     }
+
+private:
+    using Request = Exl3SampledAdmissionRequest;
+    struct Gate {
+        bool (*passes)(const Request&) noexcept;
+        Exl3SampledAdmissionDisposition refusal;
+    };
+    template <class F> static bool holds(F&& f) noexcept {   // an authority check that throws fails
+        try { f(); return true; } catch (...) { return false; }
+    }
+    static bool wants_sampling(const Request& r) noexcept { return r.policy.requires_sampled_distribution(); }
+    static bool drafter_has_q(const Request& r) noexcept {
+        return r.draft_availability.supports(Exl3SampledAcceptanceMethod::independent_rejection_with_residual);
+    }
+    static bool exposed(const Request& r) noexcept { return r.exposure == Exl3SampledApiExposure::unqualified_source_api; }
+    static bool state_current(const Request& r) noexcept {
+        const Exl3RequestSamplingState* s = r.request_state;
+        return s && !s->cancelled() && s->request_generation() == r.request_generation &&
+               s->committed_prefix() == static_cast<std::size_t>(r.first_position);
+    }
+    static bool has_draft(const Request& r) noexcept { return r.draft_q != nullptr; }
+    static bool has_target(const Request& r) noexcept { return r.target_p != nullptr; }
+    static bool draft_valid(const Request& r) noexcept {
+        return holds([&] {
+            r.draft_q->require(Exl3SampledAcceptanceMethod::independent_rejection_with_residual, r.rows, r.vocabulary,
+                               r.request_generation, r.root_revision, r.first_position);
+        });
+    }
+    static bool target_valid(const Request& r) noexcept {
+        return holds([&] {
+            Exl3SelectionAuthorityRequirement::sampled(r.rows, r.request_generation, r.first_position, r.target_serial,
+                                                       r.vocabulary).validate(*r.target_p);
+        });
+    }
+    static bool workspace_fits(const Request& r) noexcept {
+        return r.workspace && r.workspace_plan &&
+               r.workspace->matches(*r.workspace_plan, r.request_generation, r.root_revision, r.acquisition);
+    }
+    static constexpr Gate kGates[] = {
+        {&wants_sampling, Exl3SampledAdmissionDisposition::greedy},
+        {&drafter_has_q, Exl3SampledAdmissionDisposition::draft_distribution_unavailable},
+        {&exposed, Exl3SampledAdmissionDisposition::public_sampled_disabled},
+        {&state_current, Exl3SampledAdmissionDisposition::request_state_unavailable},
+        {&has_draft, Exl3SampledAdmissionDisposition::draft_distribution_invalid},
+        {&has_target, Exl3SampledAdmissionDisposition::target_distribution_unavailable},
+        {&draft_valid, Exl3SampledAdmissionDisposition::draft_distribution_invalid},
+        {&target_valid, Exl3SampledAdmissionDisposition::target_distribution_invalid},
+        {&workspace_fits, Exl3SampledAdmissionDisposition::workspace_unavailable},
+    };
 };
 
 // =====================================================================
