@@ -372,6 +372,71 @@ inline void exl3_greedy_path(std::int64_t seed, const Exl3GreedyPacket& packet, 
     for (std::size_t i = 1; i < path.size(); ++i) path[i] = packet.decisions[i - 1].token;
 }
 
+// ---------------------------------------------------------------------
+// Greedy decisions with either authority — branch_reference.h:23-31 and
+// exact_outer_reference.h:14-36.  With VOIDINFER_EXL3_DEVICE_GREEDY on, the
+// context's device greedy packet decides; with it "0", the context's logits are
+// read back and each row's first largest entry decides, every entry of every
+// row read having to be finite (std::runtime_error otherwise).
+//
+// Context is the engine's text context; these members are used:
+//   Exl3GreedyPacket greedy_packet(bool continuation, Stream stream);
+//   (a float range) logits_host(Stream stream);               // the root row
+//   (a float range) continuation_logits_host(Stream stream);  // path.size() rows of
+//                                                              // kDefaultVocabulary
+// ---------------------------------------------------------------------
+
+namespace detail {
+// Index of the first largest entry; nullopt when the row is empty or holds a
+// non-finite entry.
+inline std::optional<std::int64_t> finite_argmax(std::span<const float> row) noexcept {
+    if (row.empty()) return std::nullopt;
+    std::size_t best = 0;
+    for (std::size_t i = 0; i < row.size(); ++i) {
+        if (!std::isfinite(row[i])) return std::nullopt;
+        if (row[i] > row[best]) best = i;
+    }
+    return static_cast<std::int64_t>(best);
+}
+}  // namespace detail
+
+template <class Context, class Stream = void*>
+std::int64_t exl3_branch_greedy(Context& context, Stream stream = nullptr) {
+    if (exl3_device_greedy_enabled()) return context.greedy_packet(false, stream).decisions[0].token;
+    const auto logits = context.logits_host(stream);
+    const auto token = detail::finite_argmax(std::span<const float>(std::data(logits), std::size(logits)));
+    if (!token) throw std::runtime_error("host greedy row is empty or non-finite");
+    return *token;
+}
+
+// path[0] = seed; path[r] = the decision of continuation row r-1; the last
+// row's decision, which authorizes no path entry, goes to *deferred_bonus.
+template <class Context, class Stream>
+void exl3_outer_greedy_path(Context& exact, std::int64_t seed, std::span<std::int64_t> path, Stream stream,
+                            std::int64_t* deferred_bonus = nullptr) {
+    if (path.empty()) throw std::invalid_argument("greedy path extent");
+    if (exl3_device_greedy_enabled()) {
+        const Exl3GreedyPacket packet = exact.greedy_packet(true, stream);
+        exl3_greedy_path(seed, packet, path);
+        if (deferred_bonus) *deferred_bonus = packet.decisions[path.size() - 1].token;
+        return;
+    }
+    const auto logits = exact.continuation_logits_host(stream);
+    const std::span<const float> all(std::data(logits), std::size(logits));
+    const std::size_t v = kDefaultVocabulary;
+    std::vector<std::int64_t> decision(path.size());
+    bool usable = all.size() == path.size() * v;
+    for (std::size_t r = 0; usable && r < path.size(); ++r) {
+        const auto d = detail::finite_argmax(all.subspan(r * v, v));
+        usable = d.has_value();
+        if (usable) decision[r] = *d;
+    }
+    if (!usable) throw std::runtime_error("host continuation logits are mis-sized or non-finite");
+    path[0] = seed;
+    std::copy(decision.begin(), decision.end() - 1, path.begin() + 1);
+    if (deferred_bonus) *deferred_bonus = decision.back();
+}
+
 // =====================================================================
 // Per-request counter RNG — src/exl3/request_sampling_state.h:12-143.
 // Draw i of a request is SplitMix64(seed ^ fingerprint ^ generation ^ i); only

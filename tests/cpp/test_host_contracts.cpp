@@ -334,6 +334,94 @@ void test_greedy_packet() {
          "request authority kind");
 }
 
+// Host-logit and device-packet greedy decisions (branch_reference.h:23-31,
+// exact_outer_reference.h:14-36) over a stand-in text context.
+struct FakeTextContext {
+    std::vector<float> root;           // logits_host
+    std::vector<float> continuation;   // continuation_logits_host: rows x 248320
+    Exl3GreedyPacket packet;
+    int packet_calls = 0, host_calls = 0;
+    bool last_continuation = false;
+    Exl3GreedyPacket greedy_packet(bool continuation_rows, void*) {
+        ++packet_calls;
+        last_continuation = continuation_rows;
+        return packet;
+    }
+    std::vector<float> logits_host(void*) { ++host_calls; return root; }
+    std::vector<float> continuation_logits_host(void*) { ++host_calls; return continuation; }
+};
+
+void test_host_greedy_path() {
+    constexpr std::size_t V = 248320;
+    const unsigned rows = 5;
+    FakeTextContext ctx;
+    ctx.root.assign(V, -3.0f);
+    ctx.root[77] = 2.5f;
+    ctx.root[9000] = 2.5f;   // a tie: the first index wins
+    ctx.continuation.assign(rows * V, 0.0f);
+    const std::array<std::int64_t, rows> argmax{11, 248319, 0, 123456, 5};
+    for (unsigned r = 0; r < rows; ++r) {
+        for (std::size_t i = 0; i < V; ++i) ctx.continuation[r * V + i] = -float((i * 2654435761u + r) % 1000) / 100.0f;
+        ctx.continuation[r * V + std::size_t(argmax[r])] = 40.0f;
+    }
+    ctx.continuation[500] = 40.0f;   // row 0: a tie after its first largest entry
+    ctx.packet.rows = rows;
+    ctx.packet.generation = 3;
+    ctx.packet.position = 64;
+    ctx.packet.serial = 9;
+    ctx.packet.ready = true;
+    for (unsigned r = 0; r < rows; ++r) ctx.packet.decisions[r] = {9, static_cast<std::int32_t>(argmax[r]), 0};
+
+    // Host route.
+    ::setenv("VOIDINFER_EXL3_DEVICE_GREEDY", "0", 1);
+    need(exl3_branch_greedy(ctx) == 77, "host branch greedy takes the first largest entry");
+    std::array<std::int64_t, rows> host_path{};
+    std::int64_t host_bonus = -1;
+    exl3_outer_greedy_path(ctx, 42, std::span<std::int64_t>(host_path), nullptr, &host_bonus);
+    need(host_path[0] == 42, "host path seed");
+    for (unsigned r = 1; r < rows; ++r) need(host_path[r] == argmax[r - 1], "host path row decisions");
+    need(host_bonus == argmax[rows - 1], "host deferred bonus is the last row's decision");
+    need(ctx.packet_calls == 0, "host route reads no packet");
+    {
+        auto bad = ctx;
+        bad.continuation[3 * V + 17] = std::numeric_limits<float>::infinity();
+        need(refuses<std::runtime_error>([&] { exl3_outer_greedy_path(bad, 42, std::span<std::int64_t>(host_path), nullptr); }),
+             "host path refuses +Inf");
+        bad = ctx;
+        bad.continuation[(rows - 1) * V + 2] = std::numeric_limits<float>::quiet_NaN();
+        need(refuses<std::runtime_error>([&] { exl3_outer_greedy_path(bad, 42, std::span<std::int64_t>(host_path), nullptr); }),
+             "host path refuses NaN in the bonus row");
+        bad = ctx;
+        bad.continuation.pop_back();
+        need(refuses<std::runtime_error>([&] { exl3_outer_greedy_path(bad, 42, std::span<std::int64_t>(host_path), nullptr); }),
+             "host path refuses mis-sized logits");
+        bad = ctx;
+        bad.root[5] = -std::numeric_limits<float>::infinity();
+        need(refuses<std::runtime_error>([&] { (void)exl3_branch_greedy(bad); }), "host branch refuses -Inf");
+        bad.root.clear();
+        need(refuses<std::runtime_error>([&] { (void)exl3_branch_greedy(bad); }), "host branch refuses an empty row");
+    }
+
+    // Device route: the same decisions from the packet.
+    ::setenv("VOIDINFER_EXL3_DEVICE_GREEDY", "1", 1);
+    need(exl3_branch_greedy(ctx) == argmax[0], "device branch greedy is packet row 0");
+    need(!ctx.last_continuation, "branch greedy asks for the root packet");
+    std::array<std::int64_t, rows> dev_path{};
+    std::int64_t dev_bonus = -1;
+    exl3_outer_greedy_path(ctx, 42, std::span<std::int64_t>(dev_path), nullptr, &dev_bonus);
+    need(ctx.last_continuation, "outer path asks for the continuation packet");
+    need(dev_path == host_path && dev_bonus == host_bonus, "device and host routes agree");
+    {
+        auto stale = ctx;
+        stale.packet.decisions[rows - 1].nonfinite = 1;
+        need(refuses<std::runtime_error>([&] { exl3_outer_greedy_path(stale, 42, std::span<std::int64_t>(dev_path), nullptr); }),
+             "device path refuses a non-finite bonus row");
+    }
+    need(refuses<std::invalid_argument>([&] { exl3_outer_greedy_path(ctx, 42, std::span<std::int64_t>(), nullptr); }),
+         "empty path");
+    ::unsetenv("VOIDINFER_EXL3_DEVICE_GREEDY");
+}
+
 void test_workspace_and_admission() {
     ResolvedSamplingParameters values;
     auto policy = Exl3SamplingPolicy::normalize(values, 248320);
@@ -539,6 +627,7 @@ int main() {
     test_window_transaction();
     test_control_stop();
     test_greedy_packet();
+    test_host_greedy_path();
     test_workspace_and_admission();
     test_acceptance_and_prefix();
     test_vericache();
