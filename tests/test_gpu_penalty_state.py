@@ -141,7 +141,7 @@ def same_outputs(a, b, label):
         assert torch.equal(a.probs, b.probs), label
 
 
-@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("dtype", [0, 1, 2])
 def test_state_route_equals_history_route_over_steps(orc, dev, rng, dtype):
     """Both routes (top_k 0 / 20 / 50 / 100), five decode steps: sample from the
     state and from the equivalent history, then record the sampled tokens."""
@@ -149,7 +149,7 @@ def test_state_route_equals_history_route_over_steps(orc, dev, rng, dtype):
     from voidinfer_amd import workloads as W
     rows, vocab, L = 12, 248_320, 6000
     x = W.gaussian_zipf(rows, vocab, 1.0, int(rng.integers(1 << 30)))
-    bits = W.encode(x, {0: "bf16", 1: "f16"}[dtype])
+    bits = W.encode(x, {0: "bf16", 1: "f16", 2: "f32"}[dtype])
     p = vi.params_array(rows, seed=rng.integers(1, 2**62, rows), position=rng.integers(0, 10**5, rows),
                         temperature=rng.uniform(0.5, 1.2, rows), top_k=np.array([0, 20, 0, 50, 100, 0] * 2),
                         top_p=rng.choice([0.9, 0.95, 1.0], rows), min_p=rng.choice([0.0, 0.02], rows),

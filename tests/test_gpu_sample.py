@@ -229,19 +229,76 @@ def test_config1_fp32(orc, dev):
     compare(*run_both(orc, dev, x, 2, p, hist, offs), p, "config1")
 
 
-def test_full_route_fp32_rows_fail_loudly(orc, dev, rng):
+@pytest.mark.parametrize("vocab", [1000, 16_385, 151_936, 248_320])
+def test_full_route_fp32_filters(orc, dev, rng, vocab):
+    """fp32 logits on the full-vocabulary route (sample_wide.hip): top_k 0 or
+    above 64 with top-p / min-p, single-slice and many-slice rows."""
+    rows = 16
+    bits = make_rows(rng, rows, vocab, std=1.0, dtype=2)
+    p = params(rows, rng, temperature=rng.uniform(0.3, 1.2, rows), top_k=rng.choice([0, 0, 100, 1000], rows),
+               top_p=rng.choice([0.5, 0.8, 0.95, 1.0], rows), min_p=rng.choice([0.0, 0.0, 0.01, 0.1], rows))
+    compare(*run_both(orc, dev, bits, 2, p), p, f"full32-{vocab}")
+
+
+def test_full_route_fp32_config1_shape(orc, dev, rng):
+    """Config 1's row (1 x 151,936 fp32, its 256-token history) with top_k 0,
+    top_p 0.8 / 0.95 and penalties; then 16 x 248,320 the same way."""
+    from voidinfer_amd import workloads as W
+    x, hist, offs, p = W.config1()
+    for top_p in (0.8, 0.95):
+        q = p.copy()
+        q["top_k"], q["top_p"], q["presence_penalty"], q["frequency_penalty"] = 0, top_p, 0.3, 0.1
+        compare(*run_both(orc, dev, x, 2, q, hist, offs), q, f"config1 top_p {top_p}")
+    rows, vocab, L = 16, 248_320, 4096
+    bits = make_rows(rng, rows, vocab, std=2.0, dtype=2)
+    q = params(rows, rng, temperature=rng.uniform(0.5, 1.2, rows), top_k=0, top_p=rng.choice([0.8, 0.95], rows),
+               repetition_penalty=rng.uniform(1.0, 1.3, rows), presence_penalty=rng.uniform(0, 0.5, rows),
+               frequency_penalty=rng.uniform(0.0, 0.2, rows))
+    h = []
+    for r in range(rows):
+        top = np.argsort(-bits[r])[:200]             # penalties that reorder the top candidates
+        h.append(rng.permutation(np.concatenate([rng.integers(0, vocab, L), rng.choice(top, 300)])).astype(np.int32))
+    offs16 = np.concatenate([[0], np.cumsum([len(v) for v in h])]).astype(np.int64)
+    compare(*run_both(orc, dev, bits, 2, q, np.concatenate(h), offs16), q, "fp32 16 x 248,320")
+
+
+def test_full_route_fp32_edges(orc, dev, rng):
+    """NaN / Inf, an all-equal row (one key over every slice), signed zeros,
+    nothing finite, spreads far past the 64 binned below the top (cap and min-p
+    cut in the deep bin), values around zero across many exponents, huge values,
+    an overflow to Inf by the temperature, an unaligned row stride."""
+    rows, vocab = 12, 40_000
+    x = rng.standard_normal((rows, vocab)).astype(np.float32)
+    x[0, ::7] = np.nan
+    x[1, 5] = np.inf
+    x[2, :] = 1.0
+    x[3, :20_000] = 0.5
+    x[3, 20_000:] = -0.0
+    x[4, :] = np.nan
+    x[5] *= 100.0
+    x[6] *= np.float32(1e-30)
+    x[7, :] = -10.0
+    x[7, [123, 30_456]] = 60.0
+    x[8] *= np.float32(1e30)
+    x[9, 10] = np.float32(3e38)
+    x[10] *= 100.0
+    x[11] *= 0.01
+    p = params(rows, rng, temperature=1.0, top_k=0, top_p=0.9)
+    p["temperature"][[6, 9]] = [0.7, 0.5]
+    p["top_k"][[2, 3, 5, 10]] = [30_000, 25_000, 30_000, 39_990]
+    p["top_p"][[2, 5, 10, 11]] = [1.0, 1.0, 1.0, 0.3]
+    p["min_p"][[7, 10, 11]] = [1e-30, 1e-30, 0.5]
+    compare(*run_both(orc, dev, x, 2, p), p, "fp32 edges")
+    # the same rows at a row stride of V + 3 (rows past the first start unaligned)
     import voidinfer_amd as vi
-    x = rng.standard_normal((3, 1000)).astype(np.float32)
-    p = params(3, rng, temperature=1.0, top_k=np.array([0, 20, 0]))
-    # full-route rows of fp32 logits: the batch fails (only full rows) ...
-    with pytest.raises(vi.VIError):
-        vi.sample_rows(to_dev(x[[0]], 2, dev), p[[0]])
-    # ... or, mixed with top-k rows, those rows come back as token -1 / VI_FLAG_ERROR
-    out = vi.sample_rows(to_dev(x, 2, dev), p)
-    tok = out.tokens.cpu().numpy()
-    st = vi.stats_numpy(out.stats)
-    assert tok[0] == -1 and tok[2] == -1 and (st["flags"][[0, 2]] & 0x80000000).all()
-    assert 0 <= tok[1] < 1000 and not (st["flags"][1] & 0x80000000)
+    wide = torch.zeros(rows, vocab + 3, dtype=torch.float32)
+    wide[:, :vocab] = torch.from_numpy(x)
+    view = wide.to(dev)[:, :vocab]
+    out = vi.sample_rows(view, p, want_probs=True)
+    torch.cuda.synchronize()
+    g, w = run_both(orc, dev, x, 2, p)
+    assert np.array_equal(out.tokens.cpu().numpy(), g["tokens"])
+    assert torch.equal(out.probs.cpu(), torch.from_numpy(g["probs"]))
 
 
 def test_draw_distribution_chi_square(orc, dev, rng):

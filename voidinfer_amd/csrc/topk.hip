@@ -969,7 +969,7 @@ size_t sample_workspace(int rows, int vocabulary, int64_t max_history) {
     size_t bytes = topk_partials_bytes(rows, vocabulary);
     bytes += align_up(size_t(rows) * 4, 256);
     if (max_history > 0) bytes += align_up(size_t(rows) * history_hash_slots(max_history) * 8, 256);
-    bytes += full_workspace(rows, vocabulary);
+    bytes += std::max(full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary));
     return bytes + 1024;
 }
 
@@ -988,10 +988,13 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         shift = 32 - __builtin_ctz(unsigned(slots));
         hash = c.take<uint2>(size_t(s.rows) * slots);
     }
-    unsigned char* full_ws = c.take<unsigned char>(full_workspace(s.rows, s.vocabulary));
+    const size_t full_bytes = s.dtype == VI_F32 ? wide_workspace(s.rows, s.vocabulary)
+                                                 : full_workspace(s.rows, s.vocabulary);
+    unsigned char* full_ws = c.take<unsigned char>(full_bytes);
     if (!c.ok) return VI_ERR_WORKSPACE;
     const bool run_topk = (s.route_mask & VI_ROUTE_TOPK) != 0;
-    const bool full_ok = full_supported(s.dtype, s.vocabulary, s.stride);
+    const bool full_ok = s.dtype == VI_F32 ? wide_supported(s.vocabulary, s.stride)
+                                           : full_supported(s.dtype, s.vocabulary, s.stride);
     vi_status st = VI_OK;
     if (run_topk) {
         if (hash) {
@@ -1012,7 +1015,9 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         st = launch_mode<kModeSample>(a, s.dtype, aligned16(s.logits, s.stride, s.dtype), s.rows, plan.slices, stream);
         if (st != VI_OK) return st;
     }
-    if ((s.route_mask & VI_ROUTE_FULL) && full_ok) st = launch_full(s, full_ws, full_workspace(s.rows, s.vocabulary), stream);
+    if ((s.route_mask & VI_ROUTE_FULL) && full_ok)
+        st = s.dtype == VI_F32 ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
+                               : launch_full(s, full_ws, full_bytes, stream);
     else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) return VI_ERR_UNSUPPORTED;
     return st;
 }

@@ -156,6 +156,12 @@ vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStrea
 size_t full_workspace(int rows, int vocabulary);
 vi_status launch_full(const SampleArgs& a, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 bool full_supported(int dtype, int vocabulary, int64_t stride);
+// fp32 rows of the full route (sample_wide.hip); the history route's hash and
+// flags are the top-k route's buffers (rows of the two routes are disjoint).
+size_t wide_workspace(int rows, int vocabulary);
+bool wide_supported(int vocabulary, int64_t stride);
+vi_status launch_wide(const SampleArgs& a, unsigned char* ws, size_t ws_bytes, uint2* hash, int hash_shift,
+                      int hash_slots, uint32_t* row_flags, hipStream_t stream);
 
 // ---- verification ----------------------------------------------------------------
 struct VerifyArgs {
