@@ -292,9 +292,9 @@ vi_status vi_build_verification_tree(const int64_t* drafts, int depth, const int
  * `uniforms` (double[rows]), `probs` (float[rows][probs_stride], the filtered
  * distribution), `stats`.  `max_history` bounds every row's history length
  * (it sizes the workspace); a longer history fails that row.  Supported:
- * bf16/fp16 logits for any row; fp32 logits for rows with 1 <= top_k <= 64 or
- * temperature 0.  A row the kernels cannot finish gets token -1 and
- * VI_FLAG_ERROR in its stats. */
+ * bf16, fp16 and fp32 logits, vocabularies up to 524,288 on the
+ * full-vocabulary route (top_k 0 or > 64 with temperature > 0).  A row the
+ * kernels cannot finish gets token -1 and VI_FLAG_ERROR in its stats. */
 /* route_mask: which kernels run.  VI_ROUTE_TOPK serves rows with temperature 0
  * or 1 <= top_k <= 64, VI_ROUTE_FULL every other row; rows whose route is not in
  * the mask are left unwritten.  VI_ROUTE_ALL (or 0) runs both. */
@@ -339,10 +339,8 @@ vi_status vi_penalty_state_update(void* states, int lanes, int vocabulary, int s
  * over any history with the same occurrence counts.  record = 1 also appends
  * each row's sampled token (when it is in [0, vocabulary)) to its lane's state,
  * in the same launch: a decode step is then one call.  Workspace:
- * vi_sample_workspace_bytes(rows, vocabulary, 0).  A full-route row with
- * penalties fails (token -1, VI_FLAG_ERROR) when its lane holds more than
- * 32,768 distinct recorded tokens in one half of the vocabulary or a count
- * above 65,535 there; top-k-route rows have neither limit. */
+ * vi_sample_workspace_bytes(rows, vocabulary, 0).  No limit on a lane's
+ * distinct tokens or counts beyond the state's own (its hash slots). */
 vi_status vi_sample_rows_state(const void* logits, int dtype, int rows, int vocabulary, int64_t row_stride,
                                const vi_row_params* params, void* states, int slots, int record, int32_t* tokens,
                                double* uniforms, float* probs, int64_t probs_stride, vi_sample_stats* stats,
@@ -360,11 +358,16 @@ vi_status vi_sample_rows_state(const void* logits, int dtype, int rows, int voca
  * `position` is the absolute position of drafted row 0); terminal: optional
  * device list of stop tokens.  Outputs: accepted[lanes], committed
  * [lanes][drafts + 1] (unused slots = -1), committed_count[lanes],
- * lane_flags[lanes] (optional).  Sampled mode requires 1 <= top_k <= 64 on
- * every lane with temperature > 0: any other such lane is refused on the
- * device (accepted 0, committed_count 0, every committed slot -1,
- * lane_flags VI_FLAG_ERROR) while the other lanes are decided as usual. */
-enum { VI_VERIFY_GREEDY = 0, VI_VERIFY_SAMPLED = 1 };
+ * lane_flags[lanes] (optional).  Sampled mode takes p and q from top-k lists
+ * on lanes with 1 <= top_k <= 64 and from the full-vocabulary sampler's
+ * filtered distributions on the others (top_k 0 or above 64; vocabularies up
+ * to 524,288, 16-byte aligned 16-bit rows or 4-byte aligned fp32 rows).
+ * VI_VERIFY_SAMPLED_TOPK is sampled mode for batches whose sampled lanes all
+ * have 1 <= top_k <= 64 (the full-vocabulary launches are skipped): any other
+ * sampled lane is then refused on the device (accepted 0, committed_count 0,
+ * every committed slot -1, lane_flags VI_FLAG_ERROR), as it is when the
+ * full-vocabulary path cannot take the rows. */
+enum { VI_VERIFY_GREEDY = 0, VI_VERIFY_SAMPLED = 1, VI_VERIFY_SAMPLED_TOPK = 2 };
 size_t vi_verify_workspace_bytes(int lanes, int drafts, int vocabulary);
 vi_status vi_verify_rows(int mode, const void* target, int target_dtype,
                          int64_t target_stride, int target_rows,

@@ -954,7 +954,11 @@ int or_verify_rows(int mode, const void* target, int target_dtype, int64_t targe
                 double a = 0;
                 if (q == 0) flags |= VI_FLAG_ZERO_Q;
                 else a = std::min(1.0, pd[size_t(d)] / q);
-                if (accept_margins) accept_margins[size_t(l) * drafts + j] = std::fabs(ua - a);
+                // how close this position's decision came to turning: the accept
+                // test, and the top-p / min-p cuts of both rows (which decide p, q)
+                double margin = std::fabs(ua - a);
+                margin = std::min({margin, tp.topp_margin, tp.minp_margin, dq.topp_margin, dq.minp_margin});
+                if (accept_margins) accept_margins[size_t(l) * drafts + j] = margin;
                 if (q != 0 && ua < a) {
                     out[c++] = d; ++acc;
                     stopped = is_terminal(d);
@@ -973,14 +977,20 @@ int or_verify_rows(int mode, const void* target, int target_dtype, int64_t targe
                     }
                     if (!found) corr = last;
                 } else {
-                    double cum = 0; int32_t last = 0; bool found = false;
+                    double cum = 0, before = 0; int32_t last = 0; bool found = false;
                     for (int v = 0; v < vocabulary; ++v) {
                         const double rv = std::max(0.0, pd[size_t(v)] - qd[size_t(v)]) / sum;
                         if (rv > 0) last = v;
+                        before = cum;
                         cum += rv;
                         if (uc < cum) { corr = v; found = true; break; }
                     }
                     if (!found) corr = last;
+                    // ... and of the correction: u_c against the cumulative residual
+                    if (accept_margins) {
+                        double& m = accept_margins[size_t(l) * drafts + j];
+                        m = std::min({m, std::fabs(cum - uc), std::fabs(before - uc)});
+                    }
                 }
                 out[c++] = corr;
                 break;
@@ -989,8 +999,16 @@ int or_verify_rows(int mode, const void* target, int target_dtype, int64_t targe
                 RowDist tp;
                 build_row(target_row(drafts), target_dtype, vocabulary, p, nullptr, 0, tp, counts);
                 if (!(tp.flags & VI_FLAG_EMPTY)) {
-                    if (tp.greedy) out[c++] = tp.greedy_token;
-                    else out[c++] = tp.ids[size_t(draw_sorted(tp, or_uniform(p.seed, p.lane, p.position + drafts, 0), nullptr))];
+                    if (tp.greedy) {
+                        out[c++] = tp.greedy_token;
+                    } else {
+                        double dm = INFINITY;
+                        out[c++] = tp.ids[size_t(draw_sorted(tp, or_uniform(p.seed, p.lane, p.position + drafts, 0), &dm))];
+                        if (accept_margins) {   // (the bonus draw's margins join the last position's)
+                            double& m = accept_margins[size_t(l) * drafts + drafts - 1];
+                            m = std::min({m, dm, tp.topp_margin, tp.minp_margin});
+                        }
+                    }
                 }
             }
         }

@@ -132,6 +132,11 @@ int or_verify_rows(int mode, const void* target, int target_dtype, int64_t targe
                    int32_t* accepted, int32_t* committed, int32_t* committed_count,
                    uint32_t* lane_flags, double* accept_margins /* optional [lanes][drafts] */,
                    int threads);
+/* accept_margins (sampled mode): per decided position, the smallest distance
+ * at which the outcome would turn: |u_a - min(1, p/q)|, the top-p / min-p cut
+ * margins of the target and draft rows, at a rejection |u_c - cumulative
+ * residual| on either side of the correction, and on the last position of a
+ * lane that reached the bonus row, that draw's margins. */
 
 /* EXTENSION: filtered distribution of one row (the sampler's p), dense fp64. */
 int or_row_distribution(const void* row, int dtype, int vocabulary, const vi_row_params* params,

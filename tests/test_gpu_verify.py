@@ -37,13 +37,18 @@ def run(orc, dev, mode, tbits, dbits, drafted, p, lanes, drafts, terminal=()):
 
 
 def assert_same(g, w, exempt_lanes=()):
+    """Every lane equal to the oracle but the exempt ones; returns the lanes that
+    differ (all exempt)."""
     ga, gc, gn, gf = g
     wa, wc, wn, wf, _ = w
+    differ = []
     for l in range(len(wa)):
-        if l in exempt_lanes:
+        same = ga[l] == wa[l] and gn[l] == wn[l] and np.array_equal(gc[l], wc[l]) and gf[l] == wf[l]
+        if same:
             continue
-        assert ga[l] == wa[l] and gn[l] == wn[l] and np.array_equal(gc[l], wc[l]) and gf[l] == wf[l], (
-            l, ga[l], wa[l], gc[l], wc[l], gf[l], wf[l])
+        assert l in exempt_lanes, (l, ga[l], wa[l], gc[l], wc[l], gf[l], wf[l])
+        differ.append(l)
+    return differ
 
 
 @pytest.mark.parametrize("bonus", [False, True])
@@ -126,19 +131,101 @@ def test_sampled_nonfinite_and_overflowing_targets(orc, dev, rng):
     assert any(f != 0 for f in w[3])
 
 
-def test_sampled_refuses_top_k_outside_list_range(orc, dev):
-    """Lanes with temperature > 0 and top_k in {0, 65, 200} have no top-k list
-    (the lists hold 64 entries): they are refused with VI_FLAG_ERROR, accept and
-    commit nothing, and leave the other config-4 lanes bit-exact with the oracle."""
+def test_sampled_full_vocabulary_lanes(orc, dev):
+    """Lanes with temperature > 0 and top_k in {0, 65, 200} take p and q from the
+    full-vocabulary sampler's distributions; every lane matches the oracle
+    (accepted lengths, committed ids, flags) outside decisions that lie within
+    1e-6 of turning (1e-9 on the list lanes, whose fp64 sums are the oracle's)."""
     from voidinfer_amd import workloads as W
-    from voidinfer_amd._abi import FLAG_ERROR
+    lanes, drafts = 8, 16
+    p0 = W.config4(lanes=lanes, drafts=drafts)[3]
+    full = {1: 0, 4: 65, 6: 200}
+    for l, k in full.items():
+        p0["top_k"][l] = k
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, sample_fn=sampler_from_draft(orc, p0))
+    p[:] = p0
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    exempt = {l for l in range(lanes) if np.min(w[4][l]) < (1e-6 if l in full else 1e-9)}
+    assert len(assert_same(g, w, exempt)) <= 1
+    assert not any(g[3][l] & 0x80000000 for l in range(lanes))
+
+
+@pytest.mark.parametrize("bonus", [False, True])
+def test_sampled_config4_top_k_disabled(orc, dev, bonus):
+    """Config 4 with top_k 0 and top_p 0.8 (T 0.7) on every lane: the whole
+    verification runs on the full-vocabulary path, drafts sampled from the
+    draft's full filtered distribution."""
+    from voidinfer_amd import workloads as W
+    lanes, drafts = 8, 16
+    p0 = W.config4(lanes=lanes, drafts=drafts, bonus=bonus)[3]
+    p0["top_k"] = 0
+    p0["top_p"] = 0.8
+    tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, bonus=bonus, sample_fn=sampler_from_draft(orc, p0))
+    p[:] = p0
+    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-6}
+    assert len(assert_same(g, w, exempt)) <= 1
+    assert w[0].sum() > 0 and (w[0] < drafts).any()   # both accepts and rejections were exercised
+
+
+def test_sampled_full_vocabulary_mixed_dtypes_and_edges(orc, dev, rng):
+    """fp32 targets with bf16 drafts (and the reverse) on small vocabularies, min-p
+    and top-p cuts, zero-q proposals, temperature 0 lanes beside full lanes, a
+    bonus row."""
+    import voidinfer_amd as vi
+    lanes, drafts, vocab = 12, 5, 40_000
+    for tdt, ddt in ((2, 0), (0, 2), (1, 1)):
+        x = rng.standard_normal((lanes * (drafts + 1), vocab)).astype(np.float32) * 2.0
+        y = x[np.arange(lanes * (drafts + 1)).reshape(lanes, drafts + 1)[:, :drafts].reshape(-1)]
+        y = y + rng.standard_normal(y.shape).astype(np.float32) * 0.5
+        enc = {0: W_bf16, 1: W_f16, 2: lambda a: a}
+        tb, db = enc[tdt](x), enc[ddt](y)
+        p = vi.params_array(lanes, seed=rng.integers(1, 2**62, lanes), position=rng.integers(0, 10**5, lanes),
+                            lane=np.arange(lanes), temperature=rng.choice([0.0, 0.7, 1.0], lanes),
+                            top_k=rng.choice([0, 0, 100, 20], lanes), top_p=rng.choice([0.5, 0.9, 1.0], lanes),
+                            min_p=rng.choice([0.0, 0.05], lanes))
+        drafted = np.zeros((lanes, drafts), dtype=np.int32)
+        for l in range(lanes):
+            for j in range(drafts):
+                prob, _ = orc.row_distribution(db[l * drafts + j], ddt, p[l])
+                drafted[l, j] = rng.choice(vocab, p=prob / prob.sum()) if j != 2 or l % 4 else 7
+        t = to_dev(tb, tdt, dev)
+        d = to_dev(db, ddt, dev)
+        dr = torch.from_numpy(drafted).to(dev)
+        g = vi.verify_rows(1, t, dr, lanes, drafts, draft=d, params=p)
+        w = orc.verify_rows(1, tb, tdt, db, ddt, lanes, drafts, drafted, p)
+        exempt = {l for l in range(lanes) if np.min(w[4][l]) < 1e-6}
+        assert len(assert_same(g, w, exempt)) <= 1, (tdt, ddt, exempt)
+
+
+def W_bf16(a):
+    from voidinfer_amd import workloads as W
+    return W.encode(a, "bf16")
+
+
+def W_f16(a):
+    from voidinfer_amd import workloads as W
+    return W.encode(a, "f16")
+
+
+def test_sampled_topk_mode_refuses_full_vocabulary_lanes(orc, dev):
+    """VI_VERIFY_SAMPLED_TOPK (the caller vouches for top-k lists on every
+    sampled lane): lanes with top_k in {0, 65, 200} are refused with
+    VI_FLAG_ERROR, accept and commit nothing, and leave the other config-4 lanes
+    bit-exact with the oracle."""
+    import voidinfer_amd as vi
+    from voidinfer_amd import workloads as W
+    from voidinfer_amd._abi import FLAG_ERROR, VERIFY_SAMPLED_TOPK
     lanes, drafts = 8, 16
     p0 = W.config4(lanes=lanes, drafts=drafts)[3]
     tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, sample_fn=sampler_from_draft(orc, p0))
     refused = {1: 0, 4: 65, 6: 200}
     for l, k in refused.items():
         p["top_k"][l] = k
-    g, w = run(orc, dev, 1, tb, db, drafted, p, lanes, drafts)
+    t, d = to_dev(tb, 0, dev), to_dev(db, 1, dev)
+    dr = torch.from_numpy(np.ascontiguousarray(drafted, dtype=np.int32)).to(dev)
+    g = vi.verify_rows(VERIFY_SAMPLED_TOPK, t, dr, lanes, drafts, draft=d, params=p)
+    w = orc.verify_rows(1, tb, 0, db, 1, lanes, drafts, drafted, p)
     ga, gc, gn, gf = g
     for l in refused:
         assert gf[l] == FLAG_ERROR and ga[l] == 0 and gn[l] == 0 and np.all(gc[l] == -1), (l, ga[l], gn[l], gf[l])

@@ -21,7 +21,7 @@ BF16, F16, F32 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_DEVICE = range(6)
 FLAG_NONFINITE, FLAG_EMPTY, FLAG_ZERO_Q, FLAG_NO_RESIDUAL, FLAG_BAD_HISTORY = 1, 2, 4, 8, 16
 FLAG_ERROR = 0x80000000
-VERIFY_GREEDY, VERIFY_SAMPLED = 0, 1
+VERIFY_GREEDY, VERIFY_SAMPLED, VERIFY_SAMPLED_TOPK = 0, 1, 2
 ROUTE_TOPK, ROUTE_FULL, ROUTE_ALL = 1, 2, 3
 ABSENT_OCCURRENCE = 0x7F7F7F7F
 

@@ -275,10 +275,11 @@ vi_status vi_verify_rows(int mode, const void* target, int target_dtype, int64_t
         !target || !dtype_ok(target_dtype) || target_stride < vocabulary || !drafted || !accepted || !committed ||
         !committed_count || n_terminal < 0 || (n_terminal && !terminal))
         return VI_ERR_INVALID;
-    if (mode == VI_VERIFY_SAMPLED &&
+    if (mode != VI_VERIFY_GREEDY && mode != VI_VERIFY_SAMPLED && mode != VI_VERIFY_SAMPLED_TOPK)
+        return VI_ERR_INVALID;
+    if (mode != VI_VERIFY_GREEDY &&
         (!draft || !dtype_ok(draft_dtype) || draft_stride < vocabulary || !params))
         return VI_ERR_INVALID;
-    if (mode != VI_VERIFY_GREEDY && mode != VI_VERIFY_SAMPLED) return VI_ERR_INVALID;
     VerifyArgs a{};
     a.mode = mode; a.target = target; a.target_dtype = target_dtype; a.target_stride = target_stride;
     a.target_rows = target_rows; a.draft = draft; a.draft_dtype = draft_dtype; a.draft_stride = draft_stride;

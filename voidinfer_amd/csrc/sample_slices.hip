@@ -91,11 +91,8 @@ constexpr int kGatherBytes = 4 * kMaxSlices * kBinKeys + 4 * kBinKeys + 4 * kMax
 constexpr int kOffGather = kOffMR + 8 * kBins;
 static_assert(kOffGather + kGatherSlots * kGatherBytes <= 4 * kHW, "merge map");
 
-struct RowBound {          // what the probs kernel needs to rebuild the support
-    double z0, s_n;
-    float inv_t;
-    uint32_t end_key, end_take, valid;
-};
+using RowBound = FullBound;   // what the probs kernel and verification need to rebuild the support
+static_assert(kSL == kFullSlice16 && kMaxSlices <= kFullBaseSlots, "full-route bases");
 
 struct SliceArgs {
     const void* logits;
@@ -119,8 +116,9 @@ struct SliceArgs {
     uint32_t* lists;           // [rows][slices][kSL]; a slice's dense repeat counts before its list
     uint16_t* ptab;            // [rows][slices][kSL]: penalized patterns of the history tokens, in id order
     uint32_t* hbits;           // [rows][slices][kBW]: history bitmaps (history route; the state holds its own)
+    int want_bounds;           // bounds and bases wanted (probs, or verification)
     RowBound* bounds;          // [rows]
-    uint32_t* bases;           // [rows][kMaxSlices]: end-key logits in the slices before
+    uint32_t* bases;           // [rows][kFullBaseSlots]: end-key logits in the slices before
 };
 
 struct Shared {
@@ -862,7 +860,7 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
     if (fail || N == 0u) {
         if (tid == 0) {
             write_row(a, row, fail ? -1 : V, 0.0, out_flags | (fail ? VI_FLAG_ERROR : VI_FLAG_EMPTY), 0u, 0u, 0.0);
-            if (a.probs) a.bounds[row] = RowBound{0.0, 0.0, 0.0f, 0u, 0u, 0u};
+            if (a.want_bounds) a.bounds[row] = RowBound{0.0, 0.0, 0.0f, 0u, 0u, 0u};
         }
         __syncthreads();
         return;
@@ -1017,7 +1015,7 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
                 if ((e >> 16) == dk) PC[s] = e & 0xffffu;
             }
         }
-        if (a.probs && end_slot >= 0) {
+        if (a.want_bounds && end_slot >= 0) {
             const Slot es = slot_at(lds, end_slot);
             const uint32_t ek = sh.end_key;
             for (int idx = tid; idx < S * kBinKeys; idx += kT) {
@@ -1041,10 +1039,10 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
         } else if (lane == 0) {
             sh.ok = 0u;
         }
-        if (a.probs) {   // end-key logits in the slices before each slice (id order)
+        if (a.want_bounds) {   // end-key logits in the slices before each slice (id order)
             const uint32_t ce = lane < S ? PC[kMaxSlices + lane] : 0u;
             const uint32_t ie = wave_incl_scan_u32(ce);
-            if (lane < kMaxSlices) a.bases[size_t(row) * kMaxSlices + lane] = ie - ce;
+            if (lane < kFullBaseSlots) a.bases[size_t(row) * kFullBaseSlots + lane] = ie - ce;
         }
     }
     __syncthreads();
@@ -1186,7 +1184,7 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
                 state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
             }
         }
-        if (a.probs)
+        if (a.want_bounds)
             a.bounds[row] = RowBound{zmax, sh.s_n, inv_t, sh.end_all ? 0u : sh.end_key,
                                      sh.end_all ? kTakeAll : sh.end_take, tok >= 0 ? 1u : 0u};
     }
@@ -1678,7 +1676,7 @@ __global__ __launch_bounds__(kT) void slice_probs_kernel(SliceArgs a) {
 #pragma unroll
         for (int x = 0; x < kSeg; ++x) cnt[x] = __builtin_popcount(mask[x]);
         (void)id_order_prefix(cnt, excl, sh);
-        const uint32_t base = bd.end_take == kTakeAll ? 0u : a.bases[size_t(row) * kMaxSlices + s];
+        const uint32_t base = bd.end_take == kTakeAll ? 0u : a.bases[size_t(row) * kFullBaseSlots + s];
         auto prob = [&](uint32_t key, uint32_t rank) -> float {
             if (!key || key < ek) return 0.0f;
             if (key == ek && bd.end_take != kTakeAll && base + rank >= bd.end_take) return 0.0f;
@@ -1732,7 +1730,7 @@ size_t full_workspace(int rows, int vocabulary) {
     return align_up(rs * kHeadWords * 4, 256) + align_up(rs * kBins * 16, 256) + align_up(rs * kSL * 4, 256) +
            align_up(rs * kSL * 2, 256) + align_up(rs * kBW * 4, 256) +
            align_up(size_t(rows) * sizeof(RowBound), 256) +
-           align_up(size_t(rows) * kMaxSlices * 4, 256) + 256;
+           align_up(size_t(rows) * kFullBaseSlots * 4, 256) + 256;
 }
 
 vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream) {
@@ -1748,13 +1746,15 @@ vi_status launch_full(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, h
     a.ptab = c.take<uint16_t>(rs * kSL);
     a.hbits = c.take<uint32_t>(rs * kBW);
     a.bounds = c.take<RowBound>(size_t(s.rows));
-    a.bases = c.take<uint32_t>(size_t(s.rows) * kMaxSlices);
+    a.bases = c.take<uint32_t>(size_t(s.rows) * kFullBaseSlots);
     if (!c.ok) return VI_ERR_WORKSPACE;
     a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary; a.stride = s.stride;
     a.params = s.params; a.histories = s.histories; a.offsets = s.offsets;
     if (s.pstate) { a.pstate = s.pstate; a.pl = s.playout; a.record = s.record; }
     a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
     a.stats = s.stats;
+    if (s.full_out) { a.bounds = s.full_out->bounds; a.bases = s.full_out->bases; }
+    a.want_bounds = (s.probs || s.full_out) ? 1 : 0;
     const int items = s.rows * a.slices;
     a.grid = std::min(device_cus(), items);
     a.xcd_aware = (s.rows >= 8 && a.grid % 8 == 0) ? 1 : 0;

@@ -57,11 +57,8 @@ struct WideHead {
 };
 static_assert(sizeof(WideHead) == 32, "slice head");
 
-struct WideBound {   // what the probs kernel needs to rebuild the support
-    double z0, s_n;
-    float inv_t;
-    uint32_t end_key, end_take, valid;
-};
+using WideBound = FullBound;   // what the probs kernel and verification need to rebuild the support
+static_assert(kSL == kFullSlice32 && kMaxSlices == kFullBaseSlots, "full-route bases");
 
 struct WideArgs {
     const void* logits;
@@ -90,6 +87,7 @@ struct WideArgs {
     unsigned long long* mass;      // [rows][slices][kNB]: fixed-point bin masses
     uint32_t* keys;                // [rows][slices][kSL]: order keys, grouped by bin
     uint16_t* ids;                 // [rows][slices][kSL]: slice offsets, same order
+    int want_bounds;               // bounds and bases wanted (probs, or verification)
     WideBound* bounds;             // [rows]
     uint32_t* bases;               // [rows][kMaxSlices]: end-key logits in the slices before
 };
@@ -744,7 +742,7 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
     if (fail || N == 0u) {
         if (tid == 0) {
             write_row(a, row, fail ? -1 : V, 0.0, out_flags | (fail ? VI_FLAG_ERROR : VI_FLAG_EMPTY), 0u, 0u, 0.0);
-            if (a.probs) a.bounds[row] = WideBound{0.0, 0.0, 0.0f, 0u, 0u, 0u};
+            if (a.want_bounds) a.bounds[row] = WideBound{0.0, 0.0, 0.0f, 0u, 0u, 0u};
         }
         return;
     }
@@ -923,7 +921,7 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
     const int32_t tok = dbin >= 0 ? owner(c, L, dkey, drank) : -1;
 
     // ---- 7. results; the bases of the end key for the probs kernel
-    if (a.probs && !all && et != kTakeAll) {
+    if (a.want_bounds && !all && et != kTakeAll) {
         const BinW b = bin_weight(ek, A);
         gather_bin(c, L, b.bin);
         key_per_slice(c, L, ek);
@@ -943,7 +941,7 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
                 state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
             }
         }
-        if (a.probs)
+        if (a.want_bounds)
             a.bounds[row] = WideBound{z0, s_n, 1.0f / p.temperature, all ? 0u : ek, all ? kTakeAll : et,
                                       tok >= 0 ? 1u : 0u};
     }
@@ -1044,6 +1042,8 @@ vi_status launch_wide(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, u
     }
     a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
     a.stats = s.stats;
+    if (s.full_out) { a.bounds = s.full_out->bounds; a.bases = s.full_out->bases; }
+    a.want_bounds = (s.probs || s.full_out) ? 1 : 0;
     if (a.hash) hipLaunchKernelGGL(wide_history_kernel, dim3(s.rows), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(wide_slice_kernel, dim3(a.slices, s.rows), dim3(kT), 0, stream, a);
     hipLaunchKernelGGL(wide_merge_kernel, dim3(s.rows), dim3(kT), 0, stream, a);

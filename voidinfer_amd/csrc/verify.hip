@@ -7,8 +7,10 @@
 // = drafts + 1) a fully accepted lane also commits the bonus row's argmax.
 //
 // Sampled mode: the target and draft rows are filtered with the lane's
-// temperature / top-k / top-p / min-p (top-k lists from topk.hip, so
-// 1 <= top_k <= 64), giving p and q.  Per position, in order, the rule of
+// temperature / top-k / top-p / min-p, giving p and q: from top-k lists
+// (topk.hip) for lanes with 1 <= top_k <= 64, from the full-vocabulary
+// sampler's row distributions (sample_slices.hip / sample_wide.hip) for the
+// others.  Per position, in order, the rule of
 // Exl3IndependentAcceptanceReference::evaluate
 // (src/exl3/sampled_acceptance_reference.h:48-88): accept iff
 // u_a < min(1, p[d]/q[d]); at the first rejection draw the correction from the
@@ -17,7 +19,11 @@
 // (seed, lane, position + j, purpose 1 / 2).  Every (lane, position) decision
 // is taken at once, one wave each over the <= 64-entry lists (fp64): entry-wise
 // work on the lanes, the order-dependent sums on lane 0; a per-lane pass then
-// walks the accept chain in order.
+// walks the accept chain in order.  Full-vocabulary lanes: the accept test
+// evaluates the target softmax p and the draft q at the drafted token from the
+// rows' supports, and the correction walks the target softmax, the draft q and
+// their residual over the whole vocabulary in id order (ranges of 16,384
+// tokens summed in parallel, then the crossing range scanned again).
 #include <math.h>
 
 #include "vi_device.h"
@@ -133,7 +139,7 @@ struct PosDecision {
 __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     const float* tval, const int* tidx, const uint32_t* tvalid, const uint32_t* tflags, const float* dval,
     const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int drafts, int target_rows,
-    const int32_t* drafted, const vi_row_params* params, int vocabulary, PosDecision* dec) {
+    const int32_t* drafted, const vi_row_params* params, int vocabulary, int full_ok, PosDecision* dec) {
     __shared__ ListDist P, Q;
     __shared__ double s_rv[kMaxK], s_pv[kMaxK];
     __shared__ int s_rid[kMaxK];
@@ -142,8 +148,8 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     const vi_row_params p = params[l];
     PosDecision* out = dec + size_t(l) * (drafts + 1) + j;
     const size_t tr = size_t(l) * target_rows + j;
-    if (verify_list_refused(p)) {   // no list of this lane's top_k: refused, nothing decided
-        if (k == 0 && (j < drafts || target_rows == drafts + 1)) *out = PosDecision{-1, VI_FLAG_ERROR, 0, 0};
+    if (verify_list_refused(p)) {   // no list of this lane's top_k: the full-vocabulary path, or refused
+        if (!full_ok && k == 0 && (j < drafts || target_rows == drafts + 1)) *out = PosDecision{-1, VI_FLAG_ERROR, 0, 0};
         return;
     }
     if (j == drafts) {   // the bonus row's draw (used when every draft is accepted)
@@ -161,7 +167,7 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
                     tok = P.id[pick];
                 }
             }
-            *out = PosDecision{tok, tflags[tr], 0, 0};
+            *out = PosDecision{tok, 0u, 0, 0};
         }
         return;
     }
@@ -241,14 +247,14 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
 // commits the bonus draw.  Flags of the positions visited (and the bonus row).
 __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int drafts, int target_rows,
                                     const int32_t* drafted, const vi_row_params* params, const int64_t* terminal,
-                                    int n_terminal, int32_t* accepted, int32_t* committed,
+                                    int n_terminal, int full_ok, int32_t* accepted, int32_t* committed,
                                     int32_t* committed_count, uint32_t* lane_flags) {
     const int l = blockIdx.x * blockDim.x + threadIdx.x;
     if (l >= lanes) return;
     const PosDecision* D = dec + size_t(l) * (drafts + 1);
     int32_t* out = committed + size_t(l) * (drafts + 1);
     for (int j = 0; j <= drafts; ++j) out[j] = -1;
-    if (verify_list_refused(params[l])) {   // refused lane: nothing accepted, nothing committed
+    if (verify_list_refused(params[l]) && !full_ok) {   // refused lane: nothing accepted, nothing committed
         accepted[l] = 0;
         committed_count[l] = 0;
         if (lane_flags) lane_flags[l] = VI_FLAG_ERROR;
@@ -282,6 +288,356 @@ __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int draft
     if (lane_flags) lane_flags[l] = flags;
 }
 
+// ------------------------------------------------------- full-vocabulary lanes
+// Lanes with temperature > 0 and top_k outside [1, 64].  The full-route sampler
+// leaves every target and draft row's filtered distribution (FullBound: the
+// support's end and mass; bases: end-key logits before each slice) and every
+// target row's own draw (the bonus token); p and q are read off them.
+
+constexpr int kFT = 256;                 // accept kernel threads
+constexpr int kRT = 1024;                // residual kernels' threads
+constexpr int kRange = 16384;            // residual range (divides both routes' slices)
+constexpr int kREPT = kRange / kRT;      // tokens per thread and range
+constexpr int kW = kRT / kWave;
+static_assert(kFullSlice16 % kRange == 0 && kFullSlice32 % kRange == 0, "residual ranges");
+
+struct FullRows {
+    const void* row0;
+    int dtype;
+    int64_t stride;
+    const FullBound* bound;          // [rows]
+    const uint32_t* bases;           // [rows][kFullBaseSlots]
+    const vi_sample_stats* stats;    // [rows]
+    int slice;                       // logits per slice (bases granularity)
+};
+
+struct FullVerifyArgs {
+    FullRows t, d;                   // target rows [lanes][target_rows], draft rows [lanes][drafts]
+    const int32_t* ttok;             // the target rows' draws
+    int lanes, drafts, target_rows, vocabulary;
+    const int32_t* drafted;
+    const vi_row_params* params;
+    const int64_t* terminal;
+    int n_terminal;
+    PosDecision* dec;
+    double* rsum;                    // [lanes][ranges][2]: residual mass, p mass of each range
+    int* rlast;                      // [lanes][ranges][2]: last id with residual / with p (-1: none)
+    int ranges;
+};
+
+__device__ __forceinline__ const void* row_at(const FullRows& R, size_t r) {
+    return static_cast<const unsigned char*>(R.row0) + r * size_t(R.stride) * (R.dtype == VI_F32 ? 4u : 2u);
+}
+
+// Order key of a logit (0: not valid) in the full routes' convention: key16 of
+// the 16-bit pattern, or the 32-bit key of z for fp32 logits; and z of a key.
+template <int DT>
+__device__ __forceinline__ uint32_t dist_key(uint32_t b, float inv_t) {
+    if constexpr (DT == VI_F32) {
+        float x = __builtin_bit_cast(float, b);
+        if (!isfinite(x)) return 0u;
+        if (x == 0.0f) x = 0.0f;
+        const float z = x * inv_t;
+        if (!isfinite(z)) return 0u;
+        uint32_t u = __builtin_bit_cast(uint32_t, z);
+        if (z == 0.0f) u = 0u;
+        return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    } else {
+        if (!Elem<DT>::finite_bits(b) || !isfinite(Elem<DT>::decode(b) * inv_t)) return 0u;
+        return key16(b);
+    }
+}
+template <int DT>
+__device__ __forceinline__ float dist_z(uint32_t k, float inv_t) {
+    if constexpr (DT == VI_F32) return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+    else return Elem<DT>::decode(unkey16(k)) * inv_t;
+}
+
+// Support membership of a logit of key k; rank: its place among the row's
+// end-key logits in id order (used only when k is the end key).
+__device__ __forceinline__ bool in_support(uint32_t k, const FullBound& B, uint32_t rank) {
+    if (!k || !B.valid) return false;
+    if (k != B.end_key) return k > B.end_key;
+    return B.end_take == 0xffffffffu || rank < B.end_take;
+}
+__device__ __forceinline__ bool counts_rank(uint32_t k, const FullBound& B) {
+    return k && B.valid && k == B.end_key && B.end_take != 0xffffffffu;
+}
+
+// End-key logits of ids [lo, hi) of a row; all threads (NT of them).
+template <int DT, int NT>
+__device__ uint32_t end_key_count(const void* row, int64_t lo, int64_t hi, const FullBound& B, uint32_t* tmp) {
+    uint32_t c = 0u;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += NT) c += counts_rank(dist_key<DT>(load_bits<DT>(row, i), B.inv_t), B) ? 1u : 0u;
+    uint32_t tot = 0u;
+    (void)block_exclusive_scan_u32<NT>(c, tmp, &tot);
+    return tot;
+}
+
+// p (or q) of token x in row r; all threads.
+template <int DT, int NT>
+__device__ double prob_at(const FullRows& R, size_t r, int x, uint32_t* tmp) {
+    const FullBound B = R.bound[r];
+    const void* row = row_at(R, r);
+    const uint32_t k = dist_key<DT>(load_bits<DT>(row, x), B.inv_t);
+    uint32_t rank = 0u;
+    if (counts_rank(k, B)) {   // (uniform)
+        const int s = x / R.slice;
+        rank = R.bases[r * kFullBaseSlots + s] + end_key_count<DT, NT>(row, int64_t(s) * R.slice, x, B, tmp);
+    }
+    return in_support(k, B, rank) ? exp(double(dist_z<DT>(k, B.inv_t)) - B.z0) / B.s_n : 0.0;
+}
+
+// The accept test of every (lane, position) of the full-vocabulary lanes:
+// u_a < min(1, p(d) / q(d)) with the target softmax p and the draft q at the
+// drafted token; position `drafts` takes the bonus row's draw.
+template <int TDT, int DDT>
+__global__ __launch_bounds__(kFT) void verify_full_accept_kernel(FullVerifyArgs a) {
+    __shared__ uint32_t tmp[kFT / kWave + 1];
+    const int j = blockIdx.x, l = blockIdx.y;
+    const vi_row_params p = a.params[l];
+    if (!verify_list_refused(p)) return;
+    PosDecision* out = a.dec + size_t(l) * (a.drafts + 1) + j;
+    if (j == a.drafts) {
+        if (a.target_rows != a.drafts + 1 || threadIdx.x != 0) return;
+        const size_t tr = size_t(l) * a.target_rows + j;
+        const uint32_t f = a.t.stats[tr].flags;
+        const int32_t tok = a.ttok[tr];
+        const bool bad = (f & VI_FLAG_ERROR) || tok < 0 || tok >= a.vocabulary;
+        *out = PosDecision{bad ? -1 : tok, (f & VI_FLAG_ERROR) ? uint32_t(VI_FLAG_ERROR) : 0u, 0, 0};
+        return;
+    }
+    const size_t tr = size_t(l) * a.target_rows + j, dr = size_t(l) * a.drafts + j;
+    const int32_t x = a.drafted[dr];
+    uint32_t flags = (a.t.stats[tr].flags | a.d.stats[dr].flags) &
+                     uint32_t(VI_FLAG_NONFINITE | VI_FLAG_EMPTY | VI_FLAG_ERROR);
+    double q = 0.0, pv = 0.0;
+    if (x >= 0 && x < a.vocabulary) {
+        q = prob_at<DDT, kFT>(a.d, dr, x, tmp);
+        pv = prob_at<TDT, kFT>(a.t, tr, x, tmp);
+    }
+    if (threadIdx.x == 0) {
+        const double ua = philox_uniform(p.seed, p.lane, p.position + j, 1u);
+        double acc = 0.0;
+        if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
+        else acc = fmin(1.0, pv / q);
+        const int accept = (!(flags & VI_FLAG_ERROR) && q != 0.0 && ua < acc) ? 1 : 0;
+        *out = PosDecision{-1, flags, accept, 0};
+    }
+}
+
+// The lane's first rejected position before any accepted terminal token, or -1.
+__device__ int first_rejection(const FullVerifyArgs& a, int l) {
+    for (int j = 0; j < a.drafts; ++j) {
+        const PosDecision e = a.dec[size_t(l) * (a.drafts + 1) + j];
+        if (e.accept) {
+            if (is_terminal(a.terminal, a.n_terminal, a.drafted[size_t(l) * a.drafts + j])) return -1;
+            continue;
+        }
+        return (e.flags & VI_FLAG_ERROR) ? -1 : j;
+    }
+    return -1;
+}
+
+// End-key logits of the row before id r0 (a range start).
+template <int DT>
+__device__ uint32_t range_base(const FullRows& R, size_t r, const FullBound& B, int r0, uint32_t* tmp) {
+    if (!B.valid || B.end_take == 0xffffffffu) return 0u;   // (uniform)
+    const int s = r0 / R.slice, in = r0 - s * R.slice;
+    return R.bases[r * kFullBaseSlots + s] +
+           (in ? end_key_count<DT, kRT>(row_at(R, r), int64_t(s) * R.slice, r0, B, tmp) : 0u);
+}
+
+// Tokens [r0, r1) of the target and draft rows of one position: fn(e, id, p, q)
+// for this thread's tokens r0 + kREPT t + e, in id order; all threads.
+template <int TDT, int DDT, class F>
+__device__ __forceinline__ void range_pass(const FullVerifyArgs& a, size_t tr, size_t dr, int r0, int r1,
+                                           uint32_t* tmp, F&& fn) {
+    const FullBound TB = a.t.bound[tr], DB = a.d.bound[dr];
+    const void* trow = row_at(a.t, tr);
+    const void* drow = row_at(a.d, dr);
+    const uint32_t bt = range_base<TDT>(a.t, tr, TB, r0, tmp), bd = range_base<DDT>(a.d, dr, DB, r0, tmp);
+    const int e0 = r0 + kREPT * int(threadIdx.x);
+    uint32_t kt[kREPT], kd[kREPT], ct = 0u, cd = 0u;
+#pragma unroll
+    for (int e = 0; e < kREPT; ++e) {
+        const int i = e0 + e;
+        kt[e] = i < r1 ? dist_key<TDT>(load_bits<TDT>(trow, i), TB.inv_t) : 0u;
+        kd[e] = i < r1 ? dist_key<DDT>(load_bits<DDT>(drow, i), DB.inv_t) : 0u;
+        ct += counts_rank(kt[e], TB) ? 1u : 0u;
+        cd += counts_rank(kd[e], DB) ? 1u : 0u;
+    }
+    uint32_t tot = 0u;
+    uint32_t rt = bt + block_exclusive_scan_u32<kRT>(ct, tmp, &tot);
+    uint32_t rd = bd + block_exclusive_scan_u32<kRT>(cd, tmp, &tot);
+#pragma unroll
+    for (int e = 0; e < kREPT; ++e) {
+        const bool it = in_support(kt[e], TB, rt), id = in_support(kd[e], DB, rd);
+        rt += counts_rank(kt[e], TB) ? 1u : 0u;
+        rd += counts_rank(kd[e], DB) ? 1u : 0u;
+        const double pv = it ? exp(double(dist_z<TDT>(kt[e], TB.inv_t)) - TB.z0) / TB.s_n : 0.0;
+        const double qv = id ? exp(double(dist_z<DDT>(kd[e], DB.inv_t)) - DB.z0) / DB.s_n : 0.0;
+        fn(e, e0 + e, pv, qv);
+    }
+}
+
+// Sum over the block in a fixed order (the threads' order); every thread gets it.
+__device__ double block_sum_f64(double v, double* tmp) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    const double x = wave_incl_scan_f64(v);
+    if (lane == kWave - 1) tmp[wave] = x;
+    __syncthreads();
+    double s = 0.0;
+    for (int w = 0; w < int(blockDim.x) / kWave; ++w) s += tmp[w];
+    __syncthreads();
+    return s;
+}
+__device__ int block_max_i(int v, int* tmp) {
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+    if (lane_id() == 0) tmp[threadIdx.x / kWave] = v;
+    __syncthreads();
+    int m = -1;
+    for (int w = 0; w < int(blockDim.x) / kWave; ++w) m = max(m, tmp[w]);
+    __syncthreads();
+    return m;
+}
+
+// Residual and p mass of each range of each lane's rejected position.
+template <int TDT, int DDT>
+__global__ __launch_bounds__(kRT) void verify_full_ranges_kernel(FullVerifyArgs a) {
+    __shared__ uint32_t tmp[kW + 1];
+    __shared__ double dtmp[kW];
+    __shared__ int itmp[kW];
+    const int rg = blockIdx.x, l = blockIdx.y;
+    if (!verify_list_refused(a.params[l])) return;
+    const int js = first_rejection(a, l);
+    if (js < 0) return;
+    const size_t tr = size_t(l) * a.target_rows + js, dr = size_t(l) * a.drafts + js;
+    const int r0 = rg * kRange, r1 = min(a.vocabulary, r0 + kRange);
+    double R = 0.0, P = 0.0;
+    int lr = -1, lp = -1;
+    range_pass<TDT, DDT>(a, tr, dr, r0, r1, tmp, [&](int, int i, double pv, double qv) {
+        const double rv = fmax(0.0, pv - qv);
+        R += rv;
+        P += pv;
+        if (rv > 0.0) lr = i;
+        if (pv > 0.0) lp = i;
+    });
+    const double Rt = block_sum_f64(R, dtmp), Pt = block_sum_f64(P, dtmp);
+    const int lrt = block_max_i(lr, itmp), lpt = block_max_i(lp, itmp);
+    if (threadIdx.x == 0) {
+        const size_t at = (size_t(l) * a.ranges + rg) * 2;
+        a.rsum[at] = Rt;
+        a.rsum[at + 1] = Pt;
+        a.rlast[at] = lrt;
+        a.rlast[at + 1] = lpt;
+    }
+}
+
+// The correction of each lane's rejected position: the first token (id order)
+// whose cumulative residual exceeds u_c times the residual mass, or, with no
+// residual mass (<= 1e-9), the first whose cumulative p exceeds u_c; past the
+// end by round-off, the last token with mass.
+template <int TDT, int DDT>
+__global__ __launch_bounds__(kRT) void verify_full_correction_kernel(FullVerifyArgs a) {
+    __shared__ uint32_t tmp[kW + 1];
+    __shared__ double dtmp[kW + 1];
+    __shared__ int s_range, s_tok;
+    __shared__ double s_before, s_target;
+    __shared__ uint32_t s_nores;
+    const int l = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const vi_row_params p = a.params[l];
+    if (!verify_list_refused(p)) return;
+    const int js = first_rejection(a, l);
+    if (js < 0) return;
+    if (tid == 0) {   // the ranges in order
+        double R = 0.0, P = 0.0;
+        int lr = -1, lp = -1;
+        for (int r = 0; r < a.ranges; ++r) {
+            const size_t at = (size_t(l) * a.ranges + r) * 2;
+            R += a.rsum[at];
+            P += a.rsum[at + 1];
+            lr = max(lr, a.rlast[at]);
+            lp = max(lp, a.rlast[at + 1]);
+        }
+        const double uc = philox_uniform(p.seed, p.lane, p.position + js, 2u);
+        const bool nores = !(R > 1e-9) || !isfinite(R);
+        const double target = nores ? uc : uc * R;
+        int range = -1;
+        double cum = 0.0;
+        for (int r = 0; r < a.ranges && range < 0; ++r) {
+            const double m = a.rsum[(size_t(l) * a.ranges + r) * 2 + (nores ? 1 : 0)];
+            if (cum + m > target) range = r;
+            else cum += m;
+        }
+        s_range = range;
+        s_before = cum;
+        s_target = target;
+        s_nores = nores ? 1u : 0u;
+        s_tok = max(0, nores ? lp : lr);   // (round-off past the end)
+    }
+    __syncthreads();
+    const int range = s_range;
+    if (range >= 0) {   // (uniform) the crossing range again, token by token
+        const size_t tr = size_t(l) * a.target_rows + js, dr = size_t(l) * a.drafts + js;
+        const int r0 = range * kRange, r1 = min(a.vocabulary, r0 + kRange);
+        const bool nores = s_nores != 0u;
+        double v[kREPT], own = 0.0;
+        int last = -1;
+        range_pass<TDT, DDT>(a, tr, dr, r0, r1, tmp, [&](int e, int i, double pv, double qv) {
+            v[e] = nores ? pv : fmax(0.0, pv - qv);
+            own += v[e];
+            if (v[e] > 0.0) last = i;
+        });
+        // exclusive prefix of the threads' sums (the order block_sum_f64 sums in)
+        const double incl = wave_incl_scan_f64(own);
+        if (lane == kWave - 1) dtmp[wave] = incl;
+        __syncthreads();
+        double wb = 0.0;
+        for (int w = 0; w < wave; ++w) wb += dtmp[w];
+        const int src = max(lane - 1, 0) << 2;
+        const uint64_t ib = __builtin_bit_cast(uint64_t, incl);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(ib))));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(ib >> 32))));
+        const double ex = wb + (lane ? __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo) : 0.0);
+        const double t = s_target - s_before;
+        if (own > 0.0 && ex <= t && ex + own > t) {   // this thread's tokens hold the crossing
+            double cum = ex;
+            int pick = last;
+            bool found = false;
+            const int e0 = r0 + kREPT * tid;
+#pragma unroll
+            for (int e = 0; e < kREPT; ++e) {
+                cum += v[e];
+                if (!found && cum > t && v[e] > 0.0) { pick = e0 + e; found = true; }
+            }
+            if (pick >= 0) s_tok = pick;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        PosDecision* out = a.dec + size_t(l) * (a.drafts + 1) + js;
+        out->token = s_tok;
+        if (s_nores) out->flags |= VI_FLAG_NO_RESIDUAL;
+    }
+}
+
+// Per-row sampler parameters of the full-vocabulary lanes' rows: the lane's,
+// without penalties, at position + j.
+__global__ void verify_row_params_kernel(const vi_row_params* params, int lanes, int per_lane,
+                                         vi_row_params* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= lanes * per_lane) return;
+    vi_row_params p = params[i / per_lane];
+    p.repetition_penalty = 1.0f;
+    p.presence_penalty = 0.0f;
+    p.frequency_penalty = 0.0f;
+    p.position += i % per_lane;
+    if (!verify_list_refused(p)) p.temperature = 0.0f;   // (list lanes: not the full route's rows)
+    out[i] = p;
+}
+
 }  // namespace
 
 namespace {
@@ -299,6 +655,42 @@ VerifyLayout verify_layout(int lanes, int drafts, int vocabulary) {
 }
 }  // namespace
 
+namespace {
+inline int full_ranges(int vocabulary) { return (vocabulary + kRange - 1) / kRange; }
+inline size_t full_sampler_bytes(int rows, int vocabulary) {
+    return std::max(full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary));
+}
+// The full-vocabulary path's part of the workspace (after the list path's).
+size_t full_verify_bytes(int lanes, int drafts, int vocabulary) {
+    const size_t rows = size_t(lanes) * size_t(2 * drafts + 1);   // target (with bonus) and draft rows
+    size_t b = align_up(rows * sizeof(vi_row_params), 256) + align_up(rows * sizeof(FullBound), 256);
+    b += align_up(rows * kFullBaseSlots * 4, 256) + align_up(rows * sizeof(vi_sample_stats), 256);
+    b += align_up(rows * 4, 256);
+    b += align_up(size_t(lanes) * full_ranges(vocabulary) * 2 * 8, 256) +
+         align_up(size_t(lanes) * full_ranges(vocabulary) * 2 * 4, 256);
+    return b + full_sampler_bytes(lanes * (drafts + 1), vocabulary) + 2048;
+}
+bool full_path_ok(const void* logits, int dtype, int vocabulary, int64_t stride) {
+    if (dtype == VI_F32) return wide_supported(vocabulary, stride) && reinterpret_cast<uintptr_t>(logits) % 4 == 0;
+    return full_supported(dtype, vocabulary, stride) && reinterpret_cast<uintptr_t>(logits) % 16 == 0;
+}
+
+template <int TDT, int DDT>
+void launch_full_verify(const FullVerifyArgs& f, hipStream_t stream) {
+    hipLaunchKernelGGL((verify_full_accept_kernel<TDT, DDT>), dim3(f.drafts + 1, f.lanes), dim3(kFT), 0, stream, f);
+    hipLaunchKernelGGL((verify_full_ranges_kernel<TDT, DDT>), dim3(f.ranges, f.lanes), dim3(kRT), 0, stream, f);
+    hipLaunchKernelGGL((verify_full_correction_kernel<TDT, DDT>), dim3(f.lanes), dim3(kRT), 0, stream, f);
+}
+template <int TDT>
+void launch_full_verify_d(const FullVerifyArgs& f, hipStream_t stream) {
+    switch (f.d.dtype) {
+        case VI_BF16: launch_full_verify<TDT, VI_BF16>(f, stream); break;
+        case VI_F16: launch_full_verify<TDT, VI_F16>(f, stream); break;
+        default: launch_full_verify<TDT, VI_F32>(f, stream); break;
+    }
+}
+}  // namespace
+
 size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     const VerifyLayout v = verify_layout(lanes, drafts, vocabulary);
     size_t b = align_up(size_t(v.trows) * sizeof(vi_greedy_row), 256);
@@ -306,11 +698,13 @@ size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     b += align_up(greedy_workspace(v.trows, vocabulary), 256);
     b += topk_partials_bytes_slices(v.lrows, v.lslices);
     b += align_up(size_t(v.trows) * sizeof(PosDecision), 256);
+    b += full_verify_bytes(lanes, drafts, vocabulary);
     return b + 4096;
 }
 
 // Workspace layout (fixed for a (lanes, drafts, vocabulary) shape, whichever
-// mode runs): greedy rows | lists | greedy partials | top-k partials.
+// mode runs): greedy rows | lists | decisions | greedy partials | top-k
+// partials | the full-vocabulary path's rows and sampler workspace.
 vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStream_t stream) {
     const VerifyLayout v = verify_layout(a.lanes, a.drafts, a.vocabulary);
     const int trows = a.lanes * a.target_rows, drows = a.lanes * a.drafts;
@@ -343,6 +737,12 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
                            a.committed_count, a.lane_flags);
         return launch_status();
     }
+    // full-vocabulary lanes run unless the caller vouches that every sampled
+    // lane has 1 <= top_k <= 64 (VI_VERIFY_SAMPLED_TOPK), and both row sets fit
+    // the full routes
+    const int full_ok = (a.mode == VI_VERIFY_SAMPLED &&
+                         full_path_ok(a.target, a.target_dtype, a.vocabulary, a.target_stride) &&
+                         full_path_ok(a.draft, a.draft_dtype, a.vocabulary, a.draft_stride)) ? 1 : 0;
     st = launch_verify_lists(a.target, a.target_dtype, trows, v.lrows, v.lslices, a.vocabulary, a.target_stride,
                              a.params, a.target_rows, tval, tidx, tvalid, tflags, lws, lbytes, stream);
     if (st != VI_OK) return st;
@@ -351,11 +751,64 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     if (st != VI_OK) return st;
     hipLaunchKernelGGL(verify_position_kernel, dim3(a.drafts + 1, a.lanes), dim3(kFinalizeThreads), 0, stream, tval,
                        tidx, tvalid, tflags, dval, didx, dvalid, dflags, a.drafts, a.target_rows, a.drafted, a.params,
-                       a.vocabulary, dec);
+                       a.vocabulary, full_ok, dec);
     st = launch_status();
     if (st != VI_OK) return st;
+    if (full_ok) {
+        const size_t tn = size_t(trows), dn = size_t(drows);
+        vi_row_params* tpar = c.take<vi_row_params>(tn);
+        vi_row_params* dpar = c.take<vi_row_params>(dn);
+        FullBound* tb = c.take<FullBound>(tn);
+        FullBound* db = c.take<FullBound>(dn);
+        uint32_t* tbase = c.take<uint32_t>(tn * kFullBaseSlots);
+        uint32_t* dbase = c.take<uint32_t>(dn * kFullBaseSlots);
+        vi_sample_stats* tst = c.take<vi_sample_stats>(tn);
+        vi_sample_stats* dst = c.take<vi_sample_stats>(dn);
+        int32_t* ttok = c.take<int32_t>(tn);
+        int32_t* dtok = c.take<int32_t>(dn);
+        const int ranges = full_ranges(a.vocabulary);
+        double* rsum = c.take<double>(size_t(a.lanes) * ranges * 2);
+        int* rlast = c.take<int>(size_t(a.lanes) * ranges * 2);
+        const size_t fbytes = full_sampler_bytes(v.trows, a.vocabulary);
+        unsigned char* fws = c.take<unsigned char>(fbytes);
+        if (!c.ok) return VI_ERR_WORKSPACE;
+        hipLaunchKernelGGL(verify_row_params_kernel, dim3((trows + 255) / 256), dim3(256), 0, stream, a.params,
+                           a.lanes, a.target_rows, tpar);
+        hipLaunchKernelGGL(verify_row_params_kernel, dim3((drows + 255) / 256), dim3(256), 0, stream, a.params,
+                           a.lanes, a.drafts, dpar);
+        // the rows' filtered distributions (and the target rows' draws) from the
+        // full-vocabulary sampler, one row set after the other in one workspace
+        auto sample = [&](const void* logits, int dtype, int rows, int64_t stride, const vi_row_params* par,
+                          int32_t* tok, vi_sample_stats* stats, const FullOut* out) {
+            SampleArgs s{};
+            s.logits = logits; s.dtype = dtype; s.rows = rows; s.vocabulary = a.vocabulary; s.stride = stride;
+            s.params = par; s.tokens = tok; s.stats = stats; s.route_mask = VI_ROUTE_FULL; s.full_out = out;
+            return dtype == VI_F32 ? launch_wide(s, fws, fbytes, nullptr, 0, 0, nullptr, stream)
+                                   : launch_full(s, fws, fbytes, stream);
+        };
+        const FullOut tout{tb, tbase}, dout{db, dbase};
+        st = sample(a.target, a.target_dtype, trows, a.target_stride, tpar, ttok, tst, &tout);
+        if (st != VI_OK) return st;
+        st = sample(a.draft, a.draft_dtype, drows, a.draft_stride, dpar, dtok, dst, &dout);
+        if (st != VI_OK) return st;
+        FullVerifyArgs f{};
+        f.t = FullRows{a.target, a.target_dtype, a.target_stride, tb, tbase, tst,
+                       a.target_dtype == VI_F32 ? kFullSlice32 : kFullSlice16};
+        f.d = FullRows{a.draft, a.draft_dtype, a.draft_stride, db, dbase, dst,
+                       a.draft_dtype == VI_F32 ? kFullSlice32 : kFullSlice16};
+        f.ttok = ttok; f.lanes = a.lanes; f.drafts = a.drafts; f.target_rows = a.target_rows;
+        f.vocabulary = a.vocabulary; f.drafted = a.drafted; f.params = a.params; f.terminal = a.terminal;
+        f.n_terminal = a.n_terminal; f.dec = dec; f.rsum = rsum; f.rlast = rlast; f.ranges = ranges;
+        switch (a.target_dtype) {
+            case VI_BF16: launch_full_verify_d<VI_BF16>(f, stream); break;
+            case VI_F16: launch_full_verify_d<VI_F16>(f, stream); break;
+            default: launch_full_verify_d<VI_F32>(f, stream); break;
+        }
+        st = launch_status();
+        if (st != VI_OK) return st;
+    }
     hipLaunchKernelGGL(verify_chain_kernel, dim3(blocks), dim3(threads), 0, stream, dec, a.lanes, a.drafts,
-                       a.target_rows, a.drafted, a.params, a.terminal, a.n_terminal, a.accepted, a.committed,
+                       a.target_rows, a.drafted, a.params, a.terminal, a.n_terminal, full_ok, a.accepted, a.committed,
                        a.committed_count, a.lane_flags);
     return launch_status();
 }

@@ -131,6 +131,27 @@ vi_status launch_penalty_reset(void* states, int lanes, const PenaltyLayout& l, 
 vi_status launch_penalty_update(void* states, int lanes, int vocabulary, const PenaltyLayout& l,
                                 const int32_t* tokens, const int64_t* offsets, int sign, hipStream_t stream);
 
+// Filtered distribution of one full-route row, as the merges leave it for the
+// probabilities and for verification: the support is every valid logit whose
+// order key lies above end_key, plus the first end_take logits of end_key in id
+// order (end_take ~0u: all of them; end_key 0: every valid logit); there
+// p = exp(z - z0) / s_n.  valid = 0: no distribution (empty or failed row).
+// Order keys: key16 of the (penalized) 16-bit pattern, or the 32-bit order key
+// of z for fp32 rows.
+struct FullBound {
+    double z0, s_n;
+    float inv_t;
+    uint32_t end_key, end_take, valid;
+};
+constexpr int kFullBaseSlots = 32;   // bases per row: end-key logits in the slices before each slice
+// Optional outputs of a full-route launch (verification reads them back).
+struct FullOut {
+    FullBound* bounds;   // [rows]
+    uint32_t* bases;     // [rows][kFullBaseSlots]
+};
+// Logits per slice of the full routes (granularity of FullOut::bases).
+constexpr int kFullSlice16 = 32768, kFullSlice32 = 16384;
+
 struct SampleArgs {
     const void* logits;
     int dtype, rows, vocabulary;
@@ -148,6 +169,7 @@ struct SampleArgs {
     int64_t probs_stride;
     vi_sample_stats* stats;
     uint32_t route_mask;
+    const FullOut* full_out;   // (optional) full-route rows' distributions
 };
 size_t sample_workspace(int rows, int vocabulary, int64_t max_history);
 vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStream_t stream);

@@ -410,6 +410,11 @@ def verify_rows(mode: int, target: torch.Tensor, drafted: torch.Tensor, lanes: i
             raise ValueError("draft must be [lanes * drafts, vocabulary]")
         dptr = draft.data_ptr()
     p_dev = to_device_bytes(params, dev) if params is not None else None
+    if mode == _abi.VERIFY_SAMPLED and params is not None:
+        sampled = params["temperature"] > 0
+        k = params["top_k"]
+        if not np.any(sampled & ((k < 1) | (k > 64))):   # every sampled lane has a top-k list
+            mode = _abi.VERIFY_SAMPLED_TOPK
     term = torch.tensor(list(terminal), dtype=torch.int64, device=dev) if terminal else None
     acc = torch.empty(lanes, dtype=torch.int32, device=dev)
     com = torch.empty(lanes, drafts + 1, dtype=torch.int32, device=dev)
