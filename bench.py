@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--workload", choices=("config5", "config3", "config4"), default="config5",
+    ap.add_argument("--workload", choices=("config5", "config3", "config4", "config4-full"), default="config5",
                     help="config5 (the headline); config3 / config4 time the top-k and verification kernels")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel over 256 MiB x 10 (HBM-counter calibration) and exit")
@@ -143,7 +143,14 @@ def secondary(args):
     else:
         lanes, drafts = 8, 16
         rows = lanes * drafts
-        sets = [W.config4(seed=400 + s, lanes=lanes, drafts=drafts) for s in range(SETS)]
+        full = args.workload == "config4-full"   # top_k off, top_p .8: the full-vocabulary path
+        sets = []
+        for s in range(SETS):
+            t_, d_, x_, p_ = W.config4(seed=400 + s, lanes=lanes, drafts=drafts)
+            if full:
+                p_["top_k"] = 0
+            sets.append((t_, d_, x_, p_))
+        sampled = vi.VERIFY_SAMPLED if full else vi.VERIFY_SAMPLED_TOPK
         tgt = [t16(t, torch.bfloat16) for t, _, _, _ in sets]
         dft = [t16(d, torch.float16) for _, d, _, _ in sets]
         drafted = [torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev) for _, _, x, _ in sets]
@@ -157,16 +164,16 @@ def secondary(args):
 
         def call(i, mode):
             j = i % SETS
+            smp = mode != vi.VERIFY_GREEDY
             return lib.vi_verify_rows(mode, tgt[j].data_ptr(), vi.BF16, V, drafts,
-                                      dft[j].data_ptr() if mode == vi.VERIFY_SAMPLED else None,
-                                      vi.F16 if mode == vi.VERIFY_SAMPLED else 0, V if mode == vi.VERIFY_SAMPLED else 0,
+                                      dft[j].data_ptr() if smp else None, vi.F16 if smp else 0, V if smp else 0,
                                       lanes, drafts, V, drafted[j].data_ptr(),
-                                      params[j].data_ptr() if mode == vi.VERIFY_SAMPLED else None, None, 0,
+                                      params[j].data_ptr() if smp else None, None, 0,
                                       acc.data_ptr(), com.data_ptr(), cnt.data_ptr(), flg.data_ptr(), ws.data_ptr(),
                                       nb, sptr)
 
         def fn(i):
-            return call(i, vi.VERIFY_SAMPLED)
+            return call(i, sampled)
         g_ms, g_launch = _timed(lambda i: call(i, vi.VERIFY_GREEDY), stream, max(K // 2, 50), 10)
         extra["greedy_mode"] = {"ms_per_step": g_ms, "kernel_ms": float(g_launch.mean()),
                                 "bytes_per_launch": rows * V * 2,
@@ -174,7 +181,8 @@ def secondary(args):
         bytes_per_launch = rows * V * 2 * 2
         metric, kernel = "verified drafted rows/sec (8 lanes x 16, sampled rejection)", "verify_* (verify.hip)"
         workload = ("config4: 8 lanes x 16 drafted positions, target bf16 = draft fp16 + N(0,0.5), V=248,320, "
-                    "T .7 / top_p .8 / top_k 20; sampled rejection with the target softmax fused")
+                    + ("T .7 / top_p .8 / top_k off (full-vocabulary p and q)" if full else "T .7 / top_p .8 / top_k 20")
+                    + "; sampled rejection with the target softmax fused")
         assert fn(0) == 0
         torch.cuda.synchronize()
         gpu = (acc.cpu().numpy().copy(), com.cpu().numpy().copy())

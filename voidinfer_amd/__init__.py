@@ -8,7 +8,7 @@ falls back to a CPU implementation.
 from ._abi import (ABSENT_OCCURRENCE, BF16, F16, F32, FLAG_BAD_HISTORY, FLAG_EMPTY, FLAG_ERROR,  # noqa: F401
                    FLAG_NO_RESIDUAL, FLAG_NONFINITE, FLAG_ZERO_Q, GREEDY_ROW, LIB_PATH, ROUTE_ALL, ROUTE_FULL,
                    ROUTE_TOPK, ROW_PARAMS,
-                   SAMPLE_STATS, VERIFY_GREEDY, VERIFY_SAMPLED, DRAFT_SAMPLING, DeviceSampling, VIError, load)
+                   SAMPLE_STATS, VERIFY_GREEDY, VERIFY_SAMPLED, VERIFY_SAMPLED_TOPK, DRAFT_SAMPLING, DeviceSampling, VIError, load)
 
 load()
 

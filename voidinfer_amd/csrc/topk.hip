@@ -88,6 +88,7 @@ struct TopkArgs {
     int* lidx;
     uint32_t* lvalid;       // [rows]
     uint32_t* lflags;       // [rows]
+    int skip_unlisted;      // rows of lanes without a top-k list are left to the full-vocabulary path
 };
 
 // ----------------------------------------------------------- wave-resident list
@@ -366,8 +367,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         slack = a.cfg.presence_penalty < 0.0f ? -a.cfg.presence_penalty : 0.0f;
     } else if constexpr (MODE == kModeVerify) {
         p = a.params[r / a.params_div];
-        // a sampled lane whose top_k lies outside [1, 64] has no list here: the
-        // row is scanned with K = 1 and reported refused (VI_FLAG_ERROR)
+        // a sampled lane whose top_k lies outside [1, 64] has no list here: its
+        // rows are the full-vocabulary path's, or scanned with K = 1 and reported
+        // refused (VI_FLAG_ERROR)
+        if (a.skip_unlisted && verify_list_refused(p)) return;
         if (p.temperature > 0.0f) { K = verify_list_k(p); inv_t = 1.0f / p.temperature; }
     } else {
         p = a.params[r];
@@ -942,8 +945,8 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
 
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
-                              float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, void* ws,
-                              size_t ws_bytes, hipStream_t stream) {
+                              float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
+                              void* ws, size_t ws_bytes, hipStream_t stream) {
     // Partials carved for (layout_rows, layout_slices) so that launches over
     // different row counts share one counter layout in one workspace.
     const TopkPlan plan = topk_plan(rows, vocabulary);
@@ -955,7 +958,7 @@ vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layou
     a.logits = logits; a.vocabulary = vocabulary; a.stride = stride; a.slice_len = plan.slice_len;
     a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
     a.params = params; a.params_div = params_div;
-    a.lval = lval; a.lidx = lidx; a.lvalid = lvalid; a.lflags = lflags;
+    a.lval = lval; a.lidx = lidx; a.lvalid = lvalid; a.lflags = lflags; a.skip_unlisted = skip_unlisted;
     return launch_mode<kModeVerify>(a, dtype, aligned16(logits, stride, dtype), rows, plan.slices, stream);
 }
 

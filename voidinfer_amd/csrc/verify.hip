@@ -294,7 +294,7 @@ __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int draft
 // support's end and mass; bases: end-key logits before each slice) and every
 // target row's own draw (the bonus token); p and q are read off them.
 
-constexpr int kFT = 256;                 // accept kernel threads
+constexpr int kFT = 1024;                // accept kernel threads
 constexpr int kRT = 1024;                // residual kernels' threads
 constexpr int kRange = 16384;            // residual range (divides both routes' slices)
 constexpr int kREPT = kRange / kRT;      // tokens per thread and range
@@ -368,7 +368,18 @@ __device__ __forceinline__ bool counts_rank(uint32_t k, const FullBound& B) {
 template <int DT, int NT>
 __device__ uint32_t end_key_count(const void* row, int64_t lo, int64_t hi, const FullBound& B, uint32_t* tmp) {
     uint32_t c = 0u;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += NT) c += counts_rank(dist_key<DT>(load_bits<DT>(row, i), B.inv_t), B) ? 1u : 0u;
+    constexpr int U = 8;   // loads in flight per thread
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += int64_t(U) * NT) {
+        uint32_t b[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + int64_t(u) * NT;
+            b[u] = i < hi ? load_bits<DT>(row, i) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            c += (i0 + int64_t(u) * NT < hi && counts_rank(dist_key<DT>(b[u], B.inv_t), B)) ? 1u : 0u;
+    }
     uint32_t tot = 0u;
     (void)block_exclusive_scan_u32<NT>(c, tmp, &tot);
     return tot;
@@ -426,17 +437,30 @@ __global__ __launch_bounds__(kFT) void verify_full_accept_kernel(FullVerifyArgs 
     }
 }
 
-// The lane's first rejected position before any accepted terminal token, or -1.
+// The lane's first rejected position before any accepted terminal token, or -1:
+// 64 positions per round, one per lane of the wave (every wave alike).
 __device__ int first_rejection(const FullVerifyArgs& a, int l) {
-    for (int j = 0; j < a.drafts; ++j) {
-        const PosDecision e = a.dec[size_t(l) * (a.drafts + 1) + j];
-        if (e.accept) {
-            if (is_terminal(a.terminal, a.n_terminal, a.drafted[size_t(l) * a.drafts + j])) return -1;
-            continue;
+    const int lane = lane_id();
+    for (int j0 = 0; j0 < a.drafts; j0 += kWave) {
+        const int j = j0 + lane;
+        bool ends = false, usable = false;
+        if (j < a.drafts) {
+            const PosDecision e = a.dec[size_t(l) * (a.drafts + 1) + j];
+            ends = e.accept ? is_terminal(a.terminal, a.n_terminal, a.drafted[size_t(l) * a.drafts + j]) : true;
+            usable = !e.accept && !(e.flags & VI_FLAG_ERROR);
         }
-        return (e.flags & VI_FLAG_ERROR) ? -1 : j;
+        const uint64_t m = ballot(ends);
+        if (m) {
+            const int f = __builtin_ctzll(m);
+            return (ballot(usable) >> f) & 1ull ? j0 + f : -1;
+        }
     }
     return -1;
+}
+
+// exp(z - z0) of a support logit (z <= z0), one hardware exp2.
+__device__ __forceinline__ float weight_f(float z, float z0) {
+    return __builtin_amdgcn_exp2f((z - z0) * 1.44269504088896340736f);
 }
 
 // End-key logits of the row before id r0 (a range start).
@@ -456,6 +480,9 @@ __device__ __forceinline__ void range_pass(const FullVerifyArgs& a, size_t tr, s
     const FullBound TB = a.t.bound[tr], DB = a.d.bound[dr];
     const void* trow = row_at(a.t, tr);
     const void* drow = row_at(a.d, dr);
+    // weights exp(z - z0) in single precision (z0 is a float z); 1 / S_n in double
+    const float tz0 = float(TB.z0), dz0 = float(DB.z0);
+    const double tinv = TB.valid ? 1.0 / TB.s_n : 0.0, dinv = DB.valid ? 1.0 / DB.s_n : 0.0;
     const uint32_t bt = range_base<TDT>(a.t, tr, TB, r0, tmp), bd = range_base<DDT>(a.d, dr, DB, r0, tmp);
     const int e0 = r0 + kREPT * int(threadIdx.x);
     uint32_t kt[kREPT], kd[kREPT], ct = 0u, cd = 0u;
@@ -475,8 +502,8 @@ __device__ __forceinline__ void range_pass(const FullVerifyArgs& a, size_t tr, s
         const bool it = in_support(kt[e], TB, rt), id = in_support(kd[e], DB, rd);
         rt += counts_rank(kt[e], TB) ? 1u : 0u;
         rd += counts_rank(kd[e], DB) ? 1u : 0u;
-        const double pv = it ? exp(double(dist_z<TDT>(kt[e], TB.inv_t)) - TB.z0) / TB.s_n : 0.0;
-        const double qv = id ? exp(double(dist_z<DDT>(kd[e], DB.inv_t)) - DB.z0) / DB.s_n : 0.0;
+        const double pv = it ? double(weight_f(dist_z<TDT>(kt[e], TB.inv_t), tz0)) * tinv : 0.0;
+        const double qv = id ? double(weight_f(dist_z<DDT>(kd[e], DB.inv_t), dz0)) * dinv : 0.0;
         fn(e, e0 + e, pv, qv);
     }
 }
@@ -744,10 +771,10 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
                          full_path_ok(a.target, a.target_dtype, a.vocabulary, a.target_stride) &&
                          full_path_ok(a.draft, a.draft_dtype, a.vocabulary, a.draft_stride)) ? 1 : 0;
     st = launch_verify_lists(a.target, a.target_dtype, trows, v.lrows, v.lslices, a.vocabulary, a.target_stride,
-                             a.params, a.target_rows, tval, tidx, tvalid, tflags, lws, lbytes, stream);
+                             a.params, a.target_rows, tval, tidx, tvalid, tflags, full_ok, lws, lbytes, stream);
     if (st != VI_OK) return st;
     st = launch_verify_lists(a.draft, a.draft_dtype, drows, v.lrows, v.lslices, a.vocabulary, a.draft_stride,
-                             a.params, a.drafts, dval, didx, dvalid, dflags, lws, lbytes, stream);
+                             a.params, a.drafts, dval, didx, dvalid, dflags, full_ok, lws, lbytes, stream);
     if (st != VI_OK) return st;
     hipLaunchKernelGGL(verify_position_kernel, dim3(a.drafts + 1, a.lanes), dim3(kFinalizeThreads), 0, stream, tval,
                        tidx, tvalid, tflags, dval, didx, dvalid, dflags, a.drafts, a.target_rows, a.drafted, a.params,

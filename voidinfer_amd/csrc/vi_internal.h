@@ -82,8 +82,8 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
 // Sorted, filtered top-k lists (z values, ids) of verification rows.
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
-                              float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, void* ws,
-                              size_t ws_bytes, hipStream_t stream);
+                              float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
+                              void* ws, size_t ws_bytes, hipStream_t stream);
 size_t topk_partials_bytes_slices(int rows, int slices);
 
 // History hash (token -> count) per row for the top-k sampler route.
