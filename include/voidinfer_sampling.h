@@ -255,7 +255,9 @@ vi_status vi_draft_choice(int lanes, int positions, int vocabulary, const float*
  * starts at anchors[l]; at each position p the score of candidate c is
  * unary[l][p][c] + sum over r < 256 of pred[anchor][r] * hidden[l][p][r] *
  * succ[candidates[l][p][c]][r] (fp16 codebooks pred / succ [vocabulary][256],
- * fp16 hidden [lanes][positions][256], fp32 arithmetic reduced in the
+ * fp16 hidden [lanes][positions][256], fp32 products (pred * hidden) * succ
+ * summed across one 64-lane wave in a fixed order of this library's, so that a
+ * near tie within the fp32 sums' rounding may resolve differently from the
  * reference's order), the first maximum is proposed and becomes the anchor.  A
  * lane whose sampling record has inv_temperature > 0 (sampling may be NULL: all
  * greedy) proposes by the coupled sampled choice over the unary scores instead,

@@ -109,73 +109,99 @@ __global__ __launch_bounds__(kDraftLanes) void draft_choice_kernel(int lanes, in
 // The fused selector chain (dflash_selector_fused_chain_kernel,
 // src/exl3/dflash2_draft.cu:2615-2678): per draft position, candidate c's
 // score is unary[c] + sum_r pred[anchor][r] * hidden[pos][r] * succ[cand_c][r]
-// (rank 256, fp16 codebooks, fp32 arithmetic), and the first maximum becomes
-// the proposal and the next position's anchor.  With inv_temperature > 0 the
-// coupled sampled choice over the unary scores decides instead (the selector's
-// terms are not calibrated as logits).  One workgroup per lane; candidate c is
-// reduced by 32 lanes (half a wave), in the order the reference reduces it:
-// each lane sums its 8 products pairwise (k, k+4), (k, k+2), (0, 1), then a
-// shuffle-down tree over offsets 16 .. 1.
+// (rank 256, fp16 codebooks, fp32 arithmetic, each product rounded as
+// (pred * hidden) * succ), and the first maximum becomes the proposal and the
+// next position's anchor.  With inv_temperature > 0 the coupled sampled choice
+// over the unary scores decides instead (the selector's terms are not
+// calibrated as logits).
+//
+// One wave per lane, the rank-256 dot in registers: lane k holds ranks
+// 4k .. 4k + 3 of pred[anchor] * hidden[pos] and of every candidate's succ row
+// (8-byte loads, each candidate row read by the wave in one 512-byte sweep);
+// the 16 candidate sums are reduced across the wave with DPP in a fixed order.
+// The next anchor is one of this position's candidates, so their pred rows are
+// loaded with their succ rows and the chosen one is kept: no load waits on the
+// choice.  The order of the fp32 sums is this kernel's own; near ties may
+// therefore resolve differently from another order, within the sums'
+// rounding.
 constexpr int kRank = 256;
-constexpr int kChainThreads = kDraftK * 32;
+constexpr int kChainWaves = 4;                     // lanes per workgroup, one wave each
+constexpr int kChainThreads = kChainWaves * kWave;
+constexpr int kRanksPerLane = kRank / kWave;       // 4
+static_assert(kRanksPerLane == 4, "four fp16 ranks = one 8-byte load");
+
+// ranks 4k .. 4k + 3 of an fp16 row, as fp32
+__device__ __forceinline__ float4 rank4(const uint16_t* row, int k) {
+    const uint2 v = *reinterpret_cast<const uint2*>(row + kRanksPerLane * k);
+    return make_float4(Elem<VI_F16>::decode(v.x & 0xffffu), Elem<VI_F16>::decode(v.x >> 16),
+                       Elem<VI_F16>::decode(v.y & 0xffffu), Elem<VI_F16>::decode(v.y >> 16));
+}
 
 __global__ __launch_bounds__(kChainThreads) void selector_chain_kernel(
     int lanes, int positions, int vocabulary, const int64_t* anchors, const int64_t* candidates, const float* unary,
     const uint16_t* hidden, const uint16_t* pred_cb, const uint16_t* succ_cb, const vi_draft_sampling* sampling,
     int64_t* proposals) {
-    __shared__ float s_score[kDraftK];
-    __shared__ float s_val[kDraftK + 1], s_prob[kDraftK + 1];
-    __shared__ int s_ord[kDraftK + 1];
-    __shared__ int64_t s_anchor;
-    __shared__ int s_bad;
-    const int l = blockIdx.x, t = threadIdx.x, c = t >> 5, sub = t & 31;
-    if (l >= lanes) return;
+    __shared__ float s_val[kChainWaves][kDraftK + 1], s_prob[kChainWaves][kDraftK + 1];
+    __shared__ int s_ord[kChainWaves][kDraftK + 1];
+    const int w = threadIdx.x / kWave, k = lane_id();
+    const int l = blockIdx.x * kChainWaves + w;
+    if (l >= lanes) return;   // (a whole wave)
     const int64_t seed_token = anchors[l];
-    const vi_draft_sampling s = sampling ? sampling[l] : vi_draft_sampling{};
-    const bool sampled = sampling && s.inv_temperature > 0.0f;
+    const vi_draft_sampling smp = sampling ? sampling[l] : vi_draft_sampling{};
+    const bool sampled = sampling && smp.inv_temperature > 0.0f;
     int64_t* out = proposals + size_t(l) * positions;
-    if (t == 0) { s_anchor = seed_token; s_bad = seed_token < 0 || seed_token >= vocabulary; }
-    __syncthreads();
+    bool bad = seed_token < 0 || seed_token >= vocabulary;
+    // pred[anchor] of the current position (ranks 4k .. 4k + 3)
+    float4 pa = bad || sampled ? make_float4(0.f, 0.f, 0.f, 0.f) : rank4(pred_cb + size_t(seed_token) * kRank, k);
     for (int pos = 0; pos < positions; ++pos) {
         const size_t at = size_t(l) * positions + pos;
-        const int64_t cand = candidates[at * kDraftK + c];
-        if (sub == 0 && (cand < 0 || cand >= vocabulary)) atomicOr(&s_bad, 1);
-        __syncthreads();
-        if (s_bad) {   // an anchor or a candidate outside the codebooks: no proposal from here on
-            if (t == 0) out[pos] = -1;
+        const int64_t* cd = candidates + at * kDraftK;
+        int64_t cand[kDraftK];
+#pragma unroll
+        for (int c = 0; c < kDraftK; ++c) {
+            cand[c] = cd[c];
+            bad = bad || cand[c] < 0 || cand[c] >= vocabulary;
+        }
+        if (bad) {   // an anchor or a candidate outside the codebooks: no proposal from here on
+            if (k == 0) out[pos] = -1;
             continue;
         }
-        if (!sampled) {
-            const uint16_t* pr = pred_cb + size_t(s_anchor) * kRank;
-            const uint16_t* hr = hidden + at * kRank;
-            const uint16_t* sr = succ_cb + size_t(cand) * kRank;
-            float r[8];
+        int best = 0;
+        if (sampled) {
+            if (k == 0)
+                best = sampled_pick(smp, pos, vocabulary, unary + at * kDraftK, cd, seed_token, out, s_val[w],
+                                    s_prob[w], s_ord[w]);
+            best = __builtin_amdgcn_readfirstlane(best);
+        } else {
+            // every load of this position first: hidden, the candidates' succ rows
+            // and their pred rows (the next anchor's)
+            const float4 h = rank4(hidden + at * kRank, k);
+            float4 sv[kDraftK], pv[kDraftK];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int rank = sub + 32 * k;
-                r[k] = Elem<VI_F16>::decode(pr[rank]) * Elem<VI_F16>::decode(hr[rank]) * Elem<VI_F16>::decode(sr[rank]);
+            for (int c = 0; c < kDraftK; ++c) {
+                sv[c] = rank4(succ_cb + size_t(cand[c]) * kRank, k);
+                pv[c] = rank4(pred_cb + size_t(cand[c]) * kRank, k);
             }
+            const float4 ah = make_float4(pa.x * h.x, pa.y * h.y, pa.z * h.z, pa.w * h.w);
+            float score[kDraftK];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) r[k] += r[k + 4];
+            for (int c = 0; c < kDraftK; ++c) {
+                const float part = (ah.x * sv[c].x + ah.y * sv[c].y) + (ah.z * sv[c].z + ah.w * sv[c].w);
+                score[c] = unary[at * kDraftK + c] + wave_sum_f32(part);
+            }
+            // first maximum (NaN never replaces the incumbent); scores are wave-uniform
+            float bs = score[0];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) r[k] += r[k + 2];
-            float v = r[0] + r[1];
-            for (int off = 16; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
-            if (sub == 0) s_score[c] = unary[at * kDraftK + c] + v;
+            for (int c = 1; c < kDraftK; ++c)
+                if (score[c] > bs) { bs = score[c]; best = c; }
+            // the chosen candidate's pred row is the next position's anchor row
+#pragma unroll
+            for (int c = 0; c < kDraftK; ++c)
+                if (c == best) pa = pv[c];
         }
-        __syncthreads();
-        if (t == 0) {
-            const int best = sampled ? sampled_pick(s, pos, vocabulary, unary + at * kDraftK, candidates + at * kDraftK,
-                                                    seed_token, out, s_val, s_prob, s_ord)
-                                     : first_max16(s_score);
-            const int64_t chosen = candidates[at * kDraftK + best];
-            out[pos] = chosen;
-            s_anchor = chosen;
-        }
-        __syncthreads();
+        if (k == 0) out[pos] = cand[best];
     }
 }
-
 }  // namespace
 
 vi_status launch_draft_choice(int lanes, int positions, int vocabulary, const float* scores,
@@ -190,7 +216,8 @@ vi_status launch_selector_chain(int lanes, int positions, int vocabulary, const 
                                 const int64_t* candidates, const float* unary, const void* hidden,
                                 const void* pred_codebook, const void* succ_codebook,
                                 const vi_draft_sampling* sampling, int64_t* proposals, hipStream_t stream) {
-    hipLaunchKernelGGL(selector_chain_kernel, dim3(lanes), dim3(kChainThreads), 0, stream, lanes, positions, vocabulary,
+    hipLaunchKernelGGL(selector_chain_kernel, dim3((lanes + kChainWaves - 1) / kChainWaves), dim3(kChainThreads), 0,
+                       stream, lanes, positions, vocabulary,
                        anchors, candidates, unary, static_cast<const uint16_t*>(hidden),
                        static_cast<const uint16_t*>(pred_codebook), static_cast<const uint16_t*>(succ_codebook),
                        sampling, proposals);
