@@ -153,6 +153,15 @@ vi_status vi_topk_rows(const void* logits, int dtype, int rows, int vocabulary,
                        int64_t row_stride, int k, int64_t* ids, float* values,
                        float* logprobs, uint32_t* nonfinite_flag,
                        void* workspace, size_t workspace_bytes, void* stream);
+/* The qualification entry with the reference's own shape
+ * (dflash2_topk16_for_test, src/exl3/dflash2_draft.cu:2390-2420): top-16 of
+ * fp16 rows [rows][vocab] (stride vocab) into ids / values [rows][16].  Like
+ * the reference's, its scratch is the library's: allocated and zero-filled on
+ * the first call on a device (again, larger, when a larger shape comes) and
+ * kept until the process ends, so calls on one device must be ordered on one
+ * stream.  rows 0 is a no-op. */
+vi_status vi_topk16_for_test(const uint16_t* logits, int rows, int vocab, int64_t* ids, float* values,
+                             uint32_t* nonfinite_flag, void* stream);
 
 /* ---- coupled sampled packet (reference semantics) ----------------------------
  * Replaces exl3_launch_sampled_packet (src/exl3/sampled_select.cuh:362-377):

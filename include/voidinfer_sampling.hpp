@@ -1595,8 +1595,8 @@ inline void dflash_sampled_choices(int lanes, int positions, const float* scores
                   "draft sampled choice");
 }
 
-// Scratch of the top-k route (the reference's qualification entry allocates
-// none; this library's slices need vi_topk_workspace_bytes).
+// Scratch of the top-k route (vi_topk_workspace_bytes).  Left empty, the
+// library's own is used, as the reference's qualification entry keeps its own.
 struct Exl3TopkScratch {
     void* base = nullptr;
     std::size_t size = 0;
@@ -1610,6 +1610,10 @@ inline void dflash2_topk16_for_test(const std::uint16_t* logits, int rows, int v
     (void)parallel;
     (void)local_merge;
     if (rows == 0) return;
+    if (!scratch.base) {
+        detail::check(vi_topk16_for_test(logits, rows, vocab, ids, values, nonfinite_flag, stream), "top-16");
+        return;
+    }
     detail::check(vi_topk_rows(logits, VI_F16, rows, vocab, vocab, 16, ids, values, nullptr, nonfinite_flag,
                                scratch.base, scratch.size, stream),
                   "top-16");

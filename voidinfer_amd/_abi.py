@@ -68,6 +68,7 @@ SIGNATURES = {
     "vi_greedy_rows_noalloc": ([_vp, _i, _i, _i, _i64, _u64, _vp, _vp], _i),
     "vi_topk_workspace_bytes": ([_i, _i, _i], _sz),
     "vi_topk_rows": ([_vp, _i, _i, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i),
+    "vi_topk16_for_test": ([_vp, _i, _i, _vp, _vp, _vp, _vp], _i),
     "vi_sampled_packet_workspace_bytes": ([_i, _i], _sz),
     "vi_sampled_packet": ([_vp, _i, _i, _i, _i64, C.POINTER(DeviceSampling), _i, _vp, _i, _vp, _i, _u64,
                            _vp, _vp, _sz, _vp], _i),

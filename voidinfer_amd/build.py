@@ -60,7 +60,27 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_launcher_test(verbose)
     return LIB
+
+
+# The compiled GPU test of the C++ launchers (tests/cpp/test_launchers_gpu.cpp):
+# host code over the HIP runtime and this library, run by a -m gpu test.
+LAUNCHER_TEST = ROOT / "tests" / "cpp" / "test_launchers_gpu"
+
+
+def build_launcher_test(verbose: bool = False) -> Path:
+    rocm = Path(HIPCC).resolve().parent.parent
+    src = LAUNCHER_TEST.with_suffix(".cpp")
+    cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include", "-I",
+           str(ROOT / "include"), str(src), "-o", str(LAUNCHER_TEST), "-L", str(LIB.parent), "-lvoidinfer_sampling",
+           f"-L{rocm}/lib", "-lamdhip64", f"-Wl,-rpath,$ORIGIN/../../voidinfer_amd:{rocm}/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"launcher test build failed:\n{res.stderr}")
+    if verbose:
+        print(f"built {LAUNCHER_TEST}")
+    return LAUNCHER_TEST
 
 
 if __name__ == "__main__":

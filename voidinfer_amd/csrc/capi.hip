@@ -4,6 +4,8 @@
 // synchronizes.
 #include <string.h>
 
+#include <mutex>
+
 #include "vi_internal.h"
 #include "../../include/voidinfer_sampling.hpp"
 
@@ -79,6 +81,38 @@ vi_status vi_topk_rows(const void* logits, int dtype, int rows, int vocabulary, 
         return VI_ERR_INVALID;
     return launch_topk_rows(logits, dtype, rows, vocabulary, row_stride, k, ids, values, logprobs, nonfinite_flag,
                             workspace, workspace_bytes, as_stream(stream));
+}
+
+vi_status vi_topk16_for_test(const uint16_t* logits, int rows, int vocab, int64_t* ids, float* values,
+                             uint32_t* nonfinite_flag, void* stream) {
+    if (rows == 0) return VI_OK;
+    if (rows < 0 || vocab < 16 || !logits || !ids || !values) return VI_ERR_INVALID;
+    // the library's scratch per device, grown to the largest shape seen
+    struct Owned {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    static Owned owned[64];
+    static std::mutex guard;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return VI_ERR_DEVICE;
+    const size_t need = topk_partials_bytes(rows, vocab);
+    void* ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(guard);
+        Owned& o = owned[dev];
+        if (o.bytes < need) {
+            if (o.ptr && hipFree(o.ptr) != hipSuccess) return VI_ERR_LAUNCH;   // (waits for the device)
+            o.ptr = nullptr;
+            o.bytes = 0;
+            if (hipMalloc(&o.ptr, need) != hipSuccess) return VI_ERR_LAUNCH;
+            if (hipMemset(o.ptr, 0, need) != hipSuccess) return VI_ERR_LAUNCH;
+            o.bytes = need;
+        }
+        ws = o.ptr;
+    }
+    return launch_topk_rows(logits, VI_F16, rows, vocab, vocab, 16, ids, values, nullptr, nonfinite_flag, ws, need,
+                            as_stream(stream));
 }
 
 size_t vi_sampled_packet_workspace_bytes(int rows, int vocabulary) {
