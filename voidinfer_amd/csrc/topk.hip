@@ -668,45 +668,63 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     }
     if constexpr (MODE == kModeSample) handoff_stores_done();   // every wave's probability zeros
     __syncthreads();
-    if (wave != 0) return;
-    for (int w = 1; w < kTopkWaves; ++w)
-        list_merge(L, K, lane < K ? s_val[w][lane] : -kInfF, lane < K ? s_idx[w][lane] : kInvalidId);
+    // the four wave lists merged as a tree: waves 0 and 2 take waves 1 and 3's
+    // lists, then wave 0 takes wave 2's
+    auto tree_merge = [&]() {
+        if (!(wave & 1))
+            list_merge(L, K, lane < K ? s_val[wave + 1][lane] : -kInfF, lane < K ? s_idx[wave + 1][lane] : kInvalidId);
+        if (wave == 2) { s_val[2][lane] = L.v; s_idx[2][lane] = L.i; }
+        __syncthreads();
+        if (wave == 0) list_merge(L, K, lane < K ? s_val[2][lane] : -kInfF, lane < K ? s_idx[2][lane] : kInvalidId);
+    };
+    tree_merge();
     uint32_t f = 0, c = 0;
     float m = -kInfF;
-    for (int w = 0; w < kTopkWaves; ++w) { f |= s_flags[w]; c += s_valid[w]; m = fmaxf(m, s_lm[w]); }
     double s = 0.0;
-    for (int w = 0; w < kTopkWaves; ++w) if (s_lm[w] != -kInfF) s += s_ls[w] * exp(double(s_lm[w]) - double(m));
+    if (wave == 0) {
+        for (int w = 0; w < kTopkWaves; ++w) { f |= s_flags[w]; c += s_valid[w]; m = fmaxf(m, s_lm[w]); }
+        for (int w = 0; w < kTopkWaves; ++w) if (s_lm[w] != -kInfF) s += s_ls[w] * exp(double(s_lm[w]) - double(m));
+    }
 
     if (slices > 1) {
         // ---- publish the slice, last arriver merges
-        const size_t at = (size_t(r) * slices + slice) * kMaxK;
-        if (lane < K) { put_agent(&a.pval[at + lane], L.v); put_agent(&a.pidx[at + lane], L.i); }
-        if (lane == 0) {
-            SliceHeader& h = a.phdr[size_t(r) * slices + slice];
-            put_agent(&h.flags, f); put_agent(&h.valid, c); put_agent(&h.lse_max, m); put_agent(&h.lse_sum, s);
+        __shared__ int s_last;
+        if (wave == 0) {
+            const size_t at = (size_t(r) * slices + slice) * kMaxK;
+            if (lane < K) { put_agent(&a.pval[at + lane], L.v); put_agent(&a.pidx[at + lane], L.i); }
+            if (lane == 0) {
+                SliceHeader& h = a.phdr[size_t(r) * slices + slice];
+                put_agent(&h.flags, f); put_agent(&h.valid, c); put_agent(&h.lse_max, m); put_agent(&h.lse_sum, s);
+            }
+            handoff_stores_done();
+            if (lane == 0) s_last = atomicAdd(&a.arrivals[r], 1u) == uint32_t(slices - 1) ? 1 : 0;
         }
-        handoff_stores_done();
-        uint32_t arrived = 0;
-        if (lane == 0) arrived = atomicAdd(&a.arrivals[r], 1u);
-        if (readlane_i(int(arrived), 0) != slices - 1) return;
+        __syncthreads();
+        if (!s_last) return;
         handoff_acquire();
+        // every slice's sorted list, merged in: wave w takes a quarter of the
+        // slices (the loads of eight in flight together), then the tree above
         L = WaveList{};
-        // every slice's sorted list, merged in; the loads of eight slices are in
-        // flight together (one round trip per eight lists, not one per list)
-        for (int sl0 = 0; sl0 < slices; sl0 += 8) {
+        const int per = (slices + kTopkWaves - 1) / kTopkWaves;
+        const int s_lo = wave * per, s_hi = min(slices, s_lo + per);
+        for (int sl0 = s_lo; sl0 < s_hi; sl0 += 8) {
             float bv[8];
             int bi[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const bool ld = sl0 + u < slices && lane < K;
+                const bool ld = sl0 + u < s_hi && lane < K;
                 const size_t src = (size_t(r) * slices + size_t(min(sl0 + u, slices - 1))) * kMaxK + lane;
                 bv[u] = ld ? get_agent(&a.pval[src]) : -kInfF;
                 bi[u] = ld ? get_agent(&a.pidx[src]) : kInvalidId;
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                if (sl0 + u < slices) list_merge(L, K, bv[u], bi[u]);
+                if (sl0 + u < s_hi) list_merge(L, K, bv[u], bi[u]);
         }
+        if (wave & 1) { s_val[wave][lane] = L.v; s_idx[wave][lane] = L.i; }
+        __syncthreads();
+        tree_merge();
+        if (wave != 0) return;
         // the headers: lane sl holds slice sl's (slices <= 64), then reductions
         // across the lanes (the log-sum-exp partials summed in a fixed order)
         uint32_t hf = 0, hc = 0;
@@ -727,6 +745,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 #pragma unroll
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) a.arrivals[r] = 0u;
+    } else if (wave != 0) {
+        return;
     }
 
     // ---- finish the row (wave 0 of the last workgroup)

@@ -24,14 +24,13 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
-// Value of lane (lane - 1); lane 0 gets its own value.
-__device__ __forceinline__ float shift_up_f(float v) {
-    const int src = max(lane_id() - 1, 0) << 2;
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v)));
-}
+// Value of lane (lane - 1); lane 0 gets its own value.  DPP wave_shr:1 (a VALU
+// move across the whole wave; lane 0 keeps the `old` operand, its own value).
 __device__ __forceinline__ int shift_up_i(int v) {
-    const int src = max(lane_id() - 1, 0) << 2;
-    return __builtin_amdgcn_ds_bpermute(src, v);
+    return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float shift_up_f(float v) {
+    return __builtin_bit_cast(float, shift_up_i(__builtin_bit_cast(int, v)));
 }
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
