@@ -104,6 +104,63 @@ __device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int e
     }
 }
 
+// As scan_slice_vec, with the U vectors of a thread's batch handed over
+// together, bfn(vectors[U], first vector index of the batch, valid[U]) (vector
+// u of the batch is number vb + u * NT + threadIdx.x of the slice), and the
+// next batch's loads issued before the current batch is handed over (two
+// register buffers), so the HBM stream keeps going while a batch is worked on.
+template <int DT, bool VEC, int NT, class FB, class FBatch, class F>
+__device__ __forceinline__ void scan_slice_batches(const void* row, int begin, int end, FB&& first, FBatch&& bfn,
+                                                   F&& fn) {
+    constexpr int P = Elem<DT>::kPerVec;
+    constexpr int U = 4;
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+        const int nvec = (end - begin) / P;
+        const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
+        auto load = [&](int vb, uint4 (&d)[U], bool (&ok)[U]) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int v = vb + u * NT + tid;
+                ok[u] = v < nvec;
+                d[u] = ok[u] ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+            }
+        };
+        if (nvec > 0) {   // (uniform)
+            uint4 d[U];
+            bool ok[U];
+            load(0, d, ok);
+            first(d, ok);
+            for (int vb = 0;; vb += U * NT) {
+                const bool more = vb + U * NT < nvec;   // (uniform)
+                uint4 nd[U];
+                bool nok[U];
+                if (more) {
+                    load(vb + U * NT, nd, nok);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) { nd[u] = make_uint4(0, 0, 0, 0); nok[u] = false; }
+                }
+                bfn(d, vb, ok);
+                if (!more) break;
+#pragma unroll
+                for (int u = 0; u < U; ++u) { d[u] = nd[u]; ok[u] = nok[u]; }
+            }
+        }
+        for (int ib = begin + nvec * P; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    } else {
+        for (int ib = begin; ib < end; ib += NT) {
+            const int i = ib + tid;
+            const bool ok = i < end;
+            fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    }
+}
+
 // Slice boundaries: slice s of `slices` covers [s*len, min(V,(s+1)*len)), len a
 // multiple of 64 elements.
 __host__ __device__ inline int slice_len_for(int vocabulary, int slices) {

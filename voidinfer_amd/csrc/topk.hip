@@ -13,10 +13,11 @@
 // Shape: grid (slices, rows), 256 threads (4 waves).  Each wave keeps a sorted
 // top-K list distributed over its lanes (lane i = rank i, K <= 64): an element
 // is offered only if it beats the list's K-th entry (one compare + ballot per
-// element), and accepted candidates are inserted with a ballot/ds_bpermute
-// shift.  The four wave lists merge in LDS, each workgroup publishes its slice
-// list, and the last workgroup of a row to arrive (self-resetting counter)
-// merges the slice lists and finishes the row.  Roofline: HBM, V x sizeof(logit)
+// element), and accepted candidates are inserted with a ballot and a DPP wave
+// shift.  Lists merge by bitonic networks (ds_bpermute lane exchanges): the four
+// wave lists as a tree through LDS, each workgroup publishes its slice list,
+// and the last workgroup of a row to arrive (self-resetting counter) merges the
+// slice lists and finishes the row.  Roofline: HBM, V x sizeof(logit)
 // per row; the per-element work is a compare and a ballot.
 #include <math.h>
 
@@ -35,7 +36,7 @@ constexpr int kInvalidId = 0x7fffffff;
 struct SliceHeader {
     uint32_t flags;     // bit0 non-finite seen, bit1 NaN seen, bit2 bad history, bit3 error
     uint32_t valid;     // finite elements (sampler rows)
-    float lse_max;      // log-sum-exp partial (top-k mode)
+    float lse_max;      // log-sum-exp partial (top-k mode; base-2 units, see the kernel)
     float pad;
     double lse_sum;
 };
@@ -119,9 +120,8 @@ __device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci
 // so the list keeps its form.
 __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi) {
     const int lane = lane_id();
-    const int rsrc = (kWave - 1 - lane) << 2;
-    const float rv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(rsrc, __builtin_bit_cast(int, bv)));
-    const int ri = __builtin_amdgcn_ds_bpermute(rsrc, bi);
+    const float rv = __builtin_bit_cast(float, lanes_reverse(__builtin_bit_cast(uint32_t, bv)));
+    const int ri = int(lanes_reverse(uint32_t(bi)));
     float v = L.v;
     int i = L.i;
     if (better(rv, ri, v, i)) { v = rv; i = ri; }
@@ -139,9 +139,9 @@ __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi)
     L.ki = readlane_i(L.i, K - 1);
 }
 
-// The k-th largest (1 <= k <= 64) of the wave's 64 values (none NaN): a
-// bitonic sort, descending, across the lanes.
-__device__ __forceinline__ float wave_kth_largest(float x, int k) {
+// The wave's 64 values (none NaN) sorted descending across the lanes: a
+// bitonic sort.
+__device__ __forceinline__ float wave_sort_desc(float x) {
     const int lane = lane_id();
 #pragma unroll
     for (int size = 2; size <= kWave; size <<= 1) {
@@ -153,7 +153,21 @@ __device__ __forceinline__ float wave_kth_largest(float x, int k) {
             x = (low == desc) ? fmaxf(x, y) : fminf(x, y);
         }
     }
-    return readlane_f(x, k - 1);
+    return x;
+}
+
+// The 64 largest of two descending lane-sorted lists, sorted descending: the
+// larger of each entry and the other list's entry of rank 63 - lane forms a
+// bitonic sequence, which a descending bitonic merge puts in order.
+__device__ __forceinline__ float merge_desc_f(float a, float b) {
+    const int lane = lane_id();
+    float x = fmaxf(a, __builtin_bit_cast(float, lanes_reverse(__builtin_bit_cast(uint32_t, b))));
+#pragma unroll
+    for (int stride = kWave / 2; stride > 0; stride >>= 1) {
+        const float y = shfl_xor_f(x, stride);
+        x = (lane & stride) ? fminf(x, y) : fmaxf(x, y);
+    }
+    return x;
 }
 
 // Offer one candidate per lane (wave-uniform call).
@@ -421,16 +435,33 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     uint32_t flags = 0, valid = 0;
     float lse_m = -kInfF, lse_s = 0.0f;
     const bool want_lse = MODE == kModeTopk && a.logprobs != nullptr;
+    // Log-sum-exp state in base-2 units: lse_m is the exact f32 value m2 that the
+    // terms 2^(x log2(e) - m2) are taken against (x log2(e) as x * kL2E + x *
+    // kL2ELo, the second the rounding residual of the first), so the row's
+    // log-sum-exp is ln 2 * (m2 + log2(sum)) with no rounding of m2 left over.
     constexpr float kL2E = 1.4426950408889634f;
+    constexpr float kL2ELo = 1.925963e-8f;
+    auto lse_term = [&](float x) { return __builtin_amdgcn_exp2f(fmaf(x, kL2ELo, fmaf(x, kL2E, -lse_m))); };
+    auto lse_rebase = [&](float xmax) {   // (per lane)
+        const float m2 = xmax * kL2E;
+        if (m2 > lse_m) {
+            lse_s = lse_s * __builtin_amdgcn_exp2f(lse_m - m2);
+            lse_m = m2;
+        }
+    };
     // Whole vectors (top-k and verify modes): flags, counts and the running
     // log-sum-exp per vector (one rescale by the vector's maximum, then one exp
     // per element), and the list offered the vector's elements only when some
     // lane's vector maximum reaches the list's K-th entry (no element of a vector
     // below it can enter: it is exact).
-    // Threshold from the first batch: the K-th largest of the lanes' maxima over
-    // their first four vectors.  At least K of the wave's elements reach it, so
-    // it never exceeds the row's K-th best: elements below it are never offered.
+    // Threshold from the first batch: the K-th largest of the workgroup's 256
+    // lane maxima over their first four vectors (the four waves' sorted maxima
+    // merged).  At least K of the row's elements reach it, so it never exceeds
+    // the row's K-th best: elements below it are never offered.  (Pooling the
+    // bounds of a row's workgroups through a global atomic maximum was measured
+    // slower: the same-address atomics and reads contend.)
     float tau = -kInfF;
+    __shared__ float s_first[kTopkWaves][kWave];
     auto first_fn = [&](const uint4 (&dv)[4], const bool (&okv)[4]) {
         constexpr int P = Elem<DT>::kPerVec;
         float lm = -kInfF;
@@ -448,7 +479,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 }
             }
         }
-        tau = wave_kth_largest(lm, K);
+        s_first[wave][lane] = wave_sort_desc(lm);
+        __syncthreads();
+        float t = s_first[0][lane];
+#pragma unroll
+        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f(t, s_first[w][lane]);
+        tau = readlane_f(t, K - 1);
     };
     auto vec_exact = [&](const uint4& dv, int id0, bool ok) {
         constexpr int P = Elem<DT>::kPerVec;
@@ -471,13 +507,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
                 float m8 = -kInfF;
 #pragma unroll
                 for (int j = 0; j < P; ++j) m8 = ((finm >> j) & 1u) ? fmaxf(m8, xs[j]) : m8;
-                if (m8 > lse_m) {
-                    lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - m8) * kL2E);
-                    lse_m = m8;
-                }
+                lse_rebase(m8);
 #pragma unroll
                 for (int j = 0; j < P; ++j)
-                    lse_s += ((finm >> j) & 1u) ? __builtin_amdgcn_exp2f((xs[j] - lse_m) * kL2E) : 0.0f;
+                    lse_s += ((finm >> j) & 1u) ? lse_term(xs[j]) : 0.0f;
             }
         } else {   // kModeVerify
 #pragma unroll
@@ -508,49 +541,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         publish_kth();
     };
-    // Fast path: when no lane's vector holds a non-finite element (nor, in verify
-    // mode, one whose scaled logit overflows), every element is a candidate, no
-    // flag is raised, and the maximum bounds the vector; otherwise the wave takes
-    // vec_exact.
-    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
+    // The (lane, element) pairs of a clean vector reaching the gate, offered one
+    // at a time as wave-uniform values (the list only rises meanwhile: each is
+    // checked again against it; the final list does not depend on the order).
+    auto vec_offer = [&](const uint4& dv, int id0, bool ok, float gate) {
         constexpr int P = Elem<DT>::kPerVec;
-        float xs[P];
-        float xmax = -kInfF, xmin = kInfF;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            xs[j] = Elem<DT>::decode(vec_bits<DT>(dv, j));
-            xmax = fmaxf(xmax, xs[j]);
-            xmin = fminf(xmin, xs[j]);
-        }
-        bool clean = !any_nonfinite<DT>(dv);
         const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
-        if (scaled) clean = clean && isfinite(xmax * inv_t) && isfinite(xmin * inv_t);
-        if (ballot(ok && !clean) != 0) {
-            vec_exact(dv, id0, ok);
-            return;
-        }
-        const float vmax = scaled ? xmax * inv_t : xmax;   // (x * inv_t is monotone: the scaled maximum)
-        if constexpr (MODE == kModeTopk) {
-            if (want_lse && ok) {
-                if (xmax > lse_m) {
-                    lse_s = lse_s * __builtin_amdgcn_exp2f((lse_m - xmax) * kL2E);
-                    lse_m = xmax;
-                }
-#pragma unroll
-                for (int j = 0; j < P; ++j) lse_s += __builtin_amdgcn_exp2f((xs[j] - lse_m) * kL2E);
-            }
-        } else {
-            valid += ok ? uint32_t(P) : 0u;
-        }
-        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
-        if (ballot(ok && vmax >= gate) == 0) return;
-        // the (lane, element) pairs reaching the gate, offered one at a time as
-        // wave-uniform values (the list only rises meanwhile: each is checked
-        // again against it; the final list does not depend on the order)
         uint32_t cm = 0;
 #pragma unroll
-        for (int j = 0; j < P; ++j) cm |= uint32_t(ok && (scaled ? xs[j] * inv_t : xs[j]) >= gate) << j;
+        for (int j = 0; j < P; ++j) {
+            const float x = Elem<DT>::decode(vec_bits<DT>(dv, j));
+            cm |= uint32_t(ok && (scaled ? x * inv_t : x) >= gate) << j;
+        }
         uint64_t lanes = ballot(cm != 0u);
+        if (!lanes) return;
         if (__builtin_popcountll(lanes) > 8) {   // many (large k, early in the slice): element-wise
 #pragma unroll 1
             for (int j = 0; j < P; ++j) {
@@ -578,6 +582,96 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         publish_kth();
     };
+    // Fast path: when no lane's vector holds a non-finite element (nor, in verify
+    // mode, one whose scaled logit overflows), every element is a candidate, no
+    // flag is raised, and the maximum bounds the vector; otherwise the wave takes
+    // vec_exact.
+    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
+        constexpr int P = Elem<DT>::kPerVec;
+        float xs[P];
+        float xmax = -kInfF, xmin = kInfF;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            xs[j] = Elem<DT>::decode(vec_bits<DT>(dv, j));
+            xmax = fmaxf(xmax, xs[j]);
+            xmin = fminf(xmin, xs[j]);
+        }
+        bool clean = !any_nonfinite<DT>(dv);
+        const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
+        if (scaled) clean = clean && isfinite(xmax * inv_t) && isfinite(xmin * inv_t);
+        if (ballot(ok && !clean) != 0) {
+            vec_exact(dv, id0, ok);
+            return;
+        }
+        const float vmax = scaled ? xmax * inv_t : xmax;   // (x * inv_t is monotone: the scaled maximum)
+        if constexpr (MODE == kModeTopk) {
+            if (want_lse && ok) {
+                lse_rebase(xmax);
+#pragma unroll
+                for (int j = 0; j < P; ++j) lse_s += lse_term(xs[j]);
+            }
+        } else {
+            valid += ok ? uint32_t(P) : 0u;
+        }
+        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
+        if (ballot(ok && vmax >= gate) == 0) return;
+        vec_offer(dv, id0, ok, gate);
+    };
+    // Top-k mode, a whole batch of clean vectors at a time: one maximum over the
+    // batch for the gate and the log-sum-exp rescale, one exp per element, the
+    // shared K-th entries read once; a batch holding a non-finite element goes
+    // vector by vector through vec_exact.
+    auto batch_fn = [&](const uint4 (&dv)[4], int vb, const bool (&okv)[4]) {
+        constexpr int P = Elem<DT>::kPerVec;
+        const int id_base = begin + (vb + int(threadIdx.x)) * P;
+        bool bad = false;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bad |= okv[u] & any_nonfinite<DT>(dv[u]);
+        if (ballot(bad) != 0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vec_exact(dv[u], id_base + u * kTopkThreads * P, okv[u]);
+            return;
+        }
+        // (maxima and sums per vector, masked once per vector; the vectors of
+        // invalid lanes are zeros)
+        float vm[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float m;
+            if constexpr (DT == VI_F16) {   // packed half maxima (clean vectors: no NaN)
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                auto H = [](uint32_t w) { return __builtin_bit_cast(h2, w); };
+                const h2 t = __builtin_elementwise_max(__builtin_elementwise_max(H(dv[u].x), H(dv[u].y)),
+                                                       __builtin_elementwise_max(H(dv[u].z), H(dv[u].w)));
+                m = float(t[0] > t[1] ? t[0] : t[1]);
+            } else {
+                m = Elem<DT>::decode(vec_bits<DT>(dv[u], 0));
+#pragma unroll
+                for (int j = 1; j < P; ++j) m = fmaxf(m, Elem<DT>::decode(vec_bits<DT>(dv[u], j)));
+            }
+            vm[u] = okv[u] ? m : -kInfF;
+        }
+        const float bm = fmaxf(fmaxf(vm[0], vm[1]), fmaxf(vm[2], vm[3]));
+        if (want_lse) {
+            lse_rebase(bm);
+            float acc[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < P; ++j)
+                    a += lse_term(Elem<DT>::decode(vec_bits<DT>(dv[u], j)));
+                acc[u] = okv[u] ? a : 0.0f;
+            }
+            lse_s += (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        }
+        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
+        if (ballot(bm >= gate) == 0) return;
+        // only the vectors some lane's maximum says hold a candidate
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (ballot(vm[u] >= gate) != 0) vec_offer(dv[u], id_base + u * kTopkThreads * P, okv[u], gate);
+    };
     auto elem_fn = [&](uint32_t bits, int id, bool ok) {
         const float x = Elem<DT>::decode(bits);
         const bool finite = Elem<DT>::finite_bits(bits);
@@ -588,11 +682,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             const bool cand = ok & !nan;
             if (want_lse) {   // (uniform)
                 const bool use = ok & finite;
-                const float m_new = use ? fmaxf(lse_m, x) : lse_m;
-                const float scale = m_new == lse_m ? 1.0f : __builtin_amdgcn_exp2f((lse_m - m_new) * 1.4426950408889634f);
-                const float term = use ? __builtin_amdgcn_exp2f((x - m_new) * 1.4426950408889634f) : 0.0f;
-                lse_s = lse_s * scale + term;
-                lse_m = m_new;
+                if (use) lse_rebase(x);
+                lse_s += use ? lse_term(x) : 0.0f;
             }
             list_offer(L, K, cand, x, id);
         } else if constexpr (MODE == kModePacket) {
@@ -637,7 +728,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             list_offer(L, K, cand, v, id);
         }
     };
-    if constexpr (MODE == kModeTopk || MODE == kModeVerify)
+    if constexpr (MODE == kModeTopk)
+        scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
+    else if constexpr (MODE == kModeVerify)
         scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, first_fn, vec_fn, elem_fn);
     else
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
@@ -661,7 +754,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         float m = lse_m;
 #pragma unroll
         for (int o = 32; o; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
-        double s = (lse_m == -kInfF) ? 0.0 : double(lse_s) * exp(double(lse_m) - double(m));
+        double s = (lse_m == -kInfF) ? 0.0 : double(lse_s) * double(__builtin_amdgcn_exp2f(lse_m - m));
 #pragma unroll
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) { s_flags[wave] = f; s_valid[wave] = c; s_lm[wave] = m; s_ls[wave] = s; }
@@ -683,7 +776,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     double s = 0.0;
     if (wave == 0) {
         for (int w = 0; w < kTopkWaves; ++w) { f |= s_flags[w]; c += s_valid[w]; m = fmaxf(m, s_lm[w]); }
-        for (int w = 0; w < kTopkWaves; ++w) if (s_lm[w] != -kInfF) s += s_ls[w] * exp(double(s_lm[w]) - double(m));
+        for (int w = 0; w < kTopkWaves; ++w)
+            if (s_lm[w] != -kInfF) s += s_ls[w] * double(__builtin_amdgcn_exp2f(s_lm[w] - m));
     }
 
     if (slices > 1) {
@@ -702,6 +796,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         __syncthreads();
         if (!s_last) return;
         handoff_acquire();
+        // the headers (wave 0, lane sl holds slice sl's; slices <= 64), loaded
+        // now so that their latency overlaps the list loads and merges
+        uint32_t hf = 0, hc = 0;
+        float hm = -kInfF;
+        double hs = 0.0;
+        if (wave == 0 && lane < slices) {
+            const SliceHeader& h = a.phdr[size_t(r) * slices + lane];
+            hf = get_agent(&h.flags); hc = get_agent(&h.valid); hm = get_agent(&h.lse_max); hs = get_agent(&h.lse_sum);
+        }
         // every slice's sorted list, merged in: wave w takes a quarter of the
         // slices (the loads of eight in flight together), then the tree above
         L = WaveList{};
@@ -725,15 +828,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         __syncthreads();
         tree_merge();
         if (wave != 0) return;
-        // the headers: lane sl holds slice sl's (slices <= 64), then reductions
-        // across the lanes (the log-sum-exp partials summed in a fixed order)
-        uint32_t hf = 0, hc = 0;
-        float hm = -kInfF;
-        double hs = 0.0;
-        if (lane < slices) {
-            const SliceHeader& h = a.phdr[size_t(r) * slices + lane];
-            hf = get_agent(&h.flags); hc = get_agent(&h.valid); hm = get_agent(&h.lse_max); hs = get_agent(&h.lse_sum);
-        }
+        // reductions of the headers across the lanes (the log-sum-exp partials
+        // summed in a fixed order)
         f = hf; c = hc; m = hm;
 #pragma unroll
         for (int o = 32; o; o >>= 1) {
@@ -741,7 +837,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             c += shfl_xor_u(c, o);
             m = fmaxf(m, shfl_xor_f(m, o));
         }
-        s = (hm != -kInfF) ? hs * exp(double(hm) - double(m)) : 0.0;
+        s = (hm != -kInfF) ? hs * double(__builtin_amdgcn_exp2f(hm - m)) : 0.0;
 #pragma unroll
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) a.arrivals[r] = 0u;
@@ -771,7 +867,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             a.ids[size_t(r) * K + lane] = L.i;
             a.values[size_t(r) * K + lane] = L.v;
             if (a.logprobs) {
-                const double lse = double(m) + log(s);
+                const double lse = (double(m) + double(__builtin_amdgcn_logf(float(s)))) * 0.6931471805599453;
                 a.logprobs[size_t(r) * K + lane] = (f & kSliceNonfinite) ? __builtin_nanf("") : float(double(L.v) - lse);
             }
         }

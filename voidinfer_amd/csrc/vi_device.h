@@ -1,6 +1,6 @@
 // vi_device.h — device helpers shared by the gfx950 sampling kernels.
 //
-// Wave64 primitives (ballot / readlane / ds_bpermute), 16-byte row loads, the
+// Wave64 primitives (ballot / readlane / ds_bpermute / DPP), 16-byte row loads, the
 // 16-bit order-preserving logit keys, Philox4x32-10, the SplitMix64/Gumbel
 // noise of the coupled route, and the penalty arithmetic of the batched sampler.
 #pragma once
@@ -32,10 +32,6 @@ __device__ __forceinline__ int shift_up_i(int v) {
 __device__ __forceinline__ float shift_up_f(float v) {
     return __builtin_bit_cast(float, shift_up_i(__builtin_bit_cast(int, v)));
 }
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xor(v, m, kWave); }
 
 // (value desc, id asc): exl3_sampled_better (sampled_select.cuh:55-57).
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
@@ -263,6 +259,17 @@ __device__ __forceinline__ double dpp_f64(double v) {
     const uint64_t r = uint64_t(dpp_u32<kCtrl, kRowMask, kBound>(uint32_t(b))) |
                        (uint64_t(dpp_u32<kCtrl, kRowMask, kBound>(uint32_t(b >> 32))) << 32);
     return __builtin_bit_cast(double, r);
+}
+// Lane exchanges through ds_bpermute: the LDS crossbar, off the VALU's issue
+// slots (the kernels that use these are VALU-bound, so DPP or permlane forms of
+// xor distances 4..32, which take several VALU instructions each, cost more).
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xor(v, m, kWave); }
+// Value of lane 63 - lane.
+__device__ __forceinline__ uint32_t lanes_reverse(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_ds_bpermute((kWave - 1 - lane_id()) << 2, int(v)));
 }
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
     x += dpp_u32<0x111, 0xf, true>(x);    // row_shr:1
