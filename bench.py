@@ -53,8 +53,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--workload", choices=("config5", "config3", "config4", "config4-full"), default="config5",
-                    help="config5 (the headline); config3 / config4 time the top-k and verification kernels")
+    ap.add_argument("--workload", choices=("config5", "config1", "config2", "config3", "config4", "config4-full"),
+                    default="config5",
+                    help="config5 (the headline); config1 / config2 report decode-step latency; config3 / config4 "
+                         "time the top-k and verification kernels")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel over 256 MiB x 10 (HBM-counter calibration) and exit")
     return ap.parse_args()
@@ -101,6 +103,122 @@ def _timed(fn, stream, K: int, warmup: int):
         ends[i].record(stream)
     torch.cuda.synchronize()
     return starts[0].elapsed_time(ends[-1]) / K, np.array([a.elapsed_time(b) for a, b in zip(starts, ends)])
+
+
+def cpu_record(value: float, unit: str, cores: int, sample: str, flags: str) -> dict:
+    import oracle
+    return {"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample,
+            "cpu_model": oracle.cpu_model(), "build": flags}
+
+
+def latency(args):
+    """Configurations 1 and 2: one decode step of 1 lane (fp32, V=151,936) or 8
+    lanes (bf16, V=248,320, mixed per-lane parameters, 4,096-token histories),
+    launch-latency bound.  Per call: the GPU time (HIP events on the launch
+    stream around each call, calls back to back) and the host round trip (call,
+    then hipStreamSynchronize, wall clock), medians over the timed calls; for
+    config 1 also the greedy call (vi_greedy_rows).  value = the sampled call's
+    GPU-time median in microseconds (lower is better)."""
+    import numpy as np
+    import torch
+
+    import voidinfer_amd as vi
+    from voidinfer_amd import ops
+    from voidinfer_amd import workloads as W
+    dev = torch.device("cuda:0")
+    lib = vi.load()
+    assert lib.vi_init() == 0, "device is not gfx950"
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+    if args.workload == "config1":
+        x, h, off, p = W.config1()
+        host_logits, dtype, elem = x, vi.F32, 4
+        logits = torch.from_numpy(x).to(dev)
+        max_h = 256
+        workload = ("config1: 1 lane x 151,936 fp32 N(0,2)+Zipf; greedy, then T .7 / top_k 20 / top_p .8 / "
+                    "repetition 1.05 over a 256-token history")
+        metric = "decode-step latency, 1 x 151,936 fp32 (sampled call; greedy call beside it)"
+    else:
+        bits, h, off, p = W.config2()
+        host_logits, dtype, elem = bits, vi.BF16, 2
+        logits = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+        max_h = 4096
+        workload = ("config2: 8 lanes x 248,320 bf16 N(0,2)+Zipf, mixed per-lane T / top_k {0,20,50} / top_p / "
+                    "min_p and repetition / presence / frequency penalties over 4,096-token histories")
+        metric = "decode-step latency, 8 lanes x 248,320 bf16, mixed per-lane parameters"
+    rows, V = logits.shape
+    hist = torch.from_numpy(h).to(dev)
+    offs = torch.from_numpy(off).to(dev)
+    pdev = vi.to_device_bytes(p, dev)
+    routes = ops.route_mask(p)
+    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+    stats = torch.empty(rows * 32, dtype=torch.uint8, device=dev)
+    nb = lib.vi_sample_workspace_bytes(rows, V, max_h)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    grows = torch.empty(rows * 16, dtype=torch.uint8, device=dev)
+    nbg = lib.vi_greedy_workspace_bytes(rows, V)
+    wsg = torch.zeros(max(nbg, 1), dtype=torch.uint8, device=dev)
+
+    def sample(i):
+        return lib.vi_sample_rows(logits.data_ptr(), dtype, rows, V, V, pdev.data_ptr(), hist.data_ptr(),
+                                  offs.data_ptr(), max_h, tokens.data_ptr(), None, None, V, stats.data_ptr(), routes,
+                                  ws.data_ptr(), nb, sptr)
+
+    def greedy(i):
+        return lib.vi_greedy_rows(logits.data_ptr(), dtype, rows, V, V, i + 1, grows.data_ptr(), wsg.data_ptr(), nbg,
+                                  sptr)
+
+    K = min(args.steps, 500)
+
+    def measure(fn):
+        _, gpu_ms = _timed(fn, stream, K, args.warmup)
+        host = []
+        for i in range(K):
+            t0 = time.perf_counter()
+            assert fn(i) == 0
+            stream.synchronize()
+            host.append((time.perf_counter() - t0) * 1e6)
+        us = gpu_ms * 1e3
+        return {"gpu_us_p50": float(np.median(us)), "gpu_us_p10": float(np.percentile(us, 10)),
+                "gpu_us_p90": float(np.percentile(us, 90)), "host_round_trip_us_p50": float(np.median(host)),
+                "calls": K}
+    assert sample(0) == 0
+    torch.cuda.synchronize()
+    gpu_tok = tokens.cpu().numpy().copy()
+    s_lat = measure(sample)
+    g_lat = measure(greedy) if args.workload == "config1" else None
+    bytes_per_call = rows * V * elem + int(off[-1]) * 4
+    kernel_s = s_lat["gpu_us_p50"] / 1e6
+    achieved = bytes_per_call / kernel_s / 1e9
+    cpu = parity = None
+    if not args.no_cpu:
+        import oracle
+        flags = oracle.use_native()
+        threads = min(rows, args.cpu_threads or len(os.sched_getaffinity(0)))
+        w_tok, _, _, _, margins = oracle.sample_rows(host_logits, dtype, p, h, off, threads=threads)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < args.cpu_seconds and reps < 100000:
+            oracle.sample_rows(host_logits, dtype, p, h, off, threads=threads)
+            reps += 1
+        cpu_s = time.perf_counter() - t0
+        mism = [r for r in range(rows) if w_tok[r] != gpu_tok[r]]
+        parity = {"rows": rows, "mismatches": len(mism),
+                  "unexplained": len([r for r in mism if not (margins[r, 0] < 1e-6 or margins[r, 1] < 1e-6)])}
+        cpu = cpu_record(cpu_s / reps * 1e6, "us per call", threads,
+                         f"{reps} calls of the same step through the oracle ({threads} thread(s)), {cpu_s:.1f} s", flags)
+    print(json.dumps({
+        "metric": metric, "value": s_lat["gpu_us_p50"], "unit": "us", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": s_lat["gpu_us_p50"] / 1e3, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32" if dtype == vi.F32 else "bf16", "data": "synthetic",
+        "config": {"workload": workload, "rows": int(rows), "vocabulary": int(V), "history": max_h,
+                   "routes": int(routes), "kernel": "vi_sample_rows (topk.hip / sample_slices.hip routes)"},
+        "latency": {"sampled": s_lat, "greedy": g_lat},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_GBPS, "traffic": None, "bytes_per_launch": bytes_per_call,
+                     "kernel_ms": s_lat["gpu_us_p50"] / 1e3,
+                     "note": "latency-bound: one call reads a few hundred KB to 4 MB; frac is not the target"},
+        "cpu_baseline": cpu, "parity": parity}))
 
 
 def secondary(args):
@@ -192,12 +310,13 @@ def secondary(args):
     cpu = parity = None
     if not args.no_cpu:
         import oracle
+        flags = oracle.use_native()
         threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 64)
         t0 = time.perf_counter()
         reps = 0
         while True:
             if args.workload == "config3":
-                w_ids = oracle.topk_rows(bits[0], oracle.F16, 8)[0]
+                w_ids = oracle.topk_rows(bits[0], oracle.F16, 8, threads=threads)[0]
             else:
                 t, d, x, p = sets[0]
                 w = oracle.verify_rows(vi.VERIFY_SAMPLED, t, oracle.BF16, d, oracle.F16, 8, 16, x, p, threads=threads)
@@ -207,15 +326,15 @@ def secondary(args):
         cpu_s = time.perf_counter() - t0
         if args.workload == "config3":
             parity = {"rows": rows, "mismatched_rows": int((w_ids != gpu).any(axis=1).sum())}
-            cores = 1
+            cores = threads
         else:
             near = w[4] < 1e-6
             parity = {"lanes": 8, "accepted_mismatches": int((w[0] != gpu[0]).sum()),
                       "committed_mismatches": int(sum((w[1][l] != gpu[1][l]).any() for l in range(8)
                                                       if not near[l].any()))}
             cores = threads
-        cpu = {"value": rows * reps / cpu_s, "unit": "rows/s", "cores": cores, "kind": "port",
-               "sample": f"{reps} steps of input set 0 through oracle/liboracle.so ({cores} thread(s)), {cpu_s:.1f} s"}
+        cpu = cpu_record(rows * reps / cpu_s, "rows/s", cores,
+                         f"{reps} steps of input set 0 through the oracle ({cores} thread(s)), {cpu_s:.1f} s", flags)
     print(json.dumps({
         "metric": metric, "value": rows / (ms / 1e3), "unit": "rows/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -250,6 +369,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.workload in ("config1", "config2"):
+        latency(args)
         return
     if args.workload != "config5":
         secondary(args)
@@ -389,7 +511,7 @@ def main():
         h = hist0.cpu().numpy()
         o = offs0.cpu().numpy()
         threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 64)
-        oracle.lib()
+        flags = oracle.use_native()
         t = time.perf_counter()
         w_tok, _, _, _, margins = oracle.sample_rows(bits, oracle.BF16, p0, h, o, threads=threads)
         reps = 1
@@ -400,10 +522,10 @@ def main():
         mism = [r for r in range(rows) if w_tok[r] != gpu_tok[r]]
         unexplained = [r for r in mism if not (margins[r, 0] < 1e-6 or margins[r, 1] < 1e-6)]
         parity = {"rows": rows, "mismatches": len(mism), "unexplained": len(unexplained)}
-        cpu = {"value": rows * reps / cpu_s, "unit": "rows/s", "cores": threads, "kind": "port",
-               "sample": f"{reps} full steps of the workload ({rows} rows x {VOCAB} bf16, {HISTORY}-token "
-                         f"histories, input set 0) through oracle/liboracle.so (C++ restatement, "
-                         f"{threads} threads), {cpu_s:.1f} s"}
+        cpu = cpu_record(rows * reps / cpu_s, "rows/s", threads,
+                         f"{reps} full steps of the workload ({rows} rows x {VOCAB} bf16, {HISTORY}-token "
+                         f"histories, input set 0) through the oracle (C++ restatement, {threads} threads), "
+                         f"{cpu_s:.1f} s", flags)
 
     out = {
         "metric": METRIC,

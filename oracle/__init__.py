@@ -69,12 +69,59 @@ def build_ref() -> Path | None:
     return REF_LIB_PATH
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo), for baseline records."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+_native = None
+
+
+def native_lib() -> tuple[C.CDLL, str]:
+    """The oracle compiled for this host's CPU (g++ -O3 -march=native into a
+    temporary directory) for CPU-baseline timing, with the flags used; falls back
+    to the portable build (-march=x86-64-v2) when no compiler is available."""
+    global _native
+    if _native is None:
+        import tempfile
+        out = Path(tempfile.gettempdir()) / f"voidinfer_oracle_native_{os.getuid()}.so"
+        flags = ["-std=c++20", "-O3", "-march=native", "-fPIC", "-ffp-contract=off", "-fno-fast-math"]
+        try:
+            subprocess.run(["g++", *flags, "-shared", "-o", str(out), str(HERE / "oracle.cpp"), "-lpthread"],
+                           check=True, capture_output=True, timeout=300)
+            _native = (_load(out), " ".join(["g++", *flags]))
+        except (OSError, subprocess.SubprocessError):
+            _native = (lib(), "prebuilt oracle/liboracle.so (-O3 -march=x86-64-v2)")
+    return _native
+
+
+def use_native() -> str:
+    """Route every wrapper below through native_lib() (same IEEE semantics:
+    -ffp-contract=off, no fast math); returns the build flags."""
+    global _lib
+    L, flags = native_lib()
+    _lib = L
+    return flags
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = C.CDLL(str(LIB_PATH))
+        _lib = _load(LIB_PATH)
+    return _lib
+
+
+def _load(path) -> C.CDLL:
+    if True:
+        L = C.CDLL(str(path))
         vp, i, i64, u32, u64, d = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_double
         sig = {
             "or_decode": ([i, u32], C.c_float),
@@ -103,8 +150,7 @@ def lib() -> C.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = res
-        _lib = L
-    return _lib
+    return L
 
 
 def _p(a: np.ndarray | None):
@@ -158,18 +204,30 @@ def cpu_greedy(logits_f32: np.ndarray) -> int:
     return int(lib().or_cpu_greedy(_p(x), x.size))
 
 
-def topk_rows(logits: np.ndarray, dtype: int, k: int, vocabulary: int | None = None):
+def topk_rows(logits: np.ndarray, dtype: int, k: int, vocabulary: int | None = None, threads: int = 1):
+    """Rows split over `threads` host threads (ctypes releases the GIL)."""
     rows, width = logits.shape
     v = width if vocabulary is None else vocabulary
+    x = np.ascontiguousarray(logits)
     ids = np.zeros((rows, k), dtype=np.int64)
     vals = np.zeros((rows, k), dtype=np.float32)
     lp = np.zeros((rows, k), dtype=np.float32)
-    nf = np.zeros(1, dtype=np.uint32)
-    st = lib().or_topk_rows(_p(np.ascontiguousarray(logits)), dtype, rows, v, width, k, _p(ids), _p(vals), _p(lp),
-                            _p(nf))
-    if st:
+    nf = np.zeros(max(1, rows), dtype=np.uint32)
+
+    def part(lo: int, hi: int) -> int:
+        return lib().or_topk_rows(_p(x[lo:hi]), dtype, hi - lo, v, width, k, _p(ids[lo:hi]), _p(vals[lo:hi]),
+                                  _p(lp[lo:hi]), _p(nf[lo:]))
+    t = max(1, min(threads, rows))
+    if t == 1:
+        sts = [part(0, rows)]
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        cuts = [rows * i // t for i in range(t + 1)]
+        with ThreadPoolExecutor(t) as ex:
+            sts = list(ex.map(lambda i: part(cuts[i], cuts[i + 1]), range(t)))
+    if any(sts):
         raise ValueError("oracle top-k: invalid arguments")
-    return ids, vals, lp, int(nf[0])
+    return ids, vals, lp, int(nf.max())
 
 
 def sampled_packet(scores: np.ndarray, dtype: int, temperature: float, top_k: int, top_p: float, min_p: float,
