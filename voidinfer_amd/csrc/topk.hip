@@ -74,6 +74,7 @@ struct TopkArgs {
     int hash_shift;         // 32 - log2(hash_slots)
     int hash_slots;
     const int64_t* offsets;
+    const int32_t* histories;
     unsigned char* pstate;   // per-lane penalty states (hash and flags) instead of the above
     PenaltyLayout pl;
     int record;              // append each row's sampled token to its lane's state
@@ -83,6 +84,7 @@ struct TopkArgs {
     int64_t probs_stride;
     vi_sample_stats* stats;
     int full_rows_unsupported;  // fp32 logits: rows outside the top-k route fail
+    int pres_words;         // dynamic LDS words for the slice's history-presence bitmap (0: none)
     // kModeVerify: sorted lists of the filtered rows
     int params_div;         // params index = row / params_div
     float* lval;            // [rows][kMaxK]
@@ -116,14 +118,13 @@ __device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci
 // Merge of two sorted lists (lane = rank, (value desc, id asc), unused ranks
 // (-inf, kInvalidId)): the better of each entry and the other list's entry of
 // rank 63 - lane forms a bitonic sequence holding the best 64 of both, which a
-// descending bitonic merge puts in order.  Ranks >= K are cleared afterwards,
-// so the list keeps its form.
-__device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi) {
+// descending bitonic merge puts in order (into av, ai).
+__device__ __forceinline__ void merge_pair(float& av, int& ai, float bv, int bi) {
     const int lane = lane_id();
     const float rv = __builtin_bit_cast(float, lanes_reverse(__builtin_bit_cast(uint32_t, bv)));
     const int ri = int(lanes_reverse(uint32_t(bi)));
-    float v = L.v;
-    int i = L.i;
+    float v = av;
+    int i = ai;
     if (better(rv, ri, v, i)) { v = rv; i = ri; }
 #pragma unroll
     for (int stride = kWave / 2; stride > 0; stride >>= 1) {
@@ -133,6 +134,17 @@ __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi)
         const bool take = low ? better(pv, pi, v, i) : better(v, i, pv, pi);
         if (take) { v = pv; i = pi; }
     }
+    av = v;
+    ai = i;
+}
+
+// A sorted list merged into the wave list; ranks >= K are cleared afterwards,
+// so the list keeps its form.
+__device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi) {
+    const int lane = lane_id();
+    float v = L.v;
+    int i = L.i;
+    merge_pair(v, i, bv, bi);
     L.v = lane < K ? v : -kInfF;
     L.i = lane < K ? i : kInvalidId;
     L.kv = readlane_f(L.v, K - 1);
@@ -168,6 +180,24 @@ __device__ __forceinline__ float merge_desc_f(float a, float b) {
         x = (lane & stride) ? fminf(x, y) : fmaxf(x, y);
     }
     return x;
+}
+
+// The wave's 64 (value, id) pairs sorted (value desc, id asc) across the
+// lanes: a bitonic sort (pairs are distinct except (-inf, kInvalidId) padding).
+__device__ __forceinline__ void wave_sort_pairs(float& v, int& i) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const float pv = shfl_xor_f(v, stride);
+            const int pi = shfl_xor_i(i, stride);
+            const bool desc = (lane & size) == 0 || size == kWave;
+            const bool low = (lane & stride) == 0;
+            const bool take = (low == desc) ? better(pv, pi, v, i) : better(v, i, pv, pi);
+            if (take) { v = pv; i = pi; }
+        }
+    }
 }
 
 // Offer one candidate per lane (wave-uniform call).
@@ -353,7 +383,7 @@ __device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, c
 
 // ------------------------------------------------------------------- the kernel
 template <int DT, bool VEC, int MODE>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
+__global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
     const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     const void* row = static_cast<const unsigned char*>(a.logits) + size_t(r) * size_t(a.stride) * sizeof(typename Elem<DT>::Bits);
@@ -411,6 +441,51 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             for (int i = begin + threadIdx.x; i < end; i += kTopkThreads) put_agent(&pr[i], 0.0f);
         }
     }
+
+    // ---- sample mode: the slice's history tokens as a presence bitmap in LDS
+    // (from the lane's penalty state, or set from its history), so the penalty
+    // lookups of absent tokens (nearly all) never leave the CU
+    extern __shared__ uint32_t s_dyn[];
+    const uint32_t* pres = nullptr;
+    if constexpr (MODE == kModeSample) {
+        if (lookups && a.pres_words > 0) {
+            uint32_t* bm = s_dyn;
+            const int words = (end - begin + 31) / 32;
+            if (a.pstate) {
+                const uint32_t* b1 = reinterpret_cast<const uint32_t*>(a.pstate + size_t(r) * a.pl.lane_bytes +
+                                                                       a.pl.off_b1);
+                for (int w = threadIdx.x; w < words; w += kTopkThreads) bm[w] = b1[begin / 32 + w];
+            } else {
+                for (int w = threadIdx.x; w < words; w += kTopkThreads) bm[w] = 0u;
+                __syncthreads();
+                const int64_t hb = a.offsets[r], hn = a.offsets[r + 1] - hb;
+                constexpr int kU = 8;   // (eight loads in flight per thread)
+                for (int64_t i0 = 0; i0 < hn; i0 += kU * kTopkThreads) {
+                    int32_t t[kU];
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) {
+                        const int64_t i = i0 + u * kTopkThreads + threadIdx.x;
+                        t[u] = i < hn ? a.histories[hb + i] : -1;
+                    }
+#pragma unroll
+                    for (int u = 0; u < kU; ++u)
+                        if (t[u] >= begin && t[u] < end) atomicOr(&bm[(t[u] - begin) >> 5], 1u << ((t[u] - begin) & 31));
+                }
+            }
+            __syncthreads();
+            pres = bm;
+        }
+    }
+    // penalty count of a token of this slice (0 without lookups, or when the
+    // bitmap says the token is absent)
+    auto count_of = [&](int id) -> uint32_t {
+        if (!lookups) return 0u;
+        if (pres) {
+            const int o = id - begin;
+            if (!((pres[o >> 5] >> (o & 31)) & 1u)) return 0u;
+        }
+        return hash_count(table, a.hash_shift, a.hash_slots, id);
+    };
 
     // ---- scan the slice
     // Each wave's list K-th value, shared: an element below another wave's K-th
@@ -709,7 +784,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             float v = p.temperature > 0.0f ? x * inv_t : x;
             bool cand = live && better(v, id, L.kv, L.ki);
             if (lookups && live && (cand || lookup_all || fabsf(x) >= overflow_guard<DT>() || !isfinite(v))) {
-                const uint32_t c = hash_count(table, a.hash_shift, a.hash_slots, id);
+                const uint32_t c = count_of(id);
                 if (c) {
                     const uint32_t pb = penalize_bits<DT>(bits, c, p);
                     if (!Elem<DT>::finite_bits(pb)) { flags |= kSliceNonfinite; live = false; }
@@ -728,12 +803,165 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             list_offer(L, K, cand, v, id);
         }
     };
-    if constexpr (MODE == kModeTopk)
+    // ---- sample mode, batches.  A row qualifies when its penalties only lower a
+    // logit and cannot carry one with |x| below the overflow guard out of the
+    // dtype's range (guard * repetition + frequency * history length + presence
+    // under half the largest finite value): then, as in elem_fn, only elements
+    // whose raw scaled value reaches the gate need their penalty looked up (the
+    // penalized value is never larger), and every finite raw element of a clean
+    // batch stays finite.  A batch holding a non-finite element, an element at
+    // or past the guard or a scaled value that overflows goes element by element
+    // through elem_fn.  Other rows take elem_fn throughout.
+    bool batched = false;
+    if constexpr (MODE == kModeSample) {
+        if (!lookups) {
+            batched = true;
+        } else if (!lookup_all) {
+            const double hmax = a.pstate ? double(reinterpret_cast<const PenaltyHeader*>(
+                                               a.pstate + size_t(r) * a.pl.lane_bytes)->total)
+                                         : double(a.offsets[r + 1] - a.offsets[r]);
+            const double top = DT == VI_F16 ? 65504.0 : 3.3895313892515355e38;
+            batched = double(overflow_guard<DT>()) * double(p.repetition_penalty) +
+                      double(p.frequency_penalty) * hmax + double(p.presence_penalty) < 0.5 * top;
+        }
+    }
+    // live and value of a finite raw element after its penalty (the looked-up
+    // counts given)
+    auto penalized = [&](uint32_t bits, uint32_t c, float& v) -> bool {
+        const float x = Elem<DT>::decode(bits);
+        v = p.temperature > 0.0f ? x * inv_t : x;
+        if (c) {
+            const uint32_t pb = penalize_bits<DT>(bits, c, p);
+            if (!Elem<DT>::finite_bits(pb)) return false;
+            float xp = Elem<DT>::decode(pb);
+            if (xp == 0.0f) xp = 0.0f;
+            v = p.temperature > 0.0f ? xp * inv_t : xp;
+        }
+        return !(p.temperature > 0.0f) || isfinite(v);
+    };
+    // first batch: each lane's largest finite raw element, its penalty looked up
+    // (one lookup per lane, all in flight together), gives one exact penalized
+    // value per lane; the workgroup's K-th largest of these 256 values, from 256
+    // distinct elements, bounds the row's K-th best from below
+    auto first_sample = [&](const uint4 (&dv)[4], const bool (&okv)[4]) {
+        constexpr int P = Elem<DT>::kPerVec;
+        const int id_base = begin + int(threadIdx.x) * P;
+        float mx = -kInfF;
+        uint32_t mbits = 0u;
+        int mid = -1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const uint32_t bits = vec_bits<DT>(dv[u], j);
+                const float x = Elem<DT>::decode(bits);
+                const bool take = okv[u] && Elem<DT>::finite_bits(bits) && (mid < 0 || x > mx);
+                mx = take ? x : mx;
+                mbits = take ? bits : mbits;
+                mid = take ? id_base + u * kTopkThreads * P + j : mid;
+            }
+        float lm = -kInfF;
+        if (mid >= 0) {
+            const uint32_t c = count_of(mid);
+            float v;
+            if (penalized(mbits, c, v)) lm = v;
+        }
+        s_first[wave][lane] = wave_sort_desc(lm);
+        __syncthreads();
+        float t = s_first[0][lane];
+#pragma unroll
+        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f(t, s_first[w][lane]);
+        tau = readlane_f(t, K - 1);
+    };
+    // Candidates of a batch are staged per wave in LDS and go into the list
+    // together: sorted (bitonic, across the lanes), then merged (no insertion
+    // one element at a time; a batch can hold the row's whole top-k early on).
+    __shared__ float s_cv[kTopkWaves][kWave];
+    __shared__ int s_ci[kTopkWaves][kWave];
+    int fill = 0;   // (wave-uniform)
+    auto flush = [&]() {
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        float cv = lane < fill ? s_cv[wave][lane] : -kInfF;
+        int ci = lane < fill ? s_ci[wave][lane] : kInvalidId;
+        wave_sort_pairs(cv, ci);
+        list_merge(L, K, cv, ci);
+        fill = 0;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    };
+    auto stage = [&](bool c, float v, int id) {
+        const uint64_t m = ballot(c);
+        if (!m) return;
+        const int n = __builtin_popcountll(m);
+        if (fill + n > kWave) flush();
+        if (c) {
+            const int pos = fill + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+            s_cv[wave][pos] = v;
+            s_ci[wave][pos] = id;
+        }
+        fill += n;
+    };
+    auto sample_batch = [&](const uint4 (&dv)[4], int vb, const bool (&okv)[4]) {
+        constexpr int P = Elem<DT>::kPerVec;
+        const int id_base = begin + (vb + int(threadIdx.x)) * P;
+        bool bad = false;
+        float vm[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float mx = -kInfF, mn = kInfF;
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const float x = Elem<DT>::decode(vec_bits<DT>(dv[u], j));
+                mx = fmaxf(mx, x);
+                mn = fminf(mn, x);
+            }
+            bool b = any_nonfinite<DT>(dv[u]);
+            if (lookups) b = b || fmaxf(mx, -mn) >= overflow_guard<DT>();
+            if (p.temperature > 0.0f) b = b || !isfinite(mx * inv_t) || !isfinite(mn * inv_t);
+            bad |= okv[u] && b;
+            vm[u] = okv[u] ? (p.temperature > 0.0f ? mx * inv_t : mx) : -kInfF;
+        }
+        if (ballot(bad) != 0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < P; ++j) elem_fn(vec_bits<DT>(dv[u], j), id_base + u * kTopkThreads * P + j, okv[u]);
+            return;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) valid += okv[u] ? uint32_t(P) : 0u;
+        const float gate = fmaxf(L.kv, tau);
+        if (ballot(fmaxf(fmaxf(vm[0], vm[1]), fmaxf(vm[2], vm[3])) >= gate) == 0) return;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (ballot(vm[u] >= gate) == 0) continue;
+            const int id0 = id_base + u * kTopkThreads * P;
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const uint32_t bits = vec_bits<DT>(dv[u], j);
+                const float x = Elem<DT>::decode(bits);
+                const bool want = okv[u] && (p.temperature > 0.0f ? x * inv_t : x) >= gate;
+                if (ballot(want) == 0) continue;
+                float v = -kInfF;
+                const bool c = want && penalized(bits, want ? count_of(id0 + j) : 0u, v) && v >= gate;
+                stage(c, v, id0 + j);
+            }
+        }
+        if (fill) flush();
+    };
+    if constexpr (MODE == kModeTopk) {
         scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
-    else if constexpr (MODE == kModeVerify)
+    } else if constexpr (MODE == kModeVerify) {
         scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, first_fn, vec_fn, elem_fn);
-    else
+    } else if constexpr (MODE == kModeSample) {
+        if (batched)
+            scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
+        else
+            scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
+    } else {
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
+    }
 
     // ---- merge the wave lists in LDS
     __shared__ float s_val[kTopkWaves][kMaxK];
@@ -798,13 +1026,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         handoff_acquire();
         // the headers (wave 0, lane sl holds slice sl's; slices <= 64), loaded
         // now so that their latency overlaps the list loads and merges
-        uint32_t hf = 0, hc = 0;
-        float hm = -kInfF;
-        double hs = 0.0;
-        if (wave == 0 && lane < slices) {
-            const SliceHeader& h = a.phdr[size_t(r) * slices + lane];
-            hf = get_agent(&h.flags); hc = get_agent(&h.valid); hm = get_agent(&h.lse_max); hs = get_agent(&h.lse_sum);
-        }
+        // (loads unconditional, at clamped in-bounds addresses, and selected
+        // afterwards: predicated loads would each wait before the next is issued)
+        const SliceHeader& h = a.phdr[size_t(r) * slices + min(lane, slices - 1)];
+        const bool hl = lane < slices;
+        const uint32_t hf = hl ? get_agent(&h.flags) : 0u, hc = hl ? get_agent(&h.valid) : 0u;
+        const float hm = hl ? get_agent(&h.lse_max) : -kInfF;
+        const double hs = hl ? get_agent(&h.lse_sum) : 0.0;
         // every slice's sorted list, merged in: wave w takes a quarter of the
         // slices (the loads of eight in flight together), then the tree above
         L = WaveList{};
@@ -815,14 +1043,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
             int bi[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const bool ld = sl0 + u < s_hi && lane < K;
                 const size_t src = (size_t(r) * slices + size_t(min(sl0 + u, slices - 1))) * kMaxK + lane;
-                bv[u] = ld ? get_agent(&a.pval[src]) : -kInfF;
-                bi[u] = ld ? get_agent(&a.pidx[src]) : kInvalidId;
+                const float lv = get_agent(&a.pval[src]);
+                const int li = get_agent(&a.pidx[src]);
+                const bool ld = sl0 + u < s_hi && lane < K;
+                bv[u] = ld ? lv : -kInfF;
+                bi[u] = ld ? li : kInvalidId;
             }
+            // the batch's lists merged as a tree (independent merges interleave),
+            // then the result into the wave list
+            const int n = min(8, s_hi - sl0);
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (sl0 + u < s_hi) list_merge(L, K, bv[u], bi[u]);
+            for (int step = 1; step < 8; step <<= 1)
+#pragma unroll
+                for (int u = 0; u + step < 8; u += 2 * step)
+                    if (u + step < n) merge_pair(bv[u], bi[u], bv[u + step], bi[u + step]);
+            list_merge(L, K, bv[0], bi[0]);
         }
         if (wave & 1) { s_val[wave][lane] = L.v; s_idx[wave][lane] = L.i; }
         __syncthreads();
@@ -925,11 +1161,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     }
 }
 
-// History hash builder: one workgroup per row; table cleared, then each history
-// token inserted with CAS (open addressing, linear probing).  row_flags[r]
+// History hash builder: one workgroup per row.  Each history token is
+// inserted with compare-and-swap (open addressing, linear probing), in LDS when
+// the table fits (kHashLds slots: the CAS round trips stay on the CU), then
+// copied out; larger tables are built in place in global memory.  row_flags[r]
 // receives VI_FLAG_BAD_HISTORY for out-of-range tokens and VI_FLAG_ERROR when
 // the history exceeds the workspace's max_history.
-__global__ __launch_bounds__(256) void history_hash_kernel(
+constexpr int kHashThreads = 512;
+constexpr int kHashLds = 8192;   // 64 KB of (token + 1, count)
+__global__ __launch_bounds__(kHashThreads) void history_hash_kernel(
     const vi_row_params* params, const int32_t* histories, const int64_t* offsets, int vocabulary,
     uint2* hash, int hash_shift, int hash_slots, uint32_t* row_flags, int64_t max_history) {
     const int r = blockIdx.x;
@@ -937,14 +1177,18 @@ __global__ __launch_bounds__(256) void history_hash_kernel(
     if (!topk_route(p) || !penalties_active(p)) return;
     const int64_t b = offsets[r], n = offsets[r + 1] - b;
     __shared__ uint32_t s_flags;
+    __shared__ uint2 s_table[kHashLds];
     if (threadIdx.x == 0) s_flags = 0;
-    uint2* table = hash + size_t(r) * size_t(hash_slots);
-    for (int i = threadIdx.x; i < hash_slots; i += blockDim.x) table[i] = make_uint2(0u, 0u);
-    __syncthreads();
-    if (n > max_history) {
-        if (threadIdx.x == 0) s_flags = VI_FLAG_ERROR;
-    } else {
-        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const bool in_lds = hash_slots <= kHashLds;
+    uint2* out = hash + size_t(r) * size_t(hash_slots);
+    auto build = [&](uint2* table) {
+        for (int i = threadIdx.x; i < hash_slots; i += kHashThreads) table[i] = make_uint2(0u, 0u);
+        __syncthreads();
+        if (n > max_history) {
+            if (threadIdx.x == 0) s_flags = VI_FLAG_ERROR;
+            return;
+        }
+        for (int64_t i = threadIdx.x; i < n; i += kHashThreads) {
             const int32_t t = histories[b + i];
             if (t < 0 || t >= vocabulary) { atomicOr(&s_flags, uint32_t(VI_FLAG_BAD_HISTORY)); continue; }
             uint32_t s = (uint32_t(t) * 0x9E3779B1u) >> hash_shift;
@@ -954,8 +1198,12 @@ __global__ __launch_bounds__(256) void history_hash_kernel(
                 s = (s + 1u) & uint32_t(hash_slots - 1);
             }
         }
-    }
+    };
+    if (in_lds) build(s_table);
+    else build(out);
     __syncthreads();
+    if (in_lds)
+        for (int i = threadIdx.x; i < hash_slots; i += kHashThreads) out[i] = s_table[i];
     if (threadIdx.x == 0) row_flags[r] = s_flags;
 }
 
@@ -963,7 +1211,8 @@ template <int MODE>
 vi_status launch_mode(const TopkArgs& args, int dtype, bool vec, int rows, int slices, hipStream_t stream) {
     if (slices < 1 || slices > 64) return VI_ERR_INVALID;   // the merge reads one slice header per lane
     const dim3 grid(slices, rows), block(kTopkThreads);
-#define VI_TOPK_LAUNCH(DT, V) hipLaunchKernelGGL((topk_kernel<DT, V, MODE>), grid, block, 0, stream, args)
+    const size_t dyn = size_t(args.pres_words) * 4;
+#define VI_TOPK_LAUNCH(DT, V) hipLaunchKernelGGL((topk_kernel<DT, V, MODE>), grid, block, dyn, stream, args)
     switch (dtype) {
         case VI_BF16: if (vec) VI_TOPK_LAUNCH(VI_BF16, true); else VI_TOPK_LAUNCH(VI_BF16, false); break;
         case VI_F16: if (vec) VI_TOPK_LAUNCH(VI_F16, true); else VI_TOPK_LAUNCH(VI_F16, false); break;
@@ -995,12 +1244,14 @@ Partials carve_partials(Carver& c, int rows, int slices) {
 }  // namespace
 
 TopkPlan topk_plan(int rows, int vocabulary) {
-    // ~1024 workgroups (4 per CU: every one resident at once — the kernel fits 7
-    // per CU, and a ninth round of stragglers would double the time) where the
-    // row count allows, slices >= 2048 logits.
+    // ~1024 workgroups (4 per CU: every one resident at once — the kernels are
+    // held to 4 waves per SIMD, and a second round of stragglers would double
+    // the time) where the row count allows, slices >= 2048 logits, at most 32
+    // slices per row (the row's last workgroup merges every slice list: for
+    // one or a few rows, 32 slices measured faster than 64 or 16).
     int slices = rows >= 1024 ? 1 : (1024 + rows - 1) / rows;
     slices = std::min(slices, std::max(1, vocabulary / 2048));
-    slices = std::max(1, std::min(slices, 64));
+    slices = std::max(1, std::min(slices, 32));
     const int len = slice_len_for(vocabulary, slices);
     slices = (vocabulary + len - 1) / len;
     return {slices, len};
@@ -1117,7 +1368,7 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
     vi_status st = VI_OK;
     if (run_topk) {
         if (hash) {
-            hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(256), 0, stream, s.params, s.histories,
+            hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(kHashThreads), 0, stream, s.params, s.histories,
                                s.offsets, s.vocabulary, hash, shift, slots, row_flags, s.max_history);
             if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
         }
@@ -1125,7 +1376,13 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         a.logits = s.logits; a.vocabulary = s.vocabulary; a.stride = s.stride; a.slice_len = plan.slice_len;
         a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
         a.params = s.params; a.hash = hash; a.row_flags = row_flags; a.hash_shift = shift; a.hash_slots = slots;
-        a.offsets = s.offsets;
+        a.offsets = s.offsets; a.histories = s.histories;
+        // the presence bitmap (one bit per token of a slice, in dynamic LDS) when
+        // penalties are read: up to 64 KB (a slice of up to 524,288 tokens)
+        if (hash || s.pstate) {
+            const size_t words = size_t(plan.slice_len + 31) / 32;
+            a.pres_words = words * 4 <= 65536 ? int(words) : 0;
+        }
         a.pstate = s.pstate; a.pl = s.playout; a.record = s.record;
         a.tokens = s.tokens; a.uniforms = s.uniforms; a.probs = s.probs; a.probs_stride = s.probs_stride;
         a.stats = s.stats;
