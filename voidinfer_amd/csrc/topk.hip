@@ -657,74 +657,58 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         }
         publish_kth();
     };
-    // Fast path: when no lane's vector holds a non-finite element (nor, in verify
-    // mode, one whose scaled logit overflows), every element is a candidate, no
-    // flag is raised, and the maximum bounds the vector; otherwise the wave takes
-    // vec_exact.
-    auto vec_fn = [&](const uint4& dv, int id0, bool ok) {
-        constexpr int P = Elem<DT>::kPerVec;
-        float xs[P];
-        float xmax = -kInfF, xmin = kInfF;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            xs[j] = Elem<DT>::decode(vec_bits<DT>(dv, j));
-            xmax = fmaxf(xmax, xs[j]);
-            xmin = fminf(xmin, xs[j]);
-        }
-        bool clean = !any_nonfinite<DT>(dv);
-        const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
-        if (scaled) clean = clean && isfinite(xmax * inv_t) && isfinite(xmin * inv_t);
-        if (ballot(ok && !clean) != 0) {
-            vec_exact(dv, id0, ok);
-            return;
-        }
-        const float vmax = scaled ? xmax * inv_t : xmax;   // (x * inv_t is monotone: the scaled maximum)
-        if constexpr (MODE == kModeTopk) {
-            if (want_lse && ok) {
-                lse_rebase(xmax);
-#pragma unroll
-                for (int j = 0; j < P; ++j) lse_s += lse_term(xs[j]);
-            }
-        } else {
-            valid += ok ? uint32_t(P) : 0u;
-        }
-        const float gate = fmaxf(fmaxf(L.kv, tau), shared_kth());
-        if (ballot(ok && vmax >= gate) == 0) return;
-        vec_offer(dv, id0, ok, gate);
-    };
-    // Top-k mode, a whole batch of clean vectors at a time: one maximum over the
-    // batch for the gate and the log-sum-exp rescale, one exp per element, the
-    // shared K-th entries read once; a batch holding a non-finite element goes
-    // vector by vector through vec_exact.
+    // Top-k and verification modes, a whole batch of clean vectors at a time:
+    // the vector maxima bound the gate test and the log-sum-exp rescale, one
+    // exp per element (top-k mode's log-probs), the shared K-th entries read
+    // once; a batch holding a non-finite element (or, in verification, a scaled
+    // value that overflows) goes vector by vector through vec_exact.
     auto batch_fn = [&](const uint4 (&dv)[4], int vb, const bool (&okv)[4]) {
         constexpr int P = Elem<DT>::kPerVec;
         const int id_base = begin + (vb + int(threadIdx.x)) * P;
+        // verification scales by 1/T: a vector whose scaled maximum or minimum
+        // overflows goes through vec_exact like one holding a non-finite element
+        const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
         bool bad = false;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) bad |= okv[u] & any_nonfinite<DT>(dv[u]);
-        if (ballot(bad) != 0) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) vec_exact(dv[u], id_base + u * kTopkThreads * P, okv[u]);
-            return;
-        }
-        // (maxima and sums per vector, masked once per vector; the vectors of
-        // invalid lanes are zeros)
+        // (maxima per vector, masked once per vector; the vectors of invalid
+        // lanes are zeros)
         float vm[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            float m;
-            if constexpr (DT == VI_F16) {   // packed half maxima (clean vectors: no NaN)
+            float m, mn = 0.0f;
+            if constexpr (DT == VI_F16) {   // packed half maxima (used only when clean: no NaN)
                 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
                 auto H = [](uint32_t w) { return __builtin_bit_cast(h2, w); };
                 const h2 t = __builtin_elementwise_max(__builtin_elementwise_max(H(dv[u].x), H(dv[u].y)),
                                                        __builtin_elementwise_max(H(dv[u].z), H(dv[u].w)));
                 m = float(t[0] > t[1] ? t[0] : t[1]);
+                if (scaled) {
+                    const h2 q = __builtin_elementwise_min(__builtin_elementwise_min(H(dv[u].x), H(dv[u].y)),
+                                                           __builtin_elementwise_min(H(dv[u].z), H(dv[u].w)));
+                    mn = float(q[0] < q[1] ? q[0] : q[1]);
+                }
             } else {
                 m = Elem<DT>::decode(vec_bits<DT>(dv[u], 0));
+                mn = m;
 #pragma unroll
-                for (int j = 1; j < P; ++j) m = fmaxf(m, Elem<DT>::decode(vec_bits<DT>(dv[u], j)));
+                for (int j = 1; j < P; ++j) {
+                    const float x = Elem<DT>::decode(vec_bits<DT>(dv[u], j));
+                    m = fmaxf(m, x);
+                    mn = fminf(mn, x);
+                }
             }
-            vm[u] = okv[u] ? m : -kInfF;
+            bool b = any_nonfinite<DT>(dv[u]);
+            if (scaled) b = b || !isfinite(m * inv_t) || !isfinite(mn * inv_t);
+            bad |= okv[u] && b;
+            vm[u] = okv[u] ? (scaled ? m * inv_t : m) : -kInfF;
+        }
+        if (ballot(bad) != 0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vec_exact(dv[u], id_base + u * kTopkThreads * P, okv[u]);
+            return;
+        }
+        if constexpr (MODE == kModeVerify) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) valid += okv[u] ? uint32_t(P) : 0u;
         }
         const float bm = fmaxf(fmaxf(vm[0], vm[1]), fmaxf(vm[2], vm[3]));
         if (want_lse) {
@@ -953,7 +937,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
     if constexpr (MODE == kModeTopk) {
         scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
     } else if constexpr (MODE == kModeVerify) {
-        scan_slice_vec<DT, VEC, kTopkThreads>(row, begin, end, first_fn, vec_fn, elem_fn);
+        scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
     } else if constexpr (MODE == kModeSample) {
         if (batched)
             scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
