@@ -123,6 +123,31 @@ def test_topk_route_penalties(orc, dev, rng, dtype):
     compare(*run_both(orc, dev, bits, dtype, p, hist, offs), p, "topk-pen")
 
 
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_topk_route_ties_and_staging(orc, dev, rng, dtype):
+    """Top-k route rows built to stress the batch scan's staging: values drawn
+    from 12 levels (many exact ties, ordered by id), top_k 64 (a batch stages
+    more than a wave's 64 slots and flushes mid-batch), penalties on tokens of
+    the top level, one row with no history; and one row whose frequency
+    penalty is too large for the batch scan's range check (element path)."""
+    rows, vocab = 10, 30_000
+    levels = rng.uniform(-4, 4, 12).astype(np.float32)
+    x = levels[rng.integers(0, 12, (rows, vocab))]
+    from voidinfer_amd import workloads as W
+    bits = W.encode(x, {0: "bf16", 1: "f16", 2: "f32"}[dtype])
+    p = params(rows, rng, temperature=rng.uniform(0.5, 1.2, rows), top_k=64, top_p=1.0,
+               repetition_penalty=1.1, presence_penalty=0.25, frequency_penalty=0.05)
+    p["frequency_penalty"][3] = 1.0e35 if dtype != 1 else 1.0e4
+    vals = decode_rows(bits, dtype)
+    L = 300
+    hist = np.concatenate([rng.choice(np.flatnonzero(vals[r] == vals[r].max()), L) for r in range(rows)])
+    hist = hist.astype(np.int32)
+    offs = np.arange(rows + 1, dtype=np.int64) * L
+    offs[5:] -= L   # row 4: empty history
+    hist = np.concatenate([hist[: 4 * L], hist[5 * L:]])
+    compare(*run_both(orc, dev, bits, dtype, p, hist, offs), p, "topk-ties")
+
+
 def test_topk_route_increasing_penalties(orc, dev, rng):
     rows, vocab = 8, 20_000
     bits = make_rows(rng, rows, vocab)

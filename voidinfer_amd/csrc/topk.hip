@@ -795,7 +795,10 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
     // penalized value is never larger), and every finite raw element of a clean
     // batch stays finite.  A batch holding a non-finite element, an element at
     // or past the guard or a scaled value that overflows goes element by element
-    // through elem_fn.  Other rows take elem_fn throughout.
+    // through elem_fn.  Other rows take elem_fn throughout, and a row whose
+    // penalties fail the range check has every element looked up (a penalty
+    // could then turn a finite logit that no gate would look at non-finite,
+    // which the row's finite count and flags must see).
     bool batched = false;
     if constexpr (MODE == kModeSample) {
         if (!lookups) {
@@ -807,6 +810,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             const double top = DT == VI_F16 ? 65504.0 : 3.3895313892515355e38;
             batched = double(overflow_guard<DT>()) * double(p.repetition_penalty) +
                       double(p.frequency_penalty) * hmax + double(p.presence_penalty) < 0.5 * top;
+            lookup_all = !batched;
         }
     }
     // live and value of a finite raw element after its penalty (the looked-up
