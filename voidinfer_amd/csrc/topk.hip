@@ -911,31 +911,42 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             vm[u] = okv[u] ? (p.temperature > 0.0f ? mx * inv_t : mx) : -kInfF;
         }
         if (ballot(bad) != 0) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int j = 0; j < P; ++j) elem_fn(vec_bits<DT>(dv[u], j), id_base + u * kTopkThreads * P + j, okv[u]);
+            // (one call per vector with a constant index, each a rolled loop over
+            // its elements: no indexed copy of the batch in scratch memory)
+            auto exact_vec = [&](const uint4& v, int u, bool ok) {
+#pragma unroll 1
+                for (int j = 0; j < P; ++j) elem_fn(vec_bits<DT>(v, j), id_base + u * kTopkThreads * P + j, ok);
+            };
+            exact_vec(dv[0], 0, okv[0]);
+            exact_vec(dv[1], 1, okv[1]);
+            exact_vec(dv[2], 2, okv[2]);
+            exact_vec(dv[3], 3, okv[3]);
             return;
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) valid += okv[u] ? uint32_t(P) : 0u;
         const float gate = fmaxf(L.kv, tau);
         if (ballot(fmaxf(fmaxf(vm[0], vm[1]), fmaxf(vm[2], vm[3])) >= gate) == 0) return;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (ballot(vm[u] >= gate) == 0) continue;
+        // (one call per vector with a constant index: an indexed batch would be
+        // copied to scratch memory)
+        auto cand_vec = [&](const uint4& dvu, int u, bool ok, float vmu) {
+            if (ballot(vmu >= gate) == 0) return;
             const int id0 = id_base + u * kTopkThreads * P;
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                const uint32_t bits = vec_bits<DT>(dv[u], j);
+                const uint32_t bits = vec_bits<DT>(dvu, j);
                 const float x = Elem<DT>::decode(bits);
-                const bool want = okv[u] && (p.temperature > 0.0f ? x * inv_t : x) >= gate;
+                const bool want = ok && (p.temperature > 0.0f ? x * inv_t : x) >= gate;
                 if (ballot(want) == 0) continue;
                 float v = -kInfF;
                 const bool c = want && penalized(bits, want ? count_of(id0 + j) : 0u, v) && v >= gate;
                 stage(c, v, id0 + j);
             }
-        }
+        };
+        cand_vec(dv[0], 0, okv[0], vm[0]);
+        cand_vec(dv[1], 1, okv[1], vm[1]);
+        cand_vec(dv[2], 2, okv[2], vm[2]);
+        cand_vec(dv[3], 3, okv[3], vm[3]);
         if (fill) flush();
     };
     if constexpr (MODE == kModeTopk) {
