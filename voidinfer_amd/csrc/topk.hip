@@ -344,9 +344,8 @@ __device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, c
         token = ids[0]; support = 1; sn = 1.0;
         if (probs_row) probs_row[token] = 1.0f;
     } else {
-        const double z0 = double(z[0]);
-        double s = 0.0;
-        for (int j = 0; j < cap; ++j) { w[j] = exp(double(z[j]) - z0); s += w[j]; }
+        double s = 0.0;   // (w[j] = exp(z[j] - z[0]) filled by the caller, one entry per lane)
+        for (int j = 0; j < cap; ++j) s += w[j];
         const double minp = double(p.min_p), target = double(p.top_p) * s;
         double cum = 0.0;
         for (int j = 0; j < cap; ++j) {
@@ -1131,6 +1130,12 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             a.lflags[r] = ((f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u) | (refused ? VI_FLAG_ERROR : 0u);
         }
     } else {
+        // the candidates' fp64 weights, one per lane (the sums stay on lane 0, in order)
+        __shared__ double s_w[kMaxK];   // (in LDS, not per-lane scratch)
+        const int wcap = (p.temperature > 0.0f) ? min(K, int(c)) : 1;
+        if (p.temperature > 0.0f && lane < wcap) s_w[lane] = exp(double(s_val[0][lane]) - double(s_val[0][0]));
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
         if (lane == 0) {
             uint32_t flags_out = 0;
             if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
@@ -1143,8 +1148,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
                 if (a.stats) { a.stats[r] = vi_sample_stats{}; a.stats[r].flags = flags_out; }
                 return;
             }
-            const int cap = (p.temperature > 0.0f) ? min(K, int(c)) : 1;
-            __shared__ double s_w[kMaxK];   // the weights live in LDS, not per-lane scratch
+            const int cap = wcap;
             float* pr = a.probs ? a.probs + size_t(r) * size_t(a.probs_stride) : nullptr;
             sample_finish(p, cap, s_val[0], s_idx[0], a.vocabulary, &a.tokens[r],
                           a.uniforms ? &a.uniforms[r] : nullptr, pr, a.stats ? &a.stats[r] : nullptr,
@@ -1187,14 +1191,25 @@ __global__ __launch_bounds__(kHashThreads) void history_hash_kernel(
             if (threadIdx.x == 0) s_flags = VI_FLAG_ERROR;
             return;
         }
-        for (int64_t i = threadIdx.x; i < n; i += kHashThreads) {
-            const int32_t t = histories[b + i];
-            if (t < 0 || t >= vocabulary) { atomicOr(&s_flags, uint32_t(VI_FLAG_BAD_HISTORY)); continue; }
-            uint32_t s = (uint32_t(t) * 0x9E3779B1u) >> hash_shift;
-            for (int probe = 0; probe < hash_slots; ++probe) {
-                const uint32_t old = atomicCAS(&table[s].x, 0u, uint32_t(t) + 1u);
-                if (old == 0u || old == uint32_t(t) + 1u) { atomicAdd(&table[s].y, 1u); break; }
-                s = (s + 1u) & uint32_t(hash_slots - 1);
+        constexpr int kU = 8;   // (the history loads of a round issued together)
+        for (int64_t i0 = 0; i0 < n; i0 += int64_t(kU) * kHashThreads) {
+            int32_t tk[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int64_t i = i0 + int64_t(u) * kHashThreads + threadIdx.x;
+                tk[u] = i < n ? histories[b + i] : 0;
+            }
+#pragma unroll 1
+            for (int u = 0; u < kU; ++u) {
+                if (i0 + int64_t(u) * kHashThreads + threadIdx.x >= n) break;   // (past the history's end)
+                const int32_t t = tk[u];
+                if (t < 0 || t >= vocabulary) { atomicOr(&s_flags, uint32_t(VI_FLAG_BAD_HISTORY)); continue; }
+                uint32_t s = (uint32_t(t) * 0x9E3779B1u) >> hash_shift;
+                for (int probe = 0; probe < hash_slots; ++probe) {
+                    const uint32_t old = atomicCAS(&table[s].x, 0u, uint32_t(t) + 1u);
+                    if (old == 0u || old == uint32_t(t) + 1u) { atomicAdd(&table[s].y, 1u); break; }
+                    s = (s + 1u) & uint32_t(hash_slots - 1);
+                }
             }
         }
     };
