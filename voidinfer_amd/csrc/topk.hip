@@ -1,6 +1,6 @@
 // topk.hip — exact top-k selection over logit rows and the samplers built on it.
 //
-// One kernel family, three consumers:
+// One kernel family, four consumers:
 //  * kModeTopk   — DFlash2 draft top-k (dflash2_draft.cu:1827-2342): ids and raw
 //                  values in (value desc, id asc) order, NaN rows in the serial
 //                  insertion order of dflash_topk16_serial_row, plus log-probs.
@@ -9,16 +9,23 @@
 //                  truncation and the Gumbel-max draw.
 //  * kModeSample — rows of the batched sampler whose support lies in a top-k
 //                  list (1 <= top_k <= 64, or temperature 0).
+//  * kModeVerify — the sorted lists of sampled verification's target and draft
+//                  rows.
 //
-// Shape: grid (slices, rows), 256 threads (4 waves).  Each wave keeps a sorted
-// top-K list distributed over its lanes (lane i = rank i, K <= 64): an element
-// is offered only if it beats the list's K-th entry (one compare + ballot per
-// element), and accepted candidates are inserted with a ballot and a DPP wave
-// shift.  Lists merge by bitonic networks (ds_bpermute lane exchanges): the four
-// wave lists as a tree through LDS, each workgroup publishes its slice list,
-// and the last workgroup of a row to arrive (self-resetting counter) merges the
-// slice lists and finishes the row.  Roofline: HBM, V x sizeof(logit)
-// per row; the per-element work is a compare and a ballot.
+// Shape: grid (slices, rows), 256 threads (4 waves), at most 32 slices per row.
+// Each wave keeps a sorted top-K list distributed over its lanes (lane i = rank
+// i, K <= 64).  The slice is read a batch at a time (four 16-byte vectors per
+// lane, the next batch requested first); a batch's vector maxima are compared
+// with a gate — the list's K-th entry, and a lower bound on the row's K-th best
+// taken from the workgroup's first batch — and only vectors that reach it are
+// looked at element by element.  Candidates are inserted with a ballot and a
+// DPP wave shift (top-k and verification modes) or staged per wave and merged
+// in bulk (sampler rows).  Lists merge by bitonic networks (ds_bpermute lane
+// exchanges): the four wave lists as a tree through LDS, each workgroup
+// publishes its slice list, and the last workgroup of a row to arrive
+// (self-resetting counter) tree-merges the slice lists and finishes the row.
+// Roofline: HBM, V x sizeof(logit) per row (+ the history for penalties); the
+// kernels are VALU-issue bound in practice (decode, maxima, the log-sum-exp).
 #include <math.h>
 
 #include "penalty_state.h"
