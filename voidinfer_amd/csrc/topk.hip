@@ -122,21 +122,38 @@ __device__ __forceinline__ void list_insert(WaveList& L, int K, float cv, int ci
     L.ki = readlane_i(L.i, K - 1);
 }
 
+// Lane exchanges: ds_bpermute by default (off the VALU's issue slots, for the
+// VALU-bound scans), DPP / permlane moves when D (the sampler's few-row
+// launches, whose list merges are latency-bound chains of one wave).
+template <bool D> __device__ __forceinline__ float xor_f(float v, int m) {
+    if constexpr (D) return __builtin_bit_cast(float, lanes_xor_dpp(__builtin_bit_cast(uint32_t, v), m));
+    else return shfl_xor_f(v, m);
+}
+template <bool D> __device__ __forceinline__ int xor_i(int v, int m) {
+    if constexpr (D) return int(lanes_xor_dpp(uint32_t(v), m));
+    else return shfl_xor_i(v, m);
+}
+template <bool D> __device__ __forceinline__ uint32_t reverse_u(uint32_t v) {
+    if constexpr (D) return lanes_reverse_dpp(v);
+    else return lanes_reverse(v);
+}
+
 // Merge of two sorted lists (lane = rank, (value desc, id asc), unused ranks
 // (-inf, kInvalidId)): the better of each entry and the other list's entry of
 // rank 63 - lane forms a bitonic sequence holding the best 64 of both, which a
 // descending bitonic merge puts in order (into av, ai).
+template <bool D = false>
 __device__ __forceinline__ void merge_pair(float& av, int& ai, float bv, int bi) {
     const int lane = lane_id();
-    const float rv = __builtin_bit_cast(float, lanes_reverse(__builtin_bit_cast(uint32_t, bv)));
-    const int ri = int(lanes_reverse(uint32_t(bi)));
+    const float rv = __builtin_bit_cast(float, reverse_u<D>(__builtin_bit_cast(uint32_t, bv)));
+    const int ri = int(reverse_u<D>(uint32_t(bi)));
     float v = av;
     int i = ai;
     if (better(rv, ri, v, i)) { v = rv; i = ri; }
 #pragma unroll
     for (int stride = kWave / 2; stride > 0; stride >>= 1) {
-        const float pv = shfl_xor_f(v, stride);
-        const int pi = shfl_xor_i(i, stride);
+        const float pv = xor_f<D>(v, stride);
+        const int pi = xor_i<D>(i, stride);
         const bool low = (lane & stride) == 0;
         const bool take = low ? better(pv, pi, v, i) : better(v, i, pv, pi);
         if (take) { v = pv; i = pi; }
@@ -147,11 +164,12 @@ __device__ __forceinline__ void merge_pair(float& av, int& ai, float bv, int bi)
 
 // A sorted list merged into the wave list; ranks >= K are cleared afterwards,
 // so the list keeps its form.
+template <bool D = false>
 __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi) {
     const int lane = lane_id();
     float v = L.v;
     int i = L.i;
-    merge_pair(v, i, bv, bi);
+    merge_pair<D>(v, i, bv, bi);
     L.v = lane < K ? v : -kInfF;
     L.i = lane < K ? i : kInvalidId;
     L.kv = readlane_f(L.v, K - 1);
@@ -160,13 +178,14 @@ __device__ __forceinline__ void list_merge(WaveList& L, int K, float bv, int bi)
 
 // The wave's 64 values (none NaN) sorted descending across the lanes: a
 // bitonic sort.
+template <bool D = false>
 __device__ __forceinline__ float wave_sort_desc(float x) {
     const int lane = lane_id();
 #pragma unroll
     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const float y = shfl_xor_f(x, stride);
+            const float y = xor_f<D>(x, stride);
             const bool desc = (lane & size) == 0 || size == kWave;   // the last merge runs descending
             const bool low = (lane & stride) == 0;
             x = (low == desc) ? fmaxf(x, y) : fminf(x, y);
@@ -178,12 +197,13 @@ __device__ __forceinline__ float wave_sort_desc(float x) {
 // The 64 largest of two descending lane-sorted lists, sorted descending: the
 // larger of each entry and the other list's entry of rank 63 - lane forms a
 // bitonic sequence, which a descending bitonic merge puts in order.
+template <bool D = false>
 __device__ __forceinline__ float merge_desc_f(float a, float b) {
     const int lane = lane_id();
-    float x = fmaxf(a, __builtin_bit_cast(float, lanes_reverse(__builtin_bit_cast(uint32_t, b))));
+    float x = fmaxf(a, __builtin_bit_cast(float, reverse_u<D>(__builtin_bit_cast(uint32_t, b))));
 #pragma unroll
     for (int stride = kWave / 2; stride > 0; stride >>= 1) {
-        const float y = shfl_xor_f(x, stride);
+        const float y = xor_f<D>(x, stride);
         x = (lane & stride) ? fminf(x, y) : fmaxf(x, y);
     }
     return x;
@@ -191,14 +211,15 @@ __device__ __forceinline__ float merge_desc_f(float a, float b) {
 
 // The wave's 64 (value, id) pairs sorted (value desc, id asc) across the
 // lanes: a bitonic sort (pairs are distinct except (-inf, kInvalidId) padding).
+template <bool D = false>
 __device__ __forceinline__ void wave_sort_pairs(float& v, int& i) {
     const int lane = lane_id();
 #pragma unroll
     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const float pv = shfl_xor_f(v, stride);
-            const int pi = shfl_xor_i(i, stride);
+            const float pv = xor_f<D>(v, stride);
+            const int pi = xor_i<D>(i, stride);
             const bool desc = (lane & size) == 0 || size == kWave;
             const bool low = (lane & stride) == 0;
             const bool take = (low == desc) ? better(pv, pi, v, i) : better(v, i, pv, pi);
@@ -390,6 +411,7 @@ __device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, c
 // ------------------------------------------------------------------- the kernel
 template <int DT, bool VEC, int MODE>
 __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
+    constexpr bool kD = MODE == kModeSample;   // DPP lane exchanges in the list merges
     const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     const void* row = static_cast<const unsigned char*>(a.logits) + size_t(r) * size_t(a.stride) * sizeof(typename Elem<DT>::Bits);
@@ -560,11 +582,11 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
                 }
             }
         }
-        s_first[wave][lane] = wave_sort_desc(lm);
+        s_first[wave][lane] = wave_sort_desc<kD>(lm);
         __syncthreads();
         float t = s_first[0][lane];
 #pragma unroll
-        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f(t, s_first[w][lane]);
+        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f<kD>(t, s_first[w][lane]);
         tau = readlane_f(t, K - 1);
     };
     auto vec_exact = [&](const uint4& dv, int id0, bool ok) {
@@ -860,11 +882,11 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             float v;
             if (penalized(mbits, c, v)) lm = v;
         }
-        s_first[wave][lane] = wave_sort_desc(lm);
+        s_first[wave][lane] = wave_sort_desc<kD>(lm);
         __syncthreads();
         float t = s_first[0][lane];
 #pragma unroll
-        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f(t, s_first[w][lane]);
+        for (int w = 1; w < kTopkWaves; ++w) t = merge_desc_f<kD>(t, s_first[w][lane]);
         tau = readlane_f(t, K - 1);
     };
     // Candidates of a batch are staged per wave in LDS and go into the list
@@ -878,8 +900,8 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         float cv = lane < fill ? s_cv[wave][lane] : -kInfF;
         int ci = lane < fill ? s_ci[wave][lane] : kInvalidId;
-        wave_sort_pairs(cv, ci);
-        list_merge(L, K, cv, ci);
+        wave_sort_pairs<kD>(cv, ci);
+        list_merge<kD>(L, K, cv, ci);
         fill = 0;
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -998,10 +1020,10 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
     // lists, then wave 0 takes wave 2's
     auto tree_merge = [&]() {
         if (!(wave & 1))
-            list_merge(L, K, lane < K ? s_val[wave + 1][lane] : -kInfF, lane < K ? s_idx[wave + 1][lane] : kInvalidId);
+            list_merge<kD>(L, K, lane < K ? s_val[wave + 1][lane] : -kInfF, lane < K ? s_idx[wave + 1][lane] : kInvalidId);
         if (wave == 2) { s_val[2][lane] = L.v; s_idx[2][lane] = L.i; }
         __syncthreads();
-        if (wave == 0) list_merge(L, K, lane < K ? s_val[2][lane] : -kInfF, lane < K ? s_idx[2][lane] : kInvalidId);
+        if (wave == 0) list_merge<kD>(L, K, lane < K ? s_val[2][lane] : -kInfF, lane < K ? s_idx[2][lane] : kInvalidId);
     };
     tree_merge();
     uint32_t f = 0, c = 0;
@@ -1062,8 +1084,8 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             for (int step = 1; step < 8; step <<= 1)
 #pragma unroll
                 for (int u = 0; u + step < 8; u += 2 * step)
-                    if (u + step < n) merge_pair(bv[u], bi[u], bv[u + step], bi[u + step]);
-            list_merge(L, K, bv[0], bi[0]);
+                    if (u + step < n) merge_pair<kD>(bv[u], bi[u], bv[u + step], bi[u + step]);
+            list_merge<kD>(L, K, bv[0], bi[0]);
         }
         if (wave & 1) { s_val[wave][lane] = L.v; s_idx[wave][lane] = L.i; }
         __syncthreads();

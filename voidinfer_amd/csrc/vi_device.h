@@ -271,6 +271,44 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) { return __shfl_xo
 __device__ __forceinline__ uint32_t lanes_reverse(uint32_t v) {
     return uint32_t(__builtin_amdgcn_ds_bpermute((kWave - 1 - lane_id()) << 2, int(v)));
 }
+// The same exchanges as VALU moves, for latency-bound chains of a single wave
+// (no LDS round trip per stage): DPP quad and row patterns for xor distances
+// up to 8 (row_half_mirror then a quad reversal gives lane ^ 4, row_ror:8
+// gives lane ^ 8), gfx950's permlane swaps for 16 and 32 (with both operands
+// the same register, the swap leaves lane ^ 16 (^ 32) in the first result on
+// odd rows (the upper half) and in the second elsewhere).
+template <int M> __device__ __forceinline__ uint32_t lanes_xor_dpp(uint32_t v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xor distance");
+    if constexpr (M == 1) {
+        return dpp_u32<0xb1, 0xf, false>(v);                              // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        return dpp_u32<0x4e, 0xf, false>(v);                              // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        return dpp_u32<0x1b, 0xf, false>(dpp_u32<0x141, 0xf, false>(v));  // lane ^ 7, then ^ 3
+    } else if constexpr (M == 8) {
+        return dpp_u32<0x128, 0xf, false>(v);                             // row_ror:8
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? r[0] : r[1];
+    }
+}
+__device__ __forceinline__ uint32_t lanes_xor_dpp(uint32_t v, int m) {   // (folded when m is known)
+    switch (m) {
+        case 1: return lanes_xor_dpp<1>(v);
+        case 2: return lanes_xor_dpp<2>(v);
+        case 4: return lanes_xor_dpp<4>(v);
+        case 8: return lanes_xor_dpp<8>(v);
+        case 16: return lanes_xor_dpp<16>(v);
+        case 32: return lanes_xor_dpp<32>(v);
+        default: return uint32_t(__shfl_xor(int(v), m, kWave));
+    }
+}
+__device__ __forceinline__ uint32_t lanes_reverse_dpp(uint32_t v) {   // row_mirror (^ 15), then ^ 16, ^ 32
+    return lanes_xor_dpp<32>(lanes_xor_dpp<16>(dpp_u32<0x140, 0xf, false>(v)));
+}
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
     x += dpp_u32<0x111, 0xf, true>(x);    // row_shr:1
     x += dpp_u32<0x112, 0xf, true>(x);    // row_shr:2
