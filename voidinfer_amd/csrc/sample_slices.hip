@@ -57,7 +57,9 @@ constexpr int kBinKeys = 128;
 constexpr int kHeadWords = 32;            // slice head: n_list, n_valid, flags, top_key, bin mask [16], history tokens
 constexpr int kHash = 2048;               // LDS repeat-count hash slots
 constexpr uint32_t kHashFill = kHash * 3 / 4;
-constexpr int kStage = 4096;              // history offsets staged per penalty round (u16)
+constexpr int kStage = 7168;              // history offsets staged per penalty round (u16): a lane with a
+                                          // 32,768-token history puts ~4,050 tokens in a slice, one round
+                                          // (the LDS beside the histogram sets the limit)
 constexpr int kMaxSlices = 16;
 constexpr int kPL = 2;                    // repeat-list entries prefetched per thread
 constexpr int kPHist = 4;                 // history tokens prefetched per thread
@@ -78,6 +80,7 @@ constexpr int kQ = kHW / 2 / kT;          // 2-word histogram groups per thread 
 constexpr int kSeg = kNV + 2;             // id-order segments: head, vectors, tail
 static_assert(kWPT * kT == kBW && kSL % 32 == 0 && kSL < 65536 && kNV * 8 * kT >= kSL, "slice geometry");
 static_assert(kQ * kW == 256 && kQ * 2 * kT == kHW, "compaction blocks of 128 patterns");
+static_assert(kStage % kT == 0, "whole staging rounds per thread");
 
 // Merge map inside H (bytes): per-slice bin (first | entries << 16), the
 // slices' bin masks, bin counts and masses summed over slices, five gather
@@ -126,6 +129,7 @@ struct Shared {
     uint32_t segs[kW][kSeg];
     // slice
     uint32_t flags, n_hash, overflow;
+    uint32_t pflags[2];           // state-route penalty flags of items k (k & 1): built an item ahead
     uint32_t kmin, kmax, top_key, n_valid, n_list;
     uint32_t krange[kW];          // valid key range (kmin | kmax << 16) of items k .. k + kW - 1
     uint32_t bmask[kBins / 32];
@@ -263,15 +267,18 @@ struct SliceRegs {
     uint4 v[kNV];
     uint32_t hb, tb;
 };
+// Every load is issued, at a clamped in-bounds address (a slice holds at least one
+// logit): users test v < nvec / tid < head / tid < tail themselves.  (A load under
+// a branch is waited for where the branch joins, and a selected result is copied,
+// which waits too: either would drain the prefetch as soon as it is issued.)
 __device__ __forceinline__ void load_slice(const Geo& g, SliceRegs& r) {
     const int tid = opaque_tid();
+    const int vl = max(g.nvec - 1, 0);
+    const unsigned char* vb = g.nvec > 0 ? g.vbase : reinterpret_cast<const unsigned char*>(g.base16);
 #pragma unroll
-    for (int i = 0; i < kNV; ++i) {
-        const int v = i * kT + tid;
-        r.v[i] = v < g.nvec ? load16_cached(g.vbase + size_t(v) * 16) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    r.hb = tid < g.head ? uint32_t(g.base16[tid]) : 0u;
-    r.tb = tid < g.tail ? uint32_t(g.base16[g.head + 8 * g.nvec + tid]) : 0u;
+    for (int i = 0; i < kNV; ++i) r.v[i] = load16_cached(vb + size_t(min(i * kT + tid, vl)) * 16);
+    r.hb = uint32_t(g.base16[tid < g.head ? tid : 0]);
+    r.tb = uint32_t(g.base16[tid < g.tail ? g.head + 8 * g.nvec + tid : 0]);
 }
 
 // Item k of workgroup w: (row, slice), or false past the end.
@@ -1223,9 +1230,84 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
 #pragma unroll
     for (int q = 0; q < kHW / 4 / kT; ++q) H4[q * kT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
     if (threadIdx.x < kBins / 32) sh.bmask[threadIdx.x] = 0u;
-    if (threadIdx.x == 0) { sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u; }
+    if (threadIdx.x == 0) { sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u; sh.pflags[0] = 0u; sh.pflags[1] = 0u; }
     SliceRegs cur{};
     PenPrefetch pf{};
+    const bool state_route = a.pstate != nullptr;   // (launch-uniform)
+    uint32_t bw[kWPT], rank0 = 0u, nf = 0u;          // the item's history bitmap word(s), rank base, total
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) bw[q] = 0u;
+    uint16_t* F = reinterpret_cast<uint16_t*>(lds + kOffF);
+    // State route: an item's penalty inputs (history bitmap B, repeat hash X and
+    // bitmap R, history tokens staged in F at their id-order ranks) are built from
+    // `pf` while the previous item compacts and publishes, in two halves around a
+    // barrier.  First half: X and R emptied, B and this thread's bitmap word(s),
+    // the words' population scan within the wave.
+    uint32_t pen_incl = 0u, pen_pc = 0u;
+    auto state_pen_a = [&](int r1, int s1, int par) {
+        const int tid = opaque_tid(), lane = tid & (kWave - 1), wave = tid / kWave;
+        const Geo g1 = geo_of(a, r1, s1);
+        uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
+        uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
+        for (int i = tid; i < kHash; i += kT) X[i] = 0u;
+        if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
+        const int nw = (g1.n + 31) >> 5;
+        const uint32_t lastm = (g1.n & 31) ? (1u << (g1.n & 31)) - 1u : ~0u;
+        uint32_t pc_ = 0u;
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) {
+            const int wd = tid * kWPT + q;
+            bw[q] = wd < nw ? (pf.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
+            B[wd] = bw[q];
+            R[wd] = 0u;
+            pc_ += uint32_t(__builtin_popcount(bw[q]));
+        }
+        const uint32_t hflags = uint32_t(__builtin_amdgcn_readfirstlane(int(pf.hflags)));
+        if (tid == 0 && hflags) atomicOr(&sh.pflags[par], hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
+        pen_pc = pc_;
+        pen_incl = wave_incl_scan_u32(pc_);
+        if (lane == kWave - 1) sh.scan[wave] = pen_incl;
+    };
+    // Second half: the ranks, the repeat counts of the item's tokens from the
+    // state's repeat list, the staging (then a barrier before F is read).
+    auto state_pen_b = [&](int r1, int s1) {
+        const int tid = opaque_tid(), lane = tid & (kWave - 1), wave = tid / kWave;
+        const Geo g1 = geo_of(a, r1, s1);
+        const PenCtx c1 = pen_ctx(a, r1, a.params[r1]);
+        const uint32_t st = lane < kW ? sh.scan[lane] : 0u;
+        const uint32_t si = wave_incl_scan_u32(st);
+        nf = uint32_t(readlane_i(int(si), kW - 1));
+        rank0 = (wave > 0 ? uint32_t(readlane_i(int(si), wave - 1)) : 0u) + pen_incl - pen_pc;
+        const uint2* list = reinterpret_cast<const uint2*>(c1.lstate + a.pl.off_list);
+        const uint32_t nrep = min(uint32_t(__builtin_amdgcn_readfirstlane(int(pf.nrep))), uint32_t(a.pl.slots));
+        const int e1 = g1.s0 + g1.n;
+        auto put = [&](uint2 e) {
+            const int t = int(e.x);
+            if (e.y < 2u || t < g1.s0 || t >= e1) return;
+            repeat_put(lds, sh, uint32_t(t - g1.s0), e.y - 1u, false);
+        };
+#pragma unroll
+        for (int j = 0; j < kPL; ++j)
+            if (uint32_t(j) * kT + tid < nrep) put(pf.le[j]);
+        for (uint32_t i = uint32_t(kPL) * kT + tid; i < nrep; i += kT) put(list[i]);
+        uint32_t r = rank0;
+#pragma unroll
+        for (int q = 0; q < kWPT; ++q) {
+            uint32_t bits = bw[q];
+            while (bits && r < uint32_t(kStage)) {
+                const int j = __builtin_ctz(bits);
+                bits &= bits - 1u;
+                F[r++] = uint16_t((tid * kWPT + q) * 32 + j);
+            }
+        }
+    };
+    // (after the barrier that follows state_pen_b) the dense counts when X overflowed
+    auto state_pen_dense = [&](int r1, int s1) {
+        if (sh.overflow)   // (uniform)
+            pen_dense_fill(a, pen_ctx(a, r1, a.params[r1]), geo_of(a, r1, s1), pf,
+                           a.lists + (size_t(r1) * S + s1) * kSL);
+    };
+    bool cur_pen = false;   // the item's penalty inputs were built ahead (state route)
     {
         const vi_row_params p0 = a.params[row];
         if (full_route_row(p0)) {
@@ -1233,9 +1315,17 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             const PenCtx pc0 = pen_ctx(a, row, p0);
             load_slice(g0, cur);
             pen_prefetch_head(a, pc0, g0, pf);
+            cur_pen = state_route && pc0.pen;
         }
     }
     lds_barrier();
+    if (cur_pen) {   // (uniform) item 0's penalty inputs
+        state_pen_a(row, s, 0);
+        lds_barrier();
+        state_pen_b(row, s);
+        lds_barrier();
+        state_pen_dense(row, s);
+    }
 
     // One slice per iteration.  `cur` / `pf` hold its logits and penalty inputs,
     // requested during the previous iteration: the next slice's logits are loaded
@@ -1278,55 +1368,21 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
         uint32_t graw[kG], goff[kG];
 #pragma unroll
         for (int u = 0; u < kG; ++u) { graw[u] = 0u; goff[u] = 0xffffffffu; }
-        uint32_t bw[kWPT], rank0 = 0u, nf = 0u;
-        uint16_t* F = reinterpret_cast<uint16_t*>(lds + kOffF);
+        // the next item's penalty inputs are built during this one (state route)
+        bool next_pen = false;
+        if (state_route && has_next) {
+            const vi_row_params np = a.params[nrow];
+            next_pen = full_route_row(np) && penalties_active(np);
+        }
 
         if (full) {
             if (tid == 0) sh.flags = 0u;
             // ---- 1. penalties: the slice's history bitmap B, the repeat hash X / bitmap
             // R, and the first round of history tokens staged in id order with their
-            // raw logits requested (before the next slice's loads)
+            // raw logits requested (before the next slice's loads).  State route:
+            // built during the previous item (or before the loop), F staged.
             if (pc.pen) {
-                if (pc.state) {
-                    // the state's bitmap word is this thread's B word: two barriers
-                    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
-                    uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
-                    for (int i = tid; i < kHash; i += kT) X[i] = 0u;
-                    if (tid == 0) { sh.n_hash = 0u; sh.overflow = 0u; }
-                    const int nw = (g.n + 31) >> 5;
-                    const uint32_t lastm = (g.n & 31) ? (1u << (g.n & 31)) - 1u : ~0u;
-                    uint32_t pc_ = 0u;
-#pragma unroll
-                    for (int q = 0; q < kWPT; ++q) {
-                        const int wd = tid * kWPT + q;
-                        bw[q] = wd < nw ? (pf.bword[q] & (wd == nw - 1 ? lastm : ~0u)) : 0u;
-                        B[wd] = bw[q];
-                        R[wd] = 0u;
-                        pc_ += uint32_t(__builtin_popcount(bw[q]));
-                    }
-                    const uint32_t hflags = uint32_t(__builtin_amdgcn_readfirstlane(int(pf.hflags)));
-                    if (tid == 0 && hflags) atomicOr(&sh.flags, hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR));
-                    const uint32_t incl = wave_incl_scan_u32(pc_);
-                    if (lane == kWave - 1) sh.scan[wave] = incl;
-                    lds_barrier();
-                    const uint32_t st = lane < kW ? sh.scan[lane] : 0u;
-                    const uint32_t si = wave_incl_scan_u32(st);
-                    nf = uint32_t(readlane_i(int(si), kW - 1));
-                    rank0 = (wave > 0 ? uint32_t(readlane_i(int(si), wave - 1)) : 0u) + incl - pc_;
-                    // repeat counts of the slice's tokens from the state's repeat list
-                    const uint2* list = reinterpret_cast<const uint2*>(pc.lstate + a.pl.off_list);
-                    const uint32_t nrep = min(uint32_t(__builtin_amdgcn_readfirstlane(int(pf.nrep))), uint32_t(a.pl.slots));
-                    const int s1 = g.s0 + g.n;
-                    auto put = [&](uint2 e) {
-                        const int t = int(e.x);
-                        if (e.y < 2u || t < g.s0 || t >= s1) return;
-                        repeat_put(lds, sh, uint32_t(t - g.s0), e.y - 1u, false);
-                    };
-#pragma unroll
-                    for (int j = 0; j < kPL; ++j)
-                        if (uint32_t(j) * kT + tid < nrep) put(pf.le[j]);
-                    for (uint32_t i = uint32_t(kPL) * kT + tid; i < nrep; i += kT) put(list[i]);
-                } else {
+                if (!pc.state) {
                     pen_build<DT>(a, pc, g, pf, lds, sh, dense);
                     uint32_t pc_ = 0u;
                     uint32_t* hb = a.hbits + (size_t(row) * S + s) * kBW;   // (for the merge's owner scan)
@@ -1337,20 +1393,19 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                         pc_ += __builtin_popcount(bw[q]);
                     }
                     rank0 = block_scan_lds(pc_, sh.scan, &nf);
-                }
-                // this thread's history tokens, staged at their ranks
-                uint32_t r = rank0;
+                    // this thread's history tokens, staged at their ranks
+                    uint32_t r = rank0;
 #pragma unroll
-                for (int q = 0; q < kWPT; ++q) {
-                    uint32_t bits = bw[q];
-                    while (bits && r < uint32_t(kStage)) {
-                        const int j = __builtin_ctz(bits);
-                        bits &= bits - 1u;
-                        F[r++] = uint16_t((tid * kWPT + q) * 32 + j);
+                    for (int q = 0; q < kWPT; ++q) {
+                        uint32_t bits = bw[q];
+                        while (bits && r < uint32_t(kStage)) {
+                            const int j = __builtin_ctz(bits);
+                            bits &= bits - 1u;
+                            F[r++] = uint16_t((tid * kWPT + q) * 32 + j);
+                        }
                     }
+                    lds_barrier();
                 }
-                lds_barrier();
-                if (pc.state && sh.overflow) pen_dense_fill(a, pc, g, pf, dense);   // (uniform)
                 const uint32_t m = min(uint32_t(kStage), nf);
 #pragma unroll
                 for (int u = 0; u < kG; ++u) {
@@ -1576,6 +1631,9 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                     atomicMax(&sh.top_key, max(pkm, nkm));
                 }
             }
+            // the next item's penalty inputs, first half (B, X, R and F are free: this
+            // item's moves are done)
+            if (next_pen) state_pen_a(nrow, ns, (k + 1) & 1);
             if (ballot(invalid) && lane == 0) atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE));
             lds_barrier();
             // ---- publish the slice's head (the merge is a later launch: plain
@@ -1584,7 +1642,8 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
             if (tid == 0) {
                 hd[0] = sh.n_list;
                 hd[1] = sh.n_valid;
-                hd[2] = sh.flags;
+                hd[2] = sh.flags | sh.pflags[k & 1];
+                sh.pflags[k & 1] = 0u;
                 hd[3] = sh.top_key;
                 hd[4 + kBins / 32] = nf;
                 sh.n_list = 0u; sh.n_valid = 0u; sh.top_key = 0u;
@@ -1593,9 +1652,18 @@ __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
                 hd[4 + tid] = sh.bmask[tid];
                 sh.bmask[tid] = 0u;
             }
+            if (next_pen) state_pen_b(nrow, ns);
             lds_barrier();
+            if (next_pen) state_pen_dense(nrow, ns);
         } else {
             prefetch_next();
+            if (next_pen) {
+                state_pen_a(nrow, ns, (k + 1) & 1);
+                lds_barrier();
+                state_pen_b(nrow, ns);
+                lds_barrier();
+                state_pen_dense(nrow, ns);
+            }
         }
         if (!has_next) break;
         row = nrow; s = ns;
