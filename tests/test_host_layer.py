@@ -4,6 +4,8 @@
   (tests/test_exl3_sampling_policy.cpp and its siblings) against this layer;
 * tests/cpp/test_transport_host.cpp — the greedy-packet transport classes over
   a host stand-in of the vi_packet_* entry points;
+* tests/cpp/test_markstein.cpp — the parts route's FMA-corrected division of a
+  penalized logit by the repetition penalty, bit for bit against IEEE division;
 * oracle/_ref/ref_diff — random scripts run side by side through this layer and
   the reference's host headers compiled from /root/reference (skipped where the
   reference tree is absent and the binary was not built).
@@ -27,6 +29,19 @@ def _compile(src: Path, out: Path) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr
     return out
+
+
+def test_markstein_division_matches_ieee():
+    gxx = shutil.which("g++") or "g++"
+    BUILD.mkdir(exist_ok=True)
+    exe = BUILD / "test_markstein"
+    cmd = [gxx, "-std=c++20", "-O2", "-ffp-contract=off", "-Wall", "-Werror", str(ROOT / "tests/cpp/test_markstein.cpp"),
+           "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert " 0 mismatches" in res.stdout
 
 
 def test_host_contracts_program():

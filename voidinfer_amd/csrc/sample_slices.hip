@@ -38,6 +38,7 @@
 // bitmap (V / 8 bytes) and repeat list, or the history.
 #include <math.h>
 
+#include "keys16.h"
 #include "penalty_state.h"
 #include "vi_device.h"
 #include "vi_internal.h"
@@ -64,7 +65,6 @@ constexpr int kMaxSlices = 16;
 constexpr int kPL = 2;                    // repeat-list entries prefetched per thread
 constexpr int kPHist = 4;                 // history tokens prefetched per thread
 constexpr uint32_t kTakeAll = 0xffffffffu;
-constexpr float kMaxTemperature = 65536.0f;
 
 // LDS map (bytes).  H: histogram, u16 counts in pairs (word p & 0x7fff: low half
 // the pattern with sign 0, high half with sign 1); the merge reuses it.  B:
@@ -156,41 +156,6 @@ __device__ __forceinline__ int opaque_tid() {
 
 __device__ __forceinline__ int bin_of(uint32_t key) { return int(key >> 7); }
 __device__ __forceinline__ uint32_t bin_first_key(int b) { return uint32_t(b) * uint32_t(kBinKeys); }
-
-template <int DT>
-__device__ __forceinline__ float key_z(uint32_t key, float inv_t) {
-    return Elem<DT>::decode(unkey16(key)) * inv_t;
-}
-
-// Smallest i in [lo, hi) with pred(i) (pred monotone false -> true), or hi.
-// Wave-uniform call; 64 probes per round.
-template <class P>
-__device__ __forceinline__ int wave_search(int lo, int hi, P pred) {
-    const int lane = lane_id();
-    while (hi > lo) {
-        const int n = hi - lo;
-        if (n <= kWave) {
-            const uint64_t m = ballot(lane < n && pred(lo + lane));
-            return m ? lo + __builtin_ctzll(m) : hi;
-        }
-        const int step = (n + kWave - 1) / kWave;
-        const int p = lo + lane * step;
-        const uint64_t valid = ballot(p < hi);
-        const uint64_t m = ballot(p < hi && pred(p));
-        if (!m) {
-            const int last = 63 - __builtin_clzll(valid);
-            lo = lo + last * step + 1;
-            continue;
-        }
-        const int f = __builtin_ctzll(m);
-        if (f == 0) return lo;
-        const int nlo = lo + (f - 1) * step + 1;
-        hi = lo + f * step;
-        lo = nlo;
-        if (lo == hi) return lo;
-    }
-    return lo;
-}
 
 // value of lane `src` (per-lane source) for a 64-bit double
 __device__ __forceinline__ double bperm_f64(double v, int src) {
@@ -1199,19 +1164,6 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
 }
 
 // ------------------------------------------------------------------ kernels
-// Smallest and largest valid keys (finite pattern, finite z) at a temperature,
-// kmin | kmax << 16 (1 | 0 << 16: none); one wave.
-template <int DT>
-__device__ __forceinline__ uint32_t valid_key_range(float temperature) {
-    constexpr int kPosMax = DT == VI_BF16 ? 0xff7f : 0xfbff;   // largest finite key
-    constexpr int kNegMin = DT == VI_BF16 ? 0x0080 : 0x0400;   // smallest finite key
-    const float inv_t = 1.0f / temperature;
-    if (!(temperature <= kMaxTemperature) || !isfinite(inv_t)) return 1u;
-    const int kbad = wave_search(0x8000, kPosMax + 1, [&](int key) { return !isfinite(key_z<DT>(uint32_t(key), inv_t)); });
-    const int kgood = wave_search(kNegMin, 0x8000, [&](int key) { return isfinite(key_z<DT>(uint32_t(key), inv_t)); });
-    return uint32_t(kgood) | (uint32_t(kbad - 1) << 16);
-}
-
 template <int DT>
 __global__ __launch_bounds__(kT) void slice_kernel(SliceArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
@@ -1771,6 +1723,11 @@ __global__ __launch_bounds__(kT) void slice_probs_kernel(SliceArgs a) {
     }
 }
 
+
+inline int slices_of(int vocabulary) { return (vocabulary + kSL - 1) / kSL; }
+
+}  // namespace
+
 int device_cus() {
     static int cached[64] = {};
     int dev = 0;
@@ -1782,10 +1739,6 @@ int device_cus() {
     }
     return cached[dev];
 }
-
-inline int slices_of(int vocabulary) { return (vocabulary + kSL - 1) / kSL; }
-
-}  // namespace
 
 bool full_supported(int dtype, int vocabulary, int64_t stride) {
     return (dtype == VI_BF16 || dtype == VI_F16) && vocabulary > 0 && vocabulary <= kMaxSlices * kSL &&
