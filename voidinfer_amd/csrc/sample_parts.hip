@@ -50,12 +50,12 @@ constexpr int kW = kT / kWave;            // waves per workgroup
 constexpr int kNV = 8;                    // 16-byte vectors per thread and part
 constexpr int kPartMax = 65504;           // tokens per part (< 65,536, a multiple of 32)
 constexpr int kHW = 32768;                // histogram words
-constexpr int kHS = 4096;                 // LDS repeat-hash slots
-constexpr int kHSBits = 12;
+constexpr int kHS = 1024;                 // LDS repeat-hash slots
+constexpr int kHSBits = 10;
 constexpr uint32_t kHSFill = kHS * 3 / 4;
 constexpr uint32_t kEmpty = 0xffffffffu;
 constexpr int kBins = 512, kBinKeys = 128;
-constexpr int kHead = 4;                  // entries, flags, largest valid key + 1, valid tokens
+constexpr int kHead = 5;                  // entries, flags, largest valid key + 1, valid tokens, present tokens
 constexpr double kScale = 0x1p44;         // fixed point of the weights (row masses < 2^63)
 static_assert(kNV * 8 * kT >= kPartMax && kPartMax % 32 == 0, "part geometry");
 static_assert(kHS == 1 << kHSBits, "hash size");
@@ -66,8 +66,10 @@ constexpr int kRW = 2048;                 // repeat-bitmap words (kPartMax bits)
 constexpr int kOffH = 0;
 constexpr int kOffX = kOffH + 4 * kHW;
 constexpr int kOffR = kOffX + 4 * kHS;
-constexpr int kOffS = kOffR + 4 * kRW;    // per-wave staging of present tokens (kWave words each)
-constexpr int kLds = kOffS + 4 * kWave * kW;
+constexpr int kStage = 9216;              // present-token offsets staged per round (u16)
+constexpr int kOffF = kOffR + 4 * kRW;    // F: staged offsets of the part's present tokens
+constexpr int kLds = kOffF + 2 * kStage;
+static_assert(kStage % kT == 0, "whole staging rounds per thread");
 static_assert(kRW * 32 >= kPartMax, "repeat bitmap");
 // merge tables inside H
 constexpr int kOffFirst = 0;                                 // u32 [parts][kBins]: first entry of a bin
@@ -98,11 +100,12 @@ struct PartArgs {
     vi_sample_stats* stats;
     uint32_t* heads;           // [rows][parts][kHead]
     uint32_t* lists;           // [rows][parts][part_len]: (key << 16 | count), key order
+    uint32_t* plists;          // [rows][parts][part_len]: present tokens, (offset << 16 | final bits)
 };
 
 struct Shared {
     uint32_t scan[kW + 1];
-    uint32_t flags, n_hash, overflow, kmin, kmax, top, nvalid;
+    uint32_t flags, n_hash, overflow, kmin, kmax, top, nvalid, npres;
     // merge
     uint32_t m_flags, m_top, m_valid, m_base[kMaxParts16 + 1];
     uint32_t wc[kBins / kWave];
@@ -128,6 +131,26 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Exclusive prefix of a per-thread u32 over the workgroup with LDS-only
+// barriers (global loads in flight are not waited for); *total gets the sum.
+__device__ __forceinline__ uint32_t block_scan_lds(uint32_t v, uint32_t* tmp, uint32_t* total) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    const uint32_t x = wave_incl_scan_u32(v);
+    if (lane == kWave - 1) tmp[wave] = x;
+    lds_barrier();
+    if (wave == 0) {
+        const uint32_t t = lane < kW ? tmp[lane] : 0u;
+        const uint32_t it = wave_incl_scan_u32(t);
+        if (lane < kW) tmp[lane] = it - t;
+        if (lane == kW - 1) tmp[kW] = it;
+    }
+    lds_barrier();
+    const uint32_t r = tmp[wave] + x - v;
+    *total = tmp[kW];
+    lds_barrier();
+    return r;
 }
 
 template <int C, int R, bool B>
@@ -292,37 +315,6 @@ __device__ __forceinline__ uint32_t penalize_fast(uint32_t bits, uint32_t count,
     return Elem<DT>::round(y);
 }
 
-// Present tokens (bits mp of vector w, vector vi of the part) handed to the
-// lanes of the wave densely: each lane stages (offset << 16 | raw bits) of its
-// tokens in the wave's 64 staging words, in (lane, element) order, and lane d
-// takes the d-th staged token, 64 at a time.  fn(raw, off) runs once per
-// present token.  Every lane of the wave calls this (wave-uniform control).
-template <int DT, class F>
-__device__ __forceinline__ void dense_present(uint32_t mp, const uint4& w, int vi, uint32_t* stage, F&& fn) {
-    const int lane = lane_id();
-    const uint32_t cnt = uint32_t(__builtin_popcount(mp));
-    const uint32_t incl = wave_incl_scan_u32(cnt);
-    const uint32_t total = uint32_t(readlane_i(int(incl), kWave - 1));
-    for (uint32_t base = 0; base < total; base += kWave) {
-        uint32_t pos = incl - cnt;
-        for (uint32_t mm = mp; mm && pos < base + kWave; mm &= mm - 1u, ++pos)
-            if (pos >= base) {
-                const int e = __builtin_ctz(mm);
-                stage[pos - base] = (uint32_t(8 * vi + e) << 16) | vec_bits<DT>(w, e);
-            }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-        if (base + uint32_t(lane) < total) {
-            const uint32_t ent = stage[lane];
-            fn(ent & 0xffffu, ent >> 16);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    }
-}
-
 // Final (penalized) bits of a present token at offset off: count 1, or the
 // repeat count when its R bit is set; a non-finite raw value stays as it is.
 template <int DT>
@@ -353,27 +345,62 @@ __device__ __forceinline__ void part_pass(const PartArgs& a, int row, int q, con
     uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
     uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
     const unsigned char* R8 = reinterpret_cast<const unsigned char*>(R);
-    uint32_t* stage = reinterpret_cast<uint32_t*>(lds + kOffS) + wave * kWave;
+    uint16_t* F = reinterpret_cast<uint16_t*>(lds + kOffF);
+    uint32_t* plist = a.plists + (size_t(row) * a.parts + q) * size_t(L);
     constexpr uint32_t kExp = DT == VI_BF16 ? 0x7f80u : 0x7c00u, kExpLsb = DT == VI_BF16 ? 0x80u : 0x400u;
     uint32_t bad = 0u;
 
-    // ---- present tokens: penalized and counted by the wave's lanes densely
+    // ---- present tokens: their offsets, from the lane's presence-bitmap words
+    // (thread t holds tokens [64 t, 64 t + 64) of the part), staged in id order
+    // in F; every thread then takes every kT-th staged token, gathers its raw
+    // logit again (from cache: the part was just read), penalizes it, counts it
+    // and records (offset, final bits) in the part's present list.
     if (c.pen) {
         build_repeat_hash(a, c, s0, n, X, R, sh);
         const float inv = 1.0f / p.repetition_penalty;   // (IEEE division: correctly rounded)
         const bool rep_fast = p.repetition_penalty >= 0x1p-20f && p.repetition_penalty <= 0x1p20f;
+        const uint32_t* b1w = reinterpret_cast<const uint32_t*>(c.st + a.pl.off_b1) + (s0 >> 5);
+        const int nw = (n + 31) >> 5;
+        uint32_t bw[2];
 #pragma unroll
-        for (int i = 0; i < kNV; ++i) {
-            const int vi = i * kT + tid;
-            const uint32_t mp = vi < nvec ? pb[i] : 0u;
-            if (!ballot(mp != 0u)) continue;   // (uniform)
-            dense_present<DT>(mp, v[i], vi, stage, [&](uint32_t raw, uint32_t off) {
+        for (int u = 0; u < 2; ++u) {
+            const int wd = 2 * tid + u;
+            const int nb = min(32, n - 32 * wd);
+            bw[u] = wd < nw ? b1w[wd] & (nb >= 32 ? 0xffffffffu : (1u << nb) - 1u) : 0u;
+        }
+        uint32_t npres = 0u;
+        const uint32_t rank0 = block_scan_lds(uint32_t(__builtin_popcount(bw[0]) + __builtin_popcount(bw[1])),
+                                              sh.scan, &npres);
+        const uint16_t* row16 = static_cast<const uint16_t*>(a.logits) + size_t(row) * size_t(a.stride) + size_t(s0);
+        for (uint32_t r0 = 0; r0 < npres; r0 += kStage) {   // (uniform; one round up to 9,216 tokens)
+            uint32_t r = rank0;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                for (uint32_t bits = bw[u]; bits; bits &= bits - 1u, ++r)
+                    if (r >= r0 && r < r0 + kStage) F[r - r0] = uint16_t(64 * tid + 32 * u + __builtin_ctz(bits));
+            lds_barrier();
+            const uint32_t m = min(npres - r0, uint32_t(kStage));
+            uint32_t offs[kStage / kT], raws[kStage / kT];
+#pragma unroll
+            for (int k = 0; k < kStage / kT; ++k) {   // the gathers, all in flight
+                const uint32_t idx = uint32_t(k * kT + tid);
+                offs[k] = idx < m ? uint32_t(F[idx]) : 0u;
+                raws[k] = idx < m ? uint32_t(row16[offs[k]]) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < kStage / kT; ++k) {
+                const uint32_t idx = uint32_t(k * kT + tid);
+                if (idx >= m) break;
+                const uint32_t raw = raws[k], off = offs[k];
                 const uint32_t bits = present_final<DT>(a, c, p, X, R8, s0, inv, rep_fast, raw, off);
                 const uint32_t nf = ((bits & kExp) + kExpLsb) >> 15;
                 bad |= nf;
                 atomicAdd(&H[bits & 0x7fffu], (nf ^ 1u) * hist_inc(bits));
-            });
+                plist[r0 + idx] = (off << 16) | bits;   // (the merge's owner scan reads it)
+            }
+            lds_barrier();
         }
+        if (tid == 0) sh.npres = npres;
     }
 
     // ---- absent tokens at their raw pattern, branch-free (a present,
@@ -501,7 +528,8 @@ __device__ __forceinline__ void part_pass(const PartArgs& a, int row, int q, con
         hd[1] = sh.flags | (c.pen ? (c.hflags & (VI_FLAG_BAD_HISTORY | VI_FLAG_ERROR)) : 0u);
         hd[2] = n_all ? sh.top : 0u;
         hd[3] = sh.nvalid;
-        sh.flags = 0u; sh.top = 0u; sh.nvalid = 0u;
+        hd[4] = sh.npres;
+        sh.flags = 0u; sh.top = 0u; sh.nvalid = 0u; sh.npres = 0u;
     }
     lds_barrier();
 }
@@ -588,61 +616,54 @@ __device__ __forceinline__ void merge_row(const PartArgs& a, int row, const vi_r
     const float inv_t = 1.0f / p.temperature;
     const double z0 = double(key_z<DT>(top1 - 1u, inv_t));
 
-    // ---- every entry into the coarse bins.  A wave takes 64 consecutive entries
-    // at a time (a part's list is in key order), so equal (part, bin) tags form
-    // runs; the last lane of a run adds the run's sums (one LDS atomic per run
-    // and table).  A batch of kEB such groups is loaded, weighted and reduced
-    // before its atomics are issued (no LDS wait behind an atomic).
+    // ---- every entry into the coarse bins.  Thread t takes a contiguous run of
+    // the concatenated lists (a part's list is in key order, so equal
+    // (part, bin) tags are adjacent) and adds each tag's sums once (LDS atomics
+    // per run, exact u64 mass sums).  Entries are loaded 8 at a time.
     const uint32_t E = sh.m_base[P];
-    constexpr int kEB = 8;   // groups of 64 entries per batch
-    for (uint32_t g0 = uint32_t(wave) * kWave * kEB; g0 < E; g0 += kT * kEB) {
-        uint32_t ents[kEB], qs[kEB];
+    {
+        const uint32_t per = (E + kT - 1) / kT, e0 = min(uint32_t(tid) * per, E), e1 = min(e0 + per, E);
+        uint32_t tag = 0xffffffffu, rc = 0u, rn = 0u, rj = 0u;
+        uint64_t rm = 0ull;
+        auto flush = [&]() {
+            if (tag == 0xffffffffu) return;
+            const uint32_t q = tag >> 9, b = tag & uint32_t(kBins - 1);
+            atomicAdd(&BC[b], rc);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&BM[b]), (unsigned long long)rm);
+            atomicMin(&FIRST[q * kBins + b], rj);
+            atomicAdd(&NE[q * kBins + b], rn);
+        };
+        int q = 0;
+        while (q + 1 < P && e0 >= sh.m_base[q + 1]) ++q;
+        constexpr int kEB = 8;
+        for (uint32_t g = e0; g < e1; g += kEB) {
+            uint32_t ents[kEB], js[kEB], qs[kEB];
 #pragma unroll
-        for (int u = 0; u < kEB; ++u) {
-            const uint32_t e = g0 + uint32_t(u * kWave + lane);
-            int q = 0;
-            while (q + 1 < P && e >= sh.m_base[q + 1]) ++q;
-            qs[u] = uint32_t(q);
-            ents[u] = e < E ? list_of(q)[e - sh.m_base[q]] : 0u;
+            for (int u = 0; u < kEB; ++u) {
+                const uint32_t e = g + uint32_t(u);
+                while (e < e1 && q + 1 < P && e >= sh.m_base[q + 1]) ++q;
+                qs[u] = uint32_t(q);
+                js[u] = e - sh.m_base[q];
+                ents[u] = e < e1 ? list_of(q)[js[u]] : 0u;
+            }
+            uint64_t ms[kEB];
+#pragma unroll
+            for (int u = 0; u < kEB; ++u)   // (count 0 past the end)
+                ms[u] = uint64_t(ents[u] & 0xffffu) * weight_fx<DT>(ents[u] >> 16, inv_t, z0);
+#pragma unroll
+            for (int u = 0; u < kEB; ++u) {
+                if (g + uint32_t(u) >= e1) break;
+                const uint32_t t = (qs[u] << 9) | (ents[u] >> 23);   // (part, bin = key >> 7)
+                if (t != tag) {
+                    flush();
+                    tag = t; rc = 0u; rn = 0u; rm = 0ull; rj = js[u];
+                }
+                rc += ents[u] & 0xffffu;
+                rm += ms[u];
+                ++rn;
+            }
         }
-        uint64_t ms[kEB];
-#pragma unroll
-        for (int u = 0; u < kEB; ++u)   // (0 past the end: count 0)
-            ms[u] = uint64_t(ents[u] & 0xffffu) * weight_fx<DT>(ents[u] >> 16, inv_t, z0);
-        uint32_t rc[kEB], rj[kEB], rn[kEB], rt[kEB];
-        uint64_t rm[kEB];
-#pragma unroll
-        for (int u = 0; u < kEB; ++u) {
-            const uint32_t e = g0 + uint32_t(u * kWave + lane);
-            const bool ok = e < E;
-            const uint32_t q = qs[u], j = ok ? e - sh.m_base[q] : 0u;
-            const uint32_t tag = ok ? (q << 9) | (ents[u] >> 23) : 0xffffffffu;   // (part, bin = key >> 7)
-            const uint32_t cnt = ents[u] & 0xffffu;
-            const uint32_t prev = uint32_t(__builtin_amdgcn_ds_bpermute(max(lane - 1, 0) << 2, int(tag)));
-            const uint32_t next = uint32_t(__builtin_amdgcn_ds_bpermute(min(lane + 1, kWave - 1) << 2, int(tag)));
-            const uint64_t heads = ballot(lane == 0 || prev != tag);
-            const int start = 63 - __builtin_clzll(heads & ((2ull << lane) - 1ull));
-            const uint32_t ci = wave_incl_scan_u32(cnt);
-            const uint64_t mi = wave_incl_scan_u64(ms[u]);
-            const int sb = max(start - 1, 0) << 2;
-            const uint32_t cb = uint32_t(__builtin_amdgcn_ds_bpermute(sb, int(ci)));
-            const uint32_t mlo = uint32_t(__builtin_amdgcn_ds_bpermute(sb, int(uint32_t(mi))));
-            const uint32_t mhi = uint32_t(__builtin_amdgcn_ds_bpermute(sb, int(uint32_t(mi >> 32))));
-            rj[u] = uint32_t(__builtin_amdgcn_ds_bpermute(start << 2, int(j)));
-            rc[u] = start ? ci - cb : ci;
-            rm[u] = start ? mi - ((uint64_t(mhi) << 32) | mlo) : mi;
-            rn[u] = uint32_t(lane - start + 1);
-            rt[u] = (ok && (lane == kWave - 1 || next != tag)) ? tag : 0xffffffffu;
-        }
-#pragma unroll
-        for (int u = 0; u < kEB; ++u) {
-            if (rt[u] == 0xffffffffu) continue;
-            const uint32_t q = rt[u] >> 9, b = rt[u] & uint32_t(kBins - 1);
-            atomicAdd(&BC[b], rc[u]);
-            atomicAdd(reinterpret_cast<unsigned long long*>(&BM[b]), (unsigned long long)rm[u]);
-            atomicMin(&FIRST[q * kBins + b], rj[u]);
-            atomicAdd(&NE[q * kBins + b], rn[u]);
-        }
+        flush();
     }
     __syncthreads();
 
@@ -824,29 +845,19 @@ __device__ __forceinline__ void merge_row(const PartArgs& a, int row, const vi_r
     uint4 v[kNV];
     uint32_t pb[kNV];
     load_part<DT>(a, c, row, s0, nvec, v, pb);
-    uint32_t* X = reinterpret_cast<uint32_t*>(lds + kOffX);
-    uint32_t* R = reinterpret_cast<uint32_t*>(lds + kOffR);
-    const unsigned char* R8 = reinterpret_cast<const unsigned char*>(R);
-    uint32_t* stage = reinterpret_cast<uint32_t*>(lds + kOffS) + wave * kWave;
     uint32_t* M = reinterpret_cast<uint32_t*>(lds + kOffMatch);   // present tokens of key K
     const unsigned char* M8 = reinterpret_cast<const unsigned char*>(M);
     if (tid < kNV) sh.rnd[tid] = 0u;
     if (tid == 0) sh.token = -1;
 #pragma unroll
     for (int i = 0; i < kRW / kT; ++i) M[i * kT + tid] = 0u;
-    if (c.pen) {
-        build_repeat_hash(a, c, s0, n, X, R, sh);
-        const float inv = 1.0f / p.repetition_penalty;
-        const bool rep_fast = p.repetition_penalty >= 0x1p-20f && p.repetition_penalty <= 0x1p20f;
-#pragma unroll
-        for (int i = 0; i < kNV; ++i) {
-            const int vi = i * kT + tid;
-            const uint32_t mp = vi < nvec ? pb[i] : 0u;
-            if (!ballot(mp != 0u)) continue;   // (uniform)
-            dense_present<DT>(mp, v[i], vi, stage, [&](uint32_t raw, uint32_t off) {
-                const uint32_t bits = present_final<DT>(a, c, p, X, R8, s0, inv, rep_fast, raw, off);
-                if (Elem<DT>::finite_bits(bits) && key16(bits) == K) atomicOr(&M[off >> 5], 1u << (off & 31u));
-            });
+    __syncthreads();
+    if (c.pen) {   // present tokens of key K, from the part pass's present list
+        const uint32_t np = a.heads[(rp + qo) * kHead + 4];
+        const uint32_t* pl = a.plists + (rp + qo) * size_t(L);
+        for (uint32_t k = uint32_t(tid); k < np; k += kT) {
+            const uint32_t ent = pl[k], bits = ent & 0xffffu, off = ent >> 16;
+            if (Elem<DT>::finite_bits(bits) && key16(bits) == K) atomicOr(&M[off >> 5], 1u << (off & 31u));
         }
     }
     __syncthreads();
@@ -915,7 +926,7 @@ __global__ __launch_bounds__(kT) void part_kernel(PartArgs a) {
     uint32_t* H = reinterpret_cast<uint32_t*>(lds + kOffH);
 #pragma unroll
     for (int i = 0; i < kHW / 4 / kT; ++i) reinterpret_cast<uint4*>(H)[i * kT + tid] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid == 0) { sh.flags = 0u; sh.top = 0u; sh.nvalid = 0u; }
+    if (tid == 0) { sh.flags = 0u; sh.top = 0u; sh.nvalid = 0u; sh.npres = 0u; }
     for (int k = 0;; ++k) {
         int row, q;
         if (!item_of(a, k, &row, &q)) break;
@@ -970,7 +981,7 @@ size_t parts_workspace(int rows, int vocabulary) {
     int P = 0, L = 0;
     part_geometry(vocabulary, &P, &L);
     const size_t rp = size_t(rows) * size_t(P);
-    return align_up(rp * kHead * 4, 256) + align_up(rp * size_t(L) * 4, 256) + 512;
+    return align_up(rp * kHead * 4, 256) + 2 * align_up(rp * size_t(L) * 4, 256) + 768;
 }
 
 vi_status launch_parts(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream) {
@@ -981,6 +992,7 @@ vi_status launch_parts(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, 
     Carver c(ws, ws_bytes);
     a.heads = c.take<uint32_t>(rp * kHead);
     a.lists = c.take<uint32_t>(rp * size_t(a.part_len));
+    a.plists = c.take<uint32_t>(rp * size_t(a.part_len));
     if (!c.ok) return VI_ERR_WORKSPACE;
     a.logits = s.logits; a.rows = s.rows; a.vocabulary = s.vocabulary; a.stride = s.stride;
     a.params = s.params;
