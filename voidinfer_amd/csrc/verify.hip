@@ -18,8 +18,9 @@
 // (last positive id on round-off).  u_a, u_c are Philox draws keyed by
 // (seed, lane, position + j, purpose 1 / 2).  Every (lane, position) decision
 // is taken at once, one wave each over the <= 64-entry lists (fp64): entry-wise
-// work on the lanes, the order-dependent sums on lane 0; a per-lane pass then
-// walks the accept chain in order.  Full-vocabulary lanes: the accept test
+// work on the lanes, the order-dependent sums on lane 0; the last position of
+// a lane to finish then walks its accept chain in order (after the
+// full-vocabulary kernels, a separate per-lane pass does).  Full-vocabulary lanes: the accept test
 // evaluates the target softmax p and the draft q at the drafted token from the
 // rows' supports, and the correction walks the target softmax, the draft q and
 // their residual over the whole vocabulary in id order (ranges of 16,384
@@ -134,9 +135,16 @@ struct PosDecision {
     int32_t pad;
 };
 
-// One wave per (position, lane): every position of every lane at once; the
-// accept chain is resolved afterwards by verify_chain_kernel.
-__global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
+// A position's decision, stored with agent-scope stores (another workgroup of
+// the launch may read it: the lane's chain runs in its last position).
+__device__ __forceinline__ void put_dec(PosDecision* o, PosDecision v) {
+    put_agent(&o->token, v.token);
+    put_agent(&o->flags, v.flags);
+    put_agent(&o->accept, v.accept);
+}
+
+// One wave per (position, lane): the decision of position j of lane l.
+__device__ __forceinline__ void position_decision(
     const float* tval, const int* tidx, const uint32_t* tvalid, const uint32_t* tflags, const float* dval,
     const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int drafts, int target_rows,
     const int32_t* drafted, const vi_row_params* params, int vocabulary, int full_ok, PosDecision* dec) {
@@ -149,7 +157,7 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     PosDecision* out = dec + size_t(l) * (drafts + 1) + j;
     const size_t tr = size_t(l) * target_rows + j;
     if (verify_list_refused(p)) {   // no list of this lane's top_k: the full-vocabulary path, or refused
-        if (!full_ok && k == 0 && (j < drafts || target_rows == drafts + 1)) *out = PosDecision{-1, VI_FLAG_ERROR, 0, 0};
+        if (!full_ok && k == 0 && (j < drafts || target_rows == drafts + 1)) put_dec(out, PosDecision{-1, VI_FLAG_ERROR, 0, 0});
         return;
     }
     if (j == drafts) {   // the bonus row's draw (used when every draft is accepted)
@@ -167,7 +175,7 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
                     tok = P.id[pick];
                 }
             }
-            *out = PosDecision{tok, 0u, 0, 0};
+            put_dec(out, PosDecision{tok, 0u, 0, 0});
         }
         return;
     }
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
         if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
         else acc_p = fmin(1.0, (ip >= 0 ? P.w[ip] / P.sn : 0.0) / q);
         s_accept = (q != 0.0 && ua < acc_p) ? 1 : 0;
-        if (s_accept) *out = PosDecision{-1, flags, 1, 0};
+        if (s_accept) put_dec(out, PosDecision{-1, flags, 1, 0});
     }
     __syncthreads();
     if (s_accept) return;
@@ -237,21 +245,20 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
             }
             if (!found) corr = last;
         }
-        *out = PosDecision{corr, flags, 0, 0};
+        put_dec(out, PosDecision{corr, flags, 0, 0});
     }
 }
 
-// The accept chain of each lane over its position decisions, in order: accepted
-// drafts are committed until the first rejection (its correction is committed
-// and ends the chain) or a terminal token; a lane that accepted every draft
-// commits the bonus draw.  Flags of the positions visited (and the bonus row).
-__global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int drafts, int target_rows,
-                                    const int32_t* drafted, const vi_row_params* params, const int64_t* terminal,
-                                    int n_terminal, int full_ok, int32_t* accepted, int32_t* committed,
-                                    int32_t* committed_count, uint32_t* lane_flags) {
-    const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l >= lanes) return;
-    const PosDecision* D = dec + size_t(l) * (drafts + 1);
+// The accept chain of lane l over its position decisions (load(j)), in order:
+// accepted drafts are committed until the first rejection (its correction is
+// committed and ends the chain) or a terminal token; a lane that accepted
+// every draft commits the bonus draw.  Flags of the positions visited (and the
+// bonus row).
+template <class Load>
+__device__ __forceinline__ void lane_chain(int l, Load load, int drafts, int target_rows, const int32_t* drafted,
+                                           const vi_row_params* params, const int64_t* terminal, int n_terminal,
+                                           int full_ok, int32_t* accepted, int32_t* committed,
+                                           int32_t* committed_count, uint32_t* lane_flags) {
     int32_t* out = committed + size_t(l) * (drafts + 1);
     for (int j = 0; j <= drafts; ++j) out[j] = -1;
     if (verify_list_refused(params[l]) && !full_ok) {   // refused lane: nothing accepted, nothing committed
@@ -264,7 +271,7 @@ __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int draft
     int c = 0, acc = 0;
     bool stopped = false, rejected = false;
     for (int j = 0; j < drafts; ++j) {
-        const PosDecision e = D[j];
+        const PosDecision e = load(j);
         flags |= e.flags;
         if (e.accept) {
             const int32_t d = drafted[size_t(l) * drafts + j];
@@ -279,13 +286,51 @@ __global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int draft
         break;
     }
     if (!rejected && !stopped && acc == drafts && target_rows == drafts + 1) {
-        const PosDecision b = D[drafts];
+        const PosDecision b = load(drafts);
         flags |= b.flags;
         if (b.token >= 0) out[c++] = b.token;
     }
     accepted[l] = acc;
     committed_count[l] = c;
     if (lane_flags) lane_flags[l] = flags;
+}
+
+// Every position of every lane at once; with `arrivals` (list lanes only) the
+// last position of a lane to finish runs its chain (agent-scope hand-off of the
+// decisions, the lane's counter reset for the next call), else
+// verify_chain_kernel does after the full-vocabulary kernels.
+__global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
+    const float* tval, const int* tidx, const uint32_t* tvalid, const uint32_t* tflags, const float* dval,
+    const int* didx, const uint32_t* dvalid, const uint32_t* dflags, int drafts, int target_rows,
+    const int32_t* drafted, const vi_row_params* params, int vocabulary, int full_ok, PosDecision* dec,
+    uint32_t* arrivals, const int64_t* terminal, int n_terminal, int32_t* accepted, int32_t* committed,
+    int32_t* committed_count, uint32_t* lane_flags) {
+    position_decision(tval, tidx, tvalid, tflags, dval, didx, dvalid, dflags, drafts, target_rows, drafted, params,
+                      vocabulary, full_ok, dec);
+    if (!arrivals || threadIdx.x != 0) return;
+    const int l = blockIdx.y;
+    handoff_stores_done();
+    const uint32_t old = __hip_atomic_fetch_add(&arrivals[l], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old != uint32_t(drafts)) return;   // (drafts + 1 positions per lane)
+    handoff_acquire();
+    const PosDecision* D = dec + size_t(l) * (drafts + 1);
+    lane_chain(l, [&](int j) {
+        return PosDecision{get_agent(&D[j].token), get_agent(&D[j].flags), get_agent(&D[j].accept), 0};
+    }, drafts, target_rows, drafted, params, terminal, n_terminal, full_ok, accepted, committed, committed_count,
+               lane_flags);
+    put_agent(&arrivals[l], 0u);
+}
+
+// The accept chains after the full-vocabulary kernels (one thread per lane).
+__global__ void verify_chain_kernel(const PosDecision* dec, int lanes, int drafts, int target_rows,
+                                    const int32_t* drafted, const vi_row_params* params, const int64_t* terminal,
+                                    int n_terminal, int full_ok, int32_t* accepted, int32_t* committed,
+                                    int32_t* committed_count, uint32_t* lane_flags) {
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= lanes) return;
+    const PosDecision* D = dec + size_t(l) * (drafts + 1);
+    lane_chain(l, [&](int j) { return D[j]; }, drafts, target_rows, drafted, params, terminal, n_terminal, full_ok,
+               accepted, committed, committed_count, lane_flags);
 }
 
 // ------------------------------------------------------- full-vocabulary lanes
@@ -724,7 +769,7 @@ size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     b += 2 * align_up(size_t(v.trows + v.drows) * kMaxK * 4, 256) + 2 * align_up(size_t(v.trows + v.drows) * 4, 256);
     b += align_up(greedy_workspace(v.trows, vocabulary), 256);
     b += topk_partials_bytes_slices(v.lrows, v.lslices);
-    b += align_up(size_t(v.trows) * sizeof(PosDecision), 256);
+    b += align_up(size_t(v.trows) * sizeof(PosDecision), 256) + align_up(size_t(lanes) * 4, 256);
     b += full_verify_bytes(lanes, drafts, vocabulary);
     return b + 4096;
 }
@@ -746,6 +791,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     uint32_t* dvalid = c.take<uint32_t>(size_t(v.drows));
     uint32_t* dflags = c.take<uint32_t>(size_t(v.drows));
     PosDecision* dec = c.take<PosDecision>(size_t(v.trows));
+    uint32_t* larr = c.take<uint32_t>(size_t(a.lanes));   // positions of a lane decided (zero between calls)
     const size_t gbytes = greedy_workspace(v.trows, a.vocabulary);
     unsigned char* gws = gbytes ? c.take<unsigned char>(gbytes) : nullptr;
     const size_t lbytes = topk_partials_bytes_slices(v.lrows, v.lslices);
@@ -778,7 +824,8 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     if (st != VI_OK) return st;
     hipLaunchKernelGGL(verify_position_kernel, dim3(a.drafts + 1, a.lanes), dim3(kFinalizeThreads), 0, stream, tval,
                        tidx, tvalid, tflags, dval, didx, dvalid, dflags, a.drafts, a.target_rows, a.drafted, a.params,
-                       a.vocabulary, full_ok, dec);
+                       a.vocabulary, full_ok, dec, full_ok ? nullptr : larr, a.terminal, a.n_terminal, a.accepted,
+                       a.committed, a.committed_count, a.lane_flags);
     st = launch_status();
     if (st != VI_OK) return st;
     if (full_ok) {
@@ -834,6 +881,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
         st = launch_status();
         if (st != VI_OK) return st;
     }
+    if (!full_ok) return VI_OK;   // (the position launch ran every lane's chain)
     hipLaunchKernelGGL(verify_chain_kernel, dim3(blocks), dim3(threads), 0, stream, dec, a.lanes, a.drafts,
                        a.target_rows, a.drafted, a.params, a.terminal, a.n_terminal, full_ok, a.accepted, a.committed,
                        a.committed_count, a.lane_flags);
