@@ -67,6 +67,24 @@ def test_greedy_prefix(orc, dev, bonus):
     assert w[0].max() == drafts
 
 
+def test_greedy_bonus_then_no_bonus(orc, dev):
+    """Both row counts share one workspace per (lanes, drafts, vocabulary): a
+    call with the bonus row, then one without, must find the greedy arrival
+    counters at zero (they are carved ahead of the shape-dependent partials)."""
+    from voidinfer_amd import workloads as W
+    lanes, drafts = 8, 16
+    for bonus in (True, False, True, False):
+        tb, db, drafted, p = W.config4(lanes=lanes, drafts=drafts, bonus=bonus)
+        trows = drafts + 1 if bonus else drafts
+        targ = orc.greedy_rows(tb, 0)["token"].reshape(lanes, trows)
+        for l in range(lanes):
+            k = (3 * l + 2) % (drafts + 1)
+            drafted[l, :k] = targ[l, :k]
+        print(f"[verify] greedy bonus={bonus}", flush=True)
+        g, w = run(orc, dev, 0, tb, None, drafted, p, lanes, drafts)
+        assert_same(g, w)
+
+
 def test_greedy_terminal_stop(orc, dev):
     from voidinfer_amd import workloads as W
     lanes, drafts = 4, 8

@@ -163,7 +163,7 @@ GreedyPlan greedy_plan(int rows, int vocabulary) {
 size_t greedy_workspace(int rows, int vocabulary) {
     const GreedyPlan p = greedy_plan(rows, vocabulary);
     if (p.slices == 1) return 0;
-    return align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256) + align_up(size_t(rows) * 4, 256);
+    return align_up(size_t(rows) * 4, 256) + align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256);
 }
 
 namespace {
@@ -176,9 +176,13 @@ vi_status launch_greedy_kind(const void* logits, int dtype, int rows, int vocabu
     GreedyPartial* partials = nullptr;
     uint32_t* arrivals = nullptr;
     if (p.slices > 1) {
+        // The arrival counters come first: their offset does not depend on the
+        // shape, so a launch over fewer rows of a workspace carved for more
+        // (verification without its bonus row) finds them where the kernels
+        // left them, at zero.
         Carver c(ws, ws_bytes);
-        partials = c.take<GreedyPartial>(size_t(rows) * p.slices);
         arrivals = c.take<uint32_t>(size_t(rows));
+        partials = c.take<GreedyPartial>(size_t(rows) * p.slices);
         if (!c.ok) return VI_ERR_WORKSPACE;
     }
     const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && ((stride * elem_size(dtype)) % 16 == 0);
@@ -246,11 +250,9 @@ vi_status launch_greedy_noalloc(const void* logits, int dtype, int rows, int voc
     const vi_status st = greedy_scratch_setup(&ws);
     if (st != VI_OK) return st;
     if (need > 0) {
-        // The arrival counters must start at zero; their offset depends on the
-        // shape, and an earlier call of another shape left partials there.
-        const GreedyPlan p = greedy_plan(rows, vocabulary);
-        uint32_t* arrivals = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(ws) +
-                                                         align_up(size_t(rows) * p.slices * sizeof(GreedyPartial), 256));
+        // The arrival counters (the first rows words) must start at zero; an
+        // earlier call of more rows left its own partials past them.
+        uint32_t* arrivals = static_cast<uint32_t*>(ws);
         hipLaunchKernelGGL(zero_words_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, arrivals, rows);
         if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
     }

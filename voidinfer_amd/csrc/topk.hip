@@ -30,7 +30,6 @@
 
 #include <algorithm>
 #include <cstdlib>
-#include <cstring>
 
 #include "penalty_state.h"
 #include "row_scan.h"
@@ -1386,22 +1385,8 @@ size_t sample_workspace(int rows, int vocabulary, int64_t max_history) {
     size_t bytes = topk_partials_bytes(rows, vocabulary);
     bytes += align_up(size_t(rows) * 4, 256);
     if (max_history > 0) bytes += align_up(size_t(rows) * history_hash_slots(max_history) * 8, 256);
-    bytes += std::max({full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary),
-                       parts_workspace(rows, vocabulary)});
+    bytes += std::max(full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary));
     return bytes + 1024;
-}
-
-// The parts route (sample_parts.hip) can serve 16-bit full-route rows whose
-// penalties come from penalty states (or that have none) when no probabilities
-// or bounds are wanted; it is chosen by VOIDINFER_AMD_FULL_ROUTE=parts (read at
-// every call).  The slice / merge kernels serve every other case, and these
-// rows by default: on the configuration-5 workload they are the faster route.
-static bool use_parts(const SampleArgs& s) {
-    const char* e = std::getenv("VOIDINFER_AMD_FULL_ROUTE");
-    if (!e || std::strcmp(e, "parts") != 0) return false;
-    if (s.probs || s.full_out) return false;
-    if (!s.pstate && s.histories && s.offsets && s.max_history > 0) return false;
-    return parts_supported(s.dtype, s.vocabulary, s.stride, s.logits);
 }
 
 vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStream_t stream) {
@@ -1420,8 +1405,7 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         hash = c.take<uint2>(size_t(s.rows) * slots);
     }
     const size_t full_bytes = s.dtype == VI_F32 ? wide_workspace(s.rows, s.vocabulary)
-                                                 : std::max(full_workspace(s.rows, s.vocabulary),
-                                                            parts_workspace(s.rows, s.vocabulary));
+                                                 : full_workspace(s.rows, s.vocabulary);
     unsigned char* full_ws = c.take<unsigned char>(full_bytes);
     if (!c.ok) return VI_ERR_WORKSPACE;
     const bool run_topk = (s.route_mask & VI_ROUTE_TOPK) != 0;
@@ -1455,8 +1439,7 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
     }
     if ((s.route_mask & VI_ROUTE_FULL) && full_ok)
         st = s.dtype == VI_F32 ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
-                               : (use_parts(s) ? launch_parts(s, full_ws, full_bytes, stream)
-                                               : launch_full(s, full_ws, full_bytes, stream));
+                               : launch_full(s, full_ws, full_bytes, stream);
     else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) return VI_ERR_UNSUPPORTED;
     return st;
 }

@@ -800,8 +800,9 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     const int threads = 64, blocks = (a.lanes + threads - 1) / threads;
     vi_status st;
     if (a.mode == VI_VERIFY_GREEDY) {
-        // greedy partials are carved for v.trows rows; a launch over fewer rows
-        // (no bonus row) uses a prefix of the same arrival counters.
+        // the greedy workspace is carved for v.trows rows; a launch over fewer
+        // rows (no bonus row) uses a prefix of the same arrival counters, which
+        // the greedy launcher carves ahead of its partials.
         st = launch_greedy(a.target, a.target_dtype, trows, a.vocabulary, a.target_stride, 0, grows, gws, gbytes,
                            stream);
         if (st != VI_OK) return st;

@@ -176,12 +176,6 @@ vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStrea
 
 // ---- full-vocabulary pair kernel --------------------------------------------
 int device_cus();
-// ---- full-vocabulary rows in one launch (sample_parts.hip): 16-bit logits,
-// penalties from penalty states or none, no probabilities or bounds wanted
-constexpr int kMaxParts16 = 8;
-bool parts_supported(int dtype, int vocabulary, int64_t stride, const void* logits);
-size_t parts_workspace(int rows, int vocabulary);
-vi_status launch_parts(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 size_t full_workspace(int rows, int vocabulary);
 vi_status launch_full(const SampleArgs& a, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 bool full_supported(int dtype, int vocabulary, int64_t stride);
