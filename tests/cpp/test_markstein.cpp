@@ -1,4 +1,4 @@
-// The parts route's division x / r (csrc/sample_parts.hip, penalize_fast):
+// The samplers' division x / r (penalize_fast, voidinfer_amd/csrc/vi_device.h):
 // q0 = RN(x * inv), r0 = RN(x - r * q0) by an FMA, q = RN(q0 + r0 * inv), with
 // inv = RN(1 / r), taken for |x| in [2^-100, 2^100] and r in [2^-20, 2^20].
 // Checked bit for bit against the IEEE division: every positive finite bf16 x

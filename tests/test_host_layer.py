@@ -4,7 +4,7 @@
   (tests/test_exl3_sampling_policy.cpp and its siblings) against this layer;
 * tests/cpp/test_transport_host.cpp — the greedy-packet transport classes over
   a host stand-in of the vi_packet_* entry points;
-* tests/cpp/test_markstein.cpp — the parts route's FMA-corrected division of a
+* tests/cpp/test_markstein.cpp — the samplers' FMA-corrected division of a
   penalized logit by the repetition penalty, bit for bit against IEEE division;
 * oracle/_ref/ref_diff — random scripts run side by side through this layer and
   the reference's host headers compiled from /root/reference (skipped where the

@@ -1385,7 +1385,8 @@ size_t sample_workspace(int rows, int vocabulary, int64_t max_history) {
     size_t bytes = topk_partials_bytes(rows, vocabulary);
     bytes += align_up(size_t(rows) * 4, 256);
     if (max_history > 0) bytes += align_up(size_t(rows) * history_hash_slots(max_history) * 8, 256);
-    bytes += std::max(full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary));
+    bytes += std::max({full_workspace(rows, vocabulary), wide_workspace(rows, vocabulary),
+                       stream_workspace(rows, vocabulary, max_history)});
     return bytes + 1024;
 }
 
@@ -1405,7 +1406,8 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         hash = c.take<uint2>(size_t(s.rows) * slots);
     }
     const size_t full_bytes = s.dtype == VI_F32 ? wide_workspace(s.rows, s.vocabulary)
-                                                 : full_workspace(s.rows, s.vocabulary);
+                                                 : std::max(full_workspace(s.rows, s.vocabulary),
+                                                            stream_workspace(s.rows, s.vocabulary, s.max_history));
     unsigned char* full_ws = c.take<unsigned char>(full_bytes);
     if (!c.ok) return VI_ERR_WORKSPACE;
     const bool run_topk = (s.route_mask & VI_ROUTE_TOPK) != 0;
@@ -1438,8 +1440,9 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         if (st != VI_OK) return st;
     }
     if ((s.route_mask & VI_ROUTE_FULL) && full_ok)
-        st = s.dtype == VI_F32 ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
-                               : launch_full(s, full_ws, full_bytes, stream);
+        st = s.dtype == VI_F32     ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
+             : stream_supported(s) ? launch_stream(s, full_ws, full_bytes, stream)
+                                   : launch_full(s, full_ws, full_bytes, stream);
     else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) return VI_ERR_UNSUPPORTED;
     return st;
 }

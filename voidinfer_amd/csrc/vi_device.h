@@ -212,6 +212,40 @@ __device__ __forceinline__ uint32_t penalize_bits(uint32_t bits, uint32_t count,
     if (p.presence_penalty != 0.0f) y = y - p.presence_penalty;
     return Elem<DT>::round(y);
 }
+// penalize_bits with the division x / r done as Markstein's correction of
+// x * (1/r): with inv = 1/r correctly rounded, q0 = RN(x * inv), the residual
+// r0 = x - r * q0 exact by an FMA, and RN(q0 + r0 * inv) is the correctly
+// rounded quotient when nothing underflows or overflows (P. Markstein, "IA-64
+// and Elementary Functions", 2000, theorem 8.10) — so for |x| in [2^-100,
+// 2^100] and r in [2^-20, 2^20] (rep_fast); other values take the IEEE
+// division.  Three instructions in place of the division sequence on the
+// common path; bit-exact against penalize_bits (tests/cpp/test_markstein.cpp).
+template <int DT>
+__device__ __forceinline__ uint32_t penalize_fast(uint32_t bits, uint32_t count, const vi_row_params& p, float inv,
+                                                  bool rep_fast) {
+#pragma clang fp contract(off)
+    const float x = Elem<DT>::decode(bits);
+    float y = x;
+    if (p.repetition_penalty != 1.0f) {
+        const float q0 = x * inv;
+        const float r0 = fmaf(-q0, p.repetition_penalty, x);
+        float q = fmaf(r0, inv, q0);
+        const float ax = fabsf(x);
+        if (x > 0.0f && !(rep_fast && ax >= 0x1p-100f && ax <= 0x1p100f)) q = x / p.repetition_penalty;
+        y = x > 0.0f ? q : x * p.repetition_penalty;
+    }
+    if (p.frequency_penalty != 0.0f) {
+        const float t = p.frequency_penalty * float(count);
+        y = y - t;
+    }
+    if (p.presence_penalty != 0.0f) y = y - p.presence_penalty;
+    return Elem<DT>::round(y);
+}
+// The reciprocal and the range condition penalize_fast takes, per row.
+__device__ __forceinline__ float rep_inverse(const vi_row_params& p) { return 1.0f / p.repetition_penalty; }
+__device__ __forceinline__ bool rep_fast_ok(const vi_row_params& p) {
+    return p.repetition_penalty >= 0x1p-20f && p.repetition_penalty <= 0x1p20f;
+}
 __device__ __forceinline__ bool penalties_active(const vi_row_params& p) {
     return p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
 }

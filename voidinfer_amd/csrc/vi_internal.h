@@ -176,6 +176,11 @@ vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStrea
 
 // ---- full-vocabulary pair kernel --------------------------------------------
 int device_cus();
+// ---- full-vocabulary rows, stream and merge launches (sample_stream.hip): 16-bit logits,
+// aligned rows, vocabulary a multiple of 8, no probabilities or bounds wanted.
+bool stream_supported(const SampleArgs& s);
+size_t stream_workspace(int rows, int vocabulary, int64_t max_history);
+vi_status launch_stream(const SampleArgs& s, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 size_t full_workspace(int rows, int vocabulary);
 vi_status launch_full(const SampleArgs& a, unsigned char* ws, size_t ws_bytes, hipStream_t stream);
 bool full_supported(int dtype, int vocabulary, int64_t stride);
