@@ -17,9 +17,11 @@
 // are the values that compare greater than -Inf (NaN and -Inf never win, +Inf
 // can), nothing is flagged, and the row's writer also emits the gap
 // max - logit(next[r]) for a next in [0, V) other than the argmax (else 0).
+#include <algorithm>
 #include <mutex>
 
 #include "row_scan.h"
+
 #include "vi_internal.h"
 
 namespace vi {
@@ -171,17 +173,18 @@ namespace {
 template <bool SCORE>
 vi_status launch_greedy_kind(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                              uint64_t serial, vi_greedy_row* out, const int64_t* next, int64_t* greedy, float* gap,
-                             void* ws, size_t ws_bytes, hipStream_t stream) {
+                             void* ws, size_t ws_bytes, int arrival_rows, hipStream_t stream) {
     const GreedyPlan p = greedy_plan(rows, vocabulary);
     GreedyPartial* partials = nullptr;
     uint32_t* arrivals = nullptr;
     if (p.slices > 1) {
-        // The arrival counters come first: their offset does not depend on the
-        // shape, so a launch over fewer rows of a workspace carved for more
-        // (verification without its bonus row) finds them where the kernels
-        // left them, at zero.
+        // The arrival counters come first, as many as the workspace was carved
+        // for (arrival_rows >= rows): a launch over fewer rows of a workspace
+        // carved for more (verification without its bonus row) finds them where
+        // the kernels left them, at zero, and no partials of a smaller launch
+        // lie under them.
         Carver c(ws, ws_bytes);
-        arrivals = c.take<uint32_t>(size_t(rows));
+        arrivals = c.take<uint32_t>(size_t(std::max(rows, arrival_rows)));
         partials = c.take<GreedyPartial>(size_t(rows) * p.slices);
         if (!c.ok) return VI_ERR_WORKSPACE;
     }
@@ -203,9 +206,9 @@ vi_status launch_greedy_kind(const void* logits, int dtype, int rows, int vocabu
 
 vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                         uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
-                        hipStream_t stream) {
+                        hipStream_t stream, int arrival_rows) {
     return launch_greedy_kind<false>(logits, dtype, rows, vocabulary, stride, serial, out, nullptr, nullptr, nullptr,
-                                     ws, ws_bytes, stream);
+                                     ws, ws_bytes, arrival_rows, stream);
 }
 
 // ---- allocation-free greedy (vi_greedy_rows_noalloc) ---------------------------
@@ -257,14 +260,14 @@ vi_status launch_greedy_noalloc(const void* logits, int dtype, int rows, int voc
         if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
     }
     return launch_greedy_kind<false>(logits, dtype, rows, vocabulary, stride, serial, out, nullptr, nullptr, nullptr,
-                                     ws, kGreedyScratchBytes, stream);
+                                     ws, kGreedyScratchBytes, rows, stream);
 }
 
 vi_status launch_row_scores(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                             const int64_t* next, int64_t* greedy, float* gap, void* ws, size_t ws_bytes,
                             hipStream_t stream) {
     return launch_greedy_kind<true>(logits, dtype, rows, vocabulary, stride, 0, nullptr, next, greedy, gap, ws,
-                                    ws_bytes, stream);
+                                    ws_bytes, rows, stream);
 }
 
 }  // namespace vi

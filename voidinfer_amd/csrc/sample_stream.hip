@@ -64,8 +64,8 @@ constexpr int kDepth = 4;                // rounds of logits in flight per threa
 constexpr int kXcds = 8;
 constexpr int kRepPF = 2;                // repeat-list entries prefetched per thread
 constexpr int kMaxParts = 16;            // parts per row
-constexpr int kMaxPartLen = 65528;       // tokens per part (a multiple of 8 below 65,536)
-constexpr int kPub = 64;                 // words per part header: occupancy bitmap [32], top key
+constexpr int kMaxPartLen = 65504;       // tokens per part (a multiple of 32 below 65,536)
+constexpr int kPub = 32;                 // words per part header: the occupancy bitmap
 constexpr uint32_t kTakeAll = 0xffffffffu;
 constexpr double kFix = 0x1p40;          // fixed-point scale of the masses (w <= 1, counts <= 2^20)
 
@@ -132,6 +132,27 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+// Exclusive prefix sum of v over the workgroup (total in *total), its barriers
+// LDS-only: loads in flight stay in flight.
+__device__ __forceinline__ uint32_t block_scan_lds(uint32_t v, uint32_t* tmp, uint32_t* total) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    const uint32_t x = wave_incl_scan_u32(v);
+    if (lane == kWave - 1) tmp[wave] = x;
+    lds_barrier();
+    if (wave == 0) {
+        const uint32_t t = lane < kW ? tmp[lane] : 0u;
+        const uint32_t it = wave_incl_scan_u32(t);
+        if (lane < kW) tmp[lane] = it - t;
+        if (lane == kW - 1) tmp[kW] = it;
+    }
+    lds_barrier();
+    const uint32_t r = tmp[wave] + x - v;
+    *total = tmp[kW];
+    lds_barrier();
+    return r;
+}
+// s_waitcnt vmcnt(0): every vector memory access of the wave complete.
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local"); }
 
 __device__ __forceinline__ void lds_add(uint32_t* p, uint32_t v) {
@@ -249,12 +270,39 @@ __device__ __forceinline__ bool key_valid(uint32_t key, uint32_t kmin, uint32_t 
 }
 
 // ------------------------------------------------------------------ stream
+constexpr int kMaxItems = 1024;          // parts one workgroup can take
+
 struct StreamShared {
-    uint32_t occ[32];
-    uint32_t top_key, kmin, kmax;
+    int items[kMaxItems];                // the workgroup's parts (indices among its XCD's), in order
+    uint32_t scan[kW + 1];
+    // the part's occupied groups: byte q * 16 + wave, bit i -> group q * 128 + wave * 8 + i
+    unsigned char occb[kGroups / 8];
 };
 
-template <int DT>
+// The presence bytes (one per vector) of a row from token s0: the lane
+// state's or the history prepass's bitmap; without either, any readable byte
+// per vector (the logits; the byte is then ignored).
+__device__ __forceinline__ const unsigned char* presence_at(const StreamArgs& a, int row, int s0,
+                                                            const unsigned char* vb) {
+    if (a.pstate) return a.pstate + size_t(row) * a.pl.lane_bytes + a.pl.off_b1 + (s0 >> 3);
+    if (a.hb1) return reinterpret_cast<const unsigned char*>(a.hb1 + size_t(row) * a.hwords) + (s0 >> 3);
+    return vb;
+}
+
+// One part as the stream sees it: geometry, logits, presence bytes, repeat
+// list, penalty parameters.
+struct PartView {
+    Item it;
+    const unsigned char* vb;
+    const unsigned char* pb;
+    const uint2* list;
+    uint32_t nrep;
+    bool pen;
+    float rep, pres, freq;
+};
+
+// PB: the call has presence bytes (lane states or the history prepass).
+template <int DT, bool PB>
 __global__ __launch_bounds__(kT) void stream_kernel(StreamArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
     __shared__ StreamShared sh;
@@ -264,118 +312,162 @@ __global__ __launch_bounds__(kT) void stream_kernel(StreamArgs a) {
     const int x = a.xcd ? w % kXcds : 0;
     const int wx = a.xcd ? w / kXcds : w;   // index among the XCD's workgroups
     const int nx = xcd_wgs(a, x), items = xcd_rows(a, x) * a.parts;
-    // this workgroup's parts: wx, wx + nx, ... (rows the kernel does not serve passed over)
-    auto next_item = [&](int q) -> int {
-        for (; q < items; q += nx)
-            if (stream_row(a.params[item_at(a, x, q).row])) return q;
-        return -1;
-    };
 
     // the histogram starts empty (every part leaves it so)
 #pragma unroll
     for (int q = 0; q < kHW / 4 / kT; ++q)
         reinterpret_cast<uint4*>(H)[q * kT + tid] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < 32) sh.occ[tid] = 0u;
-    if (tid == 0) sh.top_key = 0u;
-    int cur = next_item(wx);
-
-    // Rounds in flight: global round G (counted over this workgroup's parts)
-    // sits in slot G % kDepth; tag[s] is the global round slot s holds (-1:
-    // none).  A part's rounds are G0 .. G0 + R - 1; the loads run kDepth rounds
-    // ahead, into the next part once the current one's are all requested.
-    uint4 rv[kDepth];
-    uint32_t rb[kDepth];
-    int tag[kDepth];
-    Item it{};
-    const unsigned char* vbase = nullptr;   // the part's first vector
-    const unsigned char* pbase = nullptr;   // the part's presence bytes
-    bool pen = false;
-    auto issue = [&](uint4& dv, uint32_t& db, const unsigned char* vb, const unsigned char* pb, int nvec, int rho) {
-        const int t = opaque_tid();
-        const int v = min(rho * kT + t, nvec - 1);
-        dv = load16(vb + size_t(v) * 16);
-        db = pb ? uint32_t(pb[v]) : 0u;
-    };
-    auto setup = [&](int q, Item& i, const unsigned char** vb, const unsigned char** pb, bool* pn) {
-        i = item_at(a, x, q);
-        const vi_row_params& pp = a.params[i.row];
-        const PenView pv = pen_view(a, i.row, pp);
-        *pn = pv.pen;
-        *vb = static_cast<const unsigned char*>(a.logits) + 2 * (size_t(i.row) * size_t(a.stride) + size_t(i.s0));
-        *pb = pv.pen ? pv.b1 + (i.s0 >> 3) : nullptr;
-    };
-    int G0 = 0;   // the current part's first global round
-#pragma unroll
-    for (int s = 0; s < kDepth; ++s) tag[s] = -1;
-    if (cur >= 0) {
-        setup(cur, it, &vbase, &pbase, &pen);
-#pragma unroll
-        for (int s = 0; s < kDepth; ++s) {
-            if (s < it.rounds) { issue(rv[s], rb[s], vbase, pbase, it.nvec, s); tag[s] = s; }
-        }
+    // the workgroup's parts: wx, wx + nx, ... of its XCD's (at most kMaxItems:
+    // the launch checks), rows the kernel does not serve passed over
+    int nitems;
+    {
+        const int ncand = wx < items ? (items - 1 - wx) / nx + 1 : 0;
+        const int q = wx + tid * nx;
+        const uint32_t ok = (tid < ncand && stream_row(a.params[item_at(a, x, q).row])) ? 1u : 0u;
+        uint32_t tot;
+        const uint32_t pos = block_scan_lds(ok, sh.scan, &tot);
+        if (ok) sh.items[pos] = q;
+        nitems = int(tot);
+        lds_barrier();
     }
-    __syncthreads();
+    if (nitems == 0) return;
 
-    while (cur >= 0) {
-        const vi_row_params p = a.params[it.row];
-        const PenView pv = pen_view(a, it.row, p);
-        const float inv_r = rep_inverse(p);
-        const bool rep_fast = rep_fast_ok(p);
-        if (wave == 0) {   // (read at the publication, after barriers)
-            const uint32_t km = valid_key_range<DT>(p.temperature);
-            if (lane == 0) { sh.kmin = km & 0xffffu; sh.kmax = km >> 16; }
+    // A part's description.  The penalty parameters, the repeat list's length
+    // and (a part ahead) its first entries come in through vector loads (the
+    // address laundered into a VGPR): an outstanding scalar load would hold up
+    // every LDS wait of the stream in between.
+    auto view = [&](int k) -> PartView {
+        PartView c;
+        const int q = __builtin_amdgcn_readfirstlane(sh.items[k]);
+        c.it = item_at(a, x, q);
+        c.vb = static_cast<const unsigned char*>(a.logits) + 2 * (size_t(c.it.row) * size_t(a.stride) + size_t(c.it.s0));
+        c.pb = presence_at(a, c.it.row, c.it.s0, c.vb);
+        int z = 0;
+        asm volatile("" : "+v"(z));
+        const vi_row_params* pp = a.params + c.it.row + z;
+        c.rep = pp->repetition_penalty;
+        c.pres = pp->presence_penalty;
+        c.freq = pp->frequency_penalty;
+        c.pen = false;   // (settle)
+        const uint32_t* nr;
+        if (a.pstate) {
+            const unsigned char* st = a.pstate + size_t(c.it.row) * a.pl.lane_bytes;
+            c.list = reinterpret_cast<const uint2*>(st + a.pl.off_list);
+            nr = &reinterpret_cast<const PenaltyHeader*>(st)->nrep;
+        } else if (a.hb1) {
+            c.list = a.hlist + size_t(c.it.row) * a.hcap;
+            nr = a.hhead + 2 * c.it.row;
+        } else {
+            c.list = nullptr;
+            nr = reinterpret_cast<const uint32_t*>(a.params);
         }
-        const int next = next_item(cur + nx);
-        Item nx_it{};
-        const unsigned char* nvb = nullptr;
-        const unsigned char* npb = nullptr;
-        bool npen = false;
-        if (next >= 0) setup(next, nx_it, &nvb, &npb, &npen);
-        // repeat-list entries of the lane, prefetched; their logits are gathered
-        // once the last rounds of the part are requested
-        uint2 re[kRepPF];
-        uint32_t rraw[kRepPF];
+        c.nrep = nr[z];
+        return c;
+    };
+    // the loaded fields made uniform (after their loads have landed)
+    auto settle = [&](PartView& c) {
+        auto rf = [](float f) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, f))); };
+        c.rep = rf(c.rep);
+        c.pres = rf(c.pres);
+        c.freq = rf(c.freq);
+        c.pen = PB && (c.rep != 1.0f || c.pres != 0.0f || c.freq != 0.0f);
+        c.nrep = uint32_t(__builtin_amdgcn_readfirstlane(int(c.nrep)));
+        if (a.pstate) c.nrep = min(c.nrep, uint32_t(a.pl.slots));
+    };
+    // The lane's repeat-list entries of a part (kRepPF of them), requested a
+    // part ahead, whatever the list's length (read within the list's
+    // capacity; entries past the length are dropped when used).
+    const uint32_t list_cap = a.pstate ? uint32_t(a.pl.slots) : uint32_t(max(a.hcap, 1));
+    auto load_re = [&](const PartView& c, uint2* e) {
 #pragma unroll
         for (int j = 0; j < kRepPF; ++j) {
-            const uint32_t i = uint32_t(j * kT + tid);
-            re[j] = (pen && i < pv.nrep) ? pv.list[i] : make_uint2(0u, 0u);
-            rraw[j] = 0u;
+            e[j] = make_uint2(0u, 0u);
+            if (PB) e[j] = c.list[min(uint32_t(j * kT + tid), list_cap - 1u)];
         }
+    };
+
+    PartView cur = view(0);
+    bool has_next = nitems > 1;
+    PartView nxt = has_next ? view(1) : cur;
+    uint2 re[kRepPF];   // the current part's entries (those of the next once its corrections are made)
+    load_re(cur, re);
+
+    // Rounds in flight: a part's rounds are padded to whole turns of the ring
+    // (the padding rounds count nothing), so round rho of every part sits in
+    // slot rho % kDepth.  The round kDepth ahead is requested once the current
+    // one is used: the current part's, the next part's, or (past the last
+    // part) the last vector again, never used.  Every round issues exactly one
+    // vector load (and one presence load), straight-line, so the waits count
+    // on the loads' order.
+    uint4 rv[kDepth];
+    uint32_t rb[kDepth] = {};
+    auto padded = [](int r) { return (r + kDepth - 1) & ~(kDepth - 1); };
+    auto issue = [&](uint4& dv, uint32_t& db, int rel) {   // rel: rounds after the current part's first
+        const int Rp = padded(cur.it.rounds);
+        const bool in_nxt = rel >= Rp && has_next;
+        const unsigned char* vb = in_nxt ? nxt.vb : cur.vb;
+        const unsigned char* pb = in_nxt ? nxt.pb : cur.pb;
+        const int nv = in_nxt ? nxt.it.nvec : cur.it.nvec;
+        const int rr = in_nxt ? rel - Rp : rel;
+        const int v = min(rr * kT + opaque_tid(), nv - 1);
+        dv = load16(vb + size_t(v) * 16);
+        // the dword holding the vector's presence byte (a 32-bit load result
+        // stays in its register across the loop; a byte would be re-extended)
+        if (PB) db = *reinterpret_cast<const uint32_t*>(pb + (v & ~3));
+    };
+#pragma unroll
+    for (int s = 0; s < kDepth; ++s) issue(rv[s], rb[s], s);
+    settle(cur);
+
+    for (int k = 0;;) {
+        vi_row_params p{};   // the fields the penalties read
+        p.repetition_penalty = cur.rep;
+        p.presence_penalty = cur.pres;
+        p.frequency_penalty = cur.freq;
+        const float inv_r = rep_inverse(p);
+        const bool rep_fast = rep_fast_ok(p);
+        const bool pen = cur.pen;
+        const Item it = cur.it;
         const uint16_t* row16 = reinterpret_cast<const uint16_t*>(static_cast<const unsigned char*>(a.logits) +
                                                                   2 * size_t(it.row) * size_t(a.stride));
         auto in_part = [&](uint2 e) { return e.y >= 2u && int(e.x) >= it.s0 && int(e.x) < it.s0 + it.n; };
+        // one count of a repeated token from its count-1 pattern to its count-c one
+        auto correct = [&](uint2 e, uint32_t raw) {
+            const uint32_t p1 = pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast);
+            const uint32_t pc = pen_pattern<DT>(raw, e.y, p, inv_r, rep_fast);
+            if (p1 != pc) { hist_dec(H, p1); hist_inc(H, pc); }
+        };
+        uint32_t rraw[kRepPF] = {};
 
-        // ---- the stream
-        const int R = it.rounds;
-        const int gather_round = max(0, R - kDepth);
+        // ---- the stream.  The repeat entries' logits are gathered at the
+        // start of the last turn but one and their corrections made at the
+        // start of the last turn (counts are added and taken in any order: the
+        // 32-bit word holds their sum).
+        const int Rp = padded(it.rounds);
+        const int gather_turn = max(0, Rp - 2 * kDepth), corr_turn = Rp - kDepth;
         uint4* stage = reinterpret_cast<uint4*>(lds + kOffStage) + wave * kWave;
         const uint16_t* stage16 = reinterpret_cast<const uint16_t*>(stage);
         unsigned char* list = lds + kOffList + wave * 512;
-        for (int gb = G0 & ~(kDepth - 1); gb < G0 + R; gb += kDepth) {
+        for (int gb = 0; gb < Rp; gb += kDepth) {
+            if (pen && gb == gather_turn) {
+#pragma unroll
+                for (int j = 0; j < kRepPF; ++j) {
+                    if (uint32_t(j * kT + tid) >= cur.nrep) re[j].y = 0u;
+                    rraw[j] = in_part(re[j]) ? uint32_t(row16[re[j].x]) : 0u;
+                }
+            }
+            if (pen && gb == corr_turn) {
+#pragma unroll
+                for (int j = 0; j < kRepPF; ++j)
+                    if (in_part(re[j])) correct(re[j], rraw[j]);
+            }
+            if (gb == corr_turn && has_next) load_re(nxt, re);   // (in place: no copy waits for it)
 #pragma unroll
             for (int s = 0; s < kDepth; ++s) {
-                const int G = gb + s, rho = G - G0;
-                if (rho < 0 || rho >= R) continue;   // (uniform)
-                if (rho == gather_round) {
-#pragma unroll
-                    for (int j = 0; j < kRepPF; ++j)
-                        rraw[j] = in_part(re[j]) ? uint32_t(row16[re[j].x]) : 0u;
-                }
-                if (tag[s] != G) issue(rv[s], rb[s], vbase, pbase, it.nvec, rho);   // (not requested ahead)
+                const int rho = gb + s;
                 const uint4 v = rv[s];
-                const uint32_t pbyte = rb[s];
-                // the round kDepth ahead: this part's, the next part's, or none
-                {
-                    const int ga = rho + kDepth;
-                    if (ga < R) { issue(rv[s], rb[s], vbase, pbase, it.nvec, ga); tag[s] = G + kDepth; }
-                    else if (next >= 0 && ga - R < nx_it.rounds) {
-                        issue(rv[s], rb[s], nvb, npb, nx_it.nvec, ga - R);
-                        tag[s] = G + kDepth;
-                    } else {
-                        tag[s] = -1;
-                    }
-                }
-                const bool valid = rho * kT + tid < it.nvec;
+                const bool valid = rho * kT + tid < it.nvec;   // (none on a padding round)
+                const uint32_t b = (PB && valid) ? (rb[s] >> (8 * (tid & 3))) & 0xffu : 0u;
                 if (valid) {
                     hist_inc(H, v.x & 0xffffu); hist_inc(H, v.x >> 16);
                     hist_inc(H, v.y & 0xffffu); hist_inc(H, v.y >> 16);
@@ -384,7 +476,6 @@ __global__ __launch_bounds__(kT) void stream_kernel(StreamArgs a) {
                 }
                 if (pen) {   // (uniform) the history tokens of the wave's 512 tokens
                     stage[lane] = v;
-                    const uint32_t b = valid ? pbyte : 0u;
                     const uint32_t n = uint32_t(__builtin_popcount(b));
                     const uint32_t incl = wave_incl_scan_u32(n);
                     const uint32_t N = readlane_u(incl, kWave - 1), NA = readlane_u(incl, 31);
@@ -411,89 +502,62 @@ __global__ __launch_bounds__(kT) void stream_kernel(StreamArgs a) {
                         wave_lds_fence();
                     }
                 }
+                issue(rv[s], rb[s], rho + kDepth);
             }
         }
 
-        // ---- repeated tokens: one count from the count-1 pattern to the count-c one
         lds_barrier();
-        if (pen) {
-#pragma unroll
-            for (int j = 0; j < kRepPF; ++j) {
-                if (in_part(re[j])) {
-                    const uint32_t raw = rraw[j];
-                    const uint32_t p1 = pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast);
-                    const uint32_t pc = pen_pattern<DT>(raw, re[j].y, p, inv_r, rep_fast);
-                    if (p1 != pc) { hist_dec(H, p1); hist_inc(H, pc); }
-                }
-            }
-            for (uint32_t i = uint32_t(kRepPF * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
-                const uint2 e = pv.list[i];
-                if (!in_part(e)) continue;
-                const uint32_t raw = row16[e.x];
-                const uint32_t p1 = pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast);
-                const uint32_t pc = pen_pattern<DT>(raw, e.y, p, inv_r, rep_fast);
-                if (p1 != pc) { hist_dec(H, p1); hist_inc(H, pc); }
+        if (pen && cur.nrep > uint32_t(kRepPF * kT)) {   // (long repeat lists: the rest of the entries)
+            for (uint32_t i = uint32_t(kRepPF * kT + tid); i < cur.nrep; i += kT) {
+                const uint2 e = cur.list[i];
+                if (in_part(e)) correct(e, row16[e.x]);
             }
             lds_barrier();
         }
 
         // ---- publication: the non-empty groups at their place in the part's
-        // table, the occupancy bitmap, the highest valid key; the histogram
-        // cleared.  Eight lanes hold a group (lane 8i + j: its words 4j .. 4j +
-        // 3), so the LDS reads are conflict-free and the stores coalesce.
-        // Plain stores: the merge launch reads them.
+        // table and the occupancy bitmap; the histogram cleared.  Eight lanes
+        // hold a group (lane 8i + j: its words 4j .. 4j + 3), so the LDS reads
+        // are conflict-free and the stores coalesce.  Plain stores: the merge
+        // launch reads them.
         {
             const size_t pi = size_t(it.row) * a.parts + it.part;
+            uint4* dst = a.pwords + pi * (kGroups * kGW / 4);
             const int t = opaque_tid();
-            const uint32_t kmin = sh.kmin, kmax = sh.kmax;
             uint4* H4 = reinterpret_cast<uint4*>(H);
-            uint32_t top = 0u;
 #pragma unroll
             for (int q = 0; q < kHW / 4 / kT; ++q) {
-                const int c = q * kT + t;            // 16-byte chunk: words 4c .. 4c + 3
+                const int c = q * kT + t;            // 16-byte chunk c: words 4c .. 4c + 3 of group c / 8
                 const uint4 d = H4[c];
                 H4[c] = make_uint4(0u, 0u, 0u, 0u);
-                const bool nz = (d.x | d.y | d.z | d.w) != 0u;
-                const uint64_t bm = ballot(nz);
-                const uint32_t gm = uint32_t(bm >> (lane & ~7)) & 0xffu;   // the group's eight lanes
-                const uint32_t g = uint32_t(c) >> 3;
-                if (gm) {
-                    a.pwords[(pi * kGroups + g) * (kGW / 4) + (c & 7)] = d;
-                    if ((lane & 7) == 0) atomicOr(&sh.occ[g >> 5], 1u << (g & 31u));
-                }
-                if (nz) {
-                    // highest valid key of these words: a positive one (low halves,
-                    // rising with the word) beats any negative one (high halves,
-                    // falling); -0 (the high half of word 0) counts as +0
-                    const uint32_t w0 = 4u * uint32_t(c);
-                    const uint32_t wd[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint32_t kp = 0x8000u + w0 + uint32_t(k), kn = 0x7fffu - w0 - uint32_t(k);
-                        if ((wd[k] & 0xffffu) && key_valid<DT>(kp, kmin, kmax)) top = max(top, kp);
-                        if (wd[k] >> 16) {
-                            const uint32_t kk = (w0 + uint32_t(k) == 0u) ? 0x8000u : kn;
-                            if (key_valid<DT>(kk, kmin, kmax)) top = max(top, kk);
-                        }
-                    }
+                const uint64_t bm = ballot((d.x | d.y | d.z | d.w) != 0u);
+                // bit 8i of sm: group i of the wave's eight is occupied
+                uint64_t sm = bm | (bm >> 4);
+                sm |= sm >> 2;
+                sm |= sm >> 1;
+                sm &= 0x0101010101010101ull;
+                const uint64_t lanes = (sm << 8) - sm;   // the occupied groups' lanes
+                const uint32_t half = lane < 32 ? uint32_t(lanes) : uint32_t(lanes >> 32);
+                if ((half >> (lane & 31)) & 1u) dst[c] = d;
+                if (lane == 0) {
+                    const uint32_t lo = uint32_t(sm), hi = uint32_t(sm >> 32);
+                    sh.occb[q * kW + wave] = uint8_t((((lo * 0x00204081u) >> 21) & 0xfu) | ((((hi * 0x00204081u) >> 21) & 0xfu) << 4));
                 }
             }
-#pragma unroll
-            for (int o = 32; o; o >>= 1) top = max(top, uint32_t(__shfl_xor(int(top), o, kWave)));
-            if (lane == 0 && top) atomicMax(&sh.top_key, top);
             lds_barrier();
-            if (tid < 32) {
-                a.ppub[pi * kPub + tid] = sh.occ[tid];
-                sh.occ[tid] = 0u;
-            } else if (tid == 32) {
-                a.ppub[pi * kPub + 32] = sh.top_key;
-                sh.top_key = 0u;
-            }
+            if (tid < 32) a.ppub[pi * kPub + tid] = reinterpret_cast<const uint32_t*>(sh.occb)[tid];
+            // Stores and loads share one counter and may complete out of order:
+            // with a store outstanding every wait on a load would have to drain
+            // the counter.  Drain it once here instead.
+            vm_drain();
         }
-        // the slots already hold the next part's first rounds
-        G0 += R;
-        cur = next;
-        it = nx_it; vbase = nvb; pbase = npb; pen = npen;
+
+        // ---- the next part (its first turn already in flight)
+        if (++k >= nitems) break;
+        cur = nxt;
+        settle(cur);
+        has_next = k + 1 < nitems;
+        if (has_next) nxt = view(k + 1);
     }
 }
 
@@ -502,14 +566,12 @@ struct MergeShared {
     uint32_t scan[kW + 1];
     uint32_t wtot[8][kW];
     uint64_t wmass[kW];
-    uint32_t ptop[kMaxParts];
     uint32_t nslots, total_cnt, z0key, owner, orank, flags, kmin, kmax;
     uint64_t total_mass;
-    int32_t found;
-    uint32_t cap_key, cap_take, end_key, end_take, end_all, minp_key, topp_key, topp_take, draw_key, draw_rank;
+    uint32_t draw_key, draw_rank;
     uint32_t n_support, ok, lo1, hi1, nflip;
     int32_t token;
-    double s_cap, s_n, u, target;
+    double s_n, u;
 };
 
 // Key k's histogram location: group, word inside the group, half (0: low).
@@ -561,41 +623,48 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
     const PenView pv = pen_view(a, row, p);
     const float inv_t = 1.0f / p.temperature;
 
-    // ---- 0. the parts' occupancy bitmaps and highest keys; the valid key range
+    // ---- 0. the parts' occupancy bitmaps; the valid key range
     for (int i = tid; i < P * 32; i += kT) pbits[i] = a.ppub[(pi0 + i / 32) * kPub + i % 32];
-    if (tid < P) sh.ptop[tid] = a.ppub[(pi0 + tid) * kPub + 32];
+    // The first repeat entries (two per thread) and their logits, requested
+    // now (reads within the list and the row whatever the entries hold): the
+    // flips after the draw are then arithmetic.
+    const uint16_t* row16 = reinterpret_cast<const uint16_t*>(static_cast<const unsigned char*>(a.logits) +
+                                                              2 * size_t(row) * size_t(a.stride));
+    uint2 rep[2];
+    uint32_t repraw[2];
+    {
+        const uint2* rl = pv.pen ? pv.list : reinterpret_cast<const uint2*>(a.params);
+        const uint32_t rn = pv.pen ? max(pv.nrep, 1u) : 1u;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) rep[j] = rl[min(uint32_t(j * kT + tid), rn - 1u)];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) repraw[j] = row16[min(rep[j].x, uint32_t(V - 1))];
+    }
     if (wave == 1) {
         const uint32_t km = valid_key_range<DT>(p.temperature);
         if (lane == 0) { sh.kmin = km & 0xffffu; sh.kmax = km >> 16; }
     }
     for (int i = tid; i < 2048; i += kT) { bcnt[i] = 0u; bmass[i] = 0ull; }
-    if (tid == 0) { sh.flags = pv.flags; sh.token = -1; sh.ok = 1u; }
-    __syncthreads();
+    if (tid == 0) { sh.flags = pv.flags; sh.token = -1; sh.ok = 1u; sh.z0key = 0u; }
+    lds_barrier();
     if (tid < 32) {
         uint32_t o = 0u;
         for (int pp = 0; pp < P; ++pp) o |= pbits[pp * 32 + tid];
         occ[tid] = o;
     }
-    if (tid == 0) {
-        uint32_t top = 0u;
-        for (int i = 0; i < P; ++i) top = max(top, sh.ptop[i]);
-        sh.z0key = top;
-    }
-    __syncthreads();
+    lds_barrier();
     // a slot per occupied group
     {
         const uint32_t o = (occ[tid >> 5] >> (tid & 31)) & 1u;
         uint32_t n = 0u;
-        const uint32_t e = block_exclusive_scan_u32<kT>(o, sh.scan, &n);
+        const uint32_t e = block_scan_lds(o, sh.scan, &n);
         if (o) { slot_of[tid] = uint16_t(e); group_of[e] = uint16_t(tid); }
         if (tid == 0) sh.nslots = n;
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t nslots = sh.nslots;
     const bool store_keys = nslots <= kSlotCap;
     const uint32_t kmin = sh.kmin, kmax = sh.kmax;
-    const uint32_t z0key = sh.z0key;
-    const double z0 = double(key_z<DT>(z0key, inv_t));
     const bool fail = (sh.flags & VI_FLAG_ERROR) != 0u || !(p.temperature <= kMaxTemperature);
 
     // Counts of words 2q, 2q + 1 of group g summed over the parts: (lo0, hi0,
@@ -622,33 +691,63 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         return c;
     };
     // ---- 1. per-key counts summed over the parts (a task: two words of a
-    // group; two tasks per thread, their loads issued together)
+    // group; two tasks per thread, their loads issued together) and the
+    // highest valid key present, z0's.  Past kSlotCap occupied groups the
+    // counts are not kept: a second pass adds them to the block sums.
     const uint32_t ntask = nslots * 16u;
-    for (uint32_t t0 = 0; t0 < ntask; t0 += 2 * kT) {
-        const uint32_t ta = t0 + uint32_t(tid), tb = ta + kT;
-        const bool va = ta < ntask, vb = tb < ntask;
-        const uint4 ca = va ? sum_pair(group_of[ta >> 4], ta & 15u) : make_uint4(0u, 0u, 0u, 0u);
-        const uint4 cb = vb ? sum_pair(group_of[tb >> 4], tb & 15u) : make_uint4(0u, 0u, 0u, 0u);
-        if (store_keys) {
-            if (va) keys[ta] = ca;
-            if (vb) keys[tb] = cb;
-        } else {   // (block sums straight from the counts)
-            auto add = [&](uint32_t k, uint32_t c) {
-                if (!c) return;
-                if (!key_valid<DT>(k, kmin, kmax)) { atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE)); return; }
-                atomicAdd(&bcnt[k >> 5], c);
-                atomicAdd(reinterpret_cast<unsigned long long*>(&bmass[k >> 5]),
-                          (unsigned long long)fixed_mass(c, key_weight<DT>(k, inv_t, z0)));
-            };
-            auto add4 = [&](uint32_t t, uint4 c) {
-                const uint32_t w0 = uint32_t(group_of[t >> 4]) * kGW + 2u * (t & 15u);
-                add(0x8000u + w0, c.x); add(0x7fffu - w0, c.y); add(0x8001u + w0, c.z); add(0x7ffeu - w0, c.w);
-            };
+    auto task_keys = [&](uint32_t t) { return uint32_t(group_of[t >> 4]) * kGW + 2u * (t & 15u); };
+    auto top_of = [&](uint32_t t, uint4 c) -> uint32_t {
+        const uint32_t w0 = task_keys(t);
+        uint32_t m = 0u;
+        auto consider = [&](uint32_t k, uint32_t n) {
+            if (n && key_valid<DT>(k, kmin, kmax)) m = max(m, k);
+        };
+        consider(0x8000u + w0, c.x); consider(0x7fffu - w0, c.y); consider(0x8001u + w0, c.z); consider(0x7ffeu - w0, c.w);
+        return m;
+    };
+    {
+        uint32_t top = 0u;
+        for (uint32_t t0 = 0; t0 < ntask; t0 += 2 * kT) {
+            const uint32_t ta = t0 + uint32_t(tid), tb = ta + kT;
+            const bool va = ta < ntask, vb = tb < ntask;
+            const uint4 ca = va ? sum_pair(group_of[ta >> 4], ta & 15u) : make_uint4(0u, 0u, 0u, 0u);
+            const uint4 cb = vb ? sum_pair(group_of[tb >> 4], tb & 15u) : make_uint4(0u, 0u, 0u, 0u);
+            if (store_keys) {
+                if (va) keys[ta] = ca;
+                if (vb) keys[tb] = cb;
+            }
+            if (va) top = max(top, top_of(ta, ca));
+            if (vb) top = max(top, top_of(tb, cb));
+        }
+#pragma unroll
+        for (int o = 32; o; o >>= 1) top = max(top, uint32_t(__shfl_xor(int(top), o, kWave)));
+        if (lane == 0 && top) atomicMax(&sh.z0key, top);
+    }
+    lds_barrier();
+    const uint32_t z0key = sh.z0key;
+    const double z0 = double(key_z<DT>(z0key, inv_t));
+    if (!store_keys) {   // (block sums straight from the counts)
+        auto add = [&](uint32_t k, uint32_t c) {
+            if (!c) return;
+            if (!key_valid<DT>(k, kmin, kmax)) { atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE)); return; }
+            atomicAdd(&bcnt[k >> 5], c);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&bmass[k >> 5]),
+                      (unsigned long long)fixed_mass(c, key_weight<DT>(k, inv_t, z0)));
+        };
+        auto add4 = [&](uint32_t t, uint4 c) {
+            const uint32_t w0 = task_keys(t);
+            add(0x8000u + w0, c.x); add(0x7fffu - w0, c.y); add(0x8001u + w0, c.z); add(0x7ffeu - w0, c.w);
+        };
+        for (uint32_t t0 = 0; t0 < ntask; t0 += 2 * kT) {
+            const uint32_t ta = t0 + uint32_t(tid), tb = ta + kT;
+            const bool va = ta < ntask, vb = tb < ntask;
+            const uint4 ca = va ? sum_pair(group_of[ta >> 4], ta & 15u) : make_uint4(0u, 0u, 0u, 0u);
+            const uint4 cb = vb ? sum_pair(group_of[tb >> 4], tb & 15u) : make_uint4(0u, 0u, 0u, 0u);
             if (va) add4(ta, ca);
             if (vb) add4(tb, cb);
         }
+        lds_barrier();
     }
-    __syncthreads();
     // ---- 2. block sums: four threads per 32-key block, eight keys each
     if (store_keys) {
         const uint32_t nunits = nslots * 8u;
@@ -690,7 +789,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             if (u < nunits && (u & 3u) == 0u) { bcnt[blk] = c8; bmass[blk] = m8; }
             if (ballot(bad) && lane == 0) atomicOr(&sh.flags, uint32_t(VI_FLAG_NONFINITE));
         }
-        __syncthreads();
+        lds_barrier();
     }
     // ---- 3. descending prefix sums over the 2048 blocks (thread t: blocks
     // 2047 - 2t and 2046 - 2t)
@@ -701,7 +800,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         const uint32_t ci = wave_incl_scan_u32(c0 + c1);
         const uint64_t mi = wave_incl_scan_u64(m0 + m1);
         if (lane == kWave - 1) { sh.scan[wave] = ci; sh.wmass[wave] = mi; }
-        __syncthreads();
+        lds_barrier();
         uint32_t cb = 0u;
         uint64_t mb = 0ull;
         for (int q = 0; q < wave; ++q) { cb += sh.scan[q]; mb += sh.wmass[q]; }
@@ -711,7 +810,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         cab[b0] = ce; mab[b0] = me;
         cab[b1] = ce + c0; mab[b1] = me + m0;
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t N = sh.total_cnt;
     const uint64_t Mtot = sh.total_mass;
     const uint32_t out_flags = sh.flags & (VI_FLAG_NONFINITE | VI_FLAG_BAD_HISTORY);
@@ -740,23 +839,18 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         const uint32_t lo = (kl.word & 1u) ? c.z : c.x, hi = (kl.word & 1u) ? c.w : c.y;
         return kl.hi ? hi : lo;
     };
-    // First block (descending) at which the cumulative count (mode 0: >=
-    // target) or fixed-point mass (mode 1: >= target, mode 2: > target) is
-    // reached; -1 if none.  All threads.
-    auto find_block = [&](int mode, uint64_t target) -> int {
-        if (tid == 0) sh.found = -1;
-        __syncthreads();
-        for (int b = tid; b < 2048; b += kT) {
-            bool hit = false;
-            if (bcnt[b]) {
-                if (mode == 0) hit = uint64_t(cab[b]) < target && uint64_t(cab[b]) + bcnt[b] >= target;
-                else if (mode == 1) hit = mab[b] < target && mab[b] + bmass[b] >= target;
-                else hit = mab[b] <= target && mab[b] + bmass[b] > target;
-            }
-            if (hit) atomicMax(&sh.found, b);
-        }
-        __syncthreads();
-        return sh.found;
+    // Wave 0: the first block (descending) at which the cumulative count
+    // (mode 0: >= target) or fixed-point mass (mode 1: >= target, mode 2: >
+    // target) is reached, searched over the blocks' running sums; -1 if none.
+    auto block_search = [&](int mode, uint64_t target) -> int {
+        if (mode == 1 && target == 0u) return -1;
+        const int i = wave_search(0, 2048, [&](int i) {
+            const int b = 2047 - i;
+            if (mode == 0) return uint64_t(cab[b]) + bcnt[b] >= target;
+            const uint64_t inc = mab[b] + bmass[b];
+            return mode == 1 ? inc >= target : inc > target;
+        });
+        return i < 2048 ? 2047 - i : -1;
     };
     struct Fine {
         bool found;
@@ -816,112 +910,101 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         *cnt = cab[b] + readlane_u(wave_incl_scan_u32(c), kWave - 1);
     };
 
-    // ---- 4. the decisions: the top-k cap, the min-p cut, the top-p cut, the
-    // support's end (the earliest of them) and the draw
-    const bool has_cap = p.top_k > 0 && uint32_t(p.top_k) < N;
-    if (has_cap) {
-        const int b = find_block(0, uint64_t(p.top_k));
-        if (wave == 0) {
+    // ---- 4. the decisions, in wave 0: the top-k cap, the min-p cut, the top-p
+    // cut, the support's end (the earliest of them) and the draw
+    if (wave == 0) {
+        const bool has_cap = p.top_k > 0 && uint32_t(p.top_k) < N;
+        uint32_t cap_key = 0u, cap_take = kTakeAll;
+        double s_cap = double(Mtot);
+        if (has_cap) {
+            const int b = block_search(0, uint64_t(p.top_k));
             const Fine f = fine_find(uint32_t(b), 0, uint64_t(p.top_k) - cab[b], 0u, kTakeAll);
             uint64_t m;
             uint32_t c;
             mass_through(f.key, f.take, &m, &c);
-            if (lane == 0) { sh.cap_key = f.key; sh.cap_take = f.take; sh.s_cap = double(m); }
+            cap_key = f.key;
+            cap_take = f.take;
+            s_cap = double(m);
         }
-    } else if (tid == 0) {
-        sh.s_cap = double(Mtot);
-    }
-    // min-p: the lowest key whose weight reaches min_p
-    if (wave == 1) {
-        uint32_t km = 0u;
+        // min-p: the lowest key whose weight reaches min_p
+        uint32_t minp_key = 0u;
         if (p.min_p > 0.0f) {
             const double mp = double(p.min_p);
-            km = uint32_t(wave_search(int(kmin), int(z0key) + 1, [&](int k) {
+            minp_key = uint32_t(wave_search(int(kmin), int(z0key) + 1, [&](int k) {
                 return key_weight<DT>(uint32_t(k), inv_t, z0) >= mp;
             }));
         }
-        if (lane == 0) sh.minp_key = km;
-    }
-    __syncthreads();
-    // top-p: the first position whose cumulative mass reaches top_p of the cap's
-    bool has_topp = false;
-    if (p.top_p < 1.0f) {
-        const uint64_t target = uint64_t(llrint(double(p.top_p) * sh.s_cap));
-        const int b = find_block(1, target);
-        const int lowest = has_cap ? int(sh.cap_key >> 5) : 0;
-        if (b >= lowest) {
-            if (wave == 0) {
-                const bool in_cap = has_cap && uint32_t(b) == (sh.cap_key >> 5);
-                const Fine f = fine_find(uint32_t(b), 1, target - mab[b], in_cap ? sh.cap_key : 0u,
-                                         in_cap ? sh.cap_take : kTakeAll);
-                if (lane == 0) { sh.topp_key = f.key; sh.topp_take = f.take; sh.found = f.found ? 1 : 0; }
+        // top-p: the first position whose cumulative mass reaches top_p of the cap's
+        bool has_topp = false;
+        uint32_t topp_key = 0u, topp_take = kTakeAll;
+        if (p.top_p < 1.0f) {
+            const uint64_t target = uint64_t(llrint(double(p.top_p) * s_cap));
+            const int b = block_search(1, target);
+            const int lowest = has_cap ? int(cap_key >> 5) : 0;
+            if (b >= lowest) {
+                const bool in_cap = has_cap && uint32_t(b) == (cap_key >> 5);
+                const Fine f = fine_find(uint32_t(b), 1, target - mab[b], in_cap ? cap_key : 0u,
+                                         in_cap ? cap_take : kTakeAll);
+                has_topp = f.found;
+                topp_key = f.key;
+                topp_take = f.take;
             }
-            __syncthreads();
-            has_topp = sh.found == 1;
         }
-    }
-    // the support's end, its mass, the uniform and the draw's target
-    if (wave == 0) {
+        // the support's end, its mass, the uniform and the draw's target
         bool all = true;
         uint32_t ek = 0u, et = kTakeAll;
         auto consider = [&](uint32_t k, uint32_t t) {
             if (all || k > ek || (k == ek && t < et)) { ek = k; et = t; all = false; }
         };
-        if (has_cap) consider(sh.cap_key, sh.cap_take);
-        if (p.min_p > 0.0f) consider(sh.minp_key, kTakeAll);
-        if (has_topp) consider(sh.topp_key, sh.topp_take);
+        if (has_cap) consider(cap_key, cap_take);
+        if (p.min_p > 0.0f) consider(minp_key, kTakeAll);
+        if (has_topp) consider(topp_key, topp_take);
         if (!all && ek > z0key) { ek = z0key; et = 1u; }   // no logit passes min-p: the best one
-        uint64_t m = Mtot;
-        uint32_t c = N;
-        if (!all) mass_through(ek, et, &m, &c);
-        if (lane == 0) {
-            sh.end_all = all ? 1u : 0u;
-            sh.end_key = all ? 0u : ek;
-            sh.end_take = all ? kTakeAll : et;
-            sh.s_n = double(m);
-            sh.n_support = c;
-            sh.u = philox_uniform(p.seed, p.lane, p.position, 0u);
-            sh.target = sh.u * double(m);
-        }
-    }
-    __syncthreads();
-    // the draw: the first support logit whose inclusive mass exceeds u * S_n
-    {
-        const uint64_t t = uint64_t(sh.target);
-        int b = find_block(2, t);
-        const int lowest = sh.end_all ? 0 : int(sh.end_key >> 5);
+        uint64_t sm = Mtot;
+        uint32_t sc = N;
+        if (!all) mass_through(ek, et, &sm, &sc);
+        const double u = philox_uniform(p.seed, p.lane, p.position, 0u);
+        const double target_d = u * double(sm);
+        // the draw: the first support logit whose inclusive mass exceeds u * S_n
+        const uint64_t t = uint64_t(target_d);
+        int b = block_search(2, t);
+        const int lowest = all ? 0 : int(ek >> 5);
         if (b < lowest) b = -1;
-        if (wave == 0) {
-            uint32_t dk = 0u, dr = 0u;
-            bool ok = false;
-            if (b >= 0) {
-                const bool in_end = !sh.end_all && uint32_t(b) == (sh.end_key >> 5);
-                const Fine f = fine_find(uint32_t(b), 2, t - mab[b], in_end ? sh.end_key : 0u,
-                                         in_end ? sh.end_take : kTakeAll);
-                if (f.found) { dk = f.key; dr = f.take - 1u; ok = true; }
-            }
-            if (!ok) {   // rounding past the support's last logit: that logit
-                for (int bb = lowest; bb < 2048 && !ok; ++bb) {
-                    if (!bcnt[bb]) continue;
-                    const uint32_t k = 32u * uint32_t(bb) + 31u - uint32_t(lane & 31);
-                    uint32_t c = block_key_count(uint32_t(bb));
-                    if (!sh.end_all) {
-                        if (k < sh.end_key) c = 0u;
-                        else if (k == sh.end_key) c = min(c, sh.end_take);
-                    }
-                    const uint64_t hm = ballot(c > 0u);
-                    if (hm) {
-                        const int L = 63 - __builtin_clzll(hm);
-                        dk = 32u * uint32_t(bb) + 31u - uint32_t(L);
-                        dr = readlane_u(c, L) - 1u;
-                        ok = true;
-                    }
+        uint32_t dk = 0u, dr = 0u;
+        bool ok = false;
+        if (b >= 0) {
+            const bool in_end = !all && uint32_t(b) == (ek >> 5);
+            const Fine f = fine_find(uint32_t(b), 2, t - mab[b], in_end ? ek : 0u, in_end ? et : kTakeAll);
+            if (f.found) { dk = f.key; dr = f.take - 1u; ok = true; }
+        }
+        if (!ok) {   // rounding past the support's last logit: that logit
+            for (int bb = lowest; bb < 2048 && !ok; ++bb) {
+                if (!bcnt[bb]) continue;
+                const uint32_t k = 32u * uint32_t(bb) + 31u - uint32_t(lane & 31);
+                uint32_t c = block_key_count(uint32_t(bb));
+                if (!all) {
+                    if (k < ek) c = 0u;
+                    else if (k == ek) c = min(c, et);
+                }
+                const uint64_t hm = ballot(c > 0u);
+                if (hm) {
+                    const int L = 63 - __builtin_clzll(hm);
+                    dk = 32u * uint32_t(bb) + 31u - uint32_t(L);
+                    dr = readlane_u(c, L) - 1u;
+                    ok = true;
                 }
             }
-            if (lane == 0) { sh.draw_key = dk; sh.draw_rank = dr; sh.ok = ok ? 1u : 0u; }
         }
-        __syncthreads();
+        if (lane == 0) {
+            sh.s_n = double(sm);
+            sh.n_support = sc;
+            sh.u = u;
+            sh.draw_key = dk;
+            sh.draw_rank = dr;
+            sh.ok = ok ? 1u : 0u;
+        }
     }
+    lds_barrier();
 
     // ---- 5. the part holding the drawn rank (parts in id order) and, for the
     // rescan, the drawn key's preimage under the count-1 penalty: a history
@@ -960,7 +1043,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
     }
     for (int i = tid; i < 2048; i += kT) flip[i] = 0u;
     if (tid == 0) sh.nflip = 0u;
-    __syncthreads();
+    lds_barrier();
 
     // ---- 6. the owner part read again: its orank-th logit (id order) whose
     // penalized key is the drawn key.  Repeated tokens whose count changes the
@@ -973,37 +1056,37 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
                                   2 * (size_t(row) * size_t(a.stride) + size_t(it.s0));
         const unsigned char* pb = pen ? pv.b1 + (it.s0 >> 3) : nullptr;
         static_assert(kMaxPartLen / 8 <= 8 * kT, "a part is at most 8 rounds");
+        // the part's logits and presence bytes, eight rounds of 1024 vectors,
+        // all requested before the flips are worked out
+        auto load_vec = [&](int v, uint4* d, uint32_t* b) {
+            const int vc = min(v, it.nvec - 1);
+            *d = load16_cached(vb + size_t(vc) * 16);
+            *b = pb ? uint32_t(pb[vc]) : 0u;
+        };
+        uint4 vv[8];
+        uint32_t bb[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) load_vec(k * kT + tid, &vv[k], &bb[k]);
         if (pen) {
-            const uint16_t* row16 = reinterpret_cast<const uint16_t*>(static_cast<const unsigned char*>(a.logits) +
-                                                                      2 * size_t(row) * size_t(a.stride));
-            for (uint32_t i0 = 0; i0 < pv.nrep; i0 += 2 * kT) {
-                uint2 e[2];
-                uint32_t raw[2];
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t i = i0 + uint32_t(j * kT + tid);
-                    e[j] = i < pv.nrep ? pv.list[i] : make_uint2(0u, 0u);
+            auto flip_if = [&](uint2 e, uint32_t raw) {
+                if (e.y < 2u || int(e.x) < it.s0 || int(e.x) >= it.s0 + it.n || !Elem<DT>::finite_bits(raw)) return;
+                const bool m1 = key16(pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast)) == dk;
+                const bool mc = key16(pen_pattern<DT>(raw, e.y, p, inv_r, rep_fast)) == dk;
+                if (m1 != mc) {
+                    const uint32_t off = e.x - uint32_t(it.s0);
+                    atomicOr(&flip[off >> 5], 1u << (off & 31u));
+                    atomicAdd(&sh.nflip, 1u);
                 }
+            };
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const bool in = e[j].y >= 2u && int(e[j].x) >= it.s0 && int(e[j].x) < it.s0 + it.n;
-                    raw[j] = in ? uint32_t(row16[e[j].x]) : 0x7fffu;
-                    if (!in) e[j].y = 0u;
-                }
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    if (e[j].y < 2u || !Elem<DT>::finite_bits(raw[j])) continue;
-                    const bool m1 = key16(pen_pattern<DT>(raw[j], 1u, p, inv_r, rep_fast)) == dk;
-                    const bool mc = key16(pen_pattern<DT>(raw[j], e[j].y, p, inv_r, rep_fast)) == dk;
-                    if (m1 != mc) {
-                        const uint32_t off = e[j].x - uint32_t(it.s0);
-                        atomicOr(&flip[off >> 5], 1u << (off & 31u));
-                        atomicAdd(&sh.nflip, 1u);
-                    }
-                }
+            for (int j = 0; j < 2; ++j)
+                if (uint32_t(j * kT + tid) < pv.nrep) flip_if(rep[j], repraw[j]);
+            for (uint32_t i = uint32_t(2 * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
+                const uint2 e = pv.list[i];
+                flip_if(e, uint32_t(row16[min(e.x, uint32_t(V - 1))]));
             }
         }
-        __syncthreads();
+        lds_barrier();
         // In the halves' key space (-0 just below +0): an absent token matches
         // when its key lies in [a0, a0 + w0] (the drawn key, with -0 for +0), a
         // history token when it lies in [a1, a1 + w1] (the preimage; none when
@@ -1033,51 +1116,38 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             if (flips) m ^= (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
             return m;
         };
-        // the part's logits and presence bytes, eight rounds of 1024 vectors
-        // (four rounds' loads in flight at a time); matches counted per round
-        auto load_vec = [&](int v, uint4* d, uint32_t* b) {
-            const int vc = min(v, it.nvec - 1);
-            *d = load16_cached(vb + size_t(vc) * 16);
-            *b = pb ? uint32_t(pb[vc]) : 0u;
-        };
+        // matches counted per round
         uint32_t cnt[8];
 #pragma unroll
-        for (int r0 = 0; r0 < 8; r0 += 4) {
-            uint4 vv[4];
-            uint32_t bb[4];
+        for (int r = 0; r < 8; ++r) {
+            const int v = r * kT + tid;
+            uint32_t c = 0u;
+            if (v < it.nvec) {
+                const uint32_t fl = flips ? (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu : 0u;
+                if (fl) {
+                    c = uint32_t(__builtin_popcount(match_bits(vv[r], bb[r], v)));
+                } else {
+                    const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
+                    uint32_t miss = 0u;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) load_vec((r0 + k) * kT + tid, &vv[k], &bb[k]);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int r = r0 + k, v = r * kT + tid;
-                uint32_t c = 0u;
-                if (v < it.nvec) {
-                    const uint32_t fl = flips ? (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu : 0u;
-                    if (fl) {
-                        c = uint32_t(__builtin_popcount(match_bits(vv[k], bb[k], v)));
-                    } else {
-                        const uint32_t w4[4] = {vv[k].x, vv[k].y, vv[k].z, vv[k].w};
-                        uint32_t miss = 0u;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            // presence of tokens 2q, 2q + 1 as a half mask
-                            const uint32_t M = (uint32_t(int32_t(bb[k] << (31 - 2 * q)) >> 31) & 0xffffu) |
-                                               (uint32_t(int32_t(bb[k] << (30 - 2 * q)) >> 31) & 0xffff0000u);
-                            const uint32_t k2 = halves_key(w4[q]);
-                            const uint32_t ma = halves_miss(k2, A0, W0);
-                            const uint32_t mp = empty1 ? 0x00010001u : halves_miss(k2, A1, W1);
-                            const uint32_t mm = (mp & M) | (ma & ~M);
-                            miss += (mm & 0xffffu) + (mm >> 16);
-                        }
-                        c = 8u - miss;
+                    for (int q = 0; q < 4; ++q) {
+                        // presence of tokens 2q, 2q + 1 as a half mask
+                        const uint32_t M = (uint32_t(int32_t(bb[r] << (31 - 2 * q)) >> 31) & 0xffffu) |
+                                           (uint32_t(int32_t(bb[r] << (30 - 2 * q)) >> 31) & 0xffff0000u);
+                        const uint32_t k2 = halves_key(w4[q]);
+                        const uint32_t ma = halves_miss(k2, A0, W0);
+                        const uint32_t mp = empty1 ? 0x00010001u : halves_miss(k2, A1, W1);
+                        const uint32_t mm = (mp & M) | (ma & ~M);
+                        miss += (mm & 0xffffu) + (mm >> 16);
                     }
+                    c = 8u - miss;
                 }
-                cnt[r] = c;
-                const uint32_t incl = wave_incl_scan_u32(c);
-                if (lane == kWave - 1) sh.wtot[r][wave] = incl;
             }
+            cnt[r] = c;
+            const uint32_t incl = wave_incl_scan_u32(c);
+            if (lane == kWave - 1) sh.wtot[r][wave] = incl;
         }
-        __syncthreads();
+        lds_barrier();
         // exclusive offsets of the (round, wave) blocks in id order (wave 0:
         // lane l holds blocks 2l and 2l + 1 of the 128)
         if (wave == 0) {
@@ -1086,22 +1156,19 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             sh.wtot[(2 * lane) >> 4][(2 * lane) & 15] = incl - b0 - b1;
             sh.wtot[(2 * lane + 1) >> 4][(2 * lane + 1) & 15] = incl - b1;
         }
-        __syncthreads();
+        lds_barrier();
         const uint32_t want = sh.orank;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const uint32_t e = sh.wtot[r][wave] + wave_incl_scan_u32(cnt[r]) - cnt[r];
             if (cnt[r] && want >= e && want < e + cnt[r]) {
                 const int v = r * kT + tid;
-                uint4 d;
-                uint32_t b;
-                load_vec(v, &d, &b);
-                uint32_t m = match_bits(d, b, v);
+                uint32_t m = match_bits(vv[r], bb[r], v);
                 for (uint32_t k = want - e; k > 0u; --k) m &= m - 1u;
                 sh.token = it.s0 + 8 * v + __builtin_ctz(m);
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // ---- 7. outputs
@@ -1234,7 +1301,8 @@ static StreamPlan stream_plan(int rows, int vocabulary) {
     int parts = (vocabulary + kMaxPartLen - 1) / kMaxPartLen;
     const int fill = (cus + std::max(rows, 1) - 1) / std::max(rows, 1);   // parts that give every CU one
     parts = std::max(parts, std::min(kMaxParts, fill));
-    const int len = ((vocabulary + parts - 1) / parts + 7) / 8 * 8;
+    // a multiple of 32 tokens: every part's presence bytes start 4-byte aligned
+    const int len = ((vocabulary + parts - 1) / parts + 31) / 32 * 32;
     return {(vocabulary + len - 1) / len, len};
 }
 static int hist_words(int vocabulary) { return (vocabulary + 31) / 32; }
@@ -1244,11 +1312,28 @@ static bool hist_fits(int vocabulary, int64_t max_history) {
            2 * int64_t(hist_words(vocabulary)) + hist_cap(max_history) <= kHistLdsWords;
 }
 
+// The stream launch: workgroups, XCD-aware mapping, and the most parts one
+// workgroup takes (its XCD's parts shared out in turn).
+struct StreamGrid {
+    int grid, xcd, per_wg;
+};
+static StreamGrid stream_grid(int rows, int parts) {
+    StreamGrid g;
+    const int items = rows * parts;
+    g.grid = std::min(device_cus(), items);
+    g.xcd = (rows >= kXcds && g.grid % kXcds == 0) ? 1 : 0;
+    const int xr = g.xcd ? (rows + kXcds - 1) / kXcds : rows, xw = g.xcd ? g.grid / kXcds : g.grid;
+    g.per_wg = (xr * parts + xw - 1) / xw;
+    return g;
+}
+
 bool stream_supported(const SampleArgs& s) {
     if (s.dtype != VI_BF16 && s.dtype != VI_F16) return false;
     if (s.probs || s.full_out || s.rows <= 0) return false;
     if (s.vocabulary <= 0 || s.vocabulary % 8 || s.vocabulary > kMaxParts * kMaxPartLen) return false;
     if (s.stride < s.vocabulary || s.stride % 8 || reinterpret_cast<uintptr_t>(s.logits) % 16) return false;
+    if (int64_t(s.rows) * kMaxParts > (int64_t(1) << 30)) return false;
+    if (stream_grid(s.rows, stream_plan(s.rows, s.vocabulary).parts).per_wg > kMaxItems) return false;
     const bool hist = !s.pstate && s.histories && s.offsets && s.max_history > 0;
     if (hist && !hist_fits(s.vocabulary, s.max_history)) return false;
     return true;
@@ -1293,20 +1378,23 @@ vi_status launch_stream(const SampleArgs& s, unsigned char* ws, size_t ws_bytes,
         a.hb1 = h.hb1; a.hlist = h.hlist; a.hhead = h.hhead; a.hwords = h.words; a.hcap = h.cap;
     }
     if (!c.ok) return VI_ERR_WORKSPACE;
-    const int items = s.rows * pl.parts;
-    a.grid = std::min(device_cus(), items);
-    a.xcd = (s.rows >= kXcds && a.grid % kXcds == 0) ? 1 : 0;
+    const StreamGrid sg = stream_grid(s.rows, pl.parts);
+    a.grid = sg.grid;
+    a.xcd = sg.xcd;
     if (hist) {
         hipLaunchKernelGGL(history_view_kernel, dim3(s.rows), dim3(kT), 0, stream, h);
         if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
     }
     // the merge's workgroup of row r runs on the XCD whose workgroups streamed
     // the row (workgroup r goes to XCD r % 8, as the stream's rows do)
+    const bool pb = a.pstate || a.hb1;
     if (s.dtype == VI_BF16) {
-        hipLaunchKernelGGL(stream_kernel<VI_BF16>, dim3(a.grid), dim3(kT), 0, stream, a);
+        if (pb) hipLaunchKernelGGL((stream_kernel<VI_BF16, true>), dim3(a.grid), dim3(kT), 0, stream, a);
+        else hipLaunchKernelGGL((stream_kernel<VI_BF16, false>), dim3(a.grid), dim3(kT), 0, stream, a);
         hipLaunchKernelGGL(merge_kernel<VI_BF16>, dim3(s.rows), dim3(kT), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(stream_kernel<VI_F16>, dim3(a.grid), dim3(kT), 0, stream, a);
+        if (pb) hipLaunchKernelGGL((stream_kernel<VI_F16, true>), dim3(a.grid), dim3(kT), 0, stream, a);
+        else hipLaunchKernelGGL((stream_kernel<VI_F16, false>), dim3(a.grid), dim3(kT), 0, stream, a);
         hipLaunchKernelGGL(merge_kernel<VI_F16>, dim3(s.rows), dim3(kT), 0, stream, a);
     }
     return launch_status();

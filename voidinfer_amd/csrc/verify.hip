@@ -25,6 +25,7 @@
 // rows' supports, and the correction walks the target softmax, the draft q and
 // their residual over the whole vocabulary in id order (ranges of 16,384
 // tokens summed in parallel, then the crossing range scanned again).
+#include <algorithm>
 #include <math.h>
 
 #include "vi_device.h"
@@ -763,11 +764,19 @@ void launch_full_verify_d(const FullVerifyArgs& f, hipStream_t stream) {
 }
 }  // namespace
 
+// The greedy launch's workspace: arrival counters for v.trows rows (the
+// bonus row's count) ahead of the partials of either row count.
+static size_t verify_greedy_bytes(const VerifyLayout& v, int lanes, int drafts, int vocabulary) {
+    const size_t with = greedy_workspace(v.trows, vocabulary), without = greedy_workspace(lanes * drafts, vocabulary);
+    if (!with && !without) return 0;
+    return align_up(size_t(v.trows) * 4, 256) + std::max(with, without);
+}
+
 size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     const VerifyLayout v = verify_layout(lanes, drafts, vocabulary);
     size_t b = align_up(size_t(v.trows) * sizeof(vi_greedy_row), 256);
     b += 2 * align_up(size_t(v.trows + v.drows) * kMaxK * 4, 256) + 2 * align_up(size_t(v.trows + v.drows) * 4, 256);
-    b += align_up(greedy_workspace(v.trows, vocabulary), 256);
+    b += align_up(verify_greedy_bytes(v, lanes, drafts, vocabulary), 256);
     b += topk_partials_bytes_slices(v.lrows, v.lslices);
     b += align_up(size_t(v.trows) * sizeof(PosDecision), 256) + align_up(size_t(lanes) * 4, 256);
     b += full_verify_bytes(lanes, drafts, vocabulary);
@@ -792,7 +801,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     uint32_t* dflags = c.take<uint32_t>(size_t(v.drows));
     PosDecision* dec = c.take<PosDecision>(size_t(v.trows));
     uint32_t* larr = c.take<uint32_t>(size_t(a.lanes));   // positions of a lane decided (zero between calls)
-    const size_t gbytes = greedy_workspace(v.trows, a.vocabulary);
+    const size_t gbytes = verify_greedy_bytes(v, a.lanes, a.drafts, a.vocabulary);
     unsigned char* gws = gbytes ? c.take<unsigned char>(gbytes) : nullptr;
     const size_t lbytes = topk_partials_bytes_slices(v.lrows, v.lslices);
     unsigned char* lws = c.take<unsigned char>(lbytes);
@@ -800,11 +809,10 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     const int threads = 64, blocks = (a.lanes + threads - 1) / threads;
     vi_status st;
     if (a.mode == VI_VERIFY_GREEDY) {
-        // the greedy workspace is carved for v.trows rows; a launch over fewer
-        // rows (no bonus row) uses a prefix of the same arrival counters, which
-        // the greedy launcher carves ahead of its partials.
+        // the greedy workspace is carved for v.trows rows (with the bonus row):
+        // its arrival counters stay where they are for either row count
         st = launch_greedy(a.target, a.target_dtype, trows, a.vocabulary, a.target_stride, 0, grows, gws, gbytes,
-                           stream);
+                           stream, v.trows);
         if (st != VI_OK) return st;
         hipLaunchKernelGGL(verify_greedy_kernel, dim3(blocks), dim3(threads), 0, stream, grows, a.lanes, a.drafts,
                            a.target_rows, a.drafted, a.terminal, a.n_terminal, a.accepted, a.committed,

@@ -33,9 +33,11 @@ struct GreedyPlan {
 };
 GreedyPlan greedy_plan(int rows, int vocabulary);
 size_t greedy_workspace(int rows, int vocabulary);
+// arrival_rows: the rows the workspace was carved for (its arrival counters
+// come first, that many; 0: rows).
 vi_status launch_greedy(const void* logits, int dtype, int rows, int vocabulary, int64_t stride,
                         uint64_t serial, vi_greedy_row* out, void* ws, size_t ws_bytes,
-                        hipStream_t stream);
+                        hipStream_t stream, int arrival_rows = 0);
 // Allocation-free greedy: the workspace is a 64 KiB device array of the library
 // (every shape's greedy workspace fits it), its per-device address looked up by
 // greedy_scratch_setup (vi_init, or the first call on a device).
