@@ -86,4 +86,47 @@ __device__ __forceinline__ void state_publish(const LaneState& s, int slot) {
                               __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A sampler recording its row's token: the one writer of the lane's state in
+// its launch, after every read of it.  Plain loads, issued together (the
+// first probe's entry and repeat index, the presence word, the header), then
+// plain stores: the state_apply(+1) / state_publish result without their
+// chain of returning atomics.
+__device__ inline void state_record_one(const LaneState& s, const PenaltyLayout& l, int vocabulary, int32_t t) {
+    if (t < 0 || t >= vocabulary) {
+        s.hdr->flags |= uint32_t(VI_FLAG_BAD_HISTORY);
+        return;
+    }
+    const uint32_t key = uint32_t(t) + 1u, bit = 1u << (t & 31);
+    uint32_t slot = (uint32_t(t) * 0x9E3779B1u) >> l.shift;
+    uint2 e = s.table[slot];
+    uint32_t ridx = s.ridx[slot];
+    const uint32_t word = s.b1[t >> 5];
+    uint32_t keys = s.hdr->keys, nrep = s.hdr->nrep;
+    const uint64_t total = s.hdr->total;
+    for (int probe = 1; e.x != 0u && e.x != key; ++probe) {   // (collisions: rare)
+        if (probe >= l.slots) {
+            s.hdr->flags |= uint32_t(VI_FLAG_ERROR);
+            return;
+        }
+        slot = (slot + 1u) & uint32_t(l.slots - 1);
+        e = s.table[slot];
+        ridx = s.ridx[slot];
+    }
+    if (e.x == 0u) {
+        s.table[slot].x = key;
+        s.hdr->keys = keys + 1u;
+    }
+    const uint32_t old = e.y;
+    s.table[slot].y = old + 1u;
+    if (old == 0u) s.b1[t >> 5] = word | bit;
+    if (old == 1u && ridx == 0u) {   // first repeat since the reset
+        s.list[nrep] = make_uint2(uint32_t(t), 2u);
+        s.ridx[slot] = nrep + 1u;
+        s.hdr->nrep = nrep + 1u;
+    } else if (ridx) {
+        s.list[ridx - 1u].y = old + 1u;
+    }
+    s.hdr->total = total + 1u;
+}
+
 }  // namespace vi

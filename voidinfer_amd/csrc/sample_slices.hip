@@ -1153,7 +1153,7 @@ __device__ __forceinline__ void merge_row(const SliceArgs& a, int row, const vi_
             write_row(a, row, tok, sh.u, out_flags, sh.n_support, N, sh.s_n);
             if (a.record && tok < V) {   // (the slice pass, an earlier launch, has read the state)
                 const LaneState ls = lane_state(a.pstate + size_t(row) * a.pl.lane_bytes, a.pl);
-                state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
+                state_record_one(ls, a.pl, V, tok);
             }
         }
         if (a.want_bounds)

@@ -1197,7 +1197,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             if (a.record && a.pstate && tok < V) {
                 const LaneState ls = lane_state(const_cast<unsigned char*>(a.pstate) + size_t(row) * a.pl.lane_bytes,
                                                 a.pl);
-                state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
+                state_record_one(ls, a.pl, V, tok);
             }
         }
     }

@@ -938,7 +938,7 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
             write_row(a, row, tok, u, out_flags, n_sup, N, s_n);
             if (a.record && a.pstate && tok < V) {   // (the slice pass, an earlier launch, has read the state)
                 const LaneState ls = lane_state(a.pstate + size_t(row) * a.pl.lane_bytes, a.pl);
-                state_publish(ls, state_apply(ls, a.pl, V, tok, 1));
+                state_record_one(ls, a.pl, V, tok);
             }
         }
         if (a.want_bounds)

@@ -1189,7 +1189,7 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
                 const int32_t t = a.tokens[r];
                 if (t >= 0 && t < a.vocabulary) {
                     const LaneState ls = lane_state(a.pstate + size_t(r) * a.pl.lane_bytes, a.pl);
-                    state_publish(ls, state_apply(ls, a.pl, a.vocabulary, t, 1));
+                    state_record_one(ls, a.pl, a.vocabulary, t);
                 }
             }
         }
