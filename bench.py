@@ -453,36 +453,38 @@ def main():
     gpu_tok = tokens.cpu().numpy().copy()
 
     def timed(fn, K, warmup):
+        """K steps back to back, HIP events on the launch stream at both ends of
+        the timed region only (an event between steps would add its own packet
+        to every step): per-step GPU time and host wall time."""
         for i in range(warmup):
             st = fn(i)
             assert st == 0, st
         torch.cuda.synchronize()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        start.record(stream)
         for i in range(K):
-            starts[i].record(stream)
             fn(i)
-            ends[i].record(stream)
+        end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per_launch = np.array([starts[i].elapsed_time(ends[i]) for i in range(K)])
-        return starts[0].elapsed_time(ends[-1]) / K, per_launch, wall
+        return start.elapsed_time(end) / K, wall
 
     K = args.steps
     print(f"[bench] timing {K} steps ({args.route} route)", file=sys.stderr, flush=True)
-    ms_per_step, per_launch_ms, wall = timed(step, K, args.warmup)
+    ms_per_step, wall = timed(step, K, args.warmup)
     rows_per_s = rows / (ms_per_step / 1e3)
-    kernel_ms = float(per_launch_ms.mean())
+    # the steps run back to back on one stream, so the GPU time per step is the
+    # call's kernel time (its two launches and the gap between them)
+    kernel_ms = ms_per_step
     bytes_per_launch = rows * bytes_per_row
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
     history_route = None
     if args.route == "state" and args.compare_steps > 0:
         print(f"[bench] timing {args.compare_steps} steps of the history route", file=sys.stderr, flush=True)
-        h_ms, h_launch, _ = timed(hist_step, args.compare_steps, 20)
+        h_ms, _ = timed(hist_step, args.compare_steps, 20)
         history_route = {"ms_per_step": h_ms, "rows_per_s": rows / (h_ms / 1e3),
-                         "kernel_ms": float(h_launch.mean()),
+                         "kernel_ms": h_ms,
                          "bytes_per_launch": rows * (VOCAB * 2 + HISTORY * 4), "steps": args.compare_steps}
 
     # stream-read probe (measured HBM read rate) over a 1 GiB buffer
@@ -544,11 +546,10 @@ def main():
                                "rep/presence/frequency penalties over 32,768-token histories, Philox per row",
                    "rows": rows, "vocabulary": VOCAB, "history": HISTORY, "input_sets": SETS,
                    "route": args.route, "penalty_state": state_info,
-                   "kernel": "slice_kernel<bf16> + merge_kernel<bf16> (voidinfer_amd/csrc/sample_slices.hip)"},
+                   "kernel": "stream_kernel<bf16> + merge_kernel<bf16> (voidinfer_amd/csrc/sample_stream.hip)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBPS, "traffic": traffic_from_profiles(args.route),
                      "bytes_per_launch": bytes_per_launch, "kernel_ms": kernel_ms,
-                     "kernel_ms_p50": float(np.median(per_launch_ms)),
                      "probe_read_gbps": probe_gbps, "frac_of_probe": achieved / probe_gbps},
         "history_route": history_route,
         "cpu_baseline": cpu,

@@ -625,20 +625,17 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
 
     // ---- 0. the parts' occupancy bitmaps; the valid key range
     for (int i = tid; i < P * 32; i += kT) pbits[i] = a.ppub[(pi0 + i / 32) * kPub + i % 32];
-    // The first repeat entries (two per thread) and their logits, requested
-    // now (reads within the list and the row whatever the entries hold): the
-    // flips after the draw are then arithmetic.
+    // The first repeat entries (two per thread), requested now (reads within
+    // the list whatever it holds); their logits are gathered once the owner
+    // part is known, for the entries inside it only.
     const uint16_t* row16 = reinterpret_cast<const uint16_t*>(static_cast<const unsigned char*>(a.logits) +
                                                               2 * size_t(row) * size_t(a.stride));
     uint2 rep[2];
-    uint32_t repraw[2];
     {
         const uint2* rl = pv.pen ? pv.list : reinterpret_cast<const uint2*>(a.params);
         const uint32_t rn = pv.pen ? max(pv.nrep, 1u) : 1u;
 #pragma unroll
         for (int j = 0; j < 2; ++j) rep[j] = rl[min(uint32_t(j * kT + tid), rn - 1u)];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) repraw[j] = row16[min(rep[j].x, uint32_t(V - 1))];
     }
     if (wave == 1) {
         const uint32_t km = valid_key_range<DT>(p.temperature);
@@ -1068,8 +1065,9 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) load_vec(k * kT + tid, &vv[k], &bb[k]);
         if (pen) {
+            auto in_owner = [&](uint2 e) { return e.y >= 2u && int(e.x) >= it.s0 && int(e.x) < it.s0 + it.n; };
             auto flip_if = [&](uint2 e, uint32_t raw) {
-                if (e.y < 2u || int(e.x) < it.s0 || int(e.x) >= it.s0 + it.n || !Elem<DT>::finite_bits(raw)) return;
+                if (!in_owner(e) || !Elem<DT>::finite_bits(raw)) return;
                 const bool m1 = key16(pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast)) == dk;
                 const bool mc = key16(pen_pattern<DT>(raw, e.y, p, inv_r, rep_fast)) == dk;
                 if (m1 != mc) {
@@ -1078,12 +1076,17 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
                     atomicAdd(&sh.nflip, 1u);
                 }
             };
+            uint32_t raw[2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (uint32_t(j * kT + tid) < pv.nrep) flip_if(rep[j], repraw[j]);
+            for (int j = 0; j < 2; ++j) {
+                if (uint32_t(j * kT + tid) >= pv.nrep) rep[j].y = 0u;
+                raw[j] = in_owner(rep[j]) ? uint32_t(row16[rep[j].x]) : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) flip_if(rep[j], raw[j]);
             for (uint32_t i = uint32_t(2 * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
                 const uint2 e = pv.list[i];
-                flip_if(e, uint32_t(row16[min(e.x, uint32_t(V - 1))]));
+                if (in_owner(e)) flip_if(e, uint32_t(row16[e.x]));
             }
         }
         lds_barrier();
