@@ -1237,24 +1237,39 @@ __global__ __launch_bounds__(kT) void history_view_kernel(HistArgs h) {
     if (tid == 0) flags = 0u;
     __syncthreads();
     const int V = h.vocabulary;
-    auto pass = [&](auto&& fn) {
-        for (int64_t base = b; base < e; base += int64_t(kHistBatch) * kT) {
-            int32_t t[kHistBatch];
+    // The history in batches of kHistBatch tokens per thread (one batch for
+    // up to 32,768 tokens, kept in registers for the second pass).  Each pass
+    // issues a batch's LDS operations back to back and uses their results
+    // after, so their latencies overlap.
+    const bool one_batch = e - b <= int64_t(kHistBatch) * kT;
+    int32_t t[kHistBatch];
+    auto load = [&](int64_t base) {
 #pragma unroll
-            for (int j = 0; j < kHistBatch; ++j) {
-                const int64_t i = base + int64_t(j) * kT + tid;
-                t[j] = i < e ? h.histories[i] : -1;
-            }
-#pragma unroll
-            for (int j = 0; j < kHistBatch; ++j)
-                if (base + int64_t(j) * kT + tid < e) fn(t[j]);
+        for (int j = 0; j < kHistBatch; ++j) {
+            const int64_t i = base + int64_t(j) * kT + tid;
+            t[j] = i < e ? h.histories[i] : -2;   // (-2: past the end)
         }
     };
-    pass([&](int32_t t) {
-        if (t < 0 || t >= V) { flags = VI_FLAG_BAD_HISTORY; return; }
-        const uint32_t bit = 1u << (t & 31);
-        if (atomicOr(&B1[t >> 5], bit) & bit) atomicOr(&B2[t >> 5], bit);
-    });
+    for (int64_t base = b; base < e; base += int64_t(kHistBatch) * kT) {
+        load(base);
+#pragma unroll
+        for (int j0 = 0; j0 < kHistBatch; j0 += kHistBatch / 2) {
+            uint32_t old[kHistBatch / 2];
+#pragma unroll
+            for (int j = 0; j < kHistBatch / 2; ++j) {
+                const int32_t tj = t[j0 + j];
+                old[j] = 0u;
+                if (tj >= 0 && tj < V) old[j] = atomicOr(&B1[tj >> 5], 1u << (tj & 31));
+                else if (tj != -2) flags = VI_FLAG_BAD_HISTORY;
+            }
+#pragma unroll
+            for (int j = 0; j < kHistBatch / 2; ++j) {
+                const int32_t tj = t[j0 + j];
+                const uint32_t bit = 1u << (tj & 31);
+                if (tj >= 0 && tj < V && (old[j] & bit)) atomicOr(&B2[tj >> 5], bit);
+            }
+        }
+    }
     __syncthreads();
     // B1 out; its LDS then holds the B2 rank of each word's first bit
     uint32_t* out = h.hb1 + size_t(row) * W;
@@ -1274,11 +1289,25 @@ __global__ __launch_bounds__(kT) void history_view_kernel(HistArgs h) {
     }
     for (uint32_t i = tid; i < total; i += kT) cnt[i] = 0u;
     __syncthreads();
-    pass([&](int32_t t) {
-        if (t < 0 || t >= V) return;
-        const uint32_t wd = B2[t >> 5], bit = 1u << (t & 31);
-        if (wd & bit) atomicAdd(&cnt[B1[t >> 5] + uint32_t(__builtin_popcount(wd & (bit - 1u)))], 1u);
-    });
+    for (int64_t base = b; base < e; base += int64_t(kHistBatch) * kT) {
+        if (!one_batch) load(base);
+#pragma unroll
+        for (int j0 = 0; j0 < kHistBatch; j0 += kHistBatch / 2) {   // (half a batch at a time: registers)
+            uint32_t wd[kHistBatch / 2], r0[kHistBatch / 2];
+#pragma unroll
+            for (int j = 0; j < kHistBatch / 2; ++j) {
+                const int32_t tj = t[j0 + j];
+                const bool ok = tj >= 0 && tj < V;
+                wd[j] = ok ? B2[tj >> 5] : 0u;
+                r0[j] = ok ? B1[tj >> 5] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < kHistBatch / 2; ++j) {
+                const uint32_t bit = 1u << (t[j0 + j] & 31);
+                if (wd[j] & bit) atomicAdd(&cnt[r0[j] + uint32_t(__builtin_popcount(wd[j] & (bit - 1u)))], 1u);
+            }
+        }
+    }
     __syncthreads();
     uint2* lst = h.hlist + size_t(row) * h.cap;
     for (int i = w0; i < w1; ++i) {
