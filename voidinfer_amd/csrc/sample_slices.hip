@@ -532,15 +532,15 @@ __device__ __forceinline__ uint32_t id_order_prefix(const uint32_t cnt[kSeg], ui
         if (lane == kWave - 1) sh.segs[wave][g] = incl[g];
     }
     __syncthreads();
+    // per segment: lane w holds wave w's count, one wave scan gives every
+    // wave its offset (two values per segment in registers, not kW)
     uint32_t total = 0u;
 #pragma unroll
     for (int g = 0; g < kSeg; ++g) {
-        uint32_t waves_before = 0u, seg_total = 0u;
-        for (int w = 0; w < kW; ++w) {
-            const uint32_t t = sh.segs[w][g];
-            seg_total += t;
-            if (w < wave) waves_before += t;
-        }
+        const uint32_t t = lane < kW ? sh.segs[lane][g] : 0u;
+        const uint32_t iw = wave_incl_scan_u32(t);
+        const uint32_t waves_before = uint32_t(__builtin_amdgcn_readlane(int(iw - t), wave));
+        const uint32_t seg_total = uint32_t(__builtin_amdgcn_readlane(int(iw), kW - 1));
         excl[g] = total + waves_before + incl[g] - cnt[g];
         total += seg_total;
     }
@@ -1647,9 +1647,12 @@ template <int DT>
 __global__ __launch_bounds__(kT) void slice_probs_kernel(SliceArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
     __shared__ Shared sh;
-    const int tid = threadIdx.x, w = blockIdx.x, S = a.slices;
+    const int w = blockIdx.x, S = a.slices;
     int row = 0, s = 0;
     for (int k = 0; item_of(a, w, k, &row, &s); ++k) {
+        // (the thread index laundered per item: values derived from it stay
+        // in the loop instead of being hoisted out of it and spilled)
+        const int tid = opaque_tid();
         const vi_row_params p = a.params[row];
         if (!full_route_row(p)) continue;
         const RowBound bd = a.bounds[row];
