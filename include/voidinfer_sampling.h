@@ -158,8 +158,11 @@ vi_status vi_topk_rows(const void* logits, int dtype, int rows, int vocabulary,
  * fp16 rows [rows][vocab] (stride vocab) into ids / values [rows][16].  Like
  * the reference's, its scratch is the library's: allocated and zero-filled on
  * the first call on a device (again, larger, when a larger shape comes) and
- * kept until the process ends, so calls on one device must be ordered on one
- * stream.  rows 0 is a no-op. */
+ * kept until the process ends.  Calls on one device share that scratch (its
+ * self-resetting counters too), so they must be ordered on one stream; the
+ * library holds a lock from the choice of the buffer to the launch, so a call
+ * from another thread that grows it cannot free it under a queued launch.
+ * rows 0 is a no-op. */
 vi_status vi_topk16_for_test(const uint16_t* logits, int rows, int vocab, int64_t* ids, float* values,
                              uint32_t* nonfinite_flag, void* stream);
 

@@ -97,21 +97,19 @@ vi_status vi_topk16_for_test(const uint16_t* logits, int rows, int vocab, int64_
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return VI_ERR_DEVICE;
     const size_t need = topk_partials_bytes(rows, vocab);
-    void* ws = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(guard);
-        Owned& o = owned[dev];
-        if (o.bytes < need) {
-            if (o.ptr && hipFree(o.ptr) != hipSuccess) return VI_ERR_LAUNCH;   // (waits for the device)
-            o.ptr = nullptr;
-            o.bytes = 0;
-            if (hipMalloc(&o.ptr, need) != hipSuccess) return VI_ERR_LAUNCH;
-            if (hipMemset(o.ptr, 0, need) != hipSuccess) return VI_ERR_LAUNCH;
-            o.bytes = need;
-        }
-        ws = o.ptr;
+    // held until the launch is queued: another thread cannot grow (free) the
+    // buffer between this call's choice of it and its launch
+    std::lock_guard<std::mutex> lock(guard);
+    Owned& o = owned[dev];
+    if (o.bytes < need) {
+        if (o.ptr && hipFree(o.ptr) != hipSuccess) return VI_ERR_LAUNCH;   // (waits for the device)
+        o.ptr = nullptr;
+        o.bytes = 0;
+        if (hipMalloc(&o.ptr, need) != hipSuccess) return VI_ERR_LAUNCH;
+        if (hipMemset(o.ptr, 0, need) != hipSuccess) return VI_ERR_LAUNCH;
+        o.bytes = need;
     }
-    return launch_topk_rows(logits, VI_F16, rows, vocab, vocab, 16, ids, values, nullptr, nonfinite_flag, ws, need,
+    return launch_topk_rows(logits, VI_F16, rows, vocab, vocab, 16, ids, values, nullptr, nonfinite_flag, o.ptr, need,
                             as_stream(stream));
 }
 
