@@ -33,6 +33,7 @@
 
 #include "penalty_state.h"
 #include "row_scan.h"
+#include "verify_decide.h"
 #include "vi_internal.h"
 
 namespace vi {
@@ -40,7 +41,6 @@ namespace {
 
 constexpr int kTopkThreads = 256;
 constexpr int kTopkWaves = kTopkThreads / kWave;
-constexpr int kMaxK = 64;
 constexpr int kInvalidId = 0x7fffffff;
 
 struct SliceHeader {
@@ -102,6 +102,10 @@ struct TopkArgs {
     uint32_t* lvalid;       // [rows]
     uint32_t* lflags;       // [rows]
     int skip_unlisted;      // rows of lanes without a top-k list are left to the full-vocabulary path
+    // kModeVerify over the draft rows with the decisions taken as the rows
+    // finish (decide != 0; larr: the lanes' arrival counters, zero between calls)
+    int decide;
+    VerifyDecideArgs dv;
 };
 
 // ----------------------------------------------------------- wave-resident list
@@ -980,29 +984,24 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         cand_vec(dv[3], 3, okv[3], vm[3]);
         if (fill) flush();
     };
-    if constexpr (MODE == kModeTopk) {
-        scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
-    } else if constexpr (MODE == kModeVerify) {
-        scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
-    } else if constexpr (MODE == kModeSample) {
-        if (batched)
-            scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
-        else
-            scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
-    } else {
-        scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
-    }
-
-    // ---- merge the wave lists in LDS
-    __shared__ float s_val[kTopkWaves][kMaxK];
-    __shared__ int s_idx[kTopkWaves][kMaxK];
+    // ---- held scan (top-k and verification modes, 16-bit rows whose slice
+    // gives each lane at most kHeld vectors).  Every vector of the lane is
+    // requested at once and kept in registers, and the scan is one light pass
+    // per vector: its maximum (NaN-propagating packed f16 / f32 maxima) and a
+    // running minimum; the log-sum-exp is one exp per logit against the lane's
+    // own maximum.  A workgroup with a NaN or an infinity (or, in verification,
+    // a logit whose scaled value overflows) takes the exact path, vec_exact
+    // vector by vector into the wave lists.  Otherwise the gate is the largest
+    // of the four waves' K-th largest lane maxima (distinct logits: at least K
+    // logits of the slice reach it, and every logit of the slice's top K does);
+    // the vectors whose maximum reaches it are staged in LDS, one per lane,
+    // their logits that reach it are pooled for the workgroup, and each pooled
+    // logit's rank among them (value desc, id asc) places the slice's top K.
+    // per-wave partials of the slice header (flags, finite count, log-sum-exp)
     __shared__ uint32_t s_flags[kTopkWaves], s_valid[kTopkWaves];
     __shared__ float s_lm[kTopkWaves];
     __shared__ double s_ls[kTopkWaves];
-    s_val[wave][lane] = L.v;
-    s_idx[wave][lane] = L.i;
-    // wave reductions of flags / valid / lse
-    {
+    auto wave_partials = [&]() {
         uint32_t f = flags;
 #pragma unroll
         for (int o = 32; o; o >>= 1) f |= shfl_xor_u(f, o);
@@ -1016,9 +1015,231 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
 #pragma unroll
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) { s_flags[wave] = f; s_valid[wave] = c; s_lm[wave] = m; s_ls[wave] = s; }
+    };
+    constexpr int kHeld = 16;
+    constexpr int kPool = 256;
+    __shared__ uint4 s_hv[kTopkWaves][kWave];
+    __shared__ int s_hid[kTopkWaves][kWave];
+    __shared__ float s_pv[kPool];
+    __shared__ int s_pi[kPool];
+    __shared__ float s_selv[kMaxK];
+    __shared__ int s_seli[kMaxK];
+    __shared__ float s_tw[kTopkWaves];
+    __shared__ int s_np, s_over;
+    bool pooled = false;   // (workgroup-uniform) the slice's top K is wave 0's list
+    // (16-bit vector rows; bf16 rows in top-k mode keep the batch scan: their
+    // held scan with the log-sum-exp does not fit 128 registers)
+    constexpr bool kHeldMode = VEC && (DT == VI_F16 || (DT == VI_BF16 && MODE == kModeVerify));
+    auto held_scan = [&](int nvec) {
+      if constexpr (kHeldMode) {
+        constexpr int P = Elem<DT>::kPerVec;
+        typedef _Float16 h2t __attribute__((ext_vector_type(2)));
+        auto H = [](uint32_t w) { return __builtin_bit_cast(h2t, w); };
+        const int tid = int(threadIdx.x);
+        const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * 2;
+        // (unconditional loads at clamped in-bounds addresses: past the end a
+        // lane reads the slice's last vector again and leaves it out below)
+        uint4 d[kHeld];
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) d[u] = load16(base + size_t(min(u * kTopkThreads + tid, nvec - 1)) * 16);
+        if (threadIdx.x == 0) { s_np = 0; s_over = 0; }
+        const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
+        // (vector maxima kept as their 16-bit patterns, two to a register)
+        uint32_t vm2[kHeld / 2];
+        float lmax = -kInfF, amin = kInfF;
+        h2t hmin = H(0x7c007c00u);
+        int nok = 0;
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const bool ok = u * kTopkThreads + tid < nvec;
+            float mx;
+            uint32_t mb;
+            if constexpr (DT == VI_F16) {
+                const h2t hx = H(d[u].x), hy = H(d[u].y), hz = H(d[u].z), hw = H(d[u].w);
+                const h2t t = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hx, hy),
+                                                            __builtin_elementwise_maximum(hz, hw));
+                hmin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(hmin, __builtin_elementwise_minimum(hx, hy)),
+                                                     __builtin_elementwise_minimum(hz, hw));
+                const _Float16 hm = __builtin_elementwise_maximum(t[0], t[1]);
+                mx = float(hm);
+                mb = uint32_t(__builtin_bit_cast(uint16_t, hm));
+            } else {   // (a word at a time: its two logits as floats, one three-way max / min each)
+                const uint32_t w4[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
+                mx = -kInfF;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float lo = __builtin_bit_cast(float, w4[q] << 16);
+                    const float hi = __builtin_bit_cast(float, w4[q] & 0xffff0000u);
+                    mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, lo), hi);
+                    amin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(amin, lo), hi);
+                }
+                mb = __builtin_bit_cast(uint32_t, mx) >> 16;
+            }
+            constexpr uint32_t kNegInf = DT == VI_F16 ? 0xfc00u : 0xff80u;
+            mb = ok ? mb : kNegInf;
+            if (want_lse) {   // (against the largest vector maximum so far, as it arrives)
+                lse_rebase(ok ? mx : -kInfF);
+                float sm = 0.0f;
+#pragma unroll
+                for (int j = 0; j < P; ++j) sm += lse_term(Elem<DT>::decode(vec_bits<DT>(d[u], j)));
+                lse_s += ok ? sm : 0.0f;
+            }
+            if (u & 1) vm2[u / 2] |= mb << 16;
+            else vm2[u / 2] = mb;
+            lmax = ok ? __builtin_elementwise_maximum(lmax, mx) : lmax;
+            nok += ok ? 1 : 0;
+        }
+        if constexpr (DT == VI_F16) amin = float(__builtin_elementwise_minimum(hmin[0], hmin[1]));
+        // (the minimum also covers re-read vectors: they belong to the slice, so
+        // at worst another lane's non-finite logit sends the workgroup the exact way)
+        bool bad = !isfinite(amin) || lmax == kInfF || __builtin_isnan(lmax);
+        if (scaled) bad = bad || !isfinite(amin * inv_t) || (lmax > -kInfF && !isfinite(lmax * inv_t));
+        // the wave's K-th largest lane maximum: a radix select over the order
+        // keys, one ballot per bit
+        {
+            const float lm = scaled ? lmax * inv_t : lmax;
+            const uint32_t b = __builtin_bit_cast(uint32_t, lm);
+            const uint32_t key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+            uint32_t t = 0;
+#pragma unroll
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t c = t | (1u << bit);
+                if (__builtin_popcountll(ballot(key >= c)) >= K) t = c;
+            }
+            if (lane == 0) s_tw[wave] = __builtin_bit_cast(float, (t & 0x80000000u) ? (t & 0x7fffffffu) : ~t);
+        }
+        if (__syncthreads_or(bad ? 1 : 0)) {
+            lse_m = -kInfF;   // (the exact path starts the log-sum-exp again)
+            lse_s = 0.0f;
+#pragma unroll 1
+            for (int u = 0; u < kHeld; ++u) {
+                const int v = u * kTopkThreads + tid;
+                vec_exact(load16(base + size_t(min(v, nvec - 1)) * 16), begin + v * P, v < nvec);
+            }
+            return;
+        }
+        if constexpr (MODE == kModeVerify) valid += uint32_t(nok * P);
+        // the workgroup's gate: the largest of the waves' K-th lane maxima
+        float tau_g = s_tw[0];
+#pragma unroll
+        for (int w = 1; w < kTopkWaves; ++w) tau_g = fmaxf(tau_g, s_tw[w]);
+        // the vectors reaching it, staged per wave (at most one per lane: the
+        // loop stays small enough to unroll, which keeps the vectors in registers)
+        int nst = 0;   // (wave-uniform)
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const float vr = Elem<DT>::decode((u & 1) ? vm2[u / 2] >> 16 : vm2[u / 2] & 0xffffu);
+            const float vs = scaled ? vr * inv_t : vr;
+            const bool c = u * kTopkThreads + tid < nvec && vs >= tau_g;
+            const uint64_t m = ballot(c);
+            if (m) {   // (uniform: most vectors have no candidate in the wave)
+                const int pos = nst + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+                if (c && pos < kWave) {
+                    s_hv[wave][pos] = d[u];
+                    s_hid[wave][pos] = begin + (u * kTopkThreads + tid) * P;
+                }
+                nst += int(__builtin_popcountll(m));
+            }
+        }
+        // their logits reaching it, pooled for the workgroup
+        if (nst <= kWave) {
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const bool have = lane < nst;
+            const uint4 v = s_hv[wave][lane];
+            const int id0 = s_hid[wave][lane];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                float x = Elem<DT>::decode(vec_bits<DT>(v, j));
+                if (scaled) x = x * inv_t;
+                const bool c = have && x >= tau_g;
+                const uint64_t m = ballot(c);
+                if (m) {
+                    int at = 0;
+                    if (lane == 0) at = atomicAdd(&s_np, int(__builtin_popcountll(m)));
+                    at = __builtin_amdgcn_readfirstlane(at);
+                    const int pos = at + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+                    if (c && pos < kPool) { s_pv[pos] = x; s_pi[pos] = id0 + j; }
+                }
+            }
+        } else if (lane == 0) {
+            s_over = 1;
+        }
+        wave_partials();
+        __syncthreads();
+        const int n = s_np;
+        if (s_over || n > kPool) {
+            // too many candidates to pool: read again, offered into the wave lists
+#pragma unroll 1
+            for (int u = 0; u < kHeld; ++u) {
+                const int vi = u * kTopkThreads + tid;
+                const uint4 v = load16(base + size_t(min(vi, nvec - 1)) * 16);
+                float vm = -kInfF;
+#pragma unroll
+                for (int j = 0; j < P; ++j) vm = fmaxf(vm, Elem<DT>::decode(vec_bits<DT>(v, j)));
+                if (scaled) vm = vm * inv_t;
+                const float gate = fmaxf(tau_g, L.kv);
+                if (ballot(vi < nvec && vm >= gate) != 0) vec_offer(v, begin + vi * P, vi < nvec, gate);
+            }
+            return;
+        }
+        // wave 0 places each pooled logit by its rank among them (ids are
+        // distinct, so the ranks are)
+        if (wave == 0) {
+            for (int t0 = 0; t0 < n; t0 += kWave) {
+                const int t = t0 + lane;
+                const float v = s_pv[min(t, n - 1)];
+                const int i = s_pi[min(t, n - 1)];
+                int rank = 0;
+#pragma unroll 8
+                for (int j = 0; j < n; ++j) rank += better(s_pv[j], s_pi[j], v, i) ? 1 : 0;
+                if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const bool h = lane < min(K, n);
+            L.v = h ? s_selv[lane] : -kInfF;
+            L.i = h ? s_seli[lane] : kInvalidId;
+            L.kv = readlane_f(L.v, K - 1);
+            L.ki = readlane_i(L.i, K - 1);
+        }
+        pooled = true;
+      }
+    };
+    // (the held scan when the slice gives each lane at most kHeld vectors)
+    auto held_fits = [&]() {
+        if constexpr (kHeldMode) {
+            const int nvec = (end - begin) / Elem<DT>::kPerVec;
+            return nvec > 0 && nvec <= kHeld * kTopkThreads;
+        }
+        return false;
+    };
+    auto held_then_tail = [&]() {
+        constexpr int P = Elem<DT>::kPerVec;
+        const int nvec = (end - begin) / P;
+        held_scan(nvec);
+        if (begin + nvec * P < end) pooled = false;   // (the tail enters every wave's list)
+        for (int ib = begin + nvec * P; ib < end; ib += kTopkThreads) {
+            const int i = ib + int(threadIdx.x);
+            const bool ok = i < end;
+            elem_fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
+        }
+    };
+    if constexpr (MODE == kModeTopk || MODE == kModeVerify) {
+        if (held_fits()) held_then_tail();
+        else scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
+    } else if constexpr (MODE == kModeSample) {
+        if (batched)
+            scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
+        else
+            scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
+    } else {
+        scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
     }
-    if constexpr (MODE == kModeSample) handoff_stores_done();   // every wave's probability zeros
-    __syncthreads();
+
+    // ---- merge the wave lists in LDS
+    __shared__ float s_val[kTopkWaves][kMaxK];
+    __shared__ int s_idx[kTopkWaves][kMaxK];
     // the four wave lists merged as a tree: waves 0 and 2 take waves 1 and 3's
     // lists, then wave 0 takes wave 2's
     auto tree_merge = [&]() {
@@ -1028,7 +1249,15 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         __syncthreads();
         if (wave == 0) list_merge<kD>(L, K, lane < K ? s_val[2][lane] : -kInfF, lane < K ? s_idx[2][lane] : kInvalidId);
     };
-    tree_merge();
+    // (a pooled slice has its list in wave 0 and the partials in LDS already)
+    if (!pooled) {
+        s_val[wave][lane] = L.v;
+        s_idx[wave][lane] = L.i;
+        wave_partials();
+        if constexpr (MODE == kModeSample) handoff_stores_done();   // every wave's probability zeros
+        __syncthreads();
+        tree_merge();
+    }
     uint32_t f = 0, c = 0;
     float m = -kInfF;
     double s = 0.0;
@@ -1155,11 +1384,47 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             }
         }
     } else if constexpr (MODE == kModeVerify) {
+        const bool refused = verify_list_refused(p);
+        const uint32_t rvalid = refused ? 0u : c;
+        const uint32_t rflags = ((f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u) | (refused ? VI_FLAG_ERROR : 0u);
         if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
-        if (lane == 0) {
-            const bool refused = verify_list_refused(p);
-            a.lvalid[r] = refused ? 0u : c;
-            a.lflags[r] = ((f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u) | (refused ? VI_FLAG_ERROR : 0u);
+        if (lane == 0) { a.lvalid[r] = rvalid; a.lflags[r] = rflags; }
+        if (a.decide) {
+            // draft row r is position j of lane l: its decision, from the target
+            // row's list and this row's (in LDS; entries past K are never read);
+            // the lane's last position to finish takes the bonus draw and walks
+            // the chain (agent-scope hand-off of the decisions, the lane's
+            // counter reset for the next call)
+            const int l = r / a.dv.drafts, j = r - l * a.dv.drafts;
+            const vi_row_params pl = a.params[l];
+            const size_t tr = size_t(l) * a.dv.target_rows + j;
+            position_decision(pl, j, l, a.dv.drafts, a.dv.target_rows, a.dv.tlval + tr * kMaxK, a.dv.tlidx + tr * kMaxK,
+                              a.dv.tlvalid[tr], a.dv.tlflags[tr], s_val[0], s_idx[0], rvalid, rflags, a.dv.drafted,
+                              a.vocabulary, 0, a.dv.dec);
+            uint32_t old = 0;
+            if (lane == 0) {
+                handoff_stores_done();
+                old = __hip_atomic_fetch_add(&a.dv.larr[l], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            old = __builtin_amdgcn_readfirstlane(old);
+            if (old == uint32_t(a.dv.drafts - 1)) {
+                handoff_acquire();
+                if (a.dv.target_rows == a.dv.drafts + 1) {
+                    const size_t tb = size_t(l) * a.dv.target_rows + a.dv.drafts;
+                    position_decision(pl, a.dv.drafts, l, a.dv.drafts, a.dv.target_rows, a.dv.tlval + tb * kMaxK,
+                                      a.dv.tlidx + tb * kMaxK, a.dv.tlvalid[tb], a.dv.tlflags[tb], nullptr, nullptr, 0u, 0u,
+                                      a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+                    wave_sync();
+                }
+                if (lane == 0) {
+                    const PosDecision* D = a.dv.dec + size_t(l) * (a.dv.drafts + 1);
+                    lane_chain(l, [&](int q) {
+                        return PosDecision{get_agent(&D[q].token), get_agent(&D[q].flags), get_agent(&D[q].accept), 0};
+                    }, a.dv.drafts, a.dv.target_rows, a.dv.drafted, a.params, a.dv.terminal, a.dv.n_terminal, 0, a.dv.accepted,
+                               a.dv.committed, a.dv.committed_count, a.dv.lane_flags);
+                    put_agent(&a.dv.larr[l], 0u);
+                }
+            }
         }
     } else {
         // the candidates' fp64 weights, one per lane (the sums stay on lane 0, in order)
@@ -1359,7 +1624,7 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
                               float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
-                              void* ws, size_t ws_bytes, hipStream_t stream) {
+                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide) {
     // Partials carved for (layout_rows, layout_slices) so that launches over
     // different row counts share one counter layout in one workspace.
     const TopkPlan plan = topk_plan(rows, vocabulary);
@@ -1372,6 +1637,7 @@ vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layou
     a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
     a.params = params; a.params_div = params_div;
     a.lval = lval; a.lidx = lidx; a.lvalid = lvalid; a.lflags = lflags; a.skip_unlisted = skip_unlisted;
+    if (decide) { a.decide = 1; a.dv = *decide; }
     return launch_mode<kModeVerify>(a, dtype, aligned16(logits, stride, dtype), rows, plan.slices, stream);
 }
 

@@ -81,11 +81,31 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
                                 const int64_t* next, int64_t* chosen, float* gap, void* ws, size_t ws_bytes,
                                 hipStream_t stream);
 
-// Sorted, filtered top-k lists (z values, ids) of verification rows.
+// Sorted, filtered top-k lists (z values, ids) of verification rows.  With
+// `decide` (draft rows, every lane listed, the target rows' lists complete
+// before the launch) each row's last workgroup also takes its position's
+// accept decision, and each lane's last position walks the lane's chain.
+struct PosDecision;
+struct VerifyDecideArgs {
+    int drafts, target_rows;
+    const float* tlval;
+    const int* tlidx;
+    const uint32_t* tlvalid;
+    const uint32_t* tlflags;
+    const int32_t* drafted;
+    PosDecision* dec;
+    uint32_t* larr;
+    const int64_t* terminal;
+    int n_terminal;
+    int32_t* accepted;
+    int32_t* committed;
+    int32_t* committed_count;
+    uint32_t* lane_flags;
+};
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
                               float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
-                              void* ws, size_t ws_bytes, hipStream_t stream);
+                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide = nullptr);
 size_t topk_partials_bytes_slices(int rows, int slices);
 
 // History hash (token -> count) per row for the top-k sampler route.
