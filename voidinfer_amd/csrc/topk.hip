@@ -102,10 +102,14 @@ struct TopkArgs {
     uint32_t* lvalid;       // [rows]
     uint32_t* lflags;       // [rows]
     int skip_unlisted;      // rows of lanes without a top-k list are left to the full-vocabulary path
-    // kModeVerify over the draft rows with the decisions taken as the rows
-    // finish (decide != 0; larr: the lanes' arrival counters, zero between calls)
+    // kModeVerify with the decisions taken as the rows finish: decide == 1 over
+    // the draft rows (each position's decision, each lane's chain), decide == 2
+    // over the target rows (the bonus rows' draws); in the paired launch
+    // decide == 3 (target rows) and 4 (draft rows): each position's later row
+    // decides.  larr: the lanes' arrival counters, zero between calls
     int decide;
     VerifyDecideArgs dv;
+    int pair_rows;          // (the paired launch: rows of the target half)
 };
 
 // ----------------------------------------------------------- wave-resident list
@@ -416,10 +420,10 @@ __device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, c
 }
 
 // ------------------------------------------------------------------- the kernel
+// The work of one workgroup: slice `slice` of `slices` of row r.
 template <int DT, bool VEC, int MODE>
-__global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
+__device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, const int slices, const int r) {
     constexpr bool kD = MODE == kModeSample;   // DPP lane exchanges in the list merges
-    const int slice = blockIdx.x, slices = gridDim.x, r = blockIdx.y;
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     const void* row = static_cast<const unsigned char*>(a.logits) + size_t(r) * size_t(a.stride) * sizeof(typename Elem<DT>::Bits);
     const int begin = slice * a.slice_len, end = min(a.vocabulary, begin + a.slice_len);
@@ -1237,6 +1241,24 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
     }
 
+    // Verification with decisions over the draft rows: the position's target
+    // list (entries, finite count, flags), loaded by wave 0 as early as the row's
+    // last workgroup is known
+    float tl_v = -kInfF;
+    int tl_i = kInvalidId;
+    uint32_t tl_valid = 0, tl_flags = 0;
+    bool tl_have = false;
+    auto tl_fetch = [&]() {
+        if constexpr (MODE == kModeVerify) {
+            const int l = r / a.dv.drafts, j = r - l * a.dv.drafts;
+            const size_t tr = size_t(l) * a.dv.target_rows + j;
+            tl_v = a.dv.tlval[tr * kMaxK + lane];
+            tl_i = a.dv.tlidx[tr * kMaxK + lane];
+            tl_valid = a.dv.tlvalid[tr];
+            tl_flags = a.dv.tlflags[tr];
+            tl_have = true;
+        }
+    };
     // ---- merge the wave lists in LDS
     __shared__ float s_val[kTopkWaves][kMaxK];
     __shared__ int s_idx[kTopkWaves][kMaxK];
@@ -1283,6 +1305,9 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         __syncthreads();
         if (!s_last) return;
         handoff_acquire();
+        if constexpr (MODE == kModeVerify) {   // (the target row's list, loaded under the merge below)
+            if (a.decide == 1 && wave == 0) tl_fetch();
+        }
         // the headers (wave 0, lane sl holds slice sl's; slices <= 64), loaded
         // now so that their latency overlaps the list loads and merges
         // (loads unconditional, at clamped in-bounds addresses, and selected
@@ -1292,9 +1317,48 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         const uint32_t hf = hl ? get_agent(&h.flags) : 0u, hc = hl ? get_agent(&h.valid) : 0u;
         const float hm = hl ? get_agent(&h.lse_max) : -kInfF;
         const double hs = hl ? get_agent(&h.lse_sum) : 0.0;
+        L = WaveList{};
+        if constexpr (MODE == kModeTopk || MODE == kModeVerify) {
+            if (slices * K <= kPool) {
+                // every entry of every slice list, one per thread, into LDS; each
+                // entry's rank among them places the row's top K (padding pairs
+                // (-inf, kInvalidId) are equal and rank after every entry)
+                const int n = slices * K, t = int(threadIdx.x);
+                if (t < n) {
+                    const int sl = t / K;
+                    const size_t src = (size_t(r) * slices + size_t(sl)) * kMaxK + size_t(t - sl * K);
+                    s_pv[t] = get_agent(&a.pval[src]);
+                    s_pi[t] = get_agent(&a.pidx[src]);
+                }
+                __syncthreads();
+                // (one entry per thread: more than a wave's worth of entries are
+                // ranked by every wave, then handed to wave 0 through LDS)
+                if (n > kWave || wave == 0) {
+                    if (t < n) {
+                        const float v = s_pv[t];
+                        const int i = s_pi[t];
+                        int rank = 0;
+#pragma unroll 8
+                        for (int q = 0; q < n; ++q) rank += better(s_pv[q], s_pi[q], v, i) ? 1 : 0;
+                        if (i != kInvalidId && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
+                    }
+                }
+                if (n > kWave) __syncthreads();
+                if (wave != 0) return;
+                wave_sync();
+                int real = 0;   // (entries other than padding: every rank below it is placed)
+                for (int t0 = 0; t0 < n; t0 += kWave)
+                    real += int(__builtin_popcountll(ballot(t0 + lane < n && s_pi[min(t0 + lane, n - 1)] != kInvalidId)));
+                L.v = lane < min(K, real) ? s_selv[lane] : -kInfF;
+                L.i = lane < min(K, real) ? s_seli[lane] : kInvalidId;
+                L.kv = readlane_f(L.v, K - 1);
+                L.ki = readlane_i(L.i, K - 1);
+                goto merged;
+            }
+        }
+        {
         // every slice's sorted list, merged in: wave w takes a quarter of the
         // slices (the loads of eight in flight together), then the tree above
-        L = WaveList{};
         const int per = (slices + kTopkWaves - 1) / kTopkWaves;
         const int s_lo = wave * per, s_hi = min(slices, s_lo + per);
         for (int sl0 = s_lo; sl0 < s_hi; sl0 += 8) {
@@ -1323,6 +1387,8 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         __syncthreads();
         tree_merge();
         if (wave != 0) return;
+        }
+    merged:
         // reductions of the headers across the lanes (the log-sum-exp partials
         // summed in a fixed order)
         f = hf; c = hc; m = hm;
@@ -1387,44 +1453,96 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
         const bool refused = verify_list_refused(p);
         const uint32_t rvalid = refused ? 0u : c;
         const uint32_t rflags = ((f & kSliceNonfinite) ? VI_FLAG_NONFINITE : 0u) | (refused ? VI_FLAG_ERROR : 0u);
-        if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
-        if (lane == 0) { a.lvalid[r] = rvalid; a.lflags[r] = rflags; }
-        if (a.decide) {
-            // draft row r is position j of lane l: its decision, from the target
-            // row's list and this row's (in LDS; entries past K are never read);
-            // the lane's last position to finish takes the bonus draw and walks
-            // the chain (agent-scope hand-off of the decisions, the lane's
-            // counter reset for the next call)
-            const int l = r / a.dv.drafts, j = r - l * a.dv.drafts;
-            const vi_row_params pl = a.params[l];
-            const size_t tr = size_t(l) * a.dv.target_rows + j;
-            position_decision(pl, j, l, a.dv.drafts, a.dv.target_rows, a.dv.tlval + tr * kMaxK, a.dv.tlidx + tr * kMaxK,
-                              a.dv.tlvalid[tr], a.dv.tlflags[tr], s_val[0], s_idx[0], rvalid, rflags, a.dv.drafted,
-                              a.vocabulary, 0, a.dv.dec);
+        if (a.decide >= 3) {   // (read by the position's other row, in this launch)
+            if (lane < K) { put_agent(&a.lval[size_t(r) * kMaxK + lane], L.v); put_agent(&a.lidx[size_t(r) * kMaxK + lane], L.i); }
+            if (lane == 0) { put_agent(&a.lvalid[r], rvalid); put_agent(&a.lflags[r], rflags); }
+        } else {
+            if (lane < K) { a.lval[size_t(r) * kMaxK + lane] = L.v; a.lidx[size_t(r) * kMaxK + lane] = L.i; }
+            if (lane == 0) { a.lvalid[r] = rvalid; a.lflags[r] = rflags; }
+        }
+        // the lane's decided positions counted; its last walks the chain
+        auto lane_arrive = [&](int l, uint32_t total) {
             uint32_t old = 0;
             if (lane == 0) {
                 handoff_stores_done();
                 old = __hip_atomic_fetch_add(&a.dv.larr[l], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            old = __builtin_amdgcn_readfirstlane(old);
-            if (old == uint32_t(a.dv.drafts - 1)) {
-                handoff_acquire();
-                if (a.dv.target_rows == a.dv.drafts + 1) {
-                    const size_t tb = size_t(l) * a.dv.target_rows + a.dv.drafts;
-                    position_decision(pl, a.dv.drafts, l, a.dv.drafts, a.dv.target_rows, a.dv.tlval + tb * kMaxK,
-                                      a.dv.tlidx + tb * kMaxK, a.dv.tlvalid[tb], a.dv.tlflags[tb], nullptr, nullptr, 0u, 0u,
-                                      a.dv.drafted, a.vocabulary, 0, a.dv.dec);
-                    wave_sync();
-                }
+            if (uint32_t(__builtin_amdgcn_readfirstlane(old)) != total - 1u) return;
+            handoff_acquire();
+            const PosDecision* D = a.dv.dec + size_t(l) * (a.dv.drafts + 1);
+            lane_chain_wave(l, [&](int q) {
+                return PosDecision{get_agent(&D[q].token), get_agent(&D[q].flags), get_agent(&D[q].accept), 0};
+            }, a.dv.drafts, a.dv.target_rows, a.dv.drafted, a.params, a.dv.terminal, a.dv.n_terminal, 0,
+                            a.dv.accepted, a.dv.committed, a.dv.committed_count, a.dv.lane_flags);
+            if (lane == 0) put_agent(&a.dv.larr[l], 0u);
+        };
+        if (a.decide >= 3) {
+            // paired launch: target row (l, j) or draft row (l, j); the later of
+            // the two takes position j's decision with the other's list read back
+            // (a bonus row decides alone)
+            const bool tside = a.decide == 3;
+            const int per = tside ? a.dv.target_rows : a.dv.drafts;
+            const int l = r / per, j = r - l * per;
+            const bool bonus = tside && j == a.dv.drafts;
+            bool here = bonus;
+            if (!bonus) {
+                uint32_t old = 0;
+                uint32_t* pc = &a.dv.parr[size_t(l) * (a.dv.drafts + 1) + j];
                 if (lane == 0) {
-                    const PosDecision* D = a.dv.dec + size_t(l) * (a.dv.drafts + 1);
-                    lane_chain(l, [&](int q) {
-                        return PosDecision{get_agent(&D[q].token), get_agent(&D[q].flags), get_agent(&D[q].accept), 0};
-                    }, a.dv.drafts, a.dv.target_rows, a.dv.drafted, a.params, a.dv.terminal, a.dv.n_terminal, 0, a.dv.accepted,
-                               a.dv.committed, a.dv.committed_count, a.dv.lane_flags);
-                    put_agent(&a.dv.larr[l], 0u);
+                    handoff_stores_done();
+                    old = __hip_atomic_fetch_add(pc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (old == 1u) put_agent(pc, 0u);   // (both rows arrived: reset for the next call)
                 }
+                here = __builtin_amdgcn_readfirstlane(old) == 1;
             }
+            if (here) {
+                handoff_acquire();
+                if (bonus) {
+                    position_decision(p, j, l, a.dv.drafts, a.dv.target_rows, s_val[0], s_idx[0], rvalid, rflags,
+                                      nullptr, nullptr, 0u, 0u, a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+                } else {
+                    const size_t pr = tside ? size_t(l) * a.dv.drafts + j : size_t(l) * a.dv.target_rows + j;
+                    const float* ov = tside ? a.dv.dlval : a.dv.tlval;
+                    const int* oi = tside ? a.dv.dlidx : a.dv.tlidx;
+                    __shared__ float s_ov[kMaxK];
+                    __shared__ int s_oi[kMaxK];
+                    s_ov[lane] = get_agent(&ov[pr * kMaxK + lane]);
+                    s_oi[lane] = get_agent(&oi[pr * kMaxK + lane]);
+                    const uint32_t ovalid = get_agent(tside ? &a.dv.dlvalid[pr] : &a.dv.tlvalid[pr]);
+                    const uint32_t oflags = get_agent(tside ? &a.dv.dlflags[pr] : &a.dv.tlflags[pr]);
+                    wave_sync();
+                    if (tside)
+                        position_decision(p, j, l, a.dv.drafts, a.dv.target_rows, s_val[0], s_idx[0], rvalid, rflags,
+                                          s_ov, s_oi, ovalid, oflags, a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+                    else
+                        position_decision(p, j, l, a.dv.drafts, a.dv.target_rows, s_ov, s_oi, ovalid, oflags, s_val[0],
+                                          s_idx[0], rvalid, rflags, a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+                }
+                lane_arrive(l, uint32_t(a.dv.drafts + (a.dv.target_rows == a.dv.drafts + 1 ? 1 : 0)));
+            }
+        } else if (a.decide == 2) {
+            // target row r: position j of lane l; a bonus row draws the lane's
+            // bonus token from its own list (in LDS)
+            const int l = r / a.dv.target_rows, j = r - l * a.dv.target_rows;
+            if (j == a.dv.drafts)
+                position_decision(p, j, l, a.dv.drafts, a.dv.target_rows, s_val[0], s_idx[0], rvalid, rflags,
+                                  nullptr, nullptr, 0u, 0u, a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+        } else if (a.decide == 1) {
+            // draft row r is position j of lane l: its decision, from the target
+            // row's list (in LDS) and this row's (in LDS; entries past K are never
+            // read); the lane's last position to finish walks the chain (the
+            // bonus draw is the target launch's; agent-scope hand-off of the
+            // decisions, the lane's counter reset for the next call)
+            const int l = r / a.dv.drafts, j = r - l * a.dv.drafts;
+            if (!tl_have) tl_fetch();
+            __shared__ float s_tv[kMaxK];
+            __shared__ int s_ti[kMaxK];
+            s_tv[lane] = tl_v;
+            s_ti[lane] = tl_i;
+            wave_sync();
+            position_decision(p, j, l, a.dv.drafts, a.dv.target_rows, s_tv, s_ti, tl_valid, tl_flags, s_val[0],
+                              s_idx[0], rvalid, rflags, a.dv.drafted, a.vocabulary, 0, a.dv.dec);
+            lane_arrive(l, uint32_t(a.dv.drafts));
         }
     } else {
         // the candidates' fp64 weights, one per lane (the sums stay on lane 0, in order)
@@ -1459,6 +1577,20 @@ __global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
             }
         }
     }
+}
+
+template <int DT, bool VEC, int MODE>
+__global__ __launch_bounds__(kTopkThreads, 4) void topk_kernel(TopkArgs a) {
+    topk_body<DT, VEC, MODE>(a, int(blockIdx.x), int(gridDim.x), int(blockIdx.y));
+}
+
+// Verification's target rows (first t.pair_rows rows of the grid) and draft
+// rows in one launch.
+template <int DTT, int DTD>
+__global__ __launch_bounds__(kTopkThreads, 4) void verify_pair_kernel(TopkArgs t, TopkArgs d) {
+    const int y = int(blockIdx.y);
+    if (y < t.pair_rows) topk_body<DTT, true, kModeVerify>(t, int(blockIdx.x), int(gridDim.x), y);
+    else topk_body<DTD, true, kModeVerify>(d, int(blockIdx.x), int(gridDim.x), y - t.pair_rows);
 }
 
 // History hash builder: one workgroup per row.  Each history token is
@@ -1624,7 +1756,8 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
                               float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
-                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide) {
+                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide,
+                              int decide_mode) {
     // Partials carved for (layout_rows, layout_slices) so that launches over
     // different row counts share one counter layout in one workspace.
     const TopkPlan plan = topk_plan(rows, vocabulary);
@@ -1637,8 +1770,56 @@ vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layou
     a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
     a.params = params; a.params_div = params_div;
     a.lval = lval; a.lidx = lidx; a.lvalid = lvalid; a.lflags = lflags; a.skip_unlisted = skip_unlisted;
-    if (decide) { a.decide = 1; a.dv = *decide; }
+    if (decide) { a.decide = decide_mode; a.dv = *decide; }
     return launch_mode<kModeVerify>(a, dtype, aligned16(logits, stride, dtype), rows, plan.slices, stream);
+}
+
+bool verify_pair_supported(const void* target, int target_dtype, int64_t target_stride, const void* draft,
+                           int draft_dtype, int64_t draft_stride) {
+    auto ok = [](const void* p, int dt, int64_t stride) {
+        return (dt == VI_BF16 || dt == VI_F16) && aligned16(p, stride, dt);
+    };
+    return ok(target, target_dtype, target_stride) && ok(draft, draft_dtype, draft_stride);
+}
+
+vi_status launch_verify_pair(const void* target, int target_dtype, int64_t target_stride, const void* draft,
+                             int draft_dtype, int64_t draft_stride, int lanes, int vocabulary,
+                             const vi_row_params* params, int layout_rows, int layout_slices, float* tval, int* tidx,
+                             uint32_t* tvalid, uint32_t* tflags, float* dval, int* didx, uint32_t* dvalid,
+                             uint32_t* dflags, const VerifyDecideArgs& decide, void* ws, size_t ws_bytes,
+                             hipStream_t stream) {
+    if (!verify_pair_supported(target, target_dtype, target_stride, draft, draft_dtype, draft_stride))
+        return VI_ERR_UNSUPPORTED;
+    const int trows = lanes * decide.target_rows, drows = lanes * decide.drafts;
+    // one slicing for both halves (the larger row set's)
+    const TopkPlan plan = topk_plan(std::max(trows, drows), vocabulary);
+    if (trows + drows > layout_rows || plan.slices > layout_slices) return VI_ERR_WORKSPACE;
+    Carver c(ws, ws_bytes);
+    const Partials part = carve_partials(c, layout_rows, layout_slices);
+    if (!c.ok) return VI_ERR_WORKSPACE;
+    TopkArgs t{};
+    t.logits = target; t.vocabulary = vocabulary; t.stride = target_stride; t.slice_len = plan.slice_len;
+    t.pval = part.pval; t.pidx = part.pidx; t.phdr = part.phdr; t.arrivals = part.arrivals;
+    t.params = params; t.params_div = decide.target_rows;
+    t.lval = tval; t.lidx = tidx; t.lvalid = tvalid; t.lflags = tflags;
+    t.decide = 3; t.dv = decide; t.pair_rows = trows;
+    TopkArgs d = t;   // (the draft half: its rows' partials after the target half's)
+    const size_t off = size_t(trows) * plan.slices;
+    d.logits = draft; d.stride = draft_stride;
+    d.pval = part.pval + off * kMaxK; d.pidx = part.pidx + off * kMaxK; d.phdr = part.phdr + off;
+    d.arrivals = part.arrivals + trows;
+    d.params_div = decide.drafts;
+    d.lval = dval; d.lidx = didx; d.lvalid = dvalid; d.lflags = dflags;
+    d.decide = 4;
+    const dim3 grid(plan.slices, trows + drows), block(kTopkThreads);
+#define VI_PAIR(A, B) hipLaunchKernelGGL((verify_pair_kernel<A, B>), grid, block, 0, stream, t, d)
+    if (target_dtype == VI_BF16) {
+        if (draft_dtype == VI_BF16) VI_PAIR(VI_BF16, VI_BF16); else VI_PAIR(VI_BF16, VI_F16);
+    } else {
+        if (draft_dtype == VI_BF16) VI_PAIR(VI_F16, VI_BF16); else VI_PAIR(VI_F16, VI_F16);
+    }
+#undef VI_PAIR
+    return launch_status();
 }
 
 size_t history_hash_slots(int64_t max_history) {

@@ -79,17 +79,20 @@ __global__ __launch_bounds__(kFinalizeThreads) void verify_position_kernel(
     position_decision(params[l], j, l, drafts, target_rows, tval + tr * kMaxK, tidx + tr * kMaxK,
                       has_t ? tvalid[tr] : 0u, has_t ? tflags[tr] : 0u, dval + dr * kMaxK, didx + dr * kMaxK,
                       has_d ? dvalid[dr] : 0u, has_d ? dflags[dr] : 0u, drafted, vocabulary, full_ok, dec);
-    if (!arrivals || threadIdx.x != 0) return;
-    handoff_stores_done();
-    const uint32_t old = __hip_atomic_fetch_add(&arrivals[l], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old != uint32_t(drafts)) return;   // (drafts + 1 positions per lane)
+    if (!arrivals) return;
+    uint32_t old = 0;
+    if (threadIdx.x == 0) {
+        handoff_stores_done();
+        old = __hip_atomic_fetch_add(&arrivals[l], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__builtin_amdgcn_readfirstlane(old) != uint32_t(drafts)) return;   // (drafts + 1 positions per lane)
     handoff_acquire();
     const PosDecision* D = dec + size_t(l) * (drafts + 1);
-    lane_chain(l, [&](int j) {
-        return PosDecision{get_agent(&D[j].token), get_agent(&D[j].flags), get_agent(&D[j].accept), 0};
+    lane_chain_wave(l, [&](int q) {
+        return PosDecision{get_agent(&D[q].token), get_agent(&D[q].flags), get_agent(&D[q].accept), 0};
     }, drafts, target_rows, drafted, params, terminal, n_terminal, full_ok, accepted, committed, committed_count,
-               lane_flags);
-    put_agent(&arrivals[l], 0u);
+                    lane_flags);
+    if (threadIdx.x == 0) put_agent(&arrivals[l], 0u);
 }
 
 // The accept chains after the full-vocabulary kernels (one thread per lane).
@@ -491,7 +494,7 @@ VerifyLayout verify_layout(int lanes, int drafts, int vocabulary) {
     VerifyLayout v;
     v.trows = lanes * (drafts + 1);
     v.drows = lanes * drafts;
-    v.lrows = v.trows;
+    v.lrows = v.trows + v.drows;   // (the paired launch carves both row sets' partials)
     v.lslices = std::max(topk_plan(v.trows, vocabulary).slices, topk_plan(v.drows, vocabulary).slices);
     v.lslices = std::max(v.lslices, topk_plan(lanes * drafts, vocabulary).slices);
     return v;
@@ -549,6 +552,7 @@ size_t verify_workspace(int lanes, int drafts, int vocabulary) {
     b += align_up(verify_greedy_bytes(v, lanes, drafts, vocabulary), 256);
     b += topk_partials_bytes_slices(v.lrows, v.lslices);
     b += align_up(size_t(v.trows) * sizeof(PosDecision), 256) + align_up(size_t(lanes) * 4, 256);
+    b += align_up(size_t(lanes) * (drafts + 1) * 4, 256);
     b += full_verify_bytes(lanes, drafts, vocabulary);
     return b + 4096;
 }
@@ -571,6 +575,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     uint32_t* dflags = c.take<uint32_t>(size_t(v.drows));
     PosDecision* dec = c.take<PosDecision>(size_t(v.trows));
     uint32_t* larr = c.take<uint32_t>(size_t(a.lanes));   // positions of a lane decided (zero between calls)
+    uint32_t* parr = c.take<uint32_t>(size_t(a.lanes) * (a.drafts + 1));   // rows of a position listed (the same)
     const size_t gbytes = verify_greedy_bytes(v, a.lanes, a.drafts, a.vocabulary);
     unsigned char* gws = gbytes ? c.take<unsigned char>(gbytes) : nullptr;
     const size_t lbytes = topk_partials_bytes_slices(v.lrows, v.lslices);
@@ -595,23 +600,32 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     const int full_ok = (a.mode == VI_VERIFY_SAMPLED &&
                          full_path_ok(a.target, a.target_dtype, a.vocabulary, a.target_stride) &&
                          full_path_ok(a.draft, a.draft_dtype, a.vocabulary, a.draft_stride)) ? 1 : 0;
+    // every lane listed: the target rows' scan draws the bonus tokens as its
+    // bonus rows finish, the draft rows' scan takes each position's decision as
+    // its row finishes, and each lane's last position walks the chain (two
+    // launches in all)
+    const bool fused = !full_ok;
+    VerifyDecideArgs dv{};
+    dv.drafts = a.drafts; dv.target_rows = a.target_rows;
+    dv.tlval = tval; dv.tlidx = tidx; dv.tlvalid = tvalid; dv.tlflags = tflags;
+    dv.dlval = dval; dv.dlidx = didx; dv.dlvalid = dvalid; dv.dlflags = dflags; dv.parr = parr;
+    dv.drafted = a.drafted; dv.dec = dec; dv.larr = larr;
+    dv.terminal = a.terminal; dv.n_terminal = a.n_terminal;
+    dv.accepted = a.accepted; dv.committed = a.committed; dv.committed_count = a.committed_count;
+    dv.lane_flags = a.lane_flags;
+    if (fused && verify_pair_supported(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype,
+                                       a.draft_stride))
+        // both row sets in one launch: each position decided by its later row
+        return launch_verify_pair(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype,
+                                  a.draft_stride, a.lanes, a.vocabulary, a.params, v.lrows, v.lslices, tval, tidx,
+                                  tvalid, tflags, dval, didx, dvalid, dflags, dv, lws, lbytes, stream);
     st = launch_verify_lists(a.target, a.target_dtype, trows, v.lrows, v.lslices, a.vocabulary, a.target_stride,
-                             a.params, a.target_rows, tval, tidx, tvalid, tflags, full_ok, lws, lbytes, stream);
+                             a.params, a.target_rows, tval, tidx, tvalid, tflags, full_ok, lws, lbytes, stream,
+                             fused ? &dv : nullptr, 2);
     if (st != VI_OK) return st;
-    if (!full_ok && a.drafts > 0) {
-        // every lane listed: the draft rows' scan takes each position's decision
-        // as its row finishes, and each lane's last position walks the chain
-        // (two launches in all)
-        VerifyDecideArgs dv{};
-        dv.drafts = a.drafts; dv.target_rows = a.target_rows;
-        dv.tlval = tval; dv.tlidx = tidx; dv.tlvalid = tvalid; dv.tlflags = tflags;
-        dv.drafted = a.drafted; dv.dec = dec; dv.larr = larr;
-        dv.terminal = a.terminal; dv.n_terminal = a.n_terminal;
-        dv.accepted = a.accepted; dv.committed = a.committed; dv.committed_count = a.committed_count;
-        dv.lane_flags = a.lane_flags;
+    if (fused)
         return launch_verify_lists(a.draft, a.draft_dtype, drows, v.lrows, v.lslices, a.vocabulary, a.draft_stride,
-                                   a.params, a.drafts, dval, didx, dvalid, dflags, 0, lws, lbytes, stream, &dv);
-    }
+                                   a.params, a.drafts, dval, didx, dvalid, dflags, 0, lws, lbytes, stream, &dv, 1);
     st = launch_verify_lists(a.draft, a.draft_dtype, drows, v.lrows, v.lslices, a.vocabulary, a.draft_stride,
                              a.params, a.drafts, dval, didx, dvalid, dflags, full_ok, lws, lbytes, stream);
     if (st != VI_OK) return st;

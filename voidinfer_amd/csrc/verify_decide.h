@@ -22,8 +22,9 @@ __device__ inline bool is_terminal(const int64_t* terminal, int n, int64_t t) {
     return false;
 }
 
-// Filtered distribution of one sorted list (in LDS): the lane's weights, the
-// support after the cap / min-p / top-p cuts and its mass.
+// Filtered distribution of one sorted list: entry k's weight and id (in LDS,
+// and held by lane k as w, id), the support after the cap / min-p / top-p cuts
+// and its mass.
 struct ListDist {
     double w[kMaxK];
     int id[kMaxK];
@@ -31,40 +32,58 @@ struct ListDist {
     double sn;
 };
 
-// One wave per list: lane k computes the weight of list entry k; lane 0 then
-// takes the cuts and sums sequentially, in the order of the one-thread rule
-// (the fp64 results are that rule's, bit for bit).
-__device__ inline void list_dist(const vi_row_params& p, const float* z, const int* id, uint32_t valid, ListDist& d) {
+// Lane j's value, on every lane (j wave-uniform).
+__device__ __forceinline__ double readlane_d(double v, int j) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), j));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), j));
+    return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+}
+
+// One wave per list: lane k computes the weight of list entry k; the cuts and
+// sums then run in the order of the one-thread rule on every lane (wave-uniform
+// loops over the lanes' weights, read lane by lane: the fp64 results are that
+// rule's, bit for bit).  Returns lane k's weight (0 past the cap) in w.
+__device__ inline void list_dist(const vi_row_params& p, const float* z, const int* id, uint32_t valid, ListDist& d,
+                                 double& w) {
     const int k = lane_id();
     const bool greedy = !(p.temperature > 0.0f);
     // (callers refuse lanes with top_k outside [1, kMaxK]; the clamp keeps every
     // index inside the 64-entry lists regardless)
     const int cap = valid == 0 ? 0 : (greedy ? 1 : min(min(max(p.top_k, 0), kMaxK), int(valid)));
+    w = 0.0;
     if (k < cap) {
+        w = greedy ? 1.0 : exp(double(z[k]) - double(z[0]));
         d.id[k] = id[k];
-        d.w[k] = greedy ? 1.0 : exp(double(z[k]) - double(z[0]));
+        d.w[k] = w;
     }
-    wave_sync();
-    if (k == 0) {
-        int n = 0;
-        double sn = 0.0;
-        if (cap > 0 && greedy) {
-            n = 1;
-            sn = 1.0;
-        } else if (cap > 0) {
-            double s = 0.0;
-            for (int j = 0; j < cap; ++j) s += d.w[j];
-            const double minp = double(p.min_p), target = double(p.top_p) * s;
-            double cum = 0.0;
-            for (int j = 0; j < cap; ++j) {
-                if (p.min_p > 0.0f && d.w[j] < minp * d.w[0]) break;
-                cum += d.w[j];
-                n = j + 1;
-                if (p.top_p < 1.0f && cum >= target) break;
-            }
-            if (n < 1) n = 1;
-            for (int j = 0; j < n; ++j) sn += d.w[j];
+    int n = 0;
+    double sn = 0.0;
+    if (cap > 0 && greedy) {
+        n = 1;
+        sn = 1.0;
+    } else if (cap > 0) {
+        double s = 0.0;
+        for (int j = 0; j < cap; ++j) s += readlane_d(w, j);
+        const double minp = double(p.min_p), target = double(p.top_p) * s, w0 = readlane_d(w, 0);
+        double cum = 0.0;
+        for (int j = 0; j < cap; ++j) {
+            const double wj = readlane_d(w, j);
+            if (p.min_p > 0.0f && wj < minp * w0) break;
+            cum += wj;
+            n = j + 1;
+            if (p.top_p < 1.0f && cum >= target) break;
         }
+        // the support's mass: the same additions in the same order as cum's
+        // (from 0.0, entries 0..n-1), unless no entry was taken
+        if (n < 1) {
+            n = 1;
+            sn = w0;
+        } else {
+            sn = cum;
+        }
+    }
+    if (k == 0) {
         d.support = n;
         d.sn = sn;
     }
@@ -119,34 +138,35 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
     }
     if (j == drafts) {   // the bonus row's draw (used when every draft is accepted)
         if (target_rows != drafts + 1) return;
-        list_dist(p, tv, ti, tvalid, P);
-        if (k == 0) {
-            int32_t tok = -1;
-            if (tvalid) {
-                if (!(p.temperature > 0.0f)) tok = P.id[0];
-                else {
-                    const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
-                    double cum = 0.0;
-                    int pick = P.support - 1;
-                    for (int i = 0; i < P.support; ++i) { cum += P.w[i]; if (cum > t) { pick = i; break; } }
-                    tok = P.id[pick];
-                }
+        double pw;
+        list_dist(p, tv, ti, tvalid, P, pw);
+        int32_t tok = -1;
+        if (tvalid) {
+            if (!(p.temperature > 0.0f)) tok = P.id[0];
+            else {
+                const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
+                double cum = 0.0;
+                int pick = P.support - 1;
+                for (int i = 0; i < P.support; ++i) { cum += readlane_d(pw, i); if (cum > t) { pick = i; break; } }
+                tok = P.id[pick];
             }
-            put_dec(out, PosDecision{tok, 0u, 0, 0});
         }
+        if (k == 0) put_dec(out, PosDecision{tok, 0u, 0, 0});
         return;
     }
     const size_t dr = size_t(l) * drafts + j;
-    list_dist(p, tv, ti, tvalid, P);
-    list_dist(p, dv, di, dvalid, Q);
-    const int32_t d = drafted[dr];
+    const int32_t d = drafted[dr];   // (issued first: its latency and the draws' work overlap the lists')
+    const double ua = philox_uniform(p.seed, p.lane, p.position + j, 1u);
+    const double uc = philox_uniform(p.seed, p.lane, p.position + j, 2u);
+    double pw, qw;
+    list_dist(p, tv, ti, tvalid, P, pw);
+    list_dist(p, dv, di, dvalid, Q, qw);
     const int iq = (d >= 0 && d < vocabulary) ? list_find(Q, d) : -1;
     const int ip = list_find(P, d);
     uint32_t flags = 0;   // (lane 0's)
     if (k == 0) {
         flags = tflags | dflags;
         if (tvalid == 0 || dvalid == 0) flags |= VI_FLAG_EMPTY;
-        const double ua = philox_uniform(p.seed, p.lane, p.position + j, 1u);
         const double q = iq >= 0 ? Q.w[iq] / Q.sn : 0.0;
         double acc_p = 0.0;
         if (q == 0.0) flags |= VI_FLAG_ZERO_Q;
@@ -157,53 +177,58 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
     wave_sync();
     if (s_accept) return;
     // residual max(0, p - q) over p's support, placed in token-id order by rank
-    // (ids within a list are distinct)
-    if (k < P.support) {
-        const int t = P.id[k];
-        int rank = 0;
-        for (int i = 0; i < P.support; ++i) rank += P.id[i] < t ? 1 : 0;
-        double qt = 0.0;
-        for (int i = 0; i < Q.support; ++i)
-            if (Q.id[i] == t) { qt = Q.w[i] / Q.sn; break; }
-        const double pk = P.w[k] / P.sn;
-        s_rid[rank] = t;
+    // (ids within a list are distinct); the lists' ids and weights read lane by
+    // lane from the lanes holding them
+    const int m = P.support, qs = Q.support;
+    const int pid = k < m ? P.id[k] : 0, qid = k < qs ? Q.id[k] : -1;
+    // (wave-uniform loops: every lane reads every other lane's entry)
+    int rank = 0;
+    for (int i = 0; i < m; ++i) rank += __builtin_amdgcn_readlane(pid, i) < pid ? 1 : 0;
+    int at = -1;   // (the first match: ids within a list are distinct)
+    for (int i = 0; i < qs; ++i) at = (at < 0 && __builtin_amdgcn_readlane(qid, i) == pid) ? i : at;
+    const double qt = at >= 0 ? Q.w[at] / Q.sn : 0.0;
+    if (k < m) {
+        const double pk = pw / P.sn;
+        s_rid[rank] = pid;
         s_pv[rank] = pk;
         s_rv[rank] = fmax(0.0, pk - qt);
     }
     wave_sync();
-    if (k == 0) {
-        const int m = P.support;
-        const double uc = philox_uniform(p.seed, p.lane, p.position + j, 2u);
-        double sum = 0.0;
-        for (int i = 0; i < m; ++i) sum += s_rv[i];
-        int32_t corr = 0;
-        if (!(sum > 1e-9) || !isfinite(sum)) {
-            // No residual mass: correct from p itself (inverse CDF, id order).
-            flags |= VI_FLAG_NO_RESIDUAL;
-            double cum = 0.0;
-            int32_t last = 0;
-            bool found = false;
-            for (int i = 0; i < m; ++i) {
-                const double pv = s_pv[i];
-                if (pv > 0.0) last = s_rid[i];
-                cum += pv;
-                if (uc < cum) { corr = s_rid[i]; found = true; break; }
-            }
-            if (!found) corr = last;
-        } else {
-            double cum = 0.0;
-            int32_t last = 0;
-            bool found = false;
-            for (int i = 0; i < m; ++i) {
-                const double r = s_rv[i] / sum;
-                if (r > 0.0) last = s_rid[i];
-                cum += r;
-                if (uc < cum) { corr = s_rid[i]; found = true; break; }
-            }
-            if (!found) corr = last;
+    flags = uint32_t(__builtin_amdgcn_readfirstlane(int(flags)));
+    const double rv = k < m ? s_rv[k] : 0.0, pvk = k < m ? s_pv[k] : 0.0;
+    const int rid = k < m ? s_rid[k] : 0;
+    double sum = 0.0;
+    for (int i = 0; i < m; ++i) sum += readlane_d(rv, i);
+    int32_t corr = 0;
+    if (!(sum > 1e-9) || !isfinite(sum)) {
+        // No residual mass: correct from p itself (inverse CDF, id order).
+        flags |= VI_FLAG_NO_RESIDUAL;
+        double cum = 0.0;
+        int32_t last = 0;
+        bool found = false;
+        for (int i = 0; i < m; ++i) {
+            const double pv = readlane_d(pvk, i);
+            const int32_t ri = __builtin_amdgcn_readlane(rid, i);
+            if (pv > 0.0) last = ri;
+            cum += pv;
+            if (uc < cum) { corr = ri; found = true; break; }
         }
-        put_dec(out, PosDecision{corr, flags, 0, 0});
+        if (!found) corr = last;
+    } else {
+        const double rk = rv / sum;   // (each lane's share, divided in parallel)
+        double cum = 0.0;
+        int32_t last = 0;
+        bool found = false;
+        for (int i = 0; i < m; ++i) {
+            const double r = readlane_d(rk, i);
+            const int32_t ri = __builtin_amdgcn_readlane(rid, i);
+            if (r > 0.0) last = ri;
+            cum += r;
+            if (uc < cum) { corr = ri; found = true; break; }
+        }
+        if (!found) corr = last;
     }
+    if (k == 0) put_dec(out, PosDecision{corr, flags, 0, 0});
 }
 
 // The accept chain of lane l over its position decisions (load(j)), in order:
@@ -250,6 +275,70 @@ __device__ __forceinline__ void lane_chain(int l, Load load, int drafts, int tar
     accepted[l] = acc;
     committed_count[l] = c;
     if (lane_flags) lane_flags[l] = flags;
+}
+
+// The same chain walked by one wave: 64 positions' decisions and drafted tokens
+// read at once (load(j) with a different j on every lane), the first position
+// that stops the chain (a rejection, or an accepted terminal token) found by a
+// ballot, the visited positions' flags OR-reduced; the committed entries are
+// written by the lanes that hold them.
+template <class Load>
+__device__ inline void lane_chain_wave(int l, Load load, int drafts, int target_rows, const int32_t* drafted,
+                                       const vi_row_params* params, const int64_t* terminal, int n_terminal,
+                                       int full_ok, int32_t* accepted, int32_t* committed,
+                                       int32_t* committed_count, uint32_t* lane_flags) {
+    const int k = lane_id();
+    int32_t* out = committed + size_t(l) * (drafts + 1);
+    const int32_t* dl = drafted + size_t(l) * drafts;
+    if (verify_list_refused(params[l]) && !full_ok) {   // refused lane: nothing accepted, nothing committed
+        for (int j = k; j <= drafts; j += kMaxK) out[j] = -1;
+        if (k == 0) {
+            accepted[l] = 0;
+            committed_count[l] = 0;
+            if (lane_flags) lane_flags[l] = VI_FLAG_ERROR;
+        }
+        return;
+    }
+    uint32_t flags = 0;   // (wave-uniform)
+    int c = -1, acc = 0;  // (wave-uniform; c < 0: no stop yet)
+    for (int c0 = 0; c0 < drafts && c < 0; c0 += kMaxK) {
+        const int j = c0 + k;
+        const bool in = j < drafts;
+        const PosDecision e = in ? load(j) : PosDecision{-1, 0u, 0, 0};
+        const int32_t d = in ? dl[j] : -1;
+        const bool st = in && (!e.accept || is_terminal(terminal, n_terminal, d));
+        const uint64_t m = ballot(st);
+        const int s = m ? __builtin_ctzll(m) : kMaxK;
+        uint32_t f = (in && k <= s) ? e.flags : 0u;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) f |= uint32_t(__shfl_xor(int(f), o, kMaxK));
+        flags |= f;
+        if (in && k < s) out[j] = d;                     // accepted, the chain goes on
+        if (m) {
+            const bool sa = __builtin_amdgcn_readlane(e.accept, s) != 0;
+            if (k == s) out[j] = e.accept ? d : e.token;   // an accepted terminal token, or the correction
+            c = c0 + s + 1;
+            acc = c0 + s + (sa ? 1 : 0);
+        }
+    }
+    if (c < 0) {   // every draft accepted: the bonus draw, if the lane has a bonus row
+        c = drafts;
+        acc = drafts;
+        if (target_rows == drafts + 1) {
+            const PosDecision b = load(drafts);
+            flags |= b.flags;
+            if (b.token >= 0) {
+                if (k == 0) out[drafts] = b.token;
+                c = drafts + 1;
+            }
+        }
+    }
+    for (int j = c + k; j <= drafts; j += kMaxK) out[j] = -1;
+    if (k == 0) {
+        accepted[l] = acc;
+        committed_count[l] = c;
+        if (lane_flags) lane_flags[l] = flags;
+    }
 }
 
 }  // namespace vi

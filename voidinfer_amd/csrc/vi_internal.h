@@ -82,9 +82,11 @@ vi_status launch_sampled_scores(const void* scores, int dtype, int rows, int voc
                                 hipStream_t stream);
 
 // Sorted, filtered top-k lists (z values, ids) of verification rows.  With
-// `decide` (draft rows, every lane listed, the target rows' lists complete
-// before the launch) each row's last workgroup also takes its position's
-// accept decision, and each lane's last position walks the lane's chain.
+// `decide` (every lane listed) the rows' last workgroups also take decisions:
+// decide_mode 2 over the target rows draws the bonus rows' tokens; decide_mode
+// 1 over the draft rows (the target rows' lists complete before the launch)
+// takes each position's accept decision, and each lane's last position walks
+// the lane's chain.
 struct PosDecision;
 struct VerifyDecideArgs {
     int drafts, target_rows;
@@ -92,6 +94,11 @@ struct VerifyDecideArgs {
     const int* tlidx;
     const uint32_t* tlvalid;
     const uint32_t* tlflags;
+    const float* dlval;      // (the paired launch: the draft rows' lists, and the
+    const int* dlidx;        //  positions' arrival counters [lanes][drafts + 1],
+    const uint32_t* dlvalid; //  zero between calls)
+    const uint32_t* dlflags;
+    uint32_t* parr;
     const int32_t* drafted;
     PosDecision* dec;
     uint32_t* larr;
@@ -105,7 +112,20 @@ struct VerifyDecideArgs {
 vi_status launch_verify_lists(const void* logits, int dtype, int rows, int layout_rows, int layout_slices,
                               int vocabulary, int64_t stride, const vi_row_params* params, int params_div,
                               float* lval, int* lidx, uint32_t* lvalid, uint32_t* lflags, int skip_unlisted,
-                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide = nullptr);
+                              void* ws, size_t ws_bytes, hipStream_t stream, const VerifyDecideArgs* decide = nullptr,
+                              int decide_mode = 0);
+// Target and draft rows of sampled verification in one launch (both row sets
+// 16-byte aligned 16-bit logits, every lane listed): each position's decision
+// is taken by the later of its two rows to finish (a bonus row decides alone),
+// and each lane's last decided position walks the chain.
+vi_status launch_verify_pair(const void* target, int target_dtype, int64_t target_stride, const void* draft,
+                             int draft_dtype, int64_t draft_stride, int lanes, int vocabulary,
+                             const vi_row_params* params, int layout_rows, int layout_slices, float* tval, int* tidx,
+                             uint32_t* tvalid, uint32_t* tflags, float* dval, int* didx, uint32_t* dvalid,
+                             uint32_t* dflags, const VerifyDecideArgs& decide, void* ws, size_t ws_bytes,
+                             hipStream_t stream);
+bool verify_pair_supported(const void* target, int target_dtype, int64_t target_stride, const void* draft,
+                           int draft_dtype, int64_t draft_stride);
 size_t topk_partials_bytes_slices(int rows, int slices);
 
 // History hash (token -> count) per row for the top-k sampler route.
