@@ -90,3 +90,14 @@ def test_rejects_invalid(dev):
         vi.topk_rows(t, 16)
     with pytest.raises(ValueError):
         vi.topk_rows(torch.zeros(2, 100, dtype=torch.float16, device=dev), 65)
+
+
+@pytest.mark.parametrize("k", [8, 50])
+def test_two_batch_slices(orc, dev, rng, k):
+    """300 rows of 200,000 fp16 logits: 4 slices of 50,000 per row, so each
+    lane of the held scan takes two batches of vectors (the second gated by the
+    first batch's threshold)."""
+    rows, vocab = 300, 200_000
+    x = rng.standard_normal((rows, vocab)).astype(np.float32) * 1.5
+    x[np.arange(rows)[:, None], rng.integers(0, vocab, (rows, 6))] = rng.uniform(6, 10, (rows, 6))
+    run(orc, dev, x.astype(np.float16).view(np.uint16), 1, k)

@@ -1037,146 +1037,168 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     auto held_scan = [&](int nvec) {
       if constexpr (kHeldMode) {
         constexpr int P = Elem<DT>::kPerVec;
+        constexpr int kBatch = kHeld * kTopkThreads;   // vectors of one held batch
         typedef _Float16 h2t __attribute__((ext_vector_type(2)));
         auto H = [](uint32_t w) { return __builtin_bit_cast(h2t, w); };
         const int tid = int(threadIdx.x);
         const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * 2;
-        // (unconditional loads at clamped in-bounds addresses: past the end a
-        // lane reads the slice's last vector again and leaves it out below)
-        uint4 d[kHeld];
-#pragma unroll
-        for (int u = 0; u < kHeld; ++u) d[u] = load16(base + size_t(min(u * kTopkThreads + tid, nvec - 1)) * 16);
+        const int nb = (nvec + kBatch - 1) / kBatch;   // (one or two batches; uniform)
         if (threadIdx.x == 0) { s_np = 0; s_over = 0; }
         const bool scaled = MODE == kModeVerify && p.temperature > 0.0f;
-        // (vector maxima kept as their 16-bit patterns, two to a register)
-        uint32_t vm2[kHeld / 2];
-        float lmax = -kInfF, amin = kInfF;
-        h2t hmin = H(0x7c007c00u);
-        int nok = 0;
+        uint32_t vadd = 0;      // (the fast path's finite logits, counted once every batch passed)
+        float tau_g = -kInfF;   // the workgroup's gate, from the first batch
+        bool exact = false;
+#pragma unroll 1
+        for (int bt = 0; bt < nb; ++bt) {
+            const int v0 = bt * kBatch;
+            // (unconditional loads at clamped in-bounds addresses: past the end a
+            // lane reads the slice's last vector again and leaves it out below)
+            uint4 d[kHeld];
 #pragma unroll
-        for (int u = 0; u < kHeld; ++u) {
-            const bool ok = u * kTopkThreads + tid < nvec;
-            float mx;
-            uint32_t mb;
-            if constexpr (DT == VI_F16) {
-                const h2t hx = H(d[u].x), hy = H(d[u].y), hz = H(d[u].z), hw = H(d[u].w);
-                const h2t t = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hx, hy),
-                                                            __builtin_elementwise_maximum(hz, hw));
-                hmin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(hmin, __builtin_elementwise_minimum(hx, hy)),
-                                                     __builtin_elementwise_minimum(hz, hw));
-                const _Float16 hm = __builtin_elementwise_maximum(t[0], t[1]);
-                mx = float(hm);
-                mb = uint32_t(__builtin_bit_cast(uint16_t, hm));
-            } else {   // (a word at a time: its two logits as floats, one three-way max / min each)
-                const uint32_t w4[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
-                mx = -kInfF;
+            for (int u = 0; u < kHeld; ++u)
+                d[u] = load16(base + size_t(min(v0 + u * kTopkThreads + tid, nvec - 1)) * 16);
+            // (vector maxima kept as their 16-bit patterns, two to a register)
+            uint32_t vm2[kHeld / 2];
+            float lmax = -kInfF, amin = kInfF;
+            h2t hmin = H(0x7c007c00u);
+            int nok = 0;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float lo = __builtin_bit_cast(float, w4[q] << 16);
-                    const float hi = __builtin_bit_cast(float, w4[q] & 0xffff0000u);
-                    mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, lo), hi);
-                    amin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(amin, lo), hi);
+            for (int u = 0; u < kHeld; ++u) {
+                const bool ok = v0 + u * kTopkThreads + tid < nvec;
+                float mx;
+                uint32_t mb;
+                if constexpr (DT == VI_F16) {
+                    const h2t hx = H(d[u].x), hy = H(d[u].y), hz = H(d[u].z), hw = H(d[u].w);
+                    const h2t t = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hx, hy),
+                                                                __builtin_elementwise_maximum(hz, hw));
+                    hmin = __builtin_elementwise_minimum(
+                        __builtin_elementwise_minimum(hmin, __builtin_elementwise_minimum(hx, hy)),
+                        __builtin_elementwise_minimum(hz, hw));
+                    const _Float16 hm = __builtin_elementwise_maximum(t[0], t[1]);
+                    mx = float(hm);
+                    mb = uint32_t(__builtin_bit_cast(uint16_t, hm));
+                } else {   // (a word at a time: its two logits as floats, one three-way max / min each)
+                    const uint32_t w4[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
+                    mx = -kInfF;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float lo = __builtin_bit_cast(float, w4[q] << 16);
+                        const float hi = __builtin_bit_cast(float, w4[q] & 0xffff0000u);
+                        mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, lo), hi);
+                        amin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(amin, lo), hi);
+                    }
+                    mb = __builtin_bit_cast(uint32_t, mx) >> 16;
                 }
-                mb = __builtin_bit_cast(uint32_t, mx) >> 16;
-            }
-            constexpr uint32_t kNegInf = DT == VI_F16 ? 0xfc00u : 0xff80u;
-            mb = ok ? mb : kNegInf;
-            if (want_lse) {   // (against the largest vector maximum so far, as it arrives)
-                lse_rebase(ok ? mx : -kInfF);
-                float sm = 0.0f;
+                constexpr uint32_t kNegInf = DT == VI_F16 ? 0xfc00u : 0xff80u;
+                mb = ok ? mb : kNegInf;
+                if (want_lse) {   // (against the largest vector maximum so far, as it arrives)
+                    lse_rebase(ok ? mx : -kInfF);
+                    float sm = 0.0f;
 #pragma unroll
-                for (int j = 0; j < P; ++j) sm += lse_term(Elem<DT>::decode(vec_bits<DT>(d[u], j)));
-                lse_s += ok ? sm : 0.0f;
+                    for (int j = 0; j < P; ++j) sm += lse_term(Elem<DT>::decode(vec_bits<DT>(d[u], j)));
+                    lse_s += ok ? sm : 0.0f;
+                }
+                if (u & 1) vm2[u / 2] |= mb << 16;
+                else vm2[u / 2] = mb;
+                lmax = ok ? __builtin_elementwise_maximum(lmax, mx) : lmax;
+                nok += ok ? 1 : 0;
             }
-            if (u & 1) vm2[u / 2] |= mb << 16;
-            else vm2[u / 2] = mb;
-            lmax = ok ? __builtin_elementwise_maximum(lmax, mx) : lmax;
-            nok += ok ? 1 : 0;
-        }
-        if constexpr (DT == VI_F16) amin = float(__builtin_elementwise_minimum(hmin[0], hmin[1]));
-        // (the minimum also covers re-read vectors: they belong to the slice, so
-        // at worst another lane's non-finite logit sends the workgroup the exact way)
-        bool bad = !isfinite(amin) || lmax == kInfF || __builtin_isnan(lmax);
-        if (scaled) bad = bad || !isfinite(amin * inv_t) || (lmax > -kInfF && !isfinite(lmax * inv_t));
-        // the wave's K-th largest lane maximum: a radix select over the order
-        // keys, one ballot per bit
-        {
-            const float lm = scaled ? lmax * inv_t : lmax;
-            const uint32_t b = __builtin_bit_cast(uint32_t, lm);
-            const uint32_t key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-            uint32_t t = 0;
+            if constexpr (DT == VI_F16) amin = float(__builtin_elementwise_minimum(hmin[0], hmin[1]));
+            // (the minimum also covers re-read vectors: they belong to the slice, so
+            // at worst another lane's non-finite logit sends the workgroup the exact way)
+            bool bad = !isfinite(amin) || lmax == kInfF || __builtin_isnan(lmax);
+            if (scaled) bad = bad || !isfinite(amin * inv_t) || (lmax > -kInfF && !isfinite(lmax * inv_t));
+            if (bt == 0) s_first[wave][lane] = scaled ? lmax * inv_t : lmax;
+            if (__syncthreads_or(bad ? 1 : 0)) {
+                exact = true;
+                break;
+            }
+            if (bt == 0) {
+                // The workgroup's gate: the K-th largest of its 256 lane maxima
+                // (distinct logits: at least K logits of the first batch reach
+                // it, so it gates the later batch as well), by a radix select
+                // over their order keys that every wave runs on the same four
+                // values per lane (one ballot per value and bit, no barrier).
+                uint32_t key[kTopkWaves];
 #pragma unroll
-            for (int bit = 31; bit >= 0; --bit) {
-                const uint32_t c = t | (1u << bit);
-                if (__builtin_popcountll(ballot(key >= c)) >= K) t = c;
+                for (int w = 0; w < kTopkWaves; ++w) {
+                    const uint32_t kb = __builtin_bit_cast(uint32_t, s_first[w][lane]);
+                    key[w] = (kb & 0x80000000u) ? ~kb : (kb | 0x80000000u);
+                }
+                uint32_t t = 0;
+#pragma unroll
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t c = t | (1u << bit);
+                    int cnt = 0;
+#pragma unroll
+                    for (int w = 0; w < kTopkWaves; ++w) cnt += __builtin_popcountll(ballot(key[w] >= c));
+                    if (cnt >= K) t = c;
+                }
+                tau_g = __builtin_bit_cast(float, (t & 0x80000000u) ? (t & 0x7fffffffu) : ~t);
             }
-            if (lane == 0) s_tw[wave] = __builtin_bit_cast(float, (t & 0x80000000u) ? (t & 0x7fffffffu) : ~t);
+            vadd += uint32_t(nok * P);
+            // the vectors reaching it, staged per wave (at most one per lane: the
+            // loop stays small enough to unroll, which keeps the vectors in registers)
+            int nst = 0;   // (wave-uniform)
+#pragma unroll
+            for (int u = 0; u < kHeld; ++u) {
+                const float vr = Elem<DT>::decode((u & 1) ? vm2[u / 2] >> 16 : vm2[u / 2] & 0xffffu);
+                const float vs = scaled ? vr * inv_t : vr;
+                const bool c = v0 + u * kTopkThreads + tid < nvec && vs >= tau_g;
+                const uint64_t m = ballot(c);
+                if (m) {   // (uniform: most vectors have no candidate in the wave)
+                    const int pos = nst + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+                    if (c && pos < kWave) {
+                        s_hv[wave][pos] = d[u];
+                        s_hid[wave][pos] = begin + (v0 + u * kTopkThreads + tid) * P;
+                    }
+                    nst += int(__builtin_popcountll(m));
+                }
+            }
+            // their logits reaching it, pooled for the workgroup
+            if (nst <= kWave) {
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                const bool have = lane < nst;
+                const uint4 v = s_hv[wave][lane];
+                const int id0 = s_hid[wave][lane];
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    float x = Elem<DT>::decode(vec_bits<DT>(v, j));
+                    if (scaled) x = x * inv_t;
+                    const bool c = have && x >= tau_g;
+                    const uint64_t m = ballot(c);
+                    if (m) {
+                        int at = 0;
+                        if (lane == 0) at = atomicAdd(&s_np, int(__builtin_popcountll(m)));
+                        at = __builtin_amdgcn_readfirstlane(at);
+                        const int pos = at + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+                        if (c && pos < kPool) { s_pv[pos] = x; s_pi[pos] = id0 + j; }
+                    }
+                }
+                // (the staging area is written again by the next batch)
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            } else if (lane == 0) {
+                s_over = 1;
+            }
         }
-        if (__syncthreads_or(bad ? 1 : 0)) {
-            lse_m = -kInfF;   // (the exact path starts the log-sum-exp again)
+        if (exact) {   // the element-exact path over every vector, the log-sum-exp started again
+            lse_m = -kInfF;
             lse_s = 0.0f;
 #pragma unroll 1
-            for (int u = 0; u < kHeld; ++u) {
-                const int v = u * kTopkThreads + tid;
+            for (int v = tid; v < nb * kBatch; v += kTopkThreads)
                 vec_exact(load16(base + size_t(min(v, nvec - 1)) * 16), begin + v * P, v < nvec);
-            }
             return;
         }
-        if constexpr (MODE == kModeVerify) valid += uint32_t(nok * P);
-        // the workgroup's gate: the largest of the waves' K-th lane maxima
-        float tau_g = s_tw[0];
-#pragma unroll
-        for (int w = 1; w < kTopkWaves; ++w) tau_g = fmaxf(tau_g, s_tw[w]);
-        // the vectors reaching it, staged per wave (at most one per lane: the
-        // loop stays small enough to unroll, which keeps the vectors in registers)
-        int nst = 0;   // (wave-uniform)
-#pragma unroll
-        for (int u = 0; u < kHeld; ++u) {
-            const float vr = Elem<DT>::decode((u & 1) ? vm2[u / 2] >> 16 : vm2[u / 2] & 0xffffu);
-            const float vs = scaled ? vr * inv_t : vr;
-            const bool c = u * kTopkThreads + tid < nvec && vs >= tau_g;
-            const uint64_t m = ballot(c);
-            if (m) {   // (uniform: most vectors have no candidate in the wave)
-                const int pos = nst + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
-                if (c && pos < kWave) {
-                    s_hv[wave][pos] = d[u];
-                    s_hid[wave][pos] = begin + (u * kTopkThreads + tid) * P;
-                }
-                nst += int(__builtin_popcountll(m));
-            }
-        }
-        // their logits reaching it, pooled for the workgroup
-        if (nst <= kWave) {
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            const bool have = lane < nst;
-            const uint4 v = s_hv[wave][lane];
-            const int id0 = s_hid[wave][lane];
-#pragma unroll
-            for (int j = 0; j < P; ++j) {
-                float x = Elem<DT>::decode(vec_bits<DT>(v, j));
-                if (scaled) x = x * inv_t;
-                const bool c = have && x >= tau_g;
-                const uint64_t m = ballot(c);
-                if (m) {
-                    int at = 0;
-                    if (lane == 0) at = atomicAdd(&s_np, int(__builtin_popcountll(m)));
-                    at = __builtin_amdgcn_readfirstlane(at);
-                    const int pos = at + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
-                    if (c && pos < kPool) { s_pv[pos] = x; s_pi[pos] = id0 + j; }
-                }
-            }
-        } else if (lane == 0) {
-            s_over = 1;
-        }
+        if constexpr (MODE == kModeVerify) valid += vadd;
         wave_partials();
         __syncthreads();
         const int n = s_np;
         if (s_over || n > kPool) {
             // too many candidates to pool: read again, offered into the wave lists
 #pragma unroll 1
-            for (int u = 0; u < kHeld; ++u) {
-                const int vi = u * kTopkThreads + tid;
+            for (int vi = tid; vi < nb * kBatch; vi += kTopkThreads) {
                 const uint4 v = load16(base + size_t(min(vi, nvec - 1)) * 16);
                 float vm = -kInfF;
 #pragma unroll
@@ -1190,13 +1212,20 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
         // wave 0 places each pooled logit by its rank among them (ids are
         // distinct, so the ranks are)
         if (wave == 0) {
+            // (the pooled logits a wave's worth at a time in registers; each
+            // lane counts the better ones read lane by lane)
             for (int t0 = 0; t0 < n; t0 += kWave) {
                 const int t = t0 + lane;
                 const float v = s_pv[min(t, n - 1)];
                 const int i = s_pi[min(t, n - 1)];
                 int rank = 0;
-#pragma unroll 8
-                for (int j = 0; j < n; ++j) rank += better(s_pv[j], s_pi[j], v, i) ? 1 : 0;
+                for (int c0 = 0; c0 < n; c0 += kWave) {
+                    const float cv = s_pv[min(c0 + lane, n - 1)];
+                    const int ci = s_pi[min(c0 + lane, n - 1)];
+                    const int m = min(kWave, n - c0);
+                    for (int j = 0; j < m; ++j)
+                        rank += better(readlane_f(cv, j), readlane_i(ci, j), v, i) ? 1 : 0;
+                }
                 if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
             }
             __builtin_amdgcn_wave_barrier();
@@ -1214,7 +1243,7 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     auto held_fits = [&]() {
         if constexpr (kHeldMode) {
             const int nvec = (end - begin) / Elem<DT>::kPerVec;
-            return nvec > 0 && nvec <= kHeld * kTopkThreads;
+            return nvec > 0 && nvec <= 2 * kHeld * kTopkThreads;   // (one or two held batches)
         }
         return false;
     };
@@ -1791,8 +1820,12 @@ vi_status launch_verify_pair(const void* target, int target_dtype, int64_t targe
     if (!verify_pair_supported(target, target_dtype, target_stride, draft, draft_dtype, draft_stride))
         return VI_ERR_UNSUPPORTED;
     const int trows = lanes * decide.target_rows, drows = lanes * decide.drafts;
-    // one slicing for both halves (the larger row set's)
-    const TopkPlan plan = topk_plan(std::max(trows, drows), vocabulary);
+    // one slicing for both halves, about 1,024 workgroups for the two row sets
+    // together (one round at four per CU; a slice of up to two held batches)
+    TopkPlan plan;
+    plan.slices = std::max(1, std::min({32, (1024 + trows + drows - 1) / (trows + drows), vocabulary / 2048}));
+    plan.slice_len = slice_len_for(vocabulary, plan.slices);
+    plan.slices = (vocabulary + plan.slice_len - 1) / plan.slice_len;
     if (trows + drows > layout_rows || plan.slices > layout_slices) return VI_ERR_WORKSPACE;
     Carver c(ws, ws_bytes);
     const Partials part = carve_partials(c, layout_rows, layout_slices);
