@@ -304,12 +304,34 @@ __device__ __forceinline__ void range_pass(const FullVerifyArgs& a, size_t tr, s
     const double tinv = TB.valid ? 1.0 / TB.s_n : 0.0, dinv = DB.valid ? 1.0 / DB.s_n : 0.0;
     const uint32_t bt = range_base<TDT>(a.t, tr, TB, r0, tmp), bd = range_base<DDT>(a.d, dr, DB, r0, tmp);
     const int e0 = r0 + kREPT * int(threadIdx.x);
+    // this thread's kREPT consecutive logits of each row: whole 16-byte vectors
+    // when the row is aligned and they are all inside the range (the pass is
+    // latency bound: a few wide loads instead of one 2- or 4-byte load each)
+    uint32_t bt_[kREPT], bd_[kREPT];
+    auto fetch = [&](const void* rowp, auto dt, uint32_t (&b)[kREPT]) {
+        constexpr int DT = decltype(dt)::value;
+        constexpr int PV = Elem<DT>::kPerVec;
+        const unsigned char* p = static_cast<const unsigned char*>(rowp) + size_t(e0) * (DT == VI_F32 ? 4 : 2);
+        if (e0 + kREPT <= r1 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+#pragma unroll
+            for (int q = 0; q < kREPT / PV; ++q) {
+                const uint4 v = load16_cached(p + 16 * q);
+#pragma unroll
+                for (int j = 0; j < PV; ++j) b[q * PV + j] = vec_bits<DT>(v, j);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < kREPT; ++e) b[e] = e0 + e < r1 ? load_bits<DT>(rowp, e0 + e) : 0u;
+        }
+    };
+    fetch(trow, std::integral_constant<int, TDT>{}, bt_);
+    fetch(drow, std::integral_constant<int, DDT>{}, bd_);
     uint32_t kt[kREPT], kd[kREPT], ct = 0u, cd = 0u;
 #pragma unroll
     for (int e = 0; e < kREPT; ++e) {
         const int i = e0 + e;
-        kt[e] = i < r1 ? dist_key<TDT>(load_bits<TDT>(trow, i), TB.inv_t) : 0u;
-        kd[e] = i < r1 ? dist_key<DDT>(load_bits<DDT>(drow, i), DB.inv_t) : 0u;
+        kt[e] = i < r1 ? dist_key<TDT>(bt_[e], TB.inv_t) : 0u;
+        kd[e] = i < r1 ? dist_key<DDT>(bd_[e], DB.inv_t) : 0u;
         ct += counts_rank(kt[e], TB) ? 1u : 0u;
         cd += counts_rank(kd[e], DB) ? 1u : 0u;
     }
@@ -397,31 +419,41 @@ __global__ __launch_bounds__(kRT) void verify_full_correction_kernel(FullVerifyA
     if (!verify_list_refused(p)) return;
     const int js = first_rejection(a, l);
     if (js < 0) return;
-    if (tid == 0) {   // the ranges in order
+    if (wave == 0) {   // the ranges in order (each lane loads a range's sums; the sums read lane by lane)
         double R = 0.0, P = 0.0;
         int lr = -1, lp = -1;
-        for (int r = 0; r < a.ranges; ++r) {
+        for (int r0 = 0; r0 < a.ranges; r0 += kWave) {
+            const int r = min(r0 + lane, a.ranges - 1);
             const size_t at = (size_t(l) * a.ranges + r) * 2;
-            R += a.rsum[at];
-            P += a.rsum[at + 1];
-            lr = max(lr, a.rlast[at]);
-            lp = max(lp, a.rlast[at + 1]);
+            const double rs = a.rsum[at], ps = a.rsum[at + 1];
+            const int rl = a.rlast[at], pl = a.rlast[at + 1];
+            for (int q = 0; q < min(kWave, a.ranges - r0); ++q) {
+                R += readlane_d(rs, q);
+                P += readlane_d(ps, q);
+                lr = max(lr, __builtin_amdgcn_readlane(rl, q));
+                lp = max(lp, __builtin_amdgcn_readlane(pl, q));
+            }
         }
         const double uc = philox_uniform(p.seed, p.lane, p.position + js, 2u);
         const bool nores = !(R > 1e-9) || !isfinite(R);
         const double target = nores ? uc : uc * R;
         int range = -1;
         double cum = 0.0;
-        for (int r = 0; r < a.ranges && range < 0; ++r) {
-            const double m = a.rsum[(size_t(l) * a.ranges + r) * 2 + (nores ? 1 : 0)];
-            if (cum + m > target) range = r;
-            else cum += m;
+        for (int r0 = 0; r0 < a.ranges && range < 0; r0 += kWave) {
+            const double mv = a.rsum[(size_t(l) * a.ranges + min(r0 + lane, a.ranges - 1)) * 2 + (nores ? 1 : 0)];
+            for (int q = 0; q < min(kWave, a.ranges - r0) && range < 0; ++q) {
+                const double m = readlane_d(mv, q);
+                if (cum + m > target) range = r0 + q;
+                else cum += m;
+            }
         }
-        s_range = range;
-        s_before = cum;
-        s_target = target;
-        s_nores = nores ? 1u : 0u;
-        s_tok = max(0, nores ? lp : lr);   // (round-off past the end)
+        if (lane == 0) {
+            s_range = range;
+            s_before = cum;
+            s_target = target;
+            s_nores = nores ? 1u : 0u;
+            s_tok = max(0, nores ? lp : lr);   // (round-off past the end)
+        }
     }
     __syncthreads();
     const int range = s_range;
