@@ -590,14 +590,22 @@ __device__ __forceinline__ uint32_t halves_key(uint32_t d) {
     const s2 sg = __builtin_bit_cast(s2, d) >> 15;   // 0 or -1 per half
     return d ^ (__builtin_bit_cast(uint32_t, sg) | 0x80008000u);
 }
-// Per half of the word of keys `k2`: 1 where k2 - base exceeds width (no match),
-// 0 where it lies in [base, base + width]; halves' base and width given.
-__device__ __forceinline__ uint32_t halves_miss(uint32_t k2, uint32_t base2, uint32_t width2) {
+// Per 16-bit half: a - b (wrapping), max(a - b, 0), and min(a, 1).  The last
+// two are written as the packed instructions (the compiler otherwise turns the
+// pair into a compare and a select per half).
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
     typedef unsigned short u2 __attribute__((ext_vector_type(2)));
-    const u2 t = __builtin_bit_cast(u2, k2) - __builtin_bit_cast(u2, base2);
-    const u2 u = __builtin_elementwise_sub_sat(t, __builtin_bit_cast(u2, width2));
-    const u2 m = __builtin_elementwise_min(u, u2{1, 1});
-    return __builtin_bit_cast(uint32_t, m);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u2, a) - __builtin_bit_cast(u2, b));
+}
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_nonzero_u16(uint32_t a) {
+    uint32_t r;
+    asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(0x00010001u));
+    return r;
 }
 
 template <int DT>
@@ -720,6 +728,11 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         for (int o = 32; o; o >>= 1) top = max(top, uint32_t(__shfl_xor(int(top), o, kWave)));
         if (lane == 0 && top) atomicMax(&sh.z0key, top);
     }
+    // The first repeat entries' logits, requested now (clamped into the row)
+    // and used by the rescan once the owner part is known.
+    uint32_t rraw[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) rraw[j] = uint32_t(row16[min(rep[j].x, uint32_t(V - 1))]);
     lds_barrier();
     const uint32_t z0key = sh.z0key;
     const double z0 = double(key_z<DT>(z0key, inv_t));
@@ -1076,19 +1089,26 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
                     atomicAdd(&sh.nflip, 1u);
                 }
             };
-            uint32_t raw[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if (uint32_t(j * kT + tid) >= pv.nrep) rep[j].y = 0u;
-                raw[j] = in_owner(rep[j]) ? uint32_t(row16[rep[j].x]) : 0u;
+                flip_if(rep[j], rraw[j]);
             }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) flip_if(rep[j], raw[j]);
             for (uint32_t i = uint32_t(2 * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
                 const uint2 e = pv.list[i];
                 if (in_owner(e)) flip_if(e, uint32_t(row16[e.x]));
             }
         }
+        // presence masks by byte, in the decisions' running-sum table (free
+        // now): entry b, word q: the halves of tokens 2q and 2q + 1 all ones
+        // where that token is in the history
+        uint4* pmask = reinterpret_cast<uint4*>(lds + kOffMCab);
+        {
+            const uint32_t b = uint32_t(tid) >> 2, q = uint32_t(tid) & 3u;
+            reinterpret_cast<uint32_t*>(pmask)[tid] = (((b >> (2u * q)) & 1u) ? 0x0000ffffu : 0u) |
+                                                     (((b >> (2u * q + 1u)) & 1u) ? 0xffff0000u : 0u);
+        }
+        static_assert(256 * 16 <= kOffMMab - kOffMCab && kT == 1024, "presence masks");
         lds_barrier();
         // In the halves' key space (-0 just below +0): an absent token matches
         // when its key lies in [a0, a0 + w0] (the drawn key, with -0 for +0), a
@@ -1103,6 +1123,7 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             a1 = lo; w1 = hi - lo; empty1 = false;
         }
         const uint32_t A0 = a0 | (a0 << 16), W0 = w0 | (w0 << 16), A1 = a1 | (a1 << 16), W1 = w1 | (w1 << 16);
+        const uint32_t force = empty1 ? 0xffffffffu : 0u;   // history halves never match
         const bool flips = sh.nflip != 0u;
         // exact match bits of one vector (the scalar form of the count below)
         auto match_bits = [&](uint4 d, uint32_t b, int v) -> uint32_t {
@@ -1119,36 +1140,41 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
             if (flips) m ^= (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
             return m;
         };
-        // matches counted per round
-        uint32_t cnt[8];
+        // Matches per round, three rounds to a word in 10-bit fields (a wave's
+        // sums stay below 1024): per half, the range of the token's kind is
+        // selected by the presence mask and tested as max(key - base - width, 0)
+        // == 0.
+        uint32_t pc[3] = {0u, 0u, 0u};
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const int v = r * kT + tid;
             uint32_t c = 0u;
             if (v < it.nvec) {
-                const uint32_t fl = flips ? (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu : 0u;
-                if (fl) {
-                    c = uint32_t(__builtin_popcount(match_bits(vv[r], bb[r], v)));
-                } else {
-                    const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
-                    uint32_t miss = 0u;
+                const uint4 M = pmask[bb[r]];
+                const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
+                const uint32_t m4[4] = {M.x, M.y, M.z, M.w};
+                uint32_t miss = 0u;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        // presence of tokens 2q, 2q + 1 as a half mask
-                        const uint32_t M = (uint32_t(int32_t(bb[r] << (31 - 2 * q)) >> 31) & 0xffffu) |
-                                           (uint32_t(int32_t(bb[r] << (30 - 2 * q)) >> 31) & 0xffff0000u);
-                        const uint32_t k2 = halves_key(w4[q]);
-                        const uint32_t ma = halves_miss(k2, A0, W0);
-                        const uint32_t mp = empty1 ? 0x00010001u : halves_miss(k2, A1, W1);
-                        const uint32_t mm = (mp & M) | (ma & ~M);
-                        miss += (mm & 0xffffu) + (mm >> 16);
-                    }
-                    c = 8u - miss;
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t base = (m4[q] & A1) | (~m4[q] & A0), width = (m4[q] & W1) | (~m4[q] & W0);
+                    const uint32_t t = pk_sub_u16(halves_key(w4[q]), base);
+                    miss += pk_nonzero_u16(pk_sub_sat_u16(t, width) | (m4[q] & force));
+                }
+                c = 8u - (miss & 0xffffu) - (miss >> 16);
+                if (flips) {
+                    const uint32_t fl = (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
+                    if (fl) c = uint32_t(__builtin_popcount(match_bits(vv[r], bb[r], v)));
                 }
             }
-            cnt[r] = c;
-            const uint32_t incl = wave_incl_scan_u32(c);
-            if (lane == kWave - 1) sh.wtot[r][wave] = incl;
+            pc[r / 3] += c << (10 * (r % 3));
+        }
+        uint32_t pin[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pin[i] = wave_incl_scan_u32(pc[i]);
+        auto field = [](uint32_t w, int r) { return (w >> (10 * (r % 3))) & 0x3ffu; };
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) sh.wtot[r][wave] = field(pin[r / 3], r);
         }
         lds_barrier();
         // exclusive offsets of the (round, wave) blocks in id order (wave 0:
@@ -1163,8 +1189,9 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         const uint32_t want = sh.orank;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            const uint32_t e = sh.wtot[r][wave] + wave_incl_scan_u32(cnt[r]) - cnt[r];
-            if (cnt[r] && want >= e && want < e + cnt[r]) {
+            const uint32_t c = field(pc[r / 3], r);
+            const uint32_t e = sh.wtot[r][wave] + field(pin[r / 3], r) - c;
+            if (c && want >= e && want < e + c) {
                 const int v = r * kT + tid;
                 uint32_t m = match_bits(vv[r], bb[r], v);
                 for (uint32_t k = want - e; k > 0u; --k) m &= m - 1u;
