@@ -1030,6 +1030,8 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     __shared__ int s_seli[kMaxK];
     __shared__ float s_tw[kTopkWaves];
     __shared__ int s_np, s_over;
+    constexpr int kMergeHeld = 4;   // slice-list entries per thread in the last arriver's filter
+    __shared__ float s_tauv;
     bool pooled = false;   // (workgroup-uniform) the slice's top K is wave 0's list
     // (16-bit vector rows; bf16 rows in top-k mode keep the batch scan: their
     // held scan with the log-sum-exp does not fit 128 registers)
@@ -1347,12 +1349,17 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
         const float hm = hl ? get_agent(&h.lse_max) : -kInfF;
         const double hs = hl ? get_agent(&h.lse_sum) : 0.0;
         L = WaveList{};
-        if constexpr (MODE == kModeTopk || MODE == kModeVerify) {
-            if (slices * K <= kPool) {
-                // every entry of every slice list, one per thread, into LDS; each
-                // entry's rank among them places the row's top K (padding pairs
-                // (-inf, kInvalidId) are equal and rank after every entry)
-                const int n = slices * K, t = int(threadIdx.x);
+        {
+            // The row's top K by each entry's rank among the pooled entries of
+            // the slice lists: every entry when they fit the pool, else those
+            // whose value reaches the K-th largest of the lists' first entries
+            // (K entries of the row reach it, so the row's top K all do); past
+            // the pool, the lists are merged as a tree below.
+            const int t = int(threadIdx.x);
+            int n = slices * K;
+            bool pooled_all = true;
+            if (n <= kPool) {
+                // (padding pairs (-inf, kInvalidId) are equal and rank after every entry)
                 if (t < n) {
                     const int sl = t / K;
                     const size_t src = (size_t(r) * slices + size_t(sl)) * kMaxK + size_t(t - sl * K);
@@ -1360,6 +1367,43 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
                     s_pi[t] = get_agent(&a.pidx[src]);
                 }
                 __syncthreads();
+            } else if (MODE == kModeSample && n <= kMergeHeld * kTopkThreads) {
+                // this thread's entries (loads at clamped addresses, selected after)
+                float ev[kMergeHeld];
+                int ei[kMergeHeld];
+#pragma unroll
+                for (int u = 0; u < kMergeHeld; ++u) {
+                    const int e = min(t + u * kTopkThreads, n - 1), sl = e / K;
+                    const size_t src = (size_t(r) * slices + size_t(sl)) * kMaxK + size_t(e - sl * K);
+                    ev[u] = get_agent(&a.pval[src]);
+                    ei[u] = get_agent(&a.pidx[src]);
+                }
+                if (wave == 0) {
+                    // the K-th largest value among the lists' first m entries
+                    // (at least K entries of the row reach it)
+                    const int m = max(1, kWave / slices), sl = lane / m, q = lane - sl * m;
+                    const bool ok = sl < slices && q < K;
+                    const size_t src = (size_t(r) * slices + size_t(min(sl, slices - 1))) * kMaxK + size_t(min(q, K - 1));
+                    const float v = get_agent(&a.pval[src]);
+                    const float tv = readlane_f(wave_sort_desc<kD>(ok ? v : -kInfF), K - 1);
+                    if (lane == 0) { s_tauv = tv; s_np = 0; }
+                }
+                __syncthreads();
+                const float tv = s_tauv;
+#pragma unroll
+                for (int u = 0; u < kMergeHeld; ++u) {
+                    if (t + u * kTopkThreads < n && ei[u] != kInvalidId && ev[u] >= tv) {
+                        const int pos = atomicAdd(&s_np, 1);
+                        if (pos < kPool) { s_pv[pos] = ev[u]; s_pi[pos] = ei[u]; }
+                    }
+                }
+                __syncthreads();
+                n = s_np;
+                pooled_all = n <= kPool;
+            } else {
+                pooled_all = false;
+            }
+            if (pooled_all) {
                 // (one entry per thread: more than a wave's worth of entries are
                 // ranked by every wave, then handed to wave 0 through LDS)
                 if (n > kWave || wave == 0) {
