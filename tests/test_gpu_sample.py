@@ -233,6 +233,42 @@ def test_bad_history_tokens_flagged(orc, dev, rng):
     assert (w["stats"]["flags"][0] & 16) and (w["stats"]["flags"][2] & 16)
 
 
+@pytest.mark.parametrize("dtype,vocab", [(0, 5_000), (1, 5_000), (2, 5_000), (0, 300_000)])
+def test_topk_route_bad_history_tokens_flagged(orc, dev, rng, dtype, vocab):
+    # top-k route rows whose histories hold tokens outside [0, V): flagged and
+    # ignored (slices of up to 8,192 tokens count the histories in LDS, larger
+    # ones look the counts up in the history hash)
+    rows = 4
+    bits = make_rows(rng, rows, vocab, dtype=dtype)
+    p = params(rows, rng, temperature=1.0, top_k=20, presence_penalty=0.5, repetition_penalty=1.3)
+    hist = rng.integers(0, vocab, rows * 100).astype(np.int32)
+    hist[105] = -3
+    hist[250] = vocab + 10
+    offs = np.arange(rows + 1, dtype=np.int64) * 100
+    g, w = run_both(orc, dev, bits, dtype, p, hist, offs, want_probs=False)
+    compare(g, w, p, "badhist-topk")
+    assert (w["stats"]["flags"][1] & 16) and (w["stats"]["flags"][2] & 16)
+    assert not (w["stats"]["flags"][0] & 16) and not (w["stats"]["flags"][3] & 16)
+
+
+def test_topk_route_history_past_max_is_an_error(dev, rng):
+    # a history longer than max_history: token -1 and VI_FLAG_ERROR; the other rows are served
+    import voidinfer_amd as vi
+    rows, vocab = 3, 5_000
+    bits = make_rows(rng, rows, vocab)
+    p = params(rows, rng, temperature=1.0, top_k=20, presence_penalty=0.5)
+    lens = np.array([40, 80, 40])
+    hist = rng.integers(0, vocab, int(lens.sum())).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    out = vi.sample_rows(to_dev(bits, 0, dev), p, torch.from_numpy(hist).to(dev), torch.from_numpy(offs).to(dev),
+                         max_history=50)
+    torch.cuda.synchronize()
+    tok, st = out.tokens.cpu().numpy(), vi.stats_numpy(out.stats)
+    assert tok[1] == -1 and (int(st["flags"][1]) & 0x80000000)
+    assert tok[0] >= 0 and tok[2] >= 0
+    assert not (int(st["flags"][0]) & 0x80000000) and not (int(st["flags"][2]) & 0x80000000)
+
+
 def test_config2_mixed_lanes(orc, dev):
     from voidinfer_amd import workloads as W
     bits, hist, offs, p = W.config2()

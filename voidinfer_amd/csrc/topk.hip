@@ -51,6 +51,7 @@ struct SliceHeader {
     double lse_sum;
 };
 constexpr uint32_t kSliceNonfinite = 1u, kSliceNan = 2u, kSliceBadHistory = 4u, kSliceError = 8u;
+constexpr size_t kHistCountLds = 32768;   // most dynamic LDS for a slice's history counts
 
 struct TopkArgs {
     const void* logits;
@@ -95,6 +96,9 @@ struct TopkArgs {
     vi_sample_stats* stats;
     int full_rows_unsupported;  // fp32 logits: rows outside the top-k route fail
     int pres_words;         // dynamic LDS words for the slice's history-presence bitmap (0: none)
+    int hist_counts;        // the dynamic words are the slice's history counts, one per token, counted
+                            // from the histories by every workgroup of the row (no hash)
+    int64_t max_history;
     // kModeVerify: sorted lists of the filtered rows
     int params_div;         // params index = row / params_div
     float* lval;            // [rows][kMaxK]
@@ -470,8 +474,8 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             if (lookups) table = reinterpret_cast<const uint2*>(a.pstate + size_t(r) * a.pl.lane_bytes + a.pl.off_hash);
         } else {
             const int64_t hn = a.offsets ? a.offsets[r + 1] - a.offsets[r] : 0;
-            lookups = penalties_active(p) && hn > 0 && a.hash;
-            if (lookups) table = a.hash + size_t(r) * size_t(a.hash_slots);
+            lookups = penalties_active(p) && hn > 0 && (a.hash || a.hist_counts);
+            if (lookups && a.hash) table = a.hash + size_t(r) * size_t(a.hash_slots);
         }
         lookup_all = lookups && !penalties_lower_only(p);
         if (a.probs) {   // (the row's last arriver writes the support over these zeros:
@@ -486,8 +490,39 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     // lookups of absent tokens (nearly all) never leave the CU
     extern __shared__ uint32_t s_dyn[];
     const uint32_t* pres = nullptr;
+    const uint32_t* hcnt = nullptr;
+    uint32_t hist_flags = 0;   // (this thread's share of the history's check)
     if constexpr (MODE == kModeSample) {
-        if (lookups && a.pres_words > 0) {
+        if (lookups && a.hist_counts) {
+            // the slice's tokens' counts in the lane's history, in LDS; the
+            // history checked as the hash builder checks it
+            uint32_t* cnt = s_dyn;
+            for (int w = threadIdx.x; w < end - begin; w += kTopkThreads) cnt[w] = 0u;
+            __syncthreads();
+            const int64_t hb = a.offsets[r], hn = a.offsets[r + 1] - hb;
+            if (hn > a.max_history) {
+                hist_flags = kSliceError;
+            } else {
+                constexpr int kU = 8;   // (eight loads in flight per thread)
+                for (int64_t i0 = 0; i0 < hn; i0 += kU * kTopkThreads) {
+                    int32_t t[kU];
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) {
+                        const int64_t i = i0 + u * kTopkThreads + threadIdx.x;
+                        t[u] = i < hn ? a.histories[hb + i] : begin - 1;
+                    }
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) {
+                        if (i0 + u * kTopkThreads + threadIdx.x < hn && (t[u] < 0 || t[u] >= a.vocabulary))
+                            hist_flags |= kSliceBadHistory;
+                        else if (t[u] >= begin && t[u] < end)
+                            atomicAdd(&cnt[t[u] - begin], 1u);
+                    }
+                }
+            }
+            __syncthreads();
+            hcnt = cnt;
+        } else if (lookups && a.pres_words > 0) {
             uint32_t* bm = s_dyn;
             const int words = (end - begin + 31) / 32;
             if (a.pstate) {
@@ -519,6 +554,7 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     // bitmap says the token is absent)
     auto count_of = [&](int id) -> uint32_t {
         if (!lookups) return 0u;
+        if (hcnt) return hcnt[id - begin];
         if (pres) {
             const int o = id - begin;
             if (!((pres[o >> 5] >> (o & 31)) & 1u)) return 0u;
@@ -546,7 +582,7 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     auto publish_kth = [&]() {
         if (MODE == kModeTopk && lane_id() == 0) __hip_atomic_store(&s_kth[threadIdx.x / kWave], L.kv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
-    uint32_t flags = 0, valid = 0;
+    uint32_t flags = hist_flags, valid = 0;
     float lse_m = -kInfF, lse_s = 0.0f;
     const bool want_lse = MODE == kModeTopk && a.logprobs != nullptr;
     // Log-sum-exp state in base-2 units: lse_m is the exact f32 value m2 that the
@@ -1628,8 +1664,10 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             uint32_t flags_out = 0;
             if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
             if (lookups)
-                flags_out |= a.pstate ? reinterpret_cast<const PenaltyHeader*>(a.pstate + size_t(r) * a.pl.lane_bytes)->flags
-                                      : a.row_flags[r];
+                flags_out |= a.pstate        ? reinterpret_cast<const PenaltyHeader*>(a.pstate + size_t(r) * a.pl.lane_bytes)->flags
+                             : a.hist_counts ? ((f & kSliceBadHistory) ? uint32_t(VI_FLAG_BAD_HISTORY) : 0u) |
+                                                   ((f & kSliceError) ? uint32_t(VI_FLAG_ERROR) : 0u)
+                                             : a.row_flags[r];
             if (flags_out & VI_FLAG_ERROR) {
                 a.tokens[r] = -1;
                 if (a.uniforms) a.uniforms[r] = 0.0;
@@ -1938,8 +1976,12 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
     const bool full_ok = s.dtype == VI_F32 ? wide_supported(s.vocabulary, s.stride)
                                            : full_supported(s.dtype, s.vocabulary, s.stride);
     vi_status st = VI_OK;
+    // Histories counted straight into each slice's LDS when the slice's counts
+    // fit and no fp32 full-route row needs the hash: no hash launch
+    const bool lds_counts = hash && size_t(plan.slice_len) * 4 <= kHistCountLds &&
+                            !(s.dtype == VI_F32 && (s.route_mask & VI_ROUTE_FULL) && full_ok);
     if (run_topk) {
-        if (hash) {
+        if (hash && !lds_counts) {
             hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(kHashThreads), 0, stream, s.params, s.histories,
                                s.offsets, s.vocabulary, hash, shift, slots, row_flags, s.max_history);
             if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
@@ -1947,11 +1989,15 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         TopkArgs a{};
         a.logits = s.logits; a.vocabulary = s.vocabulary; a.stride = s.stride; a.slice_len = plan.slice_len;
         a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
-        a.params = s.params; a.hash = hash; a.row_flags = row_flags; a.hash_shift = shift; a.hash_slots = slots;
-        a.offsets = s.offsets; a.histories = s.histories;
+        a.params = s.params; a.hash = lds_counts ? nullptr : hash; a.row_flags = row_flags; a.hash_shift = shift;
+        a.hash_slots = slots; a.offsets = s.offsets; a.histories = s.histories; a.max_history = s.max_history;
         // the presence bitmap (one bit per token of a slice, in dynamic LDS) when
-        // penalties are read: up to 64 KB (a slice of up to 524,288 tokens)
-        if (hash || s.pstate) {
+        // penalties are read: up to 64 KB (a slice of up to 524,288 tokens); or
+        // the slice's history counts
+        if (lds_counts) {
+            a.hist_counts = 1;
+            a.pres_words = plan.slice_len;
+        } else if (hash || s.pstate) {
             const size_t words = size_t(plan.slice_len + 31) / 32;
             a.pres_words = words * 4 <= 65536 ? int(words) : 0;
         }
