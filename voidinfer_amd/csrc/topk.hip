@@ -562,6 +562,21 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
         return hash_count(table, a.hash_shift, a.hash_slots, id);
     };
 
+    // Candidate pool of the workgroup (the held scan's and the sample mode's
+    // batched scan's), and the held scan's staging
+    constexpr int kHeld = 16;
+    constexpr int kPool = 256;
+    __shared__ uint4 s_hv[kTopkWaves][kWave];
+    __shared__ int s_hid[kTopkWaves][kWave];
+    __shared__ float s_pv[kPool];
+    __shared__ int s_pi[kPool];
+    __shared__ float s_selv[kMaxK];
+    __shared__ int s_seli[kMaxK];
+    __shared__ float s_tw[kTopkWaves];
+    __shared__ int s_np, s_over;
+    constexpr int kMergeHeld = 4;   // slice-list entries per thread in the last arriver's filter
+    __shared__ float s_tauv;
+    bool pooled = false;   // (workgroup-uniform) the slice's top K is wave 0's list
     // ---- scan the slice
     // Each wave's list K-th value, shared: an element below another wave's K-th
     // entry has K better elements in the row and cannot be in its top k, so
@@ -965,6 +980,18 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
         }
         fill += n;
     };
+    // a candidate into the workgroup's pool (past the pool: into the wave's list)
+    auto pool_put = [&](bool c, float v, int id) {
+        const uint64_t m = ballot(c);
+        if (!m) return;
+        int at = 0;
+        if (lane == 0) at = atomicAdd(&s_np, int(__builtin_popcountll(m)));
+        at = __builtin_amdgcn_readfirstlane(at);
+        const int pos = at + int(__builtin_popcountll(m & ((uint64_t(1) << lane) - 1)));
+        const bool fit = c && pos < kPool;
+        if (fit) { s_pv[pos] = v; s_pi[pos] = id; }
+        stage(c && !fit, v, id);
+    };
     auto sample_batch = [&](const uint4 (&dv)[4], int vb, const bool (&okv)[4]) {
         constexpr int P = Elem<DT>::kPerVec;
         const int id_base = begin + (vb + int(threadIdx.x)) * P;
@@ -1015,7 +1042,7 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
                 if (ballot(want) == 0) continue;
                 float v = -kInfF;
                 const bool c = want && penalized(bits, want ? count_of(id0 + j) : 0u, v) && v >= gate;
-                stage(c, v, id0 + j);
+                pool_put(c, v, id0 + j);
             }
         };
         cand_vec(dv[0], 0, okv[0], vm[0]);
@@ -1056,19 +1083,6 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
         for (int o = 32; o; o >>= 1) s += shfl_xor_d(s, o);
         if (lane == 0) { s_flags[wave] = f; s_valid[wave] = c; s_lm[wave] = m; s_ls[wave] = s; }
     };
-    constexpr int kHeld = 16;
-    constexpr int kPool = 256;
-    __shared__ uint4 s_hv[kTopkWaves][kWave];
-    __shared__ int s_hid[kTopkWaves][kWave];
-    __shared__ float s_pv[kPool];
-    __shared__ int s_pi[kPool];
-    __shared__ float s_selv[kMaxK];
-    __shared__ int s_seli[kMaxK];
-    __shared__ float s_tw[kTopkWaves];
-    __shared__ int s_np, s_over;
-    constexpr int kMergeHeld = 4;   // slice-list entries per thread in the last arriver's filter
-    __shared__ float s_tauv;
-    bool pooled = false;   // (workgroup-uniform) the slice's top K is wave 0's list
     // (16-bit vector rows; bf16 rows in top-k mode keep the batch scan: their
     // held scan with the log-sum-exp does not fit 128 registers)
     constexpr bool kHeldMode = VEC && (DT == VI_F16 || (DT == VI_BF16 && MODE == kModeVerify));
@@ -1296,14 +1310,58 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             elem_fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
         }
     };
+    // Sample mode, batched scan: the pooled candidates ranked into wave 0's
+    // list (merged with what that wave's list holds: exact-path elements and
+    // candidates past the pool); the other waves' lists join in the tree merge
+    // only when they hold anything.
+    __shared__ int s_used[kTopkWaves];
+    auto sample_pool_finish = [&]() {
+        wave_partials();
+        handoff_stores_done();   // every wave's probability zeros
+        if (lane == 0) s_used[wave] = L.v != -kInfF ? 1 : 0;   // (lane 0 holds the list's best)
+        __syncthreads();
+        // each pooled candidate placed by its rank among them (one per thread;
+        // ids are distinct, so the ranks are)
+        const int n = min(s_np, kPool);
+        for (int t = int(threadIdx.x); t - lane < n; t += kTopkThreads) {   // (wave-uniform)
+            const float v = s_pv[min(t, n - 1)];
+            const int i = s_pi[min(t, n - 1)];
+            int rank = 0;
+            for (int c0 = 0; c0 < n; c0 += kWave) {
+                const float cv = s_pv[min(c0 + lane, n - 1)];
+                const int ci = s_pi[min(c0 + lane, n - 1)];
+                const int m = min(kWave, n - c0);
+                for (int j = 0; j < m; ++j) rank += better(readlane_f(cv, j), readlane_i(ci, j), v, i) ? 1 : 0;
+            }
+            if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const bool h = lane < min(K, n);
+            const float pv = h ? s_selv[lane] : -kInfF;
+            const int pi = h ? s_seli[lane] : kInvalidId;
+            if (s_used[0]) {
+                list_merge<kD>(L, K, pv, pi);
+            } else {
+                L.v = pv;
+                L.i = pi;
+                L.kv = readlane_f(L.v, K - 1);
+                L.ki = readlane_i(L.i, K - 1);
+            }
+        }
+        pooled = !(s_used[1] | s_used[2] | s_used[3]);
+    };
     if constexpr (MODE == kModeTopk || MODE == kModeVerify) {
         if (held_fits()) held_then_tail();
         else scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_fn, batch_fn, elem_fn);
     } else if constexpr (MODE == kModeSample) {
-        if (batched)
+        if (batched) {
+            if (threadIdx.x == 0) s_np = 0;   // (ordered by the first batch's barrier)
             scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
-        else
+            sample_pool_finish();
+        } else {
             scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
+        }
     } else {
         scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
     }
