@@ -109,9 +109,11 @@ __device__ __forceinline__ void scan_slice_vec(const void* row, int begin, int e
 // u of the batch is number vb + u * NT + threadIdx.x of the slice), and the
 // next batch's loads issued before the current batch is handed over (two
 // register buffers), so the HBM stream keeps going while a batch is worked on.
+// scan_slice_batches_from: the first batch's vectors already requested by the
+// caller (pre, as loaded here: zeros past the slice's vectors) when use_pre.
 template <int DT, bool VEC, int NT, class FB, class FBatch, class F>
-__device__ __forceinline__ void scan_slice_batches(const void* row, int begin, int end, FB&& first, FBatch&& bfn,
-                                                   F&& fn) {
+__device__ __forceinline__ void scan_slice_batches_from(const void* row, int begin, int end, const uint4 (&pre)[4],
+                                                        bool use_pre, FB&& first, FBatch&& bfn, F&& fn) {
     constexpr int P = Elem<DT>::kPerVec;
     constexpr int U = 4;
     const int tid = threadIdx.x;
@@ -129,7 +131,12 @@ __device__ __forceinline__ void scan_slice_batches(const void* row, int begin, i
         if (nvec > 0) {   // (uniform)
             uint4 d[U];
             bool ok[U];
-            load(0, d, ok);
+            if (use_pre) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) { d[u] = pre[u]; ok[u] = u * NT + tid < nvec; }
+            } else {
+                load(0, d, ok);
+            }
             first(d, ok);
             for (int vb = 0;; vb += U * NT) {
                 const bool more = vb + U * NT < nvec;   // (uniform)
@@ -159,6 +166,13 @@ __device__ __forceinline__ void scan_slice_batches(const void* row, int begin, i
             fn(ok ? load_bits<DT>(row, i) : 0u, i, ok);
         }
     }
+}
+
+template <int DT, bool VEC, int NT, class FB, class FBatch, class F>
+__device__ __forceinline__ void scan_slice_batches(const void* row, int begin, int end, FB&& first, FBatch&& bfn,
+                                                   F&& fn) {
+    const uint4 none[4] = {};
+    scan_slice_batches_from<DT, VEC, NT>(row, begin, end, none, false, first, bfn, fn);
 }
 
 // Slice boundaries: slice s of `slices` covers [s*len, min(V,(s+1)*len)), len a

@@ -492,8 +492,23 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     const uint32_t* pres = nullptr;
     const uint32_t* hcnt = nullptr;
     uint32_t hist_flags = 0;   // (this thread's share of the history's check)
+    uint4 pre[4] = {};         // (sample mode with history counts: the scan's first batch)
+    bool have_pre = false;
     if constexpr (MODE == kModeSample) {
         if (lookups && a.hist_counts) {
+            // the slice's first batch of logits requested before the counting
+            // (its latency and the history's overlap)
+            if constexpr (VEC) {
+                constexpr int P = Elem<DT>::kPerVec;
+                const int nvec = (end - begin) / P;
+                const unsigned char* base = static_cast<const unsigned char*>(row) + size_t(begin) * (16 / P);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = u * kTopkThreads + int(threadIdx.x);
+                    pre[u] = v < nvec ? load16(base + size_t(v) * 16) : make_uint4(0, 0, 0, 0);
+                }
+                have_pre = nvec > 0;
+            }
             // the slice's tokens' counts in the lane's history, in LDS; the
             // history checked as the hash builder checks it
             uint32_t* cnt = s_dyn;
@@ -1327,12 +1342,8 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             const float v = s_pv[min(t, n - 1)];
             const int i = s_pi[min(t, n - 1)];
             int rank = 0;
-            for (int c0 = 0; c0 < n; c0 += kWave) {
-                const float cv = s_pv[min(c0 + lane, n - 1)];
-                const int ci = s_pi[min(c0 + lane, n - 1)];
-                const int m = min(kWave, n - c0);
-                for (int j = 0; j < m; ++j) rank += better(readlane_f(cv, j), readlane_i(ci, j), v, i) ? 1 : 0;
-            }
+#pragma unroll 8
+            for (int q = 0; q < n; ++q) rank += better(s_pv[q], s_pi[q], v, i) ? 1 : 0;   // (broadcast reads)
             if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
         }
         __syncthreads();
@@ -1357,7 +1368,8 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
     } else if constexpr (MODE == kModeSample) {
         if (batched) {
             if (threadIdx.x == 0) s_np = 0;   // (ordered by the first batch's barrier)
-            scan_slice_batches<DT, VEC, kTopkThreads>(row, begin, end, first_sample, sample_batch, elem_fn);
+            scan_slice_batches_from<DT, VEC, kTopkThreads>(row, begin, end, pre, have_pre, first_sample, sample_batch,
+                                                           elem_fn);
             sample_pool_finish();
         } else {
             scan_slice<DT, VEC, kTopkThreads>(row, begin, end, elem_fn);
