@@ -374,10 +374,18 @@ __device__ __forceinline__ float sampled_gap(const vi_device_sampling& cfg, int 
 }
 
 // Extended sampler finish over the sorted top-`cap` list (fp64 weights,
-// min_p / top_p prefix cuts, Philox inverse CDF in sorted order).
-__device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, const float* z, const int* ids,
-                              int vocabulary, int32_t* token_out, double* uniform_out, float* probs_row,
-                              vi_sample_stats* stats_out, uint32_t flags, uint32_t valid, double* w) {
+// min_p / top_p prefix cuts, Philox inverse CDF in sorted order), run by a
+// whole wave.  The one order-dependent chain, the running sums of the weights
+// w[j] = exp(z[j] - z[0]) in candidate order, is taken once by lane 0 into
+// cum[]; every later sum of the serial rule is one of them (the total, the
+// support's mass, the draw's running sums), and the cuts and the draw are the
+// first candidates whose tests hold, found by ballots.  Lane 0 writes the
+// outputs.
+__device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, const int* ids, int vocabulary,
+                              int32_t* token_out, double* uniform_out, float* probs_row,
+                              vi_sample_stats* stats_out, uint32_t flags, uint32_t valid, const double* w,
+                              double* cum) {
+    const int lane = lane_id();
     int32_t token = vocabulary;
     double u = 0.0, sn = 0.0;
     int support = 0;
@@ -385,41 +393,44 @@ __device__ __forceinline__ void sample_finish(const vi_row_params& p, int cap, c
         flags |= VI_FLAG_EMPTY;
     } else if (!(p.temperature > 0.0f)) {
         token = ids[0]; support = 1; sn = 1.0;
-        if (probs_row) probs_row[token] = 1.0f;
+        if (probs_row && lane == 0) probs_row[token] = 1.0f;
     } else {
-        double s = 0.0;   // (w[j] = exp(z[j] - z[0]) filled by the caller, one entry per lane)
-        for (int j = 0; j < cap; ++j) s += w[j];
-        const double minp = double(p.min_p), target = double(p.top_p) * s;
-        double cum = 0.0;
-        for (int j = 0; j < cap; ++j) {
-            if (p.min_p > 0.0f && w[j] < minp * w[0]) break;
-            cum += w[j];
-            support = j + 1;
-            if (p.top_p < 1.0f && cum >= target) break;
+        if (lane == 0) {
+            double c = 0.0;
+            for (int j = 0; j < cap; ++j) { c += w[j]; cum[j] = c; }
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const double s = cum[cap - 1], w0 = w[0];
+        const double minp = double(p.min_p), target = double(p.top_p) * s;
+        const bool in = lane < cap;
+        const double wj = in ? w[lane] : 0.0, cj = in ? cum[lane] : 0.0;
+        // the serial rule stops at the first candidate under min_p (support
+        // j) or the first whose running sum reaches top_p's (support j + 1)
+        const uint64_t fm = ballot(in && p.min_p > 0.0f && wj < minp * w0);
+        const uint64_t hm = ballot(in && p.top_p < 1.0f && cj >= target);
+        const int jf = fm ? __builtin_ctzll(fm) : cap, jh = hm ? __builtin_ctzll(hm) : cap;
+        support = jf <= jh ? jf : jh + 1;
         if (support < 1) support = 1;
-        for (int j = 0; j < support; ++j) sn += w[j];
+        sn = cum[support - 1];
         u = philox_uniform(p.seed, p.lane, p.position, 0u);
         const double t = u * sn;
-        int pick = support - 1;
-        cum = 0.0;
-        for (int j = 0; j < support; ++j) {
-            cum += w[j];
-            if (cum > t) { pick = j; break; }
-        }
+        const uint64_t pm = ballot(lane < support && cj > t);
+        const int pick = pm ? __builtin_ctzll(pm) : support - 1;
         token = ids[pick];
-        if (probs_row)
-            for (int j = 0; j < support; ++j) probs_row[ids[j]] = float(w[j] / sn);
+        if (probs_row && lane < support) probs_row[ids[lane]] = float(wj / sn);
     }
-    *token_out = token;
-    if (uniform_out) *uniform_out = u;
-    if (stats_out) {
-        stats_out->flags = flags;
-        stats_out->support = uint32_t(support);
-        stats_out->finite = valid;
-        stats_out->reserved = 0u;
-        stats_out->support_mass = sn;
-        stats_out->uniform = u;
+    if (lane == 0) {
+        *token_out = token;
+        if (uniform_out) *uniform_out = u;
+        if (stats_out) {
+            stats_out->flags = flags;
+            stats_out->support = uint32_t(support);
+            stats_out->finite = valid;
+            stats_out->reserved = 0u;
+            stats_out->support_mass = sn;
+            stats_out->uniform = u;
+        }
     }
 }
 
@@ -1724,37 +1735,36 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             lane_arrive(l, uint32_t(a.dv.drafts));
         }
     } else {
-        // the candidates' fp64 weights, one per lane (the sums stay on lane 0, in order)
-        __shared__ double s_w[kMaxK];   // (in LDS, not per-lane scratch)
+        // the candidates' fp64 weights, one per lane (into LDS for the running sums)
+        __shared__ double s_w[kMaxK], s_cum[kMaxK];
         const int wcap = (p.temperature > 0.0f) ? min(K, int(c)) : 1;
         if (p.temperature > 0.0f && lane < wcap) s_w[lane] = exp(double(s_val[0][lane]) - double(s_val[0][0]));
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        if (lane == 0) {
-            uint32_t flags_out = 0;
-            if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
-            if (lookups)
-                flags_out |= a.pstate        ? reinterpret_cast<const PenaltyHeader*>(a.pstate + size_t(r) * a.pl.lane_bytes)->flags
-                             : a.hist_counts ? ((f & kSliceBadHistory) ? uint32_t(VI_FLAG_BAD_HISTORY) : 0u) |
-                                                   ((f & kSliceError) ? uint32_t(VI_FLAG_ERROR) : 0u)
-                                             : a.row_flags[r];
-            if (flags_out & VI_FLAG_ERROR) {
+        uint32_t flags_out = 0;
+        if (f & kSliceNonfinite) flags_out |= VI_FLAG_NONFINITE;
+        if (lookups)
+            flags_out |= a.pstate        ? reinterpret_cast<const PenaltyHeader*>(a.pstate + size_t(r) * a.pl.lane_bytes)->flags
+                         : a.hist_counts ? ((f & kSliceBadHistory) ? uint32_t(VI_FLAG_BAD_HISTORY) : 0u) |
+                                               ((f & kSliceError) ? uint32_t(VI_FLAG_ERROR) : 0u)
+                                         : a.row_flags[r];
+        flags_out = uint32_t(__builtin_amdgcn_readfirstlane(int(flags_out)));
+        if (flags_out & VI_FLAG_ERROR) {
+            if (lane == 0) {
                 a.tokens[r] = -1;
                 if (a.uniforms) a.uniforms[r] = 0.0;
                 if (a.stats) { a.stats[r] = vi_sample_stats{}; a.stats[r].flags = flags_out; }
-                return;
             }
-            const int cap = wcap;
-            float* pr = a.probs ? a.probs + size_t(r) * size_t(a.probs_stride) : nullptr;
-            sample_finish(p, cap, s_val[0], s_idx[0], a.vocabulary, &a.tokens[r],
-                          a.uniforms ? &a.uniforms[r] : nullptr, pr, a.stats ? &a.stats[r] : nullptr,
-                          flags_out, c, s_w);
-            if (a.record) {   // every slice of this row has finished reading the state (last arriver)
-                const int32_t t = a.tokens[r];
-                if (t >= 0 && t < a.vocabulary) {
-                    const LaneState ls = lane_state(a.pstate + size_t(r) * a.pl.lane_bytes, a.pl);
-                    state_record_one(ls, a.pl, a.vocabulary, t);
-                }
+            return;
+        }
+        float* pr = a.probs ? a.probs + size_t(r) * size_t(a.probs_stride) : nullptr;
+        sample_finish(p, wcap, s_idx[0], a.vocabulary, &a.tokens[r], a.uniforms ? &a.uniforms[r] : nullptr, pr,
+                      a.stats ? &a.stats[r] : nullptr, flags_out, c, s_w, s_cum);
+        if (a.record && lane == 0) {   // every slice of this row has finished reading the state (last arriver)
+            const int32_t t = a.tokens[r];
+            if (t >= 0 && t < a.vocabulary) {
+                const LaneState ls = lane_state(a.pstate + size_t(r) * a.pl.lane_bytes, a.pl);
+                state_record_one(ls, a.pl, a.vocabulary, t);
             }
         }
     }
