@@ -813,7 +813,11 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         lds_barrier();
         uint32_t cb = 0u;
         uint64_t mb = 0ull;
-        for (int q = 0; q < wave; ++q) { cb += sh.scan[q]; mb += sh.wmass[q]; }
+        {   // the earlier waves' totals, one per lane, summed across the wave (exact integers)
+            const bool e = lane < wave;
+            cb = readlane_u(wave_incl_scan_u32(e ? sh.scan[lane] : 0u), kWave - 1);
+            mb = readlane_u64(wave_incl_scan_u64(e ? sh.wmass[lane] : 0ull), kWave - 1);
+        }
         if (tid == kT - 1) { sh.total_cnt = cb + ci; sh.total_mass = mb + mi; }
         const uint32_t ce = cb + ci - (c0 + c1);
         const uint64_t me = mb + mi - (m0 + m1);
