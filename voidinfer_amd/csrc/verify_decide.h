@@ -27,6 +27,7 @@ __device__ inline bool is_terminal(const int64_t* terminal, int n, int64_t t) {
 // and its mass.
 struct ListDist {
     double w[kMaxK];
+    double cum[kMaxK];   // running sums of w in entry order (entries below the cap)
     int id[kMaxK];
     int support;
     double sn;
@@ -40,10 +41,11 @@ __device__ __forceinline__ double readlane_d(double v, int j) {
     return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
 }
 
-// One wave per list: lane k computes the weight of list entry k; the cuts and
-// sums then run in the order of the one-thread rule on every lane (wave-uniform
-// loops over the lanes' weights, read lane by lane: the fp64 results are that
-// rule's, bit for bit).  Returns lane k's weight (0 past the cap) in w.
+// One wave per list: lane k computes the weight of list entry k; lane 0 takes
+// the running sums in entry order (the one order-dependent chain: every sum of
+// the one-thread rule is one of them), and the cuts are the first entries
+// whose tests hold, found by ballots (the fp64 results are that rule's, bit for
+// bit).  Returns lane k's weight (0 past the cap) in w.
 __device__ inline void list_dist(const vi_row_params& p, const float* z, const int* id, uint32_t valid, ListDist& d,
                                  double& w) {
     const int k = lane_id();
@@ -62,25 +64,31 @@ __device__ inline void list_dist(const vi_row_params& p, const float* z, const i
     if (cap > 0 && greedy) {
         n = 1;
         sn = 1.0;
+        if (k == 0) d.cum[0] = 1.0;
     } else if (cap > 0) {
-        double s = 0.0;
-        for (int j = 0; j < cap; ++j) s += readlane_d(w, j);
-        const double minp = double(p.min_p), target = double(p.top_p) * s, w0 = readlane_d(w, 0);
-        double cum = 0.0;
-        for (int j = 0; j < cap; ++j) {
-            const double wj = readlane_d(w, j);
-            if (p.min_p > 0.0f && wj < minp * w0) break;
-            cum += wj;
-            n = j + 1;
-            if (p.top_p < 1.0f && cum >= target) break;
+        wave_sync();
+        if (k == 0) {
+            double c = 0.0;
+            for (int j = 0; j < cap; ++j) { c += d.w[j]; d.cum[j] = c; }
         }
-        // the support's mass: the same additions in the same order as cum's
-        // (from 0.0, entries 0..n-1), unless no entry was taken
+        wave_sync();
+        const double s = d.cum[cap - 1], w0 = d.w[0];
+        const double minp = double(p.min_p), target = double(p.top_p) * s;
+        const bool in = k < cap;
+        const double ck = in ? d.cum[k] : 0.0;
+        // the rule stops at the first entry under min_p (support j) or the
+        // first whose running sum reaches top_p's (support j + 1)
+        const uint64_t fm = ballot(in && p.min_p > 0.0f && w < minp * w0);
+        const uint64_t hm = ballot(in && p.top_p < 1.0f && ck >= target);
+        const int jf = fm ? __builtin_ctzll(fm) : cap, jh = hm ? __builtin_ctzll(hm) : cap;
+        n = jf <= jh ? jf : jh + 1;
+        // the support's mass: the running sum through its last entry, unless
+        // no entry was taken
         if (n < 1) {
             n = 1;
             sn = w0;
         } else {
-            sn = cum;
+            sn = d.cum[n - 1];
         }
     }
     if (k == 0) {
@@ -127,7 +135,8 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
                                          const float* dv, const int* di, uint32_t dvalid, uint32_t dflags,
                                          const int32_t* drafted, int vocabulary, int full_ok, PosDecision* dec) {
     __shared__ ListDist P, Q;
-    __shared__ double s_rv[kMaxK], s_pv[kMaxK];
+    __shared__ double s_rv[kMaxK], s_pv[kMaxK], s_rs[kMaxK], s_rc[kMaxK];
+    __shared__ double s_sum;
     __shared__ int s_rid[kMaxK];
     __shared__ int s_accept;
     const int k = lane_id();
@@ -144,11 +153,10 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
         if (tvalid) {
             if (!(p.temperature > 0.0f)) tok = P.id[0];
             else {
+                // the first support entry whose running sum passes u * s_n
                 const double t = philox_uniform(p.seed, p.lane, p.position + drafts, 0u) * P.sn;
-                double cum = 0.0;
-                int pick = P.support - 1;
-                for (int i = 0; i < P.support; ++i) { cum += readlane_d(pw, i); if (cum > t) { pick = i; break; } }
-                tok = P.id[pick];
+                const uint64_t pm = ballot(k < P.support && P.cum[min(k, kMaxK - 1)] > t);
+                tok = P.id[pm ? __builtin_ctzll(pm) : P.support - 1];
             }
         }
         if (k == 0) put_dec(out, PosDecision{tok, 0u, 0, 0});
@@ -177,15 +185,16 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
     wave_sync();
     if (s_accept) return;
     // residual max(0, p - q) over p's support, placed in token-id order by rank
-    // (ids within a list are distinct); the lists' ids and weights read lane by
-    // lane from the lanes holding them
+    // (ids within a list are distinct); the lists' ids read back from LDS by
+    // every lane (broadcast reads)
     const int m = P.support, qs = Q.support;
-    const int pid = k < m ? P.id[k] : 0, qid = k < qs ? Q.id[k] : -1;
-    // (wave-uniform loops: every lane reads every other lane's entry)
+    const int pid = k < m ? P.id[k] : 0;
     int rank = 0;
-    for (int i = 0; i < m; ++i) rank += __builtin_amdgcn_readlane(pid, i) < pid ? 1 : 0;
+#pragma unroll 8
+    for (int i = 0; i < m; ++i) rank += P.id[i] < pid ? 1 : 0;
     int at = -1;   // (the first match: ids within a list are distinct)
-    for (int i = 0; i < qs; ++i) at = (at < 0 && __builtin_amdgcn_readlane(qid, i) == pid) ? i : at;
+#pragma unroll 8
+    for (int i = qs - 1; i >= 0; --i) at = Q.id[i] == pid ? i : at;
     const double qt = at >= 0 ? Q.w[at] / Q.sn : 0.0;
     if (k < m) {
         const double pk = pw / P.sn;
@@ -195,39 +204,30 @@ __device__ inline void position_decision(const vi_row_params& p, int j, int l, i
     }
     wave_sync();
     flags = uint32_t(__builtin_amdgcn_readfirstlane(int(flags)));
-    const double rv = k < m ? s_rv[k] : 0.0, pvk = k < m ? s_pv[k] : 0.0;
-    const int rid = k < m ? s_rid[k] : 0;
-    double sum = 0.0;
-    for (int i = 0; i < m; ++i) sum += readlane_d(rv, i);
-    int32_t corr = 0;
-    if (!(sum > 1e-9) || !isfinite(sum)) {
-        // No residual mass: correct from p itself (inverse CDF, id order).
-        flags |= VI_FLAG_NO_RESIDUAL;
-        double cum = 0.0;
-        int32_t last = 0;
-        bool found = false;
-        for (int i = 0; i < m; ++i) {
-            const double pv = readlane_d(pvk, i);
-            const int32_t ri = __builtin_amdgcn_readlane(rid, i);
-            if (pv > 0.0) last = ri;
-            cum += pv;
-            if (uc < cum) { corr = ri; found = true; break; }
-        }
-        if (!found) corr = last;
-    } else {
-        const double rk = rv / sum;   // (each lane's share, divided in parallel)
-        double cum = 0.0;
-        int32_t last = 0;
-        bool found = false;
-        for (int i = 0; i < m; ++i) {
-            const double r = readlane_d(rk, i);
-            const int32_t ri = __builtin_amdgcn_readlane(rid, i);
-            if (r > 0.0) last = ri;
-            cum += r;
-            if (uc < cum) { corr = ri; found = true; break; }
-        }
-        if (!found) corr = last;
+    if (k == 0) {
+        double c = 0.0;
+        for (int i = 0; i < m; ++i) c += s_rv[i];
+        s_sum = c;
     }
+    wave_sync();
+    const double sum = s_sum;
+    // The inverse CDF in id order: the first entry whose running sum exceeds
+    // u_c, else the last entry with a positive share (0 if none).  The shares
+    // are each lane's value over the sum (divided in parallel) or, with no
+    // residual mass, p itself; their running sums are lane 0's chain.
+    const bool nores = !(sum > 1e-9) || !isfinite(sum);
+    if (nores) flags |= VI_FLAG_NO_RESIDUAL;
+    const double share = k < m ? (nores ? s_pv[k] : s_rv[k] / sum) : 0.0;
+    if (k < m) s_rs[k] = share;
+    wave_sync();
+    if (k == 0) {
+        double c = 0.0;
+        for (int i = 0; i < m; ++i) { c += s_rs[i]; s_rc[i] = c; }
+    }
+    wave_sync();
+    const uint64_t fm = ballot(k < m && uc < s_rc[min(k, kMaxK - 1)]);
+    const uint64_t pm = ballot(k < m && share > 0.0);
+    const int32_t corr = fm ? s_rid[__builtin_ctzll(fm)] : pm ? s_rid[63 - __builtin_clzll(pm)] : 0;
     if (k == 0) put_dec(out, PosDecision{corr, flags, 0, 0});
 }
 
