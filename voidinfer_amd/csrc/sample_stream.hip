@@ -728,11 +728,6 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         for (int o = 32; o; o >>= 1) top = max(top, uint32_t(__shfl_xor(int(top), o, kWave)));
         if (lane == 0 && top) atomicMax(&sh.z0key, top);
     }
-    // The first repeat entries' logits, requested now (clamped into the row)
-    // and used by the rescan once the owner part is known.
-    uint32_t rraw[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) rraw[j] = uint32_t(row16[min(rep[j].x, uint32_t(V - 1))]);
     lds_barrier();
     const uint32_t z0key = sh.z0key;
     const double z0 = double(key_z<DT>(z0key, inv_t));
@@ -1057,6 +1052,15 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
     }
     for (int i = tid; i < 2048; i += kT) flip[i] = 0u;
     if (tid == 0) sh.nflip = 0u;
+    // presence masks by byte for the rescan, in the decisions' running-sum
+    // table (free now): entry b, word q: the halves of tokens 2q and 2q + 1 all
+    // ones where that token is in the history
+    {
+        const uint32_t b = uint32_t(tid) >> 2, q = uint32_t(tid) & 3u;
+        reinterpret_cast<uint32_t*>(lds + kOffMCab)[tid] = (((b >> (2u * q)) & 1u) ? 0x0000ffffu : 0u) |
+                                                          (((b >> (2u * q + 1u)) & 1u) ? 0xffff0000u : 0u);
+    }
+    static_assert(256 * 16 <= kOffMMab - kOffMCab && kT == 1024, "presence masks");
     lds_barrier();
 
     // ---- 6. the owner part read again: its orank-th logit (id order) whose
@@ -1081,39 +1085,18 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         uint32_t bb[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) load_vec(k * kT + tid, &vv[k], &bb[k]);
+        // the owner part's repeat entries' logits, requested behind the part
+        // (their flips are worked out after the count, which they correct)
+        auto in_owner = [&](uint2 e) { return e.y >= 2u && int(e.x) >= it.s0 && int(e.x) < it.s0 + it.n; };
+        uint32_t raw[2] = {0u, 0u};
         if (pen) {
-            auto in_owner = [&](uint2 e) { return e.y >= 2u && int(e.x) >= it.s0 && int(e.x) < it.s0 + it.n; };
-            auto flip_if = [&](uint2 e, uint32_t raw) {
-                if (!in_owner(e) || !Elem<DT>::finite_bits(raw)) return;
-                const bool m1 = key16(pen_pattern<DT>(raw, 1u, p, inv_r, rep_fast)) == dk;
-                const bool mc = key16(pen_pattern<DT>(raw, e.y, p, inv_r, rep_fast)) == dk;
-                if (m1 != mc) {
-                    const uint32_t off = e.x - uint32_t(it.s0);
-                    atomicOr(&flip[off >> 5], 1u << (off & 31u));
-                    atomicAdd(&sh.nflip, 1u);
-                }
-            };
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if (uint32_t(j * kT + tid) >= pv.nrep) rep[j].y = 0u;
-                flip_if(rep[j], rraw[j]);
-            }
-            for (uint32_t i = uint32_t(2 * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
-                const uint2 e = pv.list[i];
-                if (in_owner(e)) flip_if(e, uint32_t(row16[e.x]));
+                if (in_owner(rep[j])) raw[j] = uint32_t(row16[rep[j].x]);
             }
         }
-        // presence masks by byte, in the decisions' running-sum table (free
-        // now): entry b, word q: the halves of tokens 2q and 2q + 1 all ones
-        // where that token is in the history
-        uint4* pmask = reinterpret_cast<uint4*>(lds + kOffMCab);
-        {
-            const uint32_t b = uint32_t(tid) >> 2, q = uint32_t(tid) & 3u;
-            reinterpret_cast<uint32_t*>(pmask)[tid] = (((b >> (2u * q)) & 1u) ? 0x0000ffffu : 0u) |
-                                                     (((b >> (2u * q + 1u)) & 1u) ? 0xffff0000u : 0u);
-        }
-        static_assert(256 * 16 <= kOffMMab - kOffMCab && kT == 1024, "presence masks");
-        lds_barrier();
+        const uint4* pmask = reinterpret_cast<const uint4*>(lds + kOffMCab);
         // In the halves' key space (-0 just below +0): an absent token matches
         // when its key lies in [a0, a0 + w0] (the drawn key, with -0 for +0), a
         // history token when it lies in [a1, a1 + w1] (the preimage; none when
@@ -1128,26 +1111,10 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
         }
         const uint32_t A0 = a0 | (a0 << 16), W0 = w0 | (w0 << 16), A1 = a1 | (a1 << 16), W1 = w1 | (w1 << 16);
         const uint32_t force = empty1 ? 0xffffffffu : 0u;   // history halves never match
-        const bool flips = sh.nflip != 0u;
-        // exact match bits of one vector (the scalar form of the count below)
-        auto match_bits = [&](uint4 d, uint32_t b, int v) -> uint32_t {
-            const uint32_t w4[4] = {d.x, d.y, d.z, d.w};
-            uint32_t m = 0u;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t pat = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                const uint32_t k = (pat & 0x8000u) ? (~pat & 0xffffu) : (pat | 0x8000u);
-                const bool present = (b >> j) & 1u;
-                const bool hit = present ? (!empty1 && k - a1 <= w1) : (k - a0 <= w0);
-                m |= hit ? (1u << j) : 0u;
-            }
-            if (flips) m ^= (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
-            return m;
-        };
-        // Matches per round, three rounds to a word in 10-bit fields (a wave's
-        // sums stay below 1024): per half, the range of the token's kind is
-        // selected by the presence mask and tested as max(key - base - width, 0)
-        // == 0.
+        // Matches per round before the flips, three rounds to a word in 10-bit
+        // fields (a wave's sums stay below 1024): per half, the range of the
+        // token's kind is selected by the presence mask and tested as
+        // max(key - base - width, 0) == 0.
         uint32_t pc[3] = {0u, 0u, 0u};
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
@@ -1165,17 +1132,59 @@ __global__ __launch_bounds__(kT) void merge_kernel(StreamArgs a) {
                     miss += pk_nonzero_u16(pk_sub_sat_u16(t, width) | (m4[q] & force));
                 }
                 c = 8u - (miss & 0xffffu) - (miss >> 16);
-                if (flips) {
-                    const uint32_t fl = (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
-                    if (fl) c = uint32_t(__builtin_popcount(match_bits(vv[r], bb[r], v)));
-                }
             }
             pc[r / 3] += c << (10 * (r % 3));
+        }
+        auto field = [](uint32_t w, int r) { return (w >> (10 * (r % 3))) & 0x3ffu; };
+        // Repeated tokens whose count changes the answer are flipped
+        if (pen) {
+            auto flip_if = [&](uint2 e, uint32_t rw) {
+                if (!in_owner(e) || !Elem<DT>::finite_bits(rw)) return;
+                const bool m1 = key16(pen_pattern<DT>(rw, 1u, p, inv_r, rep_fast)) == dk;
+                const bool mc = key16(pen_pattern<DT>(rw, e.y, p, inv_r, rep_fast)) == dk;
+                if (m1 != mc) {
+                    const uint32_t off = e.x - uint32_t(it.s0);
+                    atomicOr(&flip[off >> 5], 1u << (off & 31u));
+                    atomicAdd(&sh.nflip, 1u);
+                }
+            };
+#pragma unroll
+            for (int j = 0; j < 2; ++j) flip_if(rep[j], raw[j]);
+            for (uint32_t i = uint32_t(2 * kT + tid); i < pv.nrep; i += kT) {   // (long repeat lists)
+                const uint2 e = pv.list[i];
+                if (in_owner(e)) flip_if(e, uint32_t(row16[e.x]));
+            }
+        }
+        lds_barrier();
+        const bool flips = sh.nflip != 0u;
+        // exact match bits of one vector (the scalar form of the count, flips applied)
+        auto match_bits = [&](uint4 d, uint32_t b, int v) -> uint32_t {
+            const uint32_t w4[4] = {d.x, d.y, d.z, d.w};
+            uint32_t m = 0u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t pat = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+                const uint32_t k = (pat & 0x8000u) ? (~pat & 0xffffu) : (pat | 0x8000u);
+                const bool present = (b >> j) & 1u;
+                const bool hit = present ? (!empty1 && k - a1 <= w1) : (k - a0 <= w0);
+                m |= hit ? (1u << j) : 0u;
+            }
+            if (flips) m ^= (flip[v >> 2] >> ((v & 3) * 8)) & 0xffu;
+            return m;
+        };
+        if (flips) {   // (uniform) the flipped vectors counted again
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int v = r * kT + tid;
+                if (v < it.nvec && ((flip[v >> 2] >> ((v & 3) * 8)) & 0xffu)) {
+                    const uint32_t c = uint32_t(__builtin_popcount(match_bits(vv[r], bb[r], v)));
+                    pc[r / 3] += (c - field(pc[r / 3], r)) << (10 * (r % 3));
+                }
+            }
         }
         uint32_t pin[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) pin[i] = wave_incl_scan_u32(pc[i]);
-        auto field = [](uint32_t w, int r) { return (w >> (10 * (r % 3))) & 0x3ffu; };
         if (lane == kWave - 1) {
 #pragma unroll
             for (int r = 0; r < 8; ++r) sh.wtot[r][wave] = field(pin[r / 3], r);
