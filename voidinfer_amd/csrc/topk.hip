@@ -1287,27 +1287,19 @@ __device__ __forceinline__ void topk_body(const TopkArgs& a, const int slice, co
             }
             return;
         }
-        // wave 0 places each pooled logit by its rank among them (ids are
-        // distinct, so the ranks are)
+        // each pooled logit placed by its rank among them (one per thread, the
+        // others read with broadcast LDS reads; ids are distinct, so the ranks
+        // are), then wave 0 takes the list
+        for (int t = tid; t - lane < n; t += kTopkThreads) {   // (wave-uniform)
+            const float v = s_pv[min(t, n - 1)];
+            const int i = s_pi[min(t, n - 1)];
+            int rank = 0;
+#pragma unroll 8
+            for (int q = 0; q < n; ++q) rank += better(s_pv[q], s_pi[q], v, i) ? 1 : 0;
+            if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
+        }
+        __syncthreads();
         if (wave == 0) {
-            // (the pooled logits a wave's worth at a time in registers; each
-            // lane counts the better ones read lane by lane)
-            for (int t0 = 0; t0 < n; t0 += kWave) {
-                const int t = t0 + lane;
-                const float v = s_pv[min(t, n - 1)];
-                const int i = s_pi[min(t, n - 1)];
-                int rank = 0;
-                for (int c0 = 0; c0 < n; c0 += kWave) {
-                    const float cv = s_pv[min(c0 + lane, n - 1)];
-                    const int ci = s_pi[min(c0 + lane, n - 1)];
-                    const int m = min(kWave, n - c0);
-                    for (int j = 0; j < m; ++j)
-                        rank += better(readlane_f(cv, j), readlane_i(ci, j), v, i) ? 1 : 0;
-                }
-                if (t < n && rank < K) { s_selv[rank] = v; s_seli[rank] = i; }
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             const bool h = lane < min(K, n);
             L.v = h ? s_selv[lane] : -kInfF;
             L.i = h ? s_seli[lane] : kInvalidId;
