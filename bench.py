@@ -53,10 +53,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
-    ap.add_argument("--workload", choices=("config5", "config1", "config2", "config3", "config4", "config4-full"),
+    ap.add_argument("--workload", choices=("config5", "config1", "config2", "config3", "config4", "config4-full",
+                                           "wide"),
                     default="config5",
                     help="config5 (the headline); config1 / config2 report decode-step latency; config3 / config4 "
-                         "time the top-k and verification kernels")
+                         "time the top-k and verification kernels; wide times the fp32 full-vocabulary route")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel over 256 MiB x 10 (HBM-counter calibration) and exit")
     return ap.parse_args()
@@ -239,7 +240,36 @@ def secondary(args):
     K, V = args.steps, VOCAB
     t16 = lambda bits, dt: torch.from_numpy(bits.view(np.int16)).to(dev).view(dt)   # noqa: E731
     extra = {}
-    if args.workload == "config3":
+    if args.workload == "wide":
+        # the full-vocabulary route on fp32 logits (sample_wide.hip): 128 rows x
+        # 248,320 fp32 N(0,2)+Zipf, T .7 / top_k off / top_p .95, no penalties
+        rows = 128
+        sets_w = []
+        for s in range(SETS):
+            bits_w = W.encode(W.gaussian_zipf(rows, V, 2.0, 700 + s), "f32")
+            p_w = W.lane_params(rows, 7000 + s, top_k_choices=(0,), top_p_choices=(0.95,), min_p_choices=(0.0,))
+            p_w["temperature"] = 0.7
+            p_w["repetition_penalty"] = 1.0
+            p_w["presence_penalty"] = 0.0
+            p_w["frequency_penalty"] = 0.0
+            sets_w.append((bits_w, p_w))
+        logits = [torch.from_numpy(b.view(np.float32)).to(dev) for b, _ in sets_w]
+        pdev = [vi.to_device_bytes(p_, dev) for _, p_ in sets_w]
+        tok = torch.empty(rows, dtype=torch.int32, device=dev)
+        nb = lib.vi_sample_workspace_bytes(rows, V, 0)
+        ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+
+        def fn(i):
+            j = i % SETS
+            return lib.vi_sample_rows(logits[j].data_ptr(), vi.F32, rows, V, V, pdev[j].data_ptr(), None, None, 0,
+                                      tok.data_ptr(), None, None, V, None, vi.ROUTE_FULL, ws.data_ptr(), nb, sptr)
+        bytes_per_launch = rows * V * 4
+        metric, kernel = "sampled rows/sec at 128x248,320 fp32 (full-vocabulary route)", "wide_* (sample_wide.hip)"
+        workload = "wide: 128 rows x 248,320 fp32 N(0,2)+Zipf, T .7 / top_k off / top_p .95, no penalties"
+        assert fn(0) == 0
+        torch.cuda.synchronize()
+        gpu = tok.cpu().numpy()
+    elif args.workload == "config3":
         rows, k = 128, 8
         bits = [W.config3(seed=300 + s, rows=rows) for s in range(SETS)]
         logits = [t16(b, torch.float16) for b in bits]
@@ -317,6 +347,8 @@ def secondary(args):
         while True:
             if args.workload == "config3":
                 w_ids = oracle.topk_rows(bits[0], oracle.F16, 8, threads=threads)[0]
+            elif args.workload == "wide":
+                w_tok, _, _, _, w_m = oracle.sample_rows(sets_w[0][0], oracle.F32, sets_w[0][1], threads=threads)
             else:
                 t, d, x, p = sets[0]
                 w = oracle.verify_rows(vi.VERIFY_SAMPLED, t, oracle.BF16, d, oracle.F16, 8, 16, x, p, threads=threads)
@@ -326,6 +358,11 @@ def secondary(args):
         cpu_s = time.perf_counter() - t0
         if args.workload == "config3":
             parity = {"rows": rows, "mismatched_rows": int((w_ids != gpu).any(axis=1).sum())}
+            cores = threads
+        elif args.workload == "wide":
+            mism = [r for r in range(rows) if int(w_tok[r]) != int(gpu[r])]
+            parity = {"rows": rows, "mismatches": len(mism),
+                      "unexplained": len([r for r in mism if not (w_m[r, 0] < 1e-6 or w_m[r, 1] < 1e-6)])}
             cores = threads
         else:
             near = w[4] < 1e-6
@@ -338,7 +375,8 @@ def secondary(args):
     print(json.dumps({
         "metric": metric, "value": rows / (ms / 1e3), "unit": "rows/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp16" if args.workload == "config3" else "bf16+fp16", "data": "synthetic",
+        "vs_baseline": None,
+        "dtype": {"config3": "fp16", "wide": "fp32"}.get(args.workload, "bf16+fp16"), "data": "synthetic",
         "config": {"workload": workload, "rows": rows, "vocabulary": V, "input_sets": SETS, "kernel": kernel},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBPS, "traffic": None, "bytes_per_launch": bytes_per_launch,

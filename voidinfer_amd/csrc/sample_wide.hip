@@ -231,7 +231,9 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // and one head and one tail logit.
 __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     __shared__ uint32_t CNT[kNB + 1];
-    __shared__ unsigned long long MASS[kNB];
+    __shared__ unsigned long long MASS[kNB];   // (then the staged pairs' offsets)
+    __shared__ __attribute__((aligned(16))) uint32_t SKEY[kSL];   // the staged pairs' keys
+    static_assert(sizeof(MASS) >= kSL * sizeof(uint16_t), "offset staging");
     __shared__ uint32_t s_top, s_flags, s_scan[kW + 1];
     const int s = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const vi_row_params p = a.params[row];
@@ -327,13 +329,13 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     }
     __syncthreads();
 
-    // the (key, offset) pairs grouped by bin
-    uint32_t* ko = a.keys + rs * kSL;
-    uint16_t* io = a.ids + rs * kSL;
+    // the (key, offset) pairs grouped by bin: placed in LDS, then written out
+    // whole (coalesced 16-byte stores in place of a scattered store per pair)
+    uint16_t* SOFF = reinterpret_cast<uint16_t*>(MASS);
     auto put = [&](uint32_t key, uint16_t b, int off) {
         if (!key) return;
         const uint32_t pos = atomicAdd(&CNT[b], 1u);
-        if (pos < uint32_t(kSL)) { ko[pos] = key; io[pos] = uint16_t(off); }
+        if (pos < uint32_t(kSL)) { SKEY[pos] = key; SOFF[pos] = uint16_t(off); }
     };
 #pragma unroll
     for (int i = 0; i < kVPT; ++i)
@@ -341,6 +343,12 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
         for (int e = 0; e < 4; ++e) put(k[i][e], bin[i][e], g.head + 4 * (i * kT + tid) + e);
     put(hk, hbin, tid);
     put(tk, tbin, g.head + 4 * g.nvec + tid);
+    __syncthreads();
+    const int n = int(min(total + deep, uint32_t(kSL)));
+    uint4* ko = reinterpret_cast<uint4*>(a.keys + rs * kSL);
+    uint4* io = reinterpret_cast<uint4*>(a.ids + rs * kSL);
+    for (int c = tid; c < (n + 3) / 4; c += kT) ko[c] = reinterpret_cast<const uint4*>(SKEY)[c];
+    for (int c = tid; c < (n + 7) / 8; c += kT) io[c] = reinterpret_cast<const uint4*>(SOFF)[c];
 }
 
 // ------------------------------------------------------------------ merge
