@@ -767,18 +767,35 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
 
     // ---- 1. the row's bins: counts and masses summed over the slices (thread t:
     // bins 4t .. 4t + 3), then their exclusive prefixes in bin order
+    // (four slices' loads issued together, unconditional at clamped places
+    // and dropped afterwards: a load under a branch waits for the ones before)
     uint32_t bc[4] = {0u, 0u, 0u, 0u};
     unsigned long long bf[4] = {0ull, 0ull, 0ull, 0ull};
-    for (int s = 0; s < S; ++s) {
-        const int d = L.delta[s];
-        if (d < 0 || d >= kNB) continue;
-        const uint32_t* st = a.starts + (rs0 + s) * kStarts;
-        const unsigned long long* ms = a.mass + (rs0 + s) * kNB;
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        uint32_t lo[4][4], hi[4][4];
+        unsigned long long mv[4][4];
+        bool on[4][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int j = 4 * tid + q - d;
-            if (j >= 0) { bc[q] += st[j + 1] - st[j]; bf[q] += ms[j]; }
+        for (int u = 0; u < 4; ++u) {
+            const int sc = min(s0 + u, S - 1), d = L.delta[sc];
+            const bool live = s0 + u < S && d >= 0 && d < kNB;
+            const uint32_t* st = a.starts + (rs0 + sc) * kStarts;
+            const unsigned long long* ms = a.mass + (rs0 + sc) * kNB;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = 4 * tid + q - d;
+                on[u][q] = live && j >= 0;
+                const int jc = on[u][q] ? j : 0;
+                lo[u][q] = st[jc];
+                hi[u][q] = st[jc + 1];
+                mv[u][q] = ms[jc];
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (on[u][q]) { bc[q] += hi[u][q] - lo[u][q]; bf[q] += mv[u][q]; }
     }
     double bm[4];
     uint32_t csum = 0u;
