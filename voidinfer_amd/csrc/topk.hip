@@ -1970,7 +1970,7 @@ vi_status launch_verify_pair(const void* target, int target_dtype, int64_t targe
                              const vi_row_params* params, int layout_rows, int layout_slices, float* tval, int* tidx,
                              uint32_t* tvalid, uint32_t* tflags, float* dval, int* didx, uint32_t* dvalid,
                              uint32_t* dflags, const VerifyDecideArgs& decide, void* ws, size_t ws_bytes,
-                             hipStream_t stream) {
+                             hipStream_t stream, int skip_unlisted) {
     if (!verify_pair_supported(target, target_dtype, target_stride, draft, draft_dtype, draft_stride))
         return VI_ERR_UNSUPPORTED;
     const int trows = lanes * decide.target_rows, drows = lanes * decide.drafts;
@@ -1989,7 +1989,7 @@ vi_status launch_verify_pair(const void* target, int target_dtype, int64_t targe
     t.pval = part.pval; t.pidx = part.pidx; t.phdr = part.phdr; t.arrivals = part.arrivals;
     t.params = params; t.params_div = decide.target_rows;
     t.lval = tval; t.lidx = tidx; t.lvalid = tvalid; t.lflags = tflags;
-    t.decide = 3; t.dv = decide; t.pair_rows = trows;
+    t.decide = 3; t.dv = decide; t.pair_rows = trows; t.skip_unlisted = skip_unlisted;
     TopkArgs d = t;   // (the draft half: its rows' partials after the target half's)
     const size_t off = size_t(trows) * plan.slices;
     d.logits = draft; d.stride = draft_stride;

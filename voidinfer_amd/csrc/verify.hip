@@ -504,9 +504,14 @@ __global__ __launch_bounds__(kRT) void verify_full_correction_kernel(FullVerifyA
 // Per-row sampler parameters of the full-vocabulary lanes' rows: the lane's,
 // without penalties, at position + j.
 __global__ void verify_row_params_kernel(const vi_row_params* params, int lanes, int per_lane,
-                                         vi_row_params* out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= lanes * per_lane) return;
+                                         vi_row_params* out, int per_lane2, vi_row_params* out2) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= lanes * per_lane) {   // (the second row set's rows follow the first's)
+        i -= lanes * per_lane;
+        if (i >= lanes * per_lane2) return;
+        per_lane = per_lane2;
+        out = out2;
+    }
     vi_row_params p = params[i / per_lane];
     p.repetition_penalty = 1.0f;
     p.presence_penalty = 0.0f;
@@ -645,12 +650,17 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
     dv.terminal = a.terminal; dv.n_terminal = a.n_terminal;
     dv.accepted = a.accepted; dv.committed = a.committed; dv.committed_count = a.committed_count;
     dv.lane_flags = a.lane_flags;
-    if (fused && verify_pair_supported(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype,
-                                       a.draft_stride))
-        // both row sets in one launch: each position decided by its later row
-        return launch_verify_pair(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype,
-                                  a.draft_stride, a.lanes, a.vocabulary, a.params, v.lrows, v.lslices, tval, tidx,
-                                  tvalid, tflags, dval, didx, dvalid, dflags, dv, lws, lbytes, stream);
+    const bool paired = verify_pair_supported(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype,
+                                              a.draft_stride);
+    if (paired) {
+        // both row sets in one launch: each listed position decided by its later
+        // row, each listed lane's chain walked by its last position (the lanes
+        // without a list, when the full path runs, are left to it)
+        st = launch_verify_pair(a.target, a.target_dtype, a.target_stride, a.draft, a.draft_dtype, a.draft_stride,
+                                a.lanes, a.vocabulary, a.params, v.lrows, v.lslices, tval, tidx, tvalid, tflags, dval,
+                                didx, dvalid, dflags, dv, lws, lbytes, stream, full_ok);
+        if (st != VI_OK || !full_ok) return st;
+    } else {
     st = launch_verify_lists(a.target, a.target_dtype, trows, v.lrows, v.lslices, a.vocabulary, a.target_stride,
                              a.params, a.target_rows, tval, tidx, tvalid, tflags, full_ok, lws, lbytes, stream,
                              fused ? &dv : nullptr, 2);
@@ -667,6 +677,7 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
                        a.committed, a.committed_count, a.lane_flags);
     st = launch_status();
     if (st != VI_OK) return st;
+    }
     if (full_ok) {
         const size_t tn = size_t(trows), dn = size_t(drows);
         vi_row_params* tpar = c.take<vi_row_params>(tn);
@@ -685,10 +696,8 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
         const size_t fbytes = full_sampler_bytes(v.trows, a.vocabulary);
         unsigned char* fws = c.take<unsigned char>(fbytes);
         if (!c.ok) return VI_ERR_WORKSPACE;
-        hipLaunchKernelGGL(verify_row_params_kernel, dim3((trows + 255) / 256), dim3(256), 0, stream, a.params,
-                           a.lanes, a.target_rows, tpar);
-        hipLaunchKernelGGL(verify_row_params_kernel, dim3((drows + 255) / 256), dim3(256), 0, stream, a.params,
-                           a.lanes, a.drafts, dpar);
+        hipLaunchKernelGGL(verify_row_params_kernel, dim3((trows + drows + 255) / 256), dim3(256), 0, stream,
+                           a.params, a.lanes, a.target_rows, tpar, a.drafts, dpar);
         // the rows' filtered distributions (and the target rows' draws) from the
         // full-vocabulary sampler, one row set after the other in one workspace
         auto sample = [&](const void* logits, int dtype, int rows, int64_t stride, const vi_row_params* par,

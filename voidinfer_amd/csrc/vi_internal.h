@@ -123,7 +123,7 @@ vi_status launch_verify_pair(const void* target, int target_dtype, int64_t targe
                              const vi_row_params* params, int layout_rows, int layout_slices, float* tval, int* tidx,
                              uint32_t* tvalid, uint32_t* tflags, float* dval, int* didx, uint32_t* dvalid,
                              uint32_t* dflags, const VerifyDecideArgs& decide, void* ws, size_t ws_bytes,
-                             hipStream_t stream);
+                             hipStream_t stream, int skip_unlisted);
 bool verify_pair_supported(const void* target, int target_dtype, int64_t target_stride, const void* draft,
                            int draft_dtype, int64_t draft_stride);
 size_t topk_partials_bytes_slices(int rows, int slices);
