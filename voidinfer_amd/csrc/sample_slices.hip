@@ -1731,6 +1731,25 @@ inline int slices_of(int vocabulary) { return (vocabulary + kSL - 1) / kSL; }
 
 }  // namespace
 
+SideStream* side_stream() {
+    // (one per host thread and device: concurrent callers never share events)
+    thread_local SideStream side[64];
+    thread_local bool tried[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    SideStream& x = side[dev];
+    if (!tried[dev]) {
+        tried[dev] = true;
+        if (hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&x.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&x.join, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            x.stream = nullptr;
+        }
+    }
+    return x.stream ? &x : nullptr;
+}
+
 int device_cus() {
     static int cached[64] = {};
     int dev = 0;

@@ -2052,12 +2052,26 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
     // fit and no fp32 full-route row needs the hash: no hash launch
     const bool lds_counts = hash && size_t(plan.slice_len) * 4 <= kHistCountLds &&
                             !(s.dtype == VI_F32 && (s.route_mask & VI_ROUTE_FULL) && full_ok);
+    if (run_topk && hash && !lds_counts) {
+        hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(kHashThreads), 0, stream, s.params, s.histories,
+                           s.offsets, s.vocabulary, hash, shift, slots, row_flags, s.max_history);
+        if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
+    }
+    // Rows of both routes: the top-k launch (the shorter of the two) runs on
+    // the side stream beside the full-vocabulary route's launch chain, which
+    // stays on the caller's stream, so neither cross-stream hand-over sits on
+    // the chain's path; the side stream is joined back into the caller's before
+    // the call returns.  The two routes' rows, outputs and workspace are
+    // disjoint (each kernel skips the other route's rows).
+    const bool full_run = (s.route_mask & VI_ROUTE_FULL) && full_ok;
+    SideStream* side = (run_topk && full_run) ? side_stream() : nullptr;
+    if (side && (hipEventRecord(side->fork, stream) != hipSuccess ||
+                 hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)) {
+        (void)hipGetLastError();
+        side = nullptr;
+    }
+    const hipStream_t topk_stream = side ? side->stream : stream;
     if (run_topk) {
-        if (hash && !lds_counts) {
-            hipLaunchKernelGGL(history_hash_kernel, dim3(s.rows), dim3(kHashThreads), 0, stream, s.params, s.histories,
-                               s.offsets, s.vocabulary, hash, shift, slots, row_flags, s.max_history);
-            if (launch_status() != VI_OK) return VI_ERR_LAUNCH;
-        }
         TopkArgs a{};
         a.logits = s.logits; a.vocabulary = s.vocabulary; a.stride = s.stride; a.slice_len = plan.slice_len;
         a.pval = part.pval; a.pidx = part.pidx; a.phdr = part.phdr; a.arrivals = part.arrivals;
@@ -2078,14 +2092,22 @@ vi_status launch_sample(const SampleArgs& s, void* ws, size_t ws_bytes, hipStrea
         a.stats = s.stats;
         // fp32 logits / unaligned rows: full-route rows fail loudly in the top-k launch
         a.full_rows_unsupported = (full_ok && (s.route_mask & VI_ROUTE_FULL)) ? 0 : (full_ok ? 0 : 1);
-        st = launch_mode<kModeSample>(a, s.dtype, aligned16(s.logits, s.stride, s.dtype), s.rows, plan.slices, stream);
-        if (st != VI_OK) return st;
+        st = launch_mode<kModeSample>(a, s.dtype, aligned16(s.logits, s.stride, s.dtype), s.rows, plan.slices,
+                                      topk_stream);
+        if (st != VI_OK && !side) return st;
     }
-    if ((s.route_mask & VI_ROUTE_FULL) && full_ok)
-        st = s.dtype == VI_F32     ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
-             : stream_supported(s) ? launch_stream(s, full_ws, full_bytes, stream)
-                                   : launch_full(s, full_ws, full_bytes, stream);
-    else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) return VI_ERR_UNSUPPORTED;
+    if (full_run) {
+        if (st == VI_OK)
+            st = s.dtype == VI_F32     ? launch_wide(s, full_ws, full_bytes, hash, shift, slots, row_flags, stream)
+                 : stream_supported(s) ? launch_stream(s, full_ws, full_bytes, stream)
+                                       : launch_full(s, full_ws, full_bytes, stream);
+    } else if ((s.route_mask & VI_ROUTE_FULL) && !run_topk) {
+        return VI_ERR_UNSUPPORTED;
+    }
+    // joined also when a launch failed: the side work uses the caller's workspace
+    if (side && (hipEventRecord(side->join, side->stream) != hipSuccess ||
+                 hipStreamWaitEvent(stream, side->join, 0) != hipSuccess))
+        return VI_ERR_LAUNCH;
     return st;
 }
 

@@ -218,6 +218,15 @@ vi_status launch_sample(const SampleArgs& a, void* ws, size_t ws_bytes, hipStrea
 
 // ---- full-vocabulary pair kernel --------------------------------------------
 int device_cus();
+// A second stream of the calling host thread on the current device, with a
+// fork and a join event (created on first use; nullptr when unavailable): a
+// call whose rows take both kernel routes runs the full-vocabulary route on it,
+// joined back into the caller's stream before the call returns.
+struct SideStream {
+    hipStream_t stream;
+    hipEvent_t fork, join;
+};
+SideStream* side_stream();
 // ---- full-vocabulary rows, stream and merge launches (sample_stream.hip): 16-bit logits,
 // aligned rows, vocabulary a multiple of 8, no probabilities or bounds wanted.
 bool stream_supported(const SampleArgs& s);
