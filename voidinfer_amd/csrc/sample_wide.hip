@@ -20,12 +20,15 @@
 //
 // Launches: (history route with penalties) the rows' presence bitmaps and
 // count hashes; one workgroup per (row, slice of 16,384 logits) counts and
-// weighs its bins and writes its (key, id) pairs grouped by bin; one workgroup
-// per row adds the slices' bins, places the cap, the cuts and the draw, and
-// names the token; optionally the filtered distribution.
+// weighs its bins (written over the occupied bins only) and writes the (key,
+// id) pairs of its first 4,096 list positions grouped by bin; one workgroup per
+// row adds the slices' bins, places the cap, the cuts and the draw, and names
+// the token, recomputing from the slice's logits the pairs of a bin that lies
+// past the written positions; optionally the filtered distribution.
 //
-// Roofline: HBM; V x 4 bytes of logits per row read once, V x 6 bytes of
-// grouped pairs written and a few bins of them read back.
+// Roofline: HBM; V x 4 bytes of logits per row read once; per slice the
+// occupied bins' counts and masses and at most 4,096 pairs written, a few bins
+// of them read back.
 #include <math.h>
 
 #include "penalty_state.h"
@@ -47,13 +50,17 @@ constexpr double kPerUnit = 64.0;
 constexpr float kFixUnit = 2147483648.0f;  // 2^31
 constexpr double kFixScale = 1.0 / 2147483648.0;
 constexpr int kCap = 8192;                 // logits of one bin staged in LDS (more are read from HBM)
+constexpr int kPairs = 4096;               // list positions whose pairs the slice pass writes
 constexpr int kDig = 256;
 constexpr uint32_t kTakeAll = 0xffffffffu;
 static_assert(kVPT * 4 * kT == kSL && kNB == 4 * kT, "slice and bin geometry");
 
 struct WideHead {
     double anchor;                 // floor(64 z_top) of the slice
-    uint32_t top_key, n_valid, flags, pad[3];
+    uint32_t top_key, n_valid, flags;
+    uint32_t nbins;                // bins 0 .. nbins - 1 may hold logits (the rest only the deep bin)
+    uint32_t npairs;               // list positions 0 .. npairs - 1 written
+    uint32_t pad;
 };
 static_assert(sizeof(WideHead) == 32, "slice head");
 
@@ -83,10 +90,10 @@ struct WideArgs {
     vi_sample_stats* stats;
     // workspace
     WideHead* heads;               // [rows][slices]
-    uint32_t* starts;              // [rows][slices][kStarts]
-    unsigned long long* mass;      // [rows][slices][kNB]: fixed-point bin masses
-    uint32_t* keys;                // [rows][slices][kSL]: order keys, grouped by bin
-    uint16_t* ids;                 // [rows][slices][kSL]: slice offsets, same order
+    uint32_t* starts;              // [rows][slices][kStarts]: bins 0 .. nbins, kNB, kNB + 1 written
+    unsigned long long* mass;      // [rows][slices][kNB]: fixed-point bin masses, bins 0 .. nbins - 1
+    uint32_t* keys;                // [rows][slices][kSL]: order keys, grouped by bin (first npairs
+    uint16_t* ids;                 // [rows][slices][kSL]: slice offsets, same order   written, the rest on demand)
     int want_bounds;               // bounds and bases wanted (probs, or verification)
     WideBound* bounds;             // [rows]
     uint32_t* bases;               // [rows][kMaxSlices]: end-key logits in the slices before
@@ -232,9 +239,9 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     __shared__ uint32_t CNT[kNB + 1];
     __shared__ unsigned long long MASS[kNB];   // (then the staged pairs' offsets)
-    __shared__ __attribute__((aligned(16))) uint32_t SKEY[kSL];   // the staged pairs' keys
-    static_assert(sizeof(MASS) >= kSL * sizeof(uint16_t), "offset staging");
-    __shared__ uint32_t s_top, s_flags, s_scan[kW + 1];
+    __shared__ __attribute__((aligned(16))) uint32_t SKEY[kPairs];   // the staged pairs' keys
+    static_assert(sizeof(MASS) >= kPairs * sizeof(uint16_t), "offset staging");
+    __shared__ uint32_t s_top, s_flags, s_nb, s_plim, s_scan[kW + 1];
     const int s = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const vi_row_params p = a.params[row];
     if (!full_row(p)) return;
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     const uint32_t tb = tid < g.tail ? g.base[g.head + 4 * g.nvec + tid] : 0u;
     for (int i = tid; i <= kNB; i += kT) CNT[i] = 0u;
     for (int i = tid; i < kNB; i += kT) MASS[i] = 0ull;
-    if (tid == 0) { s_top = 0u; s_flags = 0u; }
+    if (tid == 0) { s_top = 0u; s_flags = 0u; s_nb = 0u; s_plim = kNB + 1; }
 
     const WPen w = wpen(a, row, p);
     const float inv_t = 1.0f / p.temperature;
@@ -286,18 +293,22 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     const uint32_t top = s_top;
     WideHead* hd = a.heads + size_t(row) * a.slices + s;
     if (top == 0u) {
-        if (tid == 0) *hd = WideHead{0.0, 0u, 0u, s_flags, {0u, 0u, 0u}};
+        if (tid == 0) *hd = WideHead{0.0, 0u, 0u, s_flags, 0u, 0u, 0u};
         return;
     }
     const double anchor = floor(double(unkey32(top)) * kPerUnit);
 
     // counts and fixed-point masses per bin
     uint16_t bin[kVPT][4];
+    uint32_t nbl = 0u;   // one past the last non-deep bin holding logits
     auto count = [&](uint32_t key) -> uint16_t {
         if (!key) return uint16_t(0xffffu);
         const BinW b = bin_weight(key, anchor);
         atomicAdd(&CNT[b.bin], 1u);
-        if (b.bin < kNB) atomicAdd(&MASS[b.bin], (unsigned long long)b.fix);
+        if (b.bin < kNB) {
+            atomicAdd(&MASS[b.bin], (unsigned long long)b.fix);
+            nbl = max(nbl, uint32_t(b.bin) + 1u);
+        }
         return uint16_t(b.bin);
     };
 #pragma unroll
@@ -305,7 +316,10 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) bin[i][e] = count(k[i][e]);
     const uint16_t hbin = count(hk), tbin = count(tk);
+    nbl = wave_max_u32(nbl);
+    if (lane_id() == 0 && nbl) atomicMax(&s_nb, nbl);
     __syncthreads();
+    const uint32_t nb = s_nb;
 
     // list positions: bins in order (thread t: bins 4t .. 4t + 3), the deep bin last
     const size_t rs = size_t(row) * a.slices + s;
@@ -315,27 +329,40 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     const uint32_t deep = CNT[kNB];
     uint32_t total = 0u;
     const uint32_t excl = block_exclusive_scan_u32<kT>(sum, s_scan, &total);
+    // (bins past nb hold nothing: their starts, all `total`, and masses are
+    // not written; the merge reads them as empty)
     uint32_t* st = a.starts + rs * kStarts;
     uint32_t o = excl;
+    uint32_t plim = kNB + 1;   // first bin starting at or past kPairs
 #pragma unroll
-    for (int q = 0; q < 4; ++q) { st[4 * tid + q] = o; CNT[4 * tid + q] = o; o += c4[q]; }
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t j = 4 * tid + q;
+        if (j <= nb) st[j] = o;
+        if (o >= uint32_t(kPairs)) plim = min(plim, j);
+        CNT[j] = o;
+        o += c4[q];
+    }
+    if (plim <= kNB) atomicMin(&s_plim, plim);
     unsigned long long* ms = a.mass + rs * kNB;
-    for (int i = tid; i < kNB; i += kT) ms[i] = MASS[i];
+    for (int i = tid; i < int(nb); i += kT) ms[i] = MASS[i];
+    const uint32_t npairs = min(total + deep, uint32_t(kPairs));
     if (tid == 0) {
         st[kNB] = total;
         st[kNB + 1] = total + deep;
         CNT[kNB] = total;
-        *hd = WideHead{anchor, top, total + deep, s_flags, {0u, 0u, 0u}};
+        if (total >= uint32_t(kPairs)) atomicMin(&s_plim, uint32_t(kNB));
+        *hd = WideHead{anchor, top, total + deep, s_flags, nb, npairs, 0u};
     }
     __syncthreads();
 
-    // the (key, offset) pairs grouped by bin: placed in LDS, then written out
-    // whole (coalesced 16-byte stores in place of a scattered store per pair)
+    // the (key, offset) pairs of list positions below kPairs, grouped by bin:
+    // placed in LDS, then written out whole (coalesced 16-byte stores)
     uint16_t* SOFF = reinterpret_cast<uint16_t*>(MASS);
+    const uint32_t pl = s_plim;
     auto put = [&](uint32_t key, uint16_t b, int off) {
-        if (!key) return;
+        if (!key || b >= pl) return;
         const uint32_t pos = atomicAdd(&CNT[b], 1u);
-        if (pos < uint32_t(kSL)) { SKEY[pos] = key; SOFF[pos] = uint16_t(off); }
+        if (pos < uint32_t(kPairs)) { SKEY[pos] = key; SOFF[pos] = uint16_t(off); }
     };
 #pragma unroll
     for (int i = 0; i < kVPT; ++i)
@@ -344,7 +371,7 @@ __global__ __launch_bounds__(kT) void wide_slice_kernel(WideArgs a) {
     put(hk, hbin, tid);
     put(tk, tbin, g.head + 4 * g.nvec + tid);
     __syncthreads();
-    const int n = int(min(total + deep, uint32_t(kSL)));
+    const int n = int(npairs);
     uint4* ko = reinterpret_cast<uint4*>(a.keys + rs * kSL);
     uint4* io = reinterpret_cast<uint4*>(a.ids + rs * kSL);
     for (int c = tid; c < (n + 3) / 4; c += kT) ko[c] = reinterpret_cast<const uint4*>(SKEY)[c];
@@ -367,6 +394,12 @@ struct MergeLds {
     // slices
     int delta[kMaxSlices];          // A - anchor_s (kNB + 1: wholly deep; -1: no valid logit)
     uint32_t lo[kMaxSlices], pre[kMaxSlices + 1], pcnt[kMaxSlices];
+    uint32_t nbin[kMaxSlices], npairs[kMaxSlices];   // the slice heads' nbins and npairs
+    double sanc[kMaxSlices];        // the slices' anchors
+    // pairs recomputed from the logits: per slice the row bin last done, and
+    // the slice bins and list end of the current one
+    int matJ[kMaxSlices], mjlo[kMaxSlices], mjhi[kMaxSlices];
+    uint32_t mhi[kMaxSlices], mmask, mcnt;
     // scratch for block decisions
     uint32_t u0, u1, u2, u3, kmin, kmax;
     unsigned long long f0;
@@ -387,10 +420,48 @@ struct RowCtx {
     int row, S;
     size_t rs0;       // row * slices
     double A, z0;
+    const vi_row_params* p;
+    WPen w;           // the row's penalties, as the slice pass applied them
+    float inv_t;
 };
 
 __device__ __forceinline__ double unit_of(const RowCtx& c, int J) {   // 2^-31 x exp(bin floor - z0)
     return kFixScale * exp((c.A - double(J)) / kPerUnit - c.z0);
+}
+
+// Pairs of the slices in `mask` at their list ranges [lo, mhi), for bins past
+// the positions the slice pass wrote: each slice's logits are read again and
+// keyed and binned as the slice pass did (same penalties, temperature and
+// anchor), so the range receives exactly its pairs (in another order within
+// the range, which no reader depends on).  All threads.
+__device__ void materialize(const RowCtx& c, MergeLds& L, uint32_t mask) {
+    const WideArgs& a = *c.a;
+    const int tid = threadIdx.x;
+    while (mask) {
+        const int s = __builtin_ctz(mask);
+        mask &= mask - 1u;
+        if (tid == 0) L.mcnt = 0u;
+        __syncthreads();
+        const WGeo g = wgeo(a, c.row, s);
+        const double anchor = L.sanc[s];
+        const int jlo = L.mjlo[s], jhi = L.mjhi[s];
+        const uint32_t lo = L.lo[s], cnt = L.mhi[s] - lo;
+        uint32_t* ko = a.keys + (c.rs0 + s) * kSL + lo;
+        uint16_t* io = a.ids + (c.rs0 + s) * kSL + lo;
+        bool bad = false;
+        for (int x = tid; x < g.n; x += kT) {
+            const int t = g.s0 + x;
+            const uint32_t k = logit_key(c.w, *c.p, c.inv_t, t, g.base[x], c.w.on ? c.w.bits[t >> 5] : 0u, &bad);
+            if (!k) continue;
+            const int b = bin_weight(k, anchor).bin;
+            if (b < jlo || b > jhi) continue;
+            const uint32_t pos = atomicAdd(&L.mcnt, 1u);
+            if (pos < cnt) { ko[pos] = k; io[pos] = uint16_t(x); }
+        }
+        __syncthreads();
+    }
+    __threadfence();   // (the stores, then the reads of this workgroup)
+    __syncthreads();
 }
 
 // Candidates of row bin J: per slice the list range [lo, hi); staged in LDS
@@ -400,23 +471,36 @@ __device__ void gather_bin(const RowCtx& c, MergeLds& L, int J) {
     const int tid = threadIdx.x;
     if (tid < kWave) {
         uint32_t lo = 0u, hi = 0u;
+        int jlo = 0, jhi = -1;
         if (tid < c.S && L.delta[tid] >= 0) {
             const uint32_t* st = a.starts + (c.rs0 + tid) * kStarts;
-            const int d = L.delta[tid];
+            const int d = L.delta[tid], nb = int(L.nbin[tid]);
             if (J < kNB) {
-                if (d <= J) { lo = st[J - d]; hi = st[J - d + 1]; }   // (d <= J < kNB)
-            } else {
-                lo = st[max(0, kNB - d)];
+                if (d <= J && J - d < nb) { lo = st[J - d]; hi = st[J - d + 1]; jlo = jhi = J - d; }
+            } else {   // the slice's bins from kNB - d on and its deep bin
+                jlo = max(0, kNB - d);
+                jhi = kDeep;
+                lo = st[min(jlo, nb)];
                 hi = st[kNB + 1];
             }
         }
+        bool mat = false;
+        if (tid < c.S && hi > lo && hi > L.npairs[tid] && L.matJ[tid] != J) {
+            mat = true;
+            L.matJ[tid] = J;
+            L.mjlo[tid] = jlo;
+            L.mjhi[tid] = jhi;
+            L.mhi[tid] = hi;
+        }
+        const uint64_t mm = ballot(mat);
         const uint32_t cnt = hi - lo;
         const uint32_t incl = wave_incl_scan_u32(cnt);
         if (tid < kMaxSlices) { L.lo[tid] = lo; L.pre[tid] = incl - cnt; }
         if (tid == kWave - 1) { L.n = incl; L.pre[kMaxSlices] = incl; L.staged = incl <= uint32_t(kCap) ? 1u : 0u; }
-        if (tid == 0) { L.kmin = 0xffffffffu; L.kmax = 0u; }
+        if (tid == 0) { L.kmin = 0xffffffffu; L.kmax = 0u; L.mmask = uint32_t(mm); }
     }
     __syncthreads();
+    if (L.mmask) materialize(c, L, L.mmask);
     const uint32_t n = L.n;
     uint32_t mn = 0xffffffffu, mx = 0u;
     for (uint32_t i = tid; i < n; i += kT) {
@@ -761,9 +845,13 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
             d = dd < double(kNB + 1) ? int(dd) : kNB + 1;
         }
         L.delta[tid] = d;
+        L.nbin[tid] = hd.nbins;
+        L.npairs[tid] = hd.npairs;
+        L.sanc[tid] = hd.anchor;
+        L.matJ[tid] = -1;
     }
     __syncthreads();
-    RowCtx c{&a, row, S, rs0, A, z0};
+    RowCtx c{&a, row, S, rs0, A, z0, &p, wpen(a, row, p), 1.0f / p.temperature};
 
     // ---- 1. the row's bins: counts and masses summed over the slices (thread t:
     // bins 4t .. 4t + 3), then their exclusive prefixes in bin order
@@ -777,14 +865,14 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
         bool on[4][4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int sc = min(s0 + u, S - 1), d = L.delta[sc];
+            const int sc = min(s0 + u, S - 1), d = L.delta[sc], nb = int(L.nbin[sc]);
             const bool live = s0 + u < S && d >= 0 && d < kNB;
             const uint32_t* st = a.starts + (rs0 + sc) * kStarts;
             const unsigned long long* ms = a.mass + (rs0 + sc) * kNB;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int j = 4 * tid + q - d;
-                on[u][q] = live && j >= 0;
+                on[u][q] = live && j >= 0 && j < nb;
                 const int jc = on[u][q] ? j : 0;
                 lo[u][q] = st[jc];
                 hi[u][q] = st[jc + 1];
