@@ -551,7 +551,9 @@ size_t full_verify_bytes(int lanes, int drafts, int vocabulary) {
     b += align_up(rows * 4, 256);
     b += align_up(size_t(lanes) * full_ranges(vocabulary) * 2 * 8, 256) +
          align_up(size_t(lanes) * full_ranges(vocabulary) * 2 * 4, 256);
-    return b + full_sampler_bytes(lanes * (drafts + 1), vocabulary) + 2048;
+    // (one sampler workspace per row set: the two sets are sampled side by side)
+    return b + full_sampler_bytes(lanes * (drafts + 1), vocabulary) + full_sampler_bytes(lanes * drafts, vocabulary) +
+           2304;
 }
 bool full_path_ok(const void* logits, int dtype, int vocabulary, int64_t stride) {
     if (dtype == VI_F32) return wide_supported(vocabulary, stride) && reinterpret_cast<uintptr_t>(logits) % 4 == 0;
@@ -694,24 +696,39 @@ vi_status launch_verify(const VerifyArgs& a, void* ws, size_t ws_bytes, hipStrea
         double* rsum = c.take<double>(size_t(a.lanes) * ranges * 2);
         int* rlast = c.take<int>(size_t(a.lanes) * ranges * 2);
         const size_t fbytes = full_sampler_bytes(v.trows, a.vocabulary);
+        const size_t dbytes = full_sampler_bytes(a.lanes * a.drafts, a.vocabulary);
         unsigned char* fws = c.take<unsigned char>(fbytes);
+        unsigned char* dws = c.take<unsigned char>(dbytes);
         if (!c.ok) return VI_ERR_WORKSPACE;
         hipLaunchKernelGGL(verify_row_params_kernel, dim3((trows + drows + 255) / 256), dim3(256), 0, stream,
                            a.params, a.lanes, a.target_rows, tpar, a.drafts, dpar);
         // the rows' filtered distributions (and the target rows' draws) from the
-        // full-vocabulary sampler, one row set after the other in one workspace
+        // full-vocabulary sampler, each row set in its own workspace: the draft
+        // rows on the side stream beside the target rows on the caller's, joined
+        // back before the accept launch
         auto sample = [&](const void* logits, int dtype, int rows, int64_t stride, const vi_row_params* par,
-                          int32_t* tok, vi_sample_stats* stats, const FullOut* out) {
+                          int32_t* tok, vi_sample_stats* stats, const FullOut* out, unsigned char* w, size_t wb,
+                          hipStream_t on) {
             SampleArgs s{};
             s.logits = logits; s.dtype = dtype; s.rows = rows; s.vocabulary = a.vocabulary; s.stride = stride;
             s.params = par; s.tokens = tok; s.stats = stats; s.route_mask = VI_ROUTE_FULL; s.full_out = out;
-            return dtype == VI_F32 ? launch_wide(s, fws, fbytes, nullptr, 0, 0, nullptr, stream)
-                                   : launch_full(s, fws, fbytes, stream);
+            return dtype == VI_F32 ? launch_wide(s, w, wb, nullptr, 0, 0, nullptr, on) : launch_full(s, w, wb, on);
         };
         const FullOut tout{tb, tbase}, dout{db, dbase};
-        st = sample(a.target, a.target_dtype, trows, a.target_stride, tpar, ttok, tst, &tout);
-        if (st != VI_OK) return st;
-        st = sample(a.draft, a.draft_dtype, drows, a.draft_stride, dpar, dtok, dst, &dout);
+        SideStream* side = drows > 0 ? side_stream() : nullptr;
+        if (side && (hipEventRecord(side->fork, stream) != hipSuccess ||
+                     hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess)) {
+            (void)hipGetLastError();
+            side = nullptr;
+        }
+        st = sample(a.draft, a.draft_dtype, drows, a.draft_stride, dpar, dtok, dst, &dout, dws, dbytes,
+                    side ? side->stream : stream);
+        if (st == VI_OK)
+            st = sample(a.target, a.target_dtype, trows, a.target_stride, tpar, ttok, tst, &tout, fws, fbytes, stream);
+        // joined also when a launch failed: the side work uses the caller's workspace
+        if (side && (hipEventRecord(side->join, side->stream) != hipSuccess ||
+                     hipStreamWaitEvent(stream, side->join, 0) != hipSuccess))
+            return VI_ERR_LAUNCH;
         if (st != VI_OK) return st;
         FullVerifyArgs f{};
         f.t = FullRows{a.target, a.target_dtype, a.target_stride, tb, tbase, tst,
