@@ -407,6 +407,8 @@ struct MergeLds {
     uint32_t staged, n;
 };
 
+static_assert(offsetof(MergeLds, CI) % 8 == 0, "CI also holds 64-bit partial sums");
+
 // Result of narrowing one bin: the key the target falls on, the rank there,
 // and what the bin's higher keys hold.
 struct RHit {
@@ -802,8 +804,8 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
 
     // ---- 0. slice heads: the row's anchor, top key, valid logits and flags
     __shared__ double s_anchor;
-    __shared__ uint32_t s_top, s_valid, s_flags;
-    if (tid == 0) { s_top = 0u; s_valid = 0u; s_flags = 0u; s_anchor = 0.0; }
+    __shared__ uint32_t s_top, s_valid, s_flags, s_rb;
+    if (tid == 0) { s_top = 0u; s_valid = 0u; s_flags = 0u; s_anchor = 0.0; s_rb = 0u; }
     __syncthreads();
     WideHead hd{};
     if (tid < S) {
@@ -845,6 +847,7 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
             d = dd < double(kNB + 1) ? int(dd) : kNB + 1;
         }
         L.delta[tid] = d;
+        if (d >= 0 && d < kNB) atomicMax(&s_rb, uint32_t(min(kNB, d + int(hd.nbins))));   // (row bins in use)
         L.nbin[tid] = hd.nbins;
         L.npairs[tid] = hd.npairs;
         L.sanc[tid] = hd.anchor;
@@ -856,22 +859,29 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
     // ---- 1. the row's bins: counts and masses summed over the slices (thread t:
     // bins 4t .. 4t + 3), then their exclusive prefixes in bin order
     // (four slices' loads issued together, unconditional at clamped places
-    // and dropped afterwards: a load under a branch waits for the ones before)
+    // and dropped afterwards: a load under a branch waits for the ones before).
+    // When the row's bins in use fit in a half or a quarter of the 4,096, the
+    // slices are shared out between two or four groups of threads (fewer
+    // dependent load rounds each), whose sums meet in LDS.
+    const int rb = int(s_rb);
+    const int ways = rb <= kNB / 4 ? 4 : rb <= kNB / 2 ? 2 : 1;
+    const int per = kT / ways, way = tid / per, quad = tid - way * per;
+    const int sp = (S + ways - 1) / ways, sb = min(S, way * sp), se = min(S, sb + sp);
     uint32_t bc[4] = {0u, 0u, 0u, 0u};
     unsigned long long bf[4] = {0ull, 0ull, 0ull, 0ull};
-    for (int s0 = 0; s0 < S; s0 += 4) {
+    for (int s0 = sb; s0 < se; s0 += 4) {
         uint32_t lo[4][4], hi[4][4];
         unsigned long long mv[4][4];
         bool on[4][4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int sc = min(s0 + u, S - 1), d = L.delta[sc], nb = int(L.nbin[sc]);
-            const bool live = s0 + u < S && d >= 0 && d < kNB;
+            const int sc = min(s0 + u, se - 1), d = L.delta[sc], nb = int(L.nbin[sc]);
+            const bool live = s0 + u < se && d >= 0 && d < kNB;
             const uint32_t* st = a.starts + (rs0 + sc) * kStarts;
             const unsigned long long* ms = a.mass + (rs0 + sc) * kNB;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int j = 4 * tid + q - d;
+                const int j = 4 * quad + q - d;
                 on[u][q] = live && j >= 0 && j < nb;
                 const int jc = on[u][q] ? j : 0;
                 lo[u][q] = st[jc];
@@ -884,6 +894,29 @@ __global__ __launch_bounds__(kT) void wide_merge_kernel(WideArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 if (on[u][q]) { bc[q] += hi[u][q] - lo[u][q]; bf[q] += mv[u][q]; }
+    }
+    if (ways > 1) {   // (the staging arrays are free until the first gather)
+        unsigned long long* pm = reinterpret_cast<unsigned long long*>(L.CI);
+        static_assert(3 * (kT / 4) * 4 <= kCap && 3 * (kT / 4) * 4 * 2 <= kCap, "partial sums staging");
+        if (way > 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                L.CK[((way - 1) * per + quad) * 4 + q] = bc[q];
+                pm[((way - 1) * per + quad) * 4 + q] = bf[q];
+            }
+        }
+        __syncthreads();
+        if (way == 0) {
+            for (int w = 1; w < ways; ++w)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bc[q] += L.CK[((w - 1) * per + quad) * 4 + q];
+                    bf[q] += pm[((w - 1) * per + quad) * 4 + q];
+                }
+        } else {   // (their bins 4 tid .. 4 tid + 3 lie past the bins in use)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { bc[q] = 0u; bf[q] = 0ull; }
+        }
     }
     double bm[4];
     uint32_t csum = 0u;
